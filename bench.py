@@ -1,0 +1,210 @@
+"""Benchmark: llama-family decode & prefill tokens/s on one MI355X.
+
+Workload ("C2"): Llama-3.2-1B-shape decoder, bf16
+weights (random init N(0, 0.02), synthetic), batch 1, a 512-token
+uniform-random prompt prefill followed by 256 greedy decode steps. One
+"step" is that whole generation; `value` is decode tokens/s.
+
+Extra fields report the prefill rate, the decode HBM roofline fraction
+for the whole step, and the dominant kernel's roofline from HIP events
+recorded on the KV handle's stream around every launch of that kernel
+family in a profiled pass. `cpu_baseline` times the CPU restatement of
+esp's burn-ndarray path (oracle/) on a bounded sample of the same decode.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, AMD spec
+BF16_PEAK_TFLOPS = 2516.6      # MI355X dense bf16 MFMA, AMD spec
+
+
+def c2_config(max_pos=2048):
+    from tests.synth import llama_config
+    return llama_config(16, 2048, 32, 8, 8192, 128256, theta=500000.0, max_pos=max_pos,
+                        extra={"tie_word_embeddings": True})
+
+
+def decode_bytes(cfg, ctx: int, kv_bytes_per_elem: int = 4) -> dict:
+    """Algorithmic HBM bytes of one batch-1 decode step at context `ctx`."""
+    H, L, F, V = cfg.hidden_size, cfg.num_hidden_layers, cfg.intermediate_size, cfg.vocab_size
+    qw, kvw = cfg.query_width(), cfg.kv_heads() * cfg.head_dim()
+    layer_w = (H * (qw + 2 * kvw) + H * qw + 3 * H * F) * 2
+    head_w = V * H * 2
+    kv = 2 * L * kvw * ctx * kv_bytes_per_elem
+    return {"gemv_weights": L * layer_w + head_w, "kv": kv, "total": L * layer_w + head_w + kv}
+
+
+def prefill_flops(cfg, S: int) -> float:
+    H, L, F, V = cfg.hidden_size, cfg.num_hidden_layers, cfg.intermediate_size, cfg.vocab_size
+    qw, kvw, hd, nq = cfg.query_width(), cfg.kv_heads() * cfg.head_dim(), cfg.head_dim(), \
+        cfg.num_attention_heads
+    gemm = 2.0 * S * L * (H * (qw + 2 * kvw) + H * qw + 3 * H * F)
+    attn = 2.0 * 2.0 * L * nq * hd * S * (S + 1) / 2
+    head = 2.0 * H * V
+    return gemm + attn + head
+
+
+def cpu_baseline(cfg, ctx: int, budget_s: float = 15.0) -> dict:
+    """Oracle (CPU restatement of esp's f32 corridor) decode on the host
+    cores: same shape, bf16 weights widened to f32 on the fly, KV cache
+    filled synthetically to `ctx` positions."""
+    import numpy as np
+    from oracle import oracle
+    threads = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    threads = max(1, min(threads, 16))
+    oracle.set_threads(threads)
+    H, F, V = cfg.hidden_size, cfg.intermediate_size, cfg.vocab_size
+    qw, kvw = cfg.query_width(), cfg.kv_heads() * cfg.head_dim()
+    tensors = {}
+    seed = 1
+
+    def put(name, shape, one=False):
+        nonlocal seed
+        n = int(np.prod(shape))
+        if one:
+            tensors[name] = (np.ones(shape, np.float32), "F32")
+        else:
+            seed += 1
+            tensors[name] = (oracle.fill_normal(seed, n, 0.02, True).reshape(shape), "BF16")
+
+    put("model.embed_tokens.weight", (V, H))
+    put("model.norm.weight", (H,), True)
+    for l in range(cfg.num_hidden_layers):
+        p = f"model.layers.{l}."
+        put(p + "input_layernorm.weight", (H,), True)
+        put(p + "post_attention_layernorm.weight", (H,), True)
+        put(p + "self_attn.q_proj.weight", (qw, H))
+        put(p + "self_attn.k_proj.weight", (kvw, H))
+        put(p + "self_attn.v_proj.weight", (kvw, H))
+        put(p + "self_attn.o_proj.weight", (H, qw))
+        put(p + "mlp.gate_proj.weight", (F, H))
+        put(p + "mlp.up_proj.weight", (F, H))
+        put(p + "mlp.down_proj.weight", (H, F))
+    m = oracle.OracleModel(cfg, tensors)
+    kv = m.new_cache(ctx + 80)
+    kv.fill_synthetic(ctx, 5)
+    m.forward_last(kv, [1])  # warm-up
+    steps, t0 = 0, time.perf_counter()
+    while True:
+        m.forward_last(kv, [steps % V])
+        steps += 1
+        el = time.perf_counter() - t0
+        if el > budget_s or steps >= 64:
+            break
+    return {"value": round(steps / el, 4), "unit": "tokens/s", "cores": threads,
+            "kind": "port",
+            "sample": f"{steps} batch-1 decode steps at context {ctx}+ of the C2 shape "
+                      f"(16 layers, bf16 weights widened to f32), CPU restatement of esp's "
+                      f"burn-ndarray path, OpenMP over {threads} threads"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=3)
+    ap.add_argument("--warmup", type=int, default=1)
+    ap.add_argument("--prompt", type=int, default=512)
+    ap.add_argument("--decode", type=int, default=256)
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 "
+                                   "(multi-GPU sharding is design-only)"}))
+        sys.exit(2)
+    from esp_amd import DecoderModel
+    from esp_amd.model import profile_enable, profile_read
+    from tests.synth import uniform_ids
+
+    cfg = c2_config()
+    model = DecoderModel.synthetic(cfg, seed=1234, std=0.02, fmt="bf16")
+    prompt = uniform_ids(42, args.prompt, cfg.vocab_size)
+    ctx = args.prompt + args.decode
+    kv = model.new_cache(1, ctx)
+
+    def gen():
+        return model.generate_greedy_device(kv, prompt, args.decode, eos=[])
+
+    def prefill():
+        kv.reset(0)
+        model.try_forward_cached_last(prompt, kv)
+
+    for _ in range(args.warmup):
+        gen()
+        prefill()
+    t_gen, t_pre = [], []
+    for _ in range(args.steps):
+        t0 = time.perf_counter()
+        out = gen()
+        t_gen.append(time.perf_counter() - t0)
+        assert len(out) == args.decode
+    for _ in range(args.steps):
+        t0 = time.perf_counter()
+        prefill()
+        t_pre.append(time.perf_counter() - t0)
+    tg = sorted(t_gen)[len(t_gen) // 2]
+    tp = sorted(t_pre)[len(t_pre) // 2]
+    n_dec = args.decode - 1
+    t_dec = tg - tp
+    dec_tps = n_dec / t_dec
+    pre_tps = args.prompt / tp
+    avg_ctx = args.prompt + args.decode / 2
+    db = decode_bytes(cfg, int(avg_ctx))
+    # profiled pass: per-launch HIP events on the KV stream for the GEMV family
+    profile_enable("gemv", True)
+    gen_eager_steps = 16
+    kv2 = model.new_cache(1, ctx)
+    kv2.reset(0)
+    model.try_forward_cached_last(prompt, kv2)
+    n0, ms0 = profile_read("gemv")
+    for i in range(gen_eager_steps):
+        model.try_forward_cached_last([i + 1], kv2)
+    n1, ms1 = profile_read("gemv")
+    profile_enable("gemv", False)
+    gemv_launches = n1 - n0
+    gemv_ms = ms1 - ms0
+    gemv_bytes = db["gemv_weights"] * gen_eager_steps
+    gemv_gbs = gemv_bytes / (gemv_ms / 1e3) / 1e9
+    result = {
+        "metric": "decode & prefill tokens/s on 1 MI355X; % of HBM / bf16-MFMA roofline",
+        "value": round(dec_tps, 2),
+        "unit": "tokens/s (decode, batch 1)",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(tg * 1e3, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16 weights, f32 activations/accumulation",
+        "data": "synthetic (random-init N(0,0.02) weights, uniform-random prompt ids)",
+        "config": {"workload": "C2: Llama-3.2-1B shape, 512-token prefill + 256 greedy decode "
+                               "steps, batch 1 (BASELINE configs[1])",
+                   "global_batch": 1, "seq_len": ctx, "parallelism": "none (1 GPU)"},
+        "prefill_tokens_per_s": round(pre_tps, 1),
+        "prefill_ms": round(tp * 1e3, 3),
+        "prefill_mfma_frac": round(prefill_flops(cfg, args.prompt) / tp / 1e12 / BF16_PEAK_TFLOPS, 4),
+        "decode_ms_per_token": round(t_dec / n_dec * 1e3, 4),
+        "decode_hbm_frac": round(db["total"] / (t_dec / n_dec) / 1e9 / HBM_PEAK_GBS, 4),
+        "roofline": {"bound": "hbm", "kernel": "gemv (decode projections + head)",
+                     "achieved": round(gemv_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gemv_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "launches": gemv_launches,
+                     "avg_launch_us": round(gemv_ms / max(1, gemv_launches) * 1e3, 3)},
+    }
+    print(f"gpu: decode {dec_tps:.1f} tok/s, prefill {pre_tps:.1f} tok/s, gemv {gemv_gbs:.0f} GB/s",
+          file=sys.stderr, flush=True)
+    if not args.no_cpu:
+        result["cpu_baseline"] = cpu_baseline(cfg, int(avg_ctx))
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

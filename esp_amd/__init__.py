@@ -1,0 +1,13 @@
+"""MI355X-native llama-family decoder forward behind esp's model-execution API.
+
+The compute path is the HIP library esp_amd/libesp_hip.so (C ABI in
+include/esp_hip.h); this package is the host-side mirror of the reference's
+decoder interface (config parsing, model/KV handles, the generation loop and
+the sampler) driving that library through ctypes.
+"""
+from .errors import (Backend, InferError, Interrupted, InvalidConfig, InvalidRequest,  # noqa: F401
+                     InvalidWeights, ModelNotLoaded, PromptTooLong, StageUnavailable, Unsupported)
+from .config import DecoderConfig, MoeConfig, RopeScaling  # noqa: F401
+from .model import DecoderModel, KvCache  # noqa: F401
+from .generate import TokenPicker, generate_ids, generate_ids_with  # noqa: F401
+from .sample import Sampler  # noqa: F401

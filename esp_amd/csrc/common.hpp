@@ -1,0 +1,137 @@
+// Internal declarations shared by the host runtime and the HIP kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <string>
+
+#include "../../include/esp_hip.h"
+
+namespace esp {
+
+struct Error {
+    esp_status code;
+    std::string msg;
+};
+
+[[noreturn]] inline void fail(esp_status code, std::string msg) { throw Error{code, std::move(msg)}; }
+
+#define ESP_HIP(x)                                                                         \
+    do {                                                                                   \
+        hipError_t e_ = (x);                                                               \
+        if (e_ != hipSuccess)                                                              \
+            ::esp::fail(ESP_BACKEND, std::string(#x) + ": " + hipGetErrorString(e_));     \
+    } while (0)
+
+typedef uint16_t bf16_t;  // raw bf16 bits in host code
+
+// Activation/weight element kinds used to instantiate kernels.
+enum Dt { DT_F32 = 0, DT_BF16 = 1 };
+
+inline size_t dt_size(Dt d) { return d == DT_F32 ? 4 : 2; }
+
+// ---------------------------------------------------------------------------
+// Kernel launch interfaces (implemented in the .hip files). Every launcher
+// takes the stream explicitly; shapes are validated by the caller.
+
+// Row descriptors of one forward: token row r belongs to sequence
+// row_seq[r] at absolute position row_pos[r].
+struct Rows {
+    const int32_t *ids;      // [M]
+    const int32_t *row_seq;  // [M]
+    const int32_t *row_pos;  // [M]
+    int M;
+};
+
+// h[M,H] (f32) = embed[ids[m]] (wt)
+void launch_embed(Dt wt, const void *embed, const int32_t *ids, int M, int H, float *h,
+                  hipStream_t s);
+
+// out[M,H] (dt out) = x / sqrt(mean(x^2)+eps) * gamma ; rows selected by
+// row_index (nullable = identity).
+void launch_rmsnorm(const float *x, const float *gamma, float eps, int M, int H, Dt out_dt,
+                    void *out, const int32_t *row_index, hipStream_t s);
+
+// GEMV (one input row): y = W x with the input RMS-normalised on the fly
+// when gamma != nullptr. Epilogue kinds below.
+enum GemvEpi { GEMV_STORE = 0, GEMV_RESIDUAL = 1, GEMV_SWIGLU = 2 };
+struct GemvArgs {
+    const void *w;     // [N, K] wt (SWIGLU: gate rows)
+    const void *w2;    // SWIGLU: up rows [N, K]
+    const float *x;    // [K] f32
+    const float *gamma;  // nullable: fused RMSNorm of x
+    float eps;
+    const float *bias;   // nullable [N]
+    float *y;            // STORE/SWIGLU: out [N]; RESIDUAL: y[n] += result
+    int N, K;
+};
+void launch_gemv(Dt wt, GemvEpi epi, const GemvArgs &a, hipStream_t s);
+
+// GEMM (several input rows): C[M,N] = A[M,K] * W[N,K]^T with f32 activations
+// A, weights W in the model format, f32 accumulation.
+enum GemmEpi { GEMM_STORE = 0, GEMM_RESIDUAL = 1, GEMM_SWIGLU = 2 };
+struct GemmArgs {
+    const void *a;     // [M, K] act
+    const void *w;     // [N, K] wt
+    const void *w2;    // SWIGLU up rows
+    const float *bias; // nullable [N]
+    void *c;           // STORE: f32 [M, ldc]; RESIDUAL: f32 +=; SWIGLU: f32 [M, ldc]
+    int M, N, K, ldc;
+};
+void launch_gemm(Dt wt, GemmEpi epi, const GemmArgs &a, hipStream_t s);
+
+// QKV post-processing: LoRA B-adds, optional QK RMSNorm, RoPE at each row's
+// position, K/V append into the cache, q written as f32 [M, nq, hd].
+struct RopeKvArgs {
+    const float *qkv;   // [M, ldq] raw projection (+bias): q | k | v | lora t
+    int ldq;
+    float *q_out;       // [M, nq*hd] f32
+    const float *rope_cos, *rope_sin;  // [max_pos, hd]
+    const float *q_norm, *k_norm;      // nullable [hd]
+    float eps;
+    // LoRA: t for target j at qkv column lora_t_col[j] (rank lora_rank[j]),
+    // B_j [out, rank] (wt), scale lora_scale[j]; targets 0 q, 1 k, 2 v.
+    const void *lora_b[3];
+    int lora_t_col[3], lora_rank[3];
+    float lora_scale[3];
+    Rows rows;
+    void *kv;           // cache base (kv dt)
+    long long seq_stride, layer_stride, kv_half_stride, head_stride;  // elements
+    int nq, nkv, hd;
+};
+void launch_rope_kv(Dt wt, Dt kvdt, const RopeKvArgs &a, hipStream_t s);
+
+// Attention over the cache for each row (causal, optional sliding window).
+struct AttnArgs {
+    const float *q;     // [M, nq*hd] f32 (post RoPE)
+    const void *kv;     // cache base
+    long long seq_stride, layer_stride, kv_half_stride, head_stride;
+    Rows rows;
+    int nq, nkv, hd, window;  // window 0 = none
+    float *part;        // scratch partials
+    int n_split, split_len;
+    void *out;          // [M, nq*hd] out dt
+    Dt out_dt;
+};
+void launch_attention(Dt kvdt, const AttnArgs &a, hipStream_t s);
+
+// Token pick over logits rows.
+struct PickArgs {
+    const float *logits;  // [n, V]
+    int n, V;
+    const uint32_t *allowed;  // nullable [n, ceil(V/32)]
+    const esp_sampler *samplers;  // nullable device copy [n]
+    uint32_t *ids_out;     // [n]
+    uint8_t *flags_out;    // [n]
+    uint64_t *state_out;   // [n] advanced sampler states
+    void *scratch;         // sampling scratch
+    size_t scratch_bytes;
+};
+void launch_pick(const PickArgs &a, hipStream_t s);
+size_t pick_scratch_bytes(int n, int V);
+
+// Device-side generation hand-off (see k_basic.hip).
+void launch_gen_step(const uint32_t *picked, int32_t *gen, hipStream_t s);
+
+}  // namespace esp

@@ -1,0 +1,58 @@
+// Device-side helpers shared by the kernel files (gfx950, wave64).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace esp {
+
+__device__ __forceinline__ float bf2f(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
+
+// f32 -> bf16 bits, round to nearest even (quiet NaN preserved).
+__device__ __forceinline__ uint16_t f2bf(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+
+template <typename T> __device__ __forceinline__ float ld(const T *p, size_t i);
+template <> __device__ __forceinline__ float ld<float>(const float *p, size_t i) { return p[i]; }
+template <> __device__ __forceinline__ float ld<uint16_t>(const uint16_t *p, size_t i) {
+    return bf2f(p[i]);
+}
+
+template <typename T> __device__ __forceinline__ void st(T *p, size_t i, float v);
+template <> __device__ __forceinline__ void st<float>(float *p, size_t i, float v) { p[i] = v; }
+template <> __device__ __forceinline__ void st<uint16_t>(uint16_t *p, size_t i, float v) {
+    p[i] = f2bf(v);
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+
+// Block-wide sum for blockDim.x a multiple of 64 (<= 1024). `red` needs 16 floats.
+__device__ __forceinline__ float block_sum(float v, float *red) {
+    v = wave_sum(v);
+    int w = threadIdx.x >> 6, l = threadIdx.x & 63;
+    __syncthreads();
+    if (l == 0) red[w] = v;
+    __syncthreads();
+    int nw = blockDim.x >> 6;
+    float t = 0.f;
+    for (int i = 0; i < nw; ++i) t += red[i];
+    return t;
+}
+
+__device__ __forceinline__ float silu(float x) { return x * (1.0f / (1.0f + expf(-x))); }
+
+}  // namespace esp

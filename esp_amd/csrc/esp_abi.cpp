@@ -1,0 +1,338 @@
+// extern "C" entry points of include/esp_hip.h. No exception crosses this
+// boundary: every failure becomes an esp_status plus a thread-local message.
+#include <stdlib.h>
+#include <string.h>
+
+#include <algorithm>
+#include <string>
+#include <vector>
+
+#include "kernels_extra.hpp"
+#include "profile.hpp"
+#include "runtime.hpp"
+
+namespace esp {
+Model *load_model(const esp_config *cfg, const uint8_t *bytes, size_t len,
+                  const esp_lora *adapters, uint32_t n_adapters);
+Model *synthetic_model(const esp_config *cfg, uint64_t seed, float std, uint32_t lora_rank,
+                       uint32_t lora_mask, float lora_a_std, float lora_b_std, float lora_scale);
+Kv *create_kv(Model *m, uint32_t batch, uint32_t max_ctx);
+void decode_step_dev(Model &m, Kv &kv, int seq, int max_t, int32_t *gen);
+void launch_gen_step(const uint32_t *picked, int32_t *gen, hipStream_t s);
+}  // namespace esp
+
+using namespace esp;
+
+static thread_local std::string g_err;
+
+template <typename F> static esp_status guard(F &&f) {
+    try {
+        f();
+        g_err.clear();
+        return ESP_OK;
+    } catch (const Error &e) {
+        g_err = e.msg;
+        return e.code;
+    } catch (const std::bad_alloc &) {
+        g_err = "host allocation failed";
+        return ESP_BACKEND;
+    } catch (const std::exception &e) {
+        g_err = e.what();
+        return ESP_BACKEND;
+    } catch (...) {
+        g_err = "unknown failure";
+        return ESP_BACKEND;
+    }
+}
+
+extern "C" {
+
+size_t esp_last_error(char *buf, size_t len) {
+    if (buf && len) {
+        size_t n = std::min(len - 1, g_err.size());
+        memcpy(buf, g_err.data(), n);
+        buf[n] = 0;
+    }
+    return g_err.size();
+}
+
+const char *esp_version(void) { return "esp-mi355x 0.1 (gfx950)"; }
+
+esp_status esp_model_load(const esp_config *config, const uint8_t *safetensors, size_t len,
+                          const esp_lora *adapters, uint32_t n_adapters, esp_model **out) {
+    return guard([&] {
+        if (!out) fail(ESP_INVALID_REQUEST, "null output handle");
+        *out = nullptr;
+        if (n_adapters && !adapters) fail(ESP_INVALID_REQUEST, "null adapter array");
+        *out = (esp_model *)load_model(config, safetensors, len, adapters, n_adapters);
+    });
+}
+
+esp_status esp_model_create_synthetic(const esp_config *config, uint64_t seed, float std,
+                                      uint32_t lora_rank, uint32_t lora_mask, float lora_a_std,
+                                      float lora_b_std, float lora_scale, esp_model **out) {
+    return guard([&] {
+        if (!out) fail(ESP_INVALID_REQUEST, "null output handle");
+        *out = nullptr;
+        *out = (esp_model *)synthetic_model(config, seed, std, lora_rank, lora_mask, lora_a_std,
+                                            lora_b_std, lora_scale);
+    });
+}
+
+esp_status esp_model_destroy(esp_model *model) {
+    return guard([&] {
+        if (model) {
+            (void)hipDeviceSynchronize();
+            delete (Model *)model;
+        }
+    });
+}
+
+esp_status esp_model_weight_bytes(const esp_model *model, uint64_t *bytes) {
+    return guard([&] {
+        if (!model) fail(ESP_MODEL_NOT_LOADED, "model not loaded");
+        if (bytes) *bytes = ((const Model *)model)->weight_bytes;
+    });
+}
+
+esp_status esp_kv_create(esp_model *model, uint32_t batch, uint32_t max_ctx, esp_kv **out) {
+    return guard([&] {
+        if (!out) fail(ESP_INVALID_REQUEST, "null output handle");
+        *out = nullptr;
+        *out = (esp_kv *)create_kv((Model *)model, batch, max_ctx);
+    });
+}
+
+esp_status esp_kv_destroy(esp_kv *kv) {
+    return guard([&] {
+        if (kv) {
+            Kv *k = (Kv *)kv;
+            (void)hipStreamSynchronize(k->stream);
+            delete k;
+        }
+    });
+}
+
+esp_status esp_kv_reset(esp_kv *kv, uint32_t seq) {
+    return guard([&] {
+        if (!kv) fail(ESP_INVALID_REQUEST, "null kv handle");
+        Kv *k = (Kv *)kv;
+        if (seq == UINT32_MAX) std::fill(k->pos.begin(), k->pos.end(), 0);
+        else if (seq < (uint32_t)k->batch) k->pos[seq] = 0;
+        else fail(ESP_INVALID_REQUEST, "sequence index out of range");
+    });
+}
+
+esp_status esp_kv_position(const esp_kv *kv, uint32_t seq, uint32_t *position) {
+    return guard([&] {
+        if (!kv) fail(ESP_INVALID_REQUEST, "null kv handle");
+        const Kv *k = (const Kv *)kv;
+        if (seq >= (uint32_t)k->batch) fail(ESP_INVALID_REQUEST, "sequence index out of range");
+        if (position) *position = (uint32_t)k->pos[seq];
+    });
+}
+
+esp_status esp_kv_stream(const esp_kv *kv, void **stream) {
+    return guard([&] {
+        if (!kv) fail(ESP_INVALID_REQUEST, "null kv handle");
+        if (stream) *stream = (void *)((const Kv *)kv)->stream;
+    });
+}
+
+static void copy_logits(Kv &kv, int rows, float *out) {
+    if (!out) return;
+    ESP_HIP(hipMemcpy(out, kv.logits.p, (size_t)rows * kv.model->V * 4, hipMemcpyDeviceToHost));
+}
+
+esp_status esp_forward_last(esp_model *model, esp_kv *kv, uint32_t seq, const int32_t *ids,
+                            uint32_t n, float *logits_out) {
+    return guard([&] {
+        if (!model) fail(ESP_MODEL_NOT_LOADED, "model not loaded");
+        if (!kv) fail(ESP_INVALID_REQUEST, "null kv handle");
+        if (!n || !ids) fail(ESP_INVALID_REQUEST, "cached input is empty or exceeds the context window");
+        Kv &k = *(Kv *)kv;
+        if (k.model != (Model *)model) fail(ESP_INVALID_REQUEST, "kv handle belongs to another model");
+        forward(*(Model *)model, k, 1, &seq, &n, ids);
+        copy_logits(k, 1, logits_out);
+    });
+}
+
+esp_status esp_forward_batch(esp_model *model, esp_kv *kv, uint32_t n_seqs, const uint32_t *seqs,
+                             const uint32_t *seq_lens, const int32_t *ids, float *logits_out) {
+    return guard([&] {
+        if (!model) fail(ESP_MODEL_NOT_LOADED, "model not loaded");
+        if (!kv) fail(ESP_INVALID_REQUEST, "null kv handle");
+        if (!n_seqs || !seqs || !seq_lens || !ids)
+            fail(ESP_INVALID_REQUEST, "cached input is empty or exceeds the context window");
+        Kv &k = *(Kv *)kv;
+        if (k.model != (Model *)model) fail(ESP_INVALID_REQUEST, "kv handle belongs to another model");
+        forward(*(Model *)model, k, (int)n_seqs, seqs, seq_lens, ids);
+        copy_logits(k, (int)n_seqs, logits_out);
+    });
+}
+
+esp_status esp_pick(esp_kv *kv, uint32_t n_rows, const uint32_t *allowed_bits,
+                    esp_sampler *samplers, uint32_t *ids_out, uint8_t *flags_out) {
+    return guard([&] {
+        if (!kv) fail(ESP_INVALID_REQUEST, "null kv handle");
+        Kv &k = *(Kv *)kv;
+        if (!n_rows || (int)n_rows > k.logits_rows)
+            fail(ESP_INVALID_REQUEST, "pick: rows exceed the logits of the last forward");
+        if (!ids_out) fail(ESP_INVALID_REQUEST, "pick: null ids_out");
+        const int V = k.model->V, words = (V + 31) / 32;
+        const size_t mask_b = allowed_bits ? (size_t)n_rows * words * 4 : 0;
+        const size_t smp_b = samplers ? (size_t)n_rows * sizeof(esp_sampler) : 0;
+        const size_t out_b = (size_t)n_rows * (4 + 1 + 8) + 64;
+        size_t off_mask = 0, off_smp = (mask_b + 255) / 256 * 256,
+               off_out = off_smp + (smp_b + 255) / 256 * 256;
+        k.pick_io.ensure(off_out + out_b);
+        char *io = (char *)k.pick_io.p;
+        hipStream_t s = k.stream;
+        if (mask_b) ESP_HIP(hipMemcpyAsync(io + off_mask, allowed_bits, mask_b, hipMemcpyHostToDevice, s));
+        if (smp_b) ESP_HIP(hipMemcpyAsync(io + off_smp, samplers, smp_b, hipMemcpyHostToDevice, s));
+        bool any_sampled = false;
+        for (uint32_t i = 0; samplers && i < n_rows; ++i) any_sampled |= samplers[i].temperature > 0.f;
+        size_t scr = any_sampled ? pick_scratch_bytes((int)n_rows, V) : 0;
+        k.pick_scratch.ensure(scr ? scr : 64);
+        PickArgs a{};
+        a.logits = k.logits.as<float>();
+        a.n = (int)n_rows;
+        a.V = V;
+        a.allowed = mask_b ? (const uint32_t *)(io + off_mask) : nullptr;
+        a.samplers = smp_b ? (const esp_sampler *)(io + off_smp) : nullptr;
+        uint32_t *d_ids = (uint32_t *)(io + off_out);
+        uint64_t *d_state = (uint64_t *)(io + off_out + (size_t)n_rows * 4 + 8 - ((size_t)n_rows * 4) % 8);
+        uint8_t *d_flags = (uint8_t *)(d_state + n_rows);
+        a.ids_out = d_ids;
+        a.flags_out = d_flags;
+        a.state_out = d_state;
+        a.scratch = k.pick_scratch.p;
+        a.scratch_bytes = k.pick_scratch.bytes;
+        {
+            Prof p("pick", s);
+            launch_pick(a, s);
+        }
+        std::vector<uint64_t> states(n_rows);
+        std::vector<uint8_t> flags(n_rows);
+        ESP_HIP(hipMemcpyAsync(ids_out, d_ids, (size_t)n_rows * 4, hipMemcpyDeviceToHost, s));
+        ESP_HIP(hipMemcpyAsync(states.data(), d_state, (size_t)n_rows * 8, hipMemcpyDeviceToHost, s));
+        ESP_HIP(hipMemcpyAsync(flags.data(), d_flags, n_rows, hipMemcpyDeviceToHost, s));
+        ESP_HIP(hipStreamSynchronize(s));
+        bool none = false;
+        for (uint32_t i = 0; i < n_rows; ++i) {
+            if (flags_out) flags_out[i] = flags[i];
+            if (samplers && samplers[i].temperature > 0.f && !(flags[i] & ESP_PICK_NO_ELIGIBLE))
+                samplers[i].state = states[i];
+            none |= (flags[i] & ESP_PICK_NO_ELIGIBLE) != 0;
+        }
+        if (none) fail(ESP_INVALID_REQUEST, "output grammar has no finite eligible token");
+    });
+}
+
+esp_status esp_generate_greedy(esp_model *model, esp_kv *kv, uint32_t seq, const int32_t *prompt,
+                               uint32_t n_prompt, uint32_t max_new, const int32_t *eos,
+                               uint32_t n_eos, int32_t *out_ids, uint32_t *n_out) {
+    return guard([&] {
+        if (!model) fail(ESP_MODEL_NOT_LOADED, "model not loaded");
+        if (!kv) fail(ESP_INVALID_REQUEST, "null kv handle");
+        if (!prompt || !n_prompt) fail(ESP_INVALID_REQUEST, "prompt must not be empty");
+        Model &m = *(Model *)model;
+        Kv &k = *(Kv *)kv;
+        if (k.model != &m) fail(ESP_INVALID_REQUEST, "kv handle belongs to another model");
+        if (seq >= (uint32_t)k.batch) fail(ESP_INVALID_REQUEST, "sequence index out of range");
+        long long last_pos = (long long)n_prompt + (max_new ? max_new - 1 : 0);
+        if (last_pos > k.max_ctx || last_pos > (long long)m.cfg.max_position_embeddings)
+            fail(ESP_INVALID_REQUEST, "cached input is empty or exceeds the context window");
+        if (n_out) *n_out = 0;
+        k.pos[seq] = 0;  // generate.rs:141 new_cache per generation
+        forward(m, k, 1, &seq, &n_prompt, prompt);
+        if (max_new == 0) return;
+        hipStream_t s = k.stream;
+        // gen layout: [0] fed token, [1] step, [2] row_seq, [3] row_pos, [8..] list
+        DevMem gen((size_t)(8 + max_new) * 4);
+        int32_t *g = gen.as<int32_t>();
+        int32_t init[4] = {0, 0, (int32_t)seq, (int32_t)n_prompt - 1};
+        ESP_HIP(hipMemcpyAsync(g, init, sizeof(init), hipMemcpyHostToDevice, s));
+        // first token from the prefill logits
+        PickArgs a{};
+        a.logits = k.logits.as<float>();
+        a.n = 1;
+        a.V = m.V;
+        k.pick_io.ensure(64);
+        a.ids_out = (uint32_t *)k.pick_io.p;
+        a.flags_out = (uint8_t *)k.pick_io.p + 16;
+        launch_pick(a, s);
+        launch_gen_step(a.ids_out, g, s);
+        const int max_t = (int)last_pos;
+        // MoE layers read their expert row counts back to the host, which a
+        // captured graph cannot do; ESP_GRAPHS=0 replays eagerly (profilers).
+        const char *env = getenv("ESP_GRAPHS");
+        const bool capturable = std::none_of(m.layers.begin(), m.layers.end(),
+                                             [](const LayerW &w) { return w.moe; }) &&
+                                !(env && env[0] == '0');
+        uint32_t steps = max_new - 1;
+        if (steps) {
+            decode_step_dev(m, k, (int)seq, max_t, g);  // eager: sizes every scratch buffer
+            --steps;
+        }
+        if (steps && capturable) {
+            hipGraph_t graph = nullptr;
+            hipGraphExec_t exec = nullptr;
+            ESP_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
+            g_capturing = true;
+            try {
+                decode_step_dev(m, k, (int)seq, max_t, g);
+            } catch (...) {
+                g_capturing = false;
+                (void)hipStreamEndCapture(s, &graph);
+                if (graph) (void)hipGraphDestroy(graph);
+                throw;
+            }
+            g_capturing = false;
+            ESP_HIP(hipStreamEndCapture(s, &graph));
+            hipError_t ie = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+            (void)hipGraphDestroy(graph);
+            ESP_HIP(ie);
+            for (uint32_t i = 0; i < steps; ++i) {
+                hipError_t le = hipGraphLaunch(exec, s);
+                if (le != hipSuccess) {
+                    (void)hipGraphExecDestroy(exec);
+                    ESP_HIP(le);
+                }
+            }
+            (void)hipGraphExecDestroy(exec);
+        } else {
+            for (uint32_t i = 0; i < steps; ++i) decode_step_dev(m, k, (int)seq, max_t, g);
+        }
+        std::vector<int32_t> list(max_new);
+        ESP_HIP(hipMemcpyAsync(list.data(), g + 8, (size_t)max_new * 4, hipMemcpyDeviceToHost, s));
+        ESP_HIP(hipStreamSynchronize(s));
+        k.pos[seq] = (int)last_pos;
+        uint32_t n = 0;
+        for (; n < max_new; ++n) {
+            bool stop = false;
+            for (uint32_t e = 0; e < n_eos; ++e) stop |= list[n] == eos[e];
+            if (stop) break;
+            if (out_ids) out_ids[n] = list[n];
+        }
+        if (n_out) *n_out = n;
+    });
+}
+
+esp_status esp_profile_enable(const char *kernel, int enable) {
+    return guard([&] {
+        if (!kernel) fail(ESP_INVALID_REQUEST, "null kernel name");
+        prof_enable(kernel, enable);
+    });
+}
+
+esp_status esp_profile_read(const char *kernel, uint64_t *launches, double *total_ms) {
+    return guard([&] {
+        if (!kernel) fail(ESP_INVALID_REQUEST, "null kernel name");
+        unsigned long long n = 0;
+        prof_read(kernel, &n, total_ms);
+        if (launches) *launches = n;
+    });
+}
+
+}  // extern "C"

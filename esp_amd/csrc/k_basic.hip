@@ -1,0 +1,329 @@
+// Bandwidth-bound kernels of the decoder forward: embedding gather, RMSNorm,
+// the QKV epilogue (LoRA B-add, QK-norm, RoPE, KV append) and split-K
+// attention over the per-sequence cache.
+#include "common.hpp"
+#include "dev.hpp"
+
+namespace esp {
+
+// ------------------------------------------------------------------ embed
+// model.rs:57-62 TokenEmbedding::forward — gather rows of [V, H].
+template <typename WT>
+__global__ void __launch_bounds__(256) embed_k(const WT *E, const int32_t *ids, int H, float *h) {
+    int m = blockIdx.x;
+    const WT *row = E + (size_t)ids[m] * H;
+    for (int j = threadIdx.x; j < H; j += blockDim.x) h[(size_t)m * H + j] = ld(row, j);
+}
+
+void launch_embed(Dt wt, const void *embed, const int32_t *ids, int M, int H, float *h,
+                  hipStream_t s) {
+    if (wt == DT_BF16)
+        embed_k<uint16_t><<<M, 256, 0, s>>>((const uint16_t *)embed, ids, H, h);
+    else
+        embed_k<float><<<M, 256, 0, s>>>((const float *)embed, ids, H, h);
+}
+
+// ---------------------------------------------------------------- rmsnorm
+// burn-nn RmsNorm (built at layer.rs:27-33): y = x / sqrt(mean(x^2) + eps) * gamma.
+template <typename OT>
+__global__ void __launch_bounds__(256) rmsnorm_k(const float *x, const float *gamma, float eps,
+                                                 int H, OT *out, const int32_t *row_index) {
+    __shared__ float red[16];
+    int m = blockIdx.x;
+    int src = row_index ? row_index[m] : m;
+    const float *xr = x + (size_t)src * H;
+    float ss = 0.f;
+    for (int j = threadIdx.x; j < H; j += blockDim.x) ss += xr[j] * xr[j];
+    ss = block_sum(ss, red);
+    float rms = sqrtf(ss / (float)H + eps);
+    for (int j = threadIdx.x; j < H; j += blockDim.x)
+        st(out, (size_t)m * H + j, (xr[j] / rms) * gamma[j]);
+}
+
+void launch_rmsnorm(const float *x, const float *gamma, float eps, int M, int H, Dt out_dt,
+                    void *out, const int32_t *row_index, hipStream_t s) {
+    if (out_dt == DT_BF16)
+        rmsnorm_k<uint16_t><<<M, 256, 0, s>>>(x, gamma, eps, H, (uint16_t *)out, row_index);
+    else
+        rmsnorm_k<float><<<M, 256, 0, s>>>(x, gamma, eps, H, (float *)out, row_index);
+}
+
+// ----------------------------------------------------------------- rope_kv
+// attention.rs:306-326: q/k/v projections (+bias, + unmerged LoRA as in
+// lora.rs:93-97), optional QK RMSNorm over head_dim (:312-319), split-half
+// RoPE at the row's absolute position (:99-123), then K/V appended to the
+// cache (:126-148). One block per token row.
+template <typename WT, typename KT>
+__global__ void __launch_bounds__(256) rope_kv_k(RopeKvArgs a) {
+    extern __shared__ float sh[];  // [heads_per_iter][hd]
+    const int m = blockIdx.x;
+    const int hd = a.hd, half = hd / 2;
+    const int pos = a.rows.row_pos[m];
+    const int seq = a.rows.row_seq[m];
+    const float *row = a.qkv + (size_t)m * a.ldq;
+    const float *cs = a.rope_cos + (size_t)pos * hd;
+    const float *sn = a.rope_sin + (size_t)pos * hd;
+    const int hpi = blockDim.x / hd > 0 ? blockDim.x / hd : 1;
+    const int total = a.nq + 2 * a.nkv;
+    const int qw = a.nq * hd, kvw = a.nkv * hd;
+    KT *cache = (KT *)a.kv;
+    for (int base = 0; base < total; base += hpi) {
+        const int lh = threadIdx.x / hd;
+        const int head = base + lh;
+        const bool active = lh < hpi && head < total;
+        float x = 0.f;
+        int target = 0, col = 0, d = threadIdx.x % hd;
+        if (active) {
+            if (head < a.nq) {
+                target = 0;
+                col = head * hd + d;
+            } else if (head < a.nq + a.nkv) {
+                target = 1;
+                col = qw + (head - a.nq) * hd + d;
+            } else {
+                target = 2;
+                col = qw + kvw + (head - a.nq - a.nkv) * hd + d;
+            }
+            x = row[col];
+            if (a.lora_b[target]) {
+                const WT *B = (const WT *)a.lora_b[target];
+                int r = a.lora_rank[target];
+                int o = col - (target == 0 ? 0 : (target == 1 ? qw : qw + kvw));
+                const float *t = row + a.lora_t_col[target];
+                float acc = 0.f;
+                for (int i = 0; i < r; ++i) acc += ld(B, (size_t)o * r + i) * t[i];
+                x = x + acc * a.lora_scale[target];
+            }
+            sh[lh * hd + d] = x;
+        }
+        __syncthreads();
+        if (active && target < 2) {
+            const float *g = target == 0 ? a.q_norm : a.k_norm;
+            if (g) {
+                float ss = 0.f;
+                for (int i = 0; i < hd; ++i) ss += sh[lh * hd + i] * sh[lh * hd + i];
+                float rms = sqrtf(ss / (float)hd + a.eps);
+                x = (x / rms) * g[d];
+            }
+        }
+        __syncthreads();
+        if (active && target < 2) sh[lh * hd + d] = x;
+        __syncthreads();
+        if (active) {
+            if (target < 2) {
+                float rot = d < half ? -sh[lh * hd + d + half] : sh[lh * hd + d - half];
+                float y = x * cs[d] + rot * sn[d];
+                if (target == 0) {
+                    a.q_out[(size_t)m * qw + head * hd + d] = y;
+                } else {
+                    int kh = head - a.nq;
+                    size_t off = (size_t)seq * a.seq_stride + (size_t)kh * a.head_stride +
+                                 (size_t)pos * hd + d;
+                    st(cache, off, y);
+                }
+            } else {
+                int vh = head - a.nq - a.nkv;
+                size_t off = (size_t)seq * a.seq_stride + a.kv_half_stride +
+                             (size_t)vh * a.head_stride + (size_t)pos * hd + d;
+                st(cache, off, x);
+            }
+        }
+        __syncthreads();
+    }
+}
+
+void launch_rope_kv(Dt wt, Dt kvdt, const RopeKvArgs &a, hipStream_t s) {
+    int hpi = 256 / a.hd > 0 ? 256 / a.hd : 1;
+    int threads = a.hd > 256 ? 0 : 256;
+    if (!threads) fail(ESP_UNSUPPORTED, "head_dim: values above 256 are not implemented");
+    size_t shm = sizeof(float) * hpi * a.hd;
+    if (wt == DT_BF16 && kvdt == DT_BF16)
+        rope_kv_k<uint16_t, uint16_t><<<a.rows.M, threads, shm, s>>>(a);
+    else if (wt == DT_BF16 && kvdt == DT_F32)
+        rope_kv_k<uint16_t, float><<<a.rows.M, threads, shm, s>>>(a);
+    else if (wt == DT_F32 && kvdt == DT_F32)
+        rope_kv_k<float, float><<<a.rows.M, threads, shm, s>>>(a);
+    else
+        fail(ESP_BACKEND, "rope_kv: unsupported dtype pair");
+}
+
+// --------------------------------------------------------------- attention
+// attention.rs:345-397: softmax((q.k)/sqrt(hd) + mask) . v, with the causal
+// rule `key > past + query` and the sliding rule `pos - key >= window`
+// (:362-368). GQA: q head i reads kv head i / group (:333-343), served here
+// by one block per (row, kv head, key split) without materialising copies.
+// Partials (running max, sum, unnormalised output) are merged by
+// attn_reduce_k.
+constexpr int ATT_KT = 32;  // keys per LDS tile
+
+template <typename KT>
+__global__ void __launch_bounds__(256) attn_split_k(AttnArgs a) {
+    extern __shared__ float sm[];
+    const int split = blockIdx.x, g = blockIdx.y, row = blockIdx.z;
+    const int hd = a.hd, G = a.nq / a.nkv;
+    const int pos = a.rows.row_pos[row], seq = a.rows.row_seq[row];
+    int lo = a.window > 0 ? max(0, pos - a.window + 1) : 0;
+    int hi = pos + 1;
+    lo = max(lo, split * a.split_len);
+    hi = min(hi, (split + 1) * a.split_len);
+    float *qs = sm;                        // [G][hd]
+    float *ks = qs + G * hd;               // [KT][hd+1]
+    float *vs = ks + ATT_KT * (hd + 1);    // [KT][hd]
+    float *ss = vs + ATT_KT * hd;          // [G][KT]
+    float *mrow = ss + G * ATT_KT;         // [G] running max
+    float *lrow = mrow + G;                // [G] running sum
+    float *alpha = lrow + G;               // [G] rescale for this tile
+    const int tid = threadIdx.x;
+    const size_t pbase = (((size_t)row * a.nq + (size_t)g * G) * a.n_split + split) * (hd + 2);
+    if (lo >= hi) {
+        for (int i = tid; i < G * (hd + 2); i += blockDim.x) {
+            int j = i / (hd + 2), c = i % (hd + 2);
+            float *p = a.part + pbase + (size_t)j * a.n_split * (hd + 2);
+            p[c] = c == 0 ? -INFINITY : 0.f;
+        }
+        return;
+    }
+    const float scale = sqrtf((float)hd);
+    const float *qrow = a.q + (size_t)row * a.nq * hd + (size_t)g * G * hd;
+    for (int i = tid; i < G * hd; i += blockDim.x) qs[i] = qrow[i];
+    if (tid < G) {
+        mrow[tid] = -INFINITY;
+        lrow[tid] = 0.f;
+    }
+    // each thread owns outputs (j, d) = o, o + 256, ...
+    constexpr int MAXO = 8;  // G*hd <= 2048
+    float acc[MAXO];
+#pragma unroll
+    for (int i = 0; i < MAXO; ++i) acc[i] = 0.f;
+    const KT *kbase = (const KT *)a.kv + (size_t)seq * a.seq_stride + (size_t)g * a.head_stride;
+    const KT *vbase = kbase + a.kv_half_stride;
+    for (int t0 = lo; t0 < hi; t0 += ATT_KT) {
+        const int nt = min(ATT_KT, hi - t0);
+        __syncthreads();
+        for (int i = tid; i < nt * hd; i += blockDim.x) {
+            int t = i / hd, d = i % hd;
+            ks[t * (hd + 1) + d] = ld(kbase, (size_t)(t0 + t) * hd + d);
+            vs[t * hd + d] = ld(vbase, (size_t)(t0 + t) * hd + d);
+        }
+        __syncthreads();
+        for (int i = tid; i < G * ATT_KT; i += blockDim.x) {
+            int j = i / ATT_KT, t = i % ATT_KT;
+            float s = -INFINITY;
+            if (t < nt) {
+                float dot = 0.f;
+                for (int d = 0; d < hd; ++d) dot += qs[j * hd + d] * ks[t * (hd + 1) + d];
+                s = dot / scale;
+            }
+            ss[j * ATT_KT + t] = s;
+        }
+        __syncthreads();
+        if (tid < G) {
+            float mx = mrow[tid];
+            for (int t = 0; t < nt; ++t) mx = fmaxf(mx, ss[tid * ATT_KT + t]);
+            float al = __expf(mrow[tid] - mx);
+            float l = lrow[tid] * al;
+            for (int t = 0; t < nt; ++t) {
+                float p = __expf(ss[tid * ATT_KT + t] - mx);
+                ss[tid * ATT_KT + t] = p;
+                l += p;
+            }
+            mrow[tid] = mx;
+            lrow[tid] = l;
+            alpha[tid] = al;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < MAXO; ++i) {
+            int o = tid + i * blockDim.x;
+            if (o < G * hd) {
+                int j = o / hd, d = o % hd;
+                float v = acc[i] * alpha[j];
+                for (int t = 0; t < nt; ++t) v += ss[j * ATT_KT + t] * vs[t * hd + d];
+                acc[i] = v;
+            }
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < MAXO; ++i) {
+        int o = tid + i * blockDim.x;
+        if (o < G * hd) {
+            int j = o / hd, d = o % hd;
+            a.part[pbase + (size_t)j * a.n_split * (hd + 2) + 2 + d] = acc[i];
+        }
+    }
+    if (tid < G) {
+        float *p = a.part + pbase + (size_t)tid * a.n_split * (hd + 2);
+        p[0] = mrow[tid];
+        p[1] = lrow[tid];
+    }
+}
+
+template <typename OT>
+__global__ void __launch_bounds__(256) attn_reduce_k(AttnArgs a, OT *out) {
+    const int qh = blockIdx.x, row = blockIdx.y;
+    const int hd = a.hd;
+    const float *p = a.part + ((size_t)row * a.nq + qh) * a.n_split * (hd + 2);
+    float mx = -INFINITY;
+    for (int s = 0; s < a.n_split; ++s) mx = fmaxf(mx, p[(size_t)s * (hd + 2)]);
+    float l = 0.f;
+    for (int s = 0; s < a.n_split; ++s) {
+        float ms = p[(size_t)s * (hd + 2)];
+        if (ms != -INFINITY) l += p[(size_t)s * (hd + 2) + 1] * __expf(ms - mx);
+    }
+    for (int d = threadIdx.x; d < hd; d += blockDim.x) {
+        float v = 0.f;
+        for (int s = 0; s < a.n_split; ++s) {
+            float ms = p[(size_t)s * (hd + 2)];
+            if (ms != -INFINITY) v += p[(size_t)s * (hd + 2) + 2 + d] * __expf(ms - mx);
+        }
+        st(out, (size_t)row * a.nq * hd + (size_t)qh * hd + d, v / l);
+    }
+}
+
+void launch_attention(Dt kvdt, const AttnArgs &a, hipStream_t s) {
+    const int G = a.nq / a.nkv;
+    if (G * a.hd > 8 * 256) fail(ESP_UNSUPPORTED, "attention: group*head_dim above 2048");
+    size_t shm = sizeof(float) * ((size_t)G * a.hd + ATT_KT * (a.hd + 1) + ATT_KT * a.hd +
+                                  (size_t)G * ATT_KT + 3 * G);
+    dim3 grid(a.n_split, a.nkv, a.rows.M);
+    if (shm > 64 * 1024) {
+        static bool set[2] = {false, false};
+        int i = kvdt == DT_BF16;
+        if (!set[i]) {
+            ESP_HIP(hipFuncSetAttribute(i ? (const void *)attn_split_k<uint16_t>
+                                          : (const void *)attn_split_k<float>,
+                                        hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
+            set[i] = true;
+        }
+    }
+    if (kvdt == DT_BF16)
+        attn_split_k<uint16_t><<<grid, 256, shm, s>>>(a);
+    else
+        attn_split_k<float><<<grid, 256, shm, s>>>(a);
+    dim3 g2(a.nq, a.rows.M);
+    int th = a.hd >= 64 ? 64 * ((a.hd + 63) / 64) : 64;
+    if (th > 256) th = 256;
+    if (a.out_dt == DT_BF16)
+        attn_reduce_k<uint16_t><<<g2, th, 0, s>>>(a, (uint16_t *)a.out);
+    else
+        attn_reduce_k<float><<<g2, th, 0, s>>>(a, (float *)a.out);
+}
+
+// ------------------------------------------------------------ generation
+// Device-side token hand-off for the captured decode step. gen[0] = token
+// fed to the next step, gen[1] = step index, gen[3] = its position,
+// gen[8 + i] = i-th generated id.
+__global__ void gen_step_k(const uint32_t *picked, int32_t *gen) {
+    int32_t t = (int32_t)picked[0];
+    gen[0] = t;
+    gen[8 + gen[1]] = t;
+    gen[1] += 1;
+    gen[3] += 1;
+}
+
+void launch_gen_step(const uint32_t *picked, int32_t *gen, hipStream_t s) {
+    gen_step_k<<<1, 1, 0, s>>>(picked, gen);
+}
+
+}  // namespace esp

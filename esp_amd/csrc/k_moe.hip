@@ -1,0 +1,194 @@
+// Routed experts (moe.rs:135-256): fp32 softmax router, top-k by
+// probability with ties to the lower expert id, optional renormalisation,
+// per-expert row grouping, and the combine that adds each token's expert
+// outputs in ascending expert order before the sigmoid-gated shared expert.
+#include "common.hpp"
+#include "dev.hpp"
+#include "kernels_extra.hpp"
+
+namespace esp {
+
+__global__ void __launch_bounds__(256) route_k(RouteArgs a) {
+    const int E = a.E, k = a.k;
+    __shared__ int status;
+    if (threadIdx.x == 0) status = 0;
+    __syncthreads();
+    for (int t = threadIdx.x; t < a.M; t += blockDim.x) {
+        const float *l = a.logits + (size_t)t * E;
+        float mx = -INFINITY;
+        for (int e = 0; e < E; ++e) mx = fmaxf(mx, l[e]);
+        float sum = 0.f;
+        for (int e = 0; e < E; ++e) sum += expf(l[e] - mx);
+        bool bad = false;
+        for (int e = 0; e < E; ++e) bad |= !isfinite(expf(l[e] - mx) / sum);
+        if (bad) {
+            atomicMax(&status, 2);
+            continue;
+        }
+        // top-k by (probability desc, id asc) (moe.rs:166)
+        int chosen[8];
+        float prob[8];
+        for (int j = 0; j < k; ++j) {
+            int best = -1;
+            float bp = 0.f;
+            for (int e = 0; e < E; ++e) {
+                bool used = false;
+                for (int i = 0; i < j; ++i) used |= chosen[i] == e;
+                if (used) continue;
+                float p = expf(l[e] - mx) / sum;
+                if (best < 0 || p > bp) {
+                    best = e;
+                    bp = p;
+                }
+            }
+            chosen[j] = best;
+            prob[j] = bp;
+        }
+        float mass = 1.0f;
+        if (a.norm_topk) {
+            mass = 0.f;
+            for (int j = 0; j < k; ++j) mass += prob[j];
+        }
+        if (!isfinite(mass) || mass <= 0.f) {
+            atomicMax(&status, 3);
+            continue;
+        }
+        // store ascending by expert id
+        for (int j = 0; j < k; ++j) {
+            int rank = 0;
+            for (int i = 0; i < k; ++i) rank += chosen[i] < chosen[j];
+            a.sel[(size_t)t * k + rank] = chosen[j];
+            a.w[(size_t)t * k + rank] = prob[j] / mass;
+        }
+    }
+    __syncthreads();
+    if (status) {
+        if (threadIdx.x == 0) {
+            for (int e = 0; e <= E; ++e) a.offs[e] = 0;
+            a.offs[E + 1] = status;
+        }
+        return;
+    }
+    __shared__ int cnt[257];
+    for (int e = threadIdx.x; e < E; e += blockDim.x) {
+        int c = 0;
+        for (int i = 0; i < a.M * k; ++i) c += a.sel[i] == e;
+        cnt[e] = c;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        int acc = 0;
+        for (int e = 0; e < E; ++e) {
+            a.offs[e] = acc;
+            int c = cnt[e];
+            cnt[e] = acc;
+            acc += c;
+        }
+        a.offs[E] = acc;
+        a.offs[E + 1] = 0;
+    }
+    __syncthreads();
+    for (int e = threadIdx.x; e < E; e += blockDim.x) {
+        int c = cnt[e];
+        for (int i = 0; i < a.M * k; ++i)
+            if (a.sel[i] == e) {
+                a.perm[c] = i / k;
+                a.slot[i] = c;
+                ++c;
+            }
+    }
+}
+
+void launch_route(const RouteArgs &a, hipStream_t s) {
+    if (a.E > 256 || a.k > 8) fail(ESP_UNSUPPORTED, "config.experts: more than 256 experts or top-k above 8");
+    route_k<<<1, 256, 0, s>>>(a);
+}
+
+template <typename T>
+__global__ void __launch_bounds__(256) gather_k(const T *src, const int32_t *perm, int H, T *dst) {
+    int r = blockIdx.x;
+    const T *s = src + (size_t)perm[r] * H;
+    for (int j = threadIdx.x; j < H; j += blockDim.x) dst[(size_t)r * H + j] = s[j];
+}
+
+void launch_gather_rows(Dt dt, const void *src, const int32_t *perm, int rows, int H, void *dst,
+                        hipStream_t s) {
+    if (!rows) return;
+    if (dt == DT_BF16) gather_k<uint16_t><<<rows, 256, 0, s>>>((const uint16_t *)src, perm, H, (uint16_t *)dst);
+    else gather_k<float><<<rows, 256, 0, s>>>((const float *)src, perm, H, (float *)dst);
+}
+
+__global__ void __launch_bounds__(256) combine_k(CombineArgs a) {
+    int t = blockIdx.x;
+    float g = 0.f;
+    if (a.sg) g = 1.0f / (1.0f + expf(-a.sg[t]));
+    for (int d = threadIdx.x; d < a.H; d += blockDim.x) {
+        float out = 0.f;
+        for (int j = 0; j < a.k; ++j) {
+            float y = a.y[(size_t)a.slot[(size_t)t * a.k + j] * a.H + d];
+            out = out + y * a.w[(size_t)t * a.k + j];
+        }
+        if (a.ys) out = out + g * a.ys[(size_t)t * a.H + d];
+        a.h[(size_t)t * a.H + d] += out;
+    }
+}
+
+void launch_combine(const CombineArgs &a, hipStream_t s) { combine_k<<<a.M, 256, 0, s>>>(a); }
+
+// --------------------------------------------------------------- fills
+
+__device__ __forceinline__ uint64_t mix64(uint64_t z) {
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+template <typename T>
+__global__ void __launch_bounds__(256) fill_normal_k(T *dst, size_t n, uint64_t seed, float sd) {
+    size_t pairs = (n + 1) / 2;
+    for (size_t p = blockIdx.x * (size_t)blockDim.x + threadIdx.x; p < pairs;
+         p += (size_t)gridDim.x * blockDim.x) {
+        uint64_t base = seed + 0x9E3779B97F4A7C15ull * (2 * p);
+        uint64_t x1 = mix64(base + 0x9E3779B97F4A7C15ull);
+        uint64_t x2 = mix64(base + 2 * 0x9E3779B97F4A7C15ull);
+        float u1 = ((float)(x1 >> 40) + 1.0f) * (1.0f / 16777216.0f);
+        float u2 = (float)(x2 >> 40) * (1.0f / 16777216.0f);
+        float r = sqrtf(-2.0f * logf(u1));
+        float sv, cv;
+        sincosf(6.2831853071795864f * u2, &sv, &cv);
+        st(dst, 2 * p, r * cv * sd);
+        if (2 * p + 1 < n) st(dst, 2 * p + 1, r * sv * sd);
+    }
+}
+
+void launch_fill_normal(Dt dt, void *dst, size_t n, uint64_t seed, float sd, hipStream_t s) {
+    if (!n) return;
+    size_t pairs = (n + 1) / 2;
+    int blocks = (int)std::min<size_t>((pairs + 255) / 256, 65536);
+    if (dt == DT_BF16) fill_normal_k<uint16_t><<<blocks, 256, 0, s>>>((uint16_t *)dst, n, seed, sd);
+    else fill_normal_k<float><<<blocks, 256, 0, s>>>((float *)dst, n, seed, sd);
+}
+
+__global__ void fill_const_k(float *dst, size_t n, float v) {
+    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+        dst[i] = v;
+}
+
+void launch_fill_const(float *dst, size_t n, float v, hipStream_t s) {
+    if (!n) return;
+    int blocks = (int)std::min<size_t>((n + 255) / 256, 65536);
+    fill_const_k<<<blocks, 256, 0, s>>>(dst, n, v);
+}
+
+__global__ void fill_bits_k(uint16_t *dst, size_t n, uint16_t b) {
+    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+        dst[i] = b;
+}
+
+void launch_fill_bits(uint16_t *dst, size_t n, uint16_t bits, hipStream_t s) {
+    if (!n) return;
+    int blocks = (int)std::min<size_t>((n + 255) / 256, 65536);
+    fill_bits_k<<<blocks, 256, 0, s>>>(dst, n, bits);
+}
+
+}  // namespace esp

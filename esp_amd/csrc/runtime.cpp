@@ -1,0 +1,972 @@
+// Host runtime of the MI355X decoder: weight staging into HBM, per-sequence
+// KV caches, the layer-by-layer forward over token rows, token choice and
+// the device-resident greedy loop. Every public entry point is in
+// esp_abi.cpp; this file holds the machinery.
+#include "runtime.hpp"
+
+#include <math.h>
+#include <string.h>
+
+#include <algorithm>
+#include <mutex>
+#include <set>
+
+#include "kernels_extra.hpp"
+#include "profile.hpp"
+#include "safetensors.hpp"
+
+namespace esp {
+
+Kv::~Kv() {
+    if (gen_exec) (void)hipGraphExecDestroy(gen_exec);
+    if (pinned) (void)hipHostFree(pinned);
+    if (stream) (void)hipStreamDestroy(stream);
+}
+
+// ------------------------------------------------------------------ RoPE
+// decoder/config.rs:158-180 RopeScaling::apply
+static float rope_scale(const esp_config &c, float freq) {
+    if (c.rope_scaling == ESP_ROPE_LINEAR) return freq / c.rope_factor;
+    if (c.rope_scaling == ESP_ROPE_LLAMA3) {
+        const float tau = 6.28318530717958647692f;
+        float wavelength = tau / freq;
+        float original = (float)c.rope_original_max_position_embeddings;
+        if (wavelength < original / c.rope_high_freq_factor) return freq;
+        if (wavelength > original / c.rope_low_freq_factor) return freq / c.rope_factor;
+        float smooth = (original / wavelength - c.rope_low_freq_factor) /
+                       (c.rope_high_freq_factor - c.rope_low_freq_factor);
+        return (1.0f - smooth) * freq / c.rope_factor + smooth * freq;
+    }
+    return freq;
+}
+
+// decoder/attention.rs:58-95: the host f32 table [max_pos, hd], each half
+// duplicated (cos/sin of position * inverse frequency).
+static void build_rope(const esp_config &c, std::vector<float> &cs, std::vector<float> &sn) {
+    const int hd = (int)c.head_dim, half = hd / 2, mp = (int)c.max_position_embeddings;
+    cs.assign((size_t)mp * hd, 0.f);
+    sn.assign((size_t)mp * hd, 0.f);
+    std::vector<float> inv(half);
+    for (int i = 0; i < half; ++i)
+        inv[i] = rope_scale(c, 1.0f / powf(c.rope_theta, (float)(2 * i) / (float)hd));
+    for (int p = 0; p < mp; ++p)
+        for (int i = 0; i < half; ++i) {
+            float angle = (float)p * inv[i];
+            float cv = cosf(angle), sv = sinf(angle);
+            cs[(size_t)p * hd + i] = cs[(size_t)p * hd + half + i] = cv;
+            sn[(size_t)p * hd + i] = sn[(size_t)p * hd + half + i] = sv;
+        }
+}
+
+// --------------------------------------------------------------- staging
+
+static void validate_config(const esp_config &c) {
+    if (!c.vocab_size || !c.hidden_size || !c.intermediate_size || !c.num_hidden_layers ||
+        !c.num_attention_heads || !c.num_key_value_heads || !c.head_dim ||
+        !c.max_position_embeddings)
+        fail(ESP_INVALID_CONFIG, "zero, non-finite or overflowing decoder dimensions/settings");
+    if (c.num_attention_heads % c.num_key_value_heads)
+        fail(ESP_INVALID_CONFIG, "num_attention_heads not divisible by num_key_value_heads");
+    if (c.head_dim % 2) fail(ESP_INVALID_CONFIG, "head_dim must be even for rotary encoding");
+    if (!(c.rms_norm_eps > 0.f) || !isfinite(c.rms_norm_eps) || !(c.rope_theta > 0.f) ||
+        !isfinite(c.rope_theta))
+        fail(ESP_INVALID_CONFIG, "zero, non-finite or overflowing decoder dimensions/settings");
+    if (c.format != ESP_FORMAT_F32 && c.format != ESP_FORMAT_BF16)
+        fail(ESP_UNSUPPORTED, "weight format: only f32 and bf16 are implemented");
+    if (c.head_dim > 256) fail(ESP_UNSUPPORTED, "head_dim: values above 256 are not implemented");
+    if (c.num_attention_heads / c.num_key_value_heads * c.head_dim > 2048)
+        fail(ESP_UNSUPPORTED, "attention: query group x head_dim above 2048 is not implemented");
+    if (c.num_experts) {
+        if (!c.num_experts_per_tok || c.num_experts_per_tok > c.num_experts ||
+            !c.moe_intermediate_size)
+            fail(ESP_UNSUPPORTED,
+                 "config.experts: invalid expert count, routing, intermediate size or sparse-layer "
+                 "selection");
+        if (c.num_experts > 256) fail(ESP_UNSUPPORTED, "config.experts: more than 256 experts");
+        if (c.num_experts_per_tok > 8) fail(ESP_UNSUPPORTED, "config.experts: top-k above 8");
+    }
+}
+
+static void init_model_shape(Model &m, const esp_config &c) {
+    m.cfg = c;
+    m.cfg.layer_window = nullptr;
+    m.cfg.layer_is_moe = nullptr;
+    m.wt = c.format == ESP_FORMAT_BF16 ? DT_BF16 : DT_F32;
+    m.H = c.hidden_size;
+    m.L = c.num_hidden_layers;
+    m.nq = c.num_attention_heads;
+    m.nkv = c.num_key_value_heads;
+    m.hd = c.head_dim;
+    m.F = c.intermediate_size;
+    m.V = c.vocab_size;
+    m.qw = m.nq * m.hd;
+    m.kvw = m.nkv * m.hd;
+    m.E = c.num_experts;
+    m.topk = c.num_experts_per_tok;
+    m.Fe = c.moe_intermediate_size;
+    m.Fs = c.shared_expert_intermediate_size;
+    m.norm_topk = c.norm_topk_prob != 0;
+    m.layers.assign(m.L, LayerW());
+    for (int l = 0; l < m.L; ++l) {
+        m.layers[l].window = c.layer_window ? (int)c.layer_window[l] : 0;
+        m.layers[l].moe = m.E && c.layer_is_moe && c.layer_is_moe[l];
+    }
+    ESP_HIP(hipGetDevice(&m.device));
+}
+
+static void upload(void *dst, const void *src, size_t bytes) {
+    ESP_HIP(hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice));
+}
+
+static void stage_rope(Model &m) {
+    std::vector<float> cs, sn;
+    build_rope(m.cfg, cs, sn);
+    m.rope_cos = (float *)m.alloc(cs.size() * 4);
+    m.rope_sin = (float *)m.alloc(sn.size() * 4);
+    upload(m.rope_cos, cs.data(), cs.size() * 4);
+    upload(m.rope_sin, sn.data(), sn.size() * 4);
+}
+
+static inline float half_to_f32(uint16_t h) {
+    uint32_t s = (h >> 15) & 1, e = (h >> 10) & 0x1f, f = h & 0x3ff;
+    uint32_t out;
+    if (e == 0) {
+        if (f == 0) out = s << 31;
+        else {
+            int ee = -1;
+            do {
+                ++ee;
+                f <<= 1;
+            } while (!(f & 0x400));
+            out = (s << 31) | ((uint32_t)(127 - 15 - ee) << 23) | ((f & 0x3ff) << 13);
+        }
+    } else if (e == 31) {
+        out = (s << 31) | 0x7f800000u | (f << 13);
+    } else {
+        out = (s << 31) | ((e + 127 - 15) << 23) | (f << 13);
+    }
+    float r;
+    memcpy(&r, &out, 4);
+    return r;
+}
+
+// Reads checkpoint tensors into a host staging vector in the model's
+// format, checking shape, dtype admission and finiteness
+// (decoder/weight_format.rs:110-133, 225-315; tensors.rs:22-66).
+struct Stager {
+    Model &m;
+    const std::map<std::string, StTensor> &t;
+    std::set<std::string> consumed;
+
+    const StTensor &get(const std::string &name, std::vector<uint64_t> shape) {
+        auto it = t.find(name);
+        if (it == t.end()) fail(ESP_INVALID_WEIGHTS, "missing tensor: " + name);
+        if (it->second.shape != shape) {
+            std::string e = "weight format: expected [";
+            for (size_t i = 0; i < shape.size(); ++i) e += (i ? ", " : "") + std::to_string(shape[i]);
+            e += "], got [";
+            for (size_t i = 0; i < it->second.shape.size(); ++i)
+                e += (i ? ", " : "") + std::to_string(it->second.shape[i]);
+            fail(ESP_INVALID_WEIGHTS, e + "] for " + name);
+        }
+        consumed.insert(name);
+        return it->second;
+    }
+    bool has(const std::string &name) const { return t.count(name) != 0; }
+
+    // Append the tensor's elements (converted) to `out` as the model dtype
+    // (or f32 when force_f32).
+    void read(const std::string &name, std::vector<uint64_t> shape, std::vector<uint8_t> &out,
+              bool force_f32 = false) {
+        const StTensor &s = get(name, shape);
+        size_t n = 1;
+        for (auto d : shape) n *= d;
+        Dt dst = force_f32 ? DT_F32 : m.wt;
+        if (m.wt == DT_BF16 && !force_f32 && s.dtype != "BF16")
+            fail(ESP_INVALID_WEIGHTS, "weight format: artifact dtype disagrees with declared format (" +
+                                          name + ")");
+        size_t base = out.size();
+        out.resize(base + n * dt_size(dst));
+        uint8_t *o = out.data() + base;
+        for (size_t i = 0; i < n; ++i) {
+            float v;
+            if (s.dtype == "F32") memcpy(&v, s.data + 4 * i, 4);
+            else if (s.dtype == "BF16") {
+                uint32_t u = (uint32_t)(s.data[2 * i] | (s.data[2 * i + 1] << 8)) << 16;
+                memcpy(&v, &u, 4);
+            } else if (s.dtype == "F16") {
+                v = half_to_f32((uint16_t)(s.data[2 * i] | (s.data[2 * i + 1] << 8)));
+            } else {
+                fail(ESP_INVALID_WEIGHTS, "weight format: cannot import " + s.dtype + " (" + name + ")");
+            }
+            if (!isfinite(v)) fail(ESP_INVALID_WEIGHTS, "weight format: non-finite weight in " + name);
+            if (dst == DT_F32) memcpy(o + 4 * i, &v, 4);
+            else {
+                uint16_t b = (uint16_t)(s.data[2 * i] | (s.data[2 * i + 1] << 8));
+                memcpy(o + 2 * i, &b, 2);
+            }
+        }
+    }
+    void *to_device(const std::vector<uint8_t> &host) {
+        void *d = m.alloc(host.size());
+        upload(d, host.data(), host.size());
+        return d;
+    }
+    void *tensor(const std::string &name, std::vector<uint64_t> shape, bool force_f32 = false) {
+        std::vector<uint8_t> h;
+        read(name, shape, h, force_f32);
+        return to_device(h);
+    }
+};
+
+static void refuse_unconsumed(const Stager &s) {
+    std::vector<std::string> left;
+    for (auto &kv : s.t) {
+        const std::string &n = kv.first;
+        if (s.consumed.count(n)) continue;
+        if (n.size() >= 20 && n.compare(n.size() - 20, 20, ".rotary_emb.inv_freq") == 0) continue;
+        left.push_back(n);
+    }
+    if (left.empty()) return;
+    std::sort(left.begin(), left.end());
+    const std::string &first = left[0];
+    // decoder/loader.rs:257-275 why_unconsumed
+    std::string why;
+    auto ends = [&](const char *suf) {
+        size_t k = strlen(suf);
+        return first.size() >= k && first.compare(first.size() - k, k, suf) == 0;
+    };
+    if (ends(".bias")) why = "this bias is not declared by the decoder configuration";
+    else if (first.find("q_norm") != std::string::npos || first.find("k_norm") != std::string::npos)
+        why = "this head norm is not declared by the decoder configuration";
+    else if (first.find("experts") != std::string::npos ||
+             first.find("block_sparse_moe") != std::string::npos || ends(".mlp.gate.weight"))
+        why = "this expert or router is not declared by the decoder configuration";
+    else if (first.find("norm") != std::string::npos)
+        why = "normalization layers beyond the Llama block's two per layer are not implemented";
+    else why = "the Llama-block decoder does not consume this tensor";
+    fail(ESP_UNSUPPORTED, "tensor " + first + ": " + why + "; " + std::to_string(left.size()) +
+                              " unconsumed tensor(s) in this checkpoint");
+}
+
+static const char *kTargets[4] = {"q_proj", "k_proj", "v_proj", "o_proj"};
+
+Model *load_model(const esp_config *cfg, const uint8_t *bytes, size_t len,
+                  const esp_lora *adapters, uint32_t n_adapters) {
+    if (!cfg) fail(ESP_INVALID_CONFIG, "null config");
+    validate_config(*cfg);
+    std::unique_ptr<Model> mp(new Model());
+    Model &m = *mp;
+    init_model_shape(m, *cfg);
+    auto tensors = parse_safetensors(bytes, len);
+    Stager s{m, tensors, {}};
+    const uint64_t H = m.H, qw = m.qw, kvw = m.kvw, hd = m.hd;
+
+    // adapters: parse each; per target the ranks stack in adapter order
+    std::vector<std::map<std::string, StTensor>> ad_t(n_adapters);
+    int rank_sum[4] = {0, 0, 0, 0};
+    float tscale[4] = {0, 0, 0, 0};
+    for (uint32_t a = 0; a < n_adapters; ++a) {
+        const esp_lora &ad = adapters[a];
+        if (!ad.rank || !isfinite(ad.scale))
+            fail(ESP_INVALID_CONFIG, "adapter " + std::to_string(a) +
+                                         ": PEFT rank must be positive and alpha finite");
+        if (ad.target_mask & 8u)
+            fail(ESP_UNSUPPORTED, "adapter o_proj: unmerged LoRA on o_proj is not implemented");
+        if (m.E) fail(ESP_UNSUPPORTED, "MoE adapters/training: expert routing is inference-only");
+        ad_t[a] = parse_safetensors(ad.safetensors, ad.safetensors_len);
+        int nt = 0;
+        for (int j = 0; j < 3; ++j)
+            if (ad.target_mask & (1u << j)) {
+                ++nt;
+                if (rank_sum[j] && tscale[j] != ad.scale)
+                    fail(ESP_UNSUPPORTED, "adapters: stacked adapters on one projection must share "
+                                          "a scale");
+                rank_sum[j] += ad.rank;
+                tscale[j] = ad.scale;
+            }
+        if (ad_t[a].size() != (size_t)m.L * nt * 2)
+            fail(ESP_INVALID_WEIGHTS, "adapter " + std::to_string(a) +
+                                          ": adapter tensor count mismatch: expected " +
+                                          std::to_string((size_t)m.L * nt * 2) + ", got " +
+                                          std::to_string(ad_t[a].size()));
+    }
+    const int lora_total = rank_sum[0] + rank_sum[1] + rank_sum[2];
+
+    for (int l = 0; l < m.L; ++l) {
+        LayerW &w = m.layers[l];
+        const std::string p = "model.layers." + std::to_string(l) + ".";
+        w.in_norm = (float *)s.tensor(p + "input_layernorm.weight", {H}, true);
+        w.post_norm = (float *)s.tensor(p + "post_attention_layernorm.weight", {H}, true);
+        // fused q | k | v | LoRA-A rows (loader.rs:508-535 read order)
+        std::vector<uint8_t> qkv;
+        s.read(p + "self_attn.q_proj.weight", {qw, H}, qkv);
+        s.read(p + "self_attn.k_proj.weight", {kvw, H}, qkv);
+        s.read(p + "self_attn.v_proj.weight", {kvw, H}, qkv);
+        w.qkv_rows = (int)(qw + 2 * kvw) + lora_total;
+        int tcol = (int)(qw + 2 * kvw);
+        for (int j = 0; j < 3; ++j) {
+            if (!rank_sum[j]) continue;
+            uint64_t outf = j == 0 ? qw : kvw;
+            std::vector<uint8_t> bcat((size_t)outf * rank_sum[j] * dt_size(m.wt));
+            int roff = 0;
+            for (uint32_t a = 0; a < n_adapters; ++a) {
+                if (!(adapters[a].target_mask & (1u << j))) continue;
+                uint64_t r = adapters[a].rank;
+                Stager sa{m, ad_t[a], {}};
+                std::string pre = "base_model.model.model.layers." + std::to_string(l) +
+                                  ".self_attn." + kTargets[j];
+                sa.read(pre + ".lora_A.weight", {r, H}, qkv);
+                std::vector<uint8_t> b;
+                sa.read(pre + ".lora_B.weight", {outf, r}, b);
+                size_t es = dt_size(m.wt);
+                for (uint64_t o = 0; o < outf; ++o)
+                    memcpy(bcat.data() + ((size_t)o * rank_sum[j] + roff) * es,
+                           b.data() + (size_t)o * r * es, r * es);
+                roff += (int)r;
+            }
+            w.lora_b[j] = s.to_device(bcat);
+            w.lora_rank[j] = rank_sum[j];
+            w.lora_t_col[j] = tcol;
+            w.lora_scale[j] = tscale[j];
+            tcol += rank_sum[j];
+        }
+        w.qkv = s.to_device(qkv);
+        if (cfg->qkv_bias) {
+            std::vector<uint8_t> b;
+            s.read(p + "self_attn.q_proj.bias", {qw}, b, true);
+            s.read(p + "self_attn.k_proj.bias", {kvw}, b, true);
+            s.read(p + "self_attn.v_proj.bias", {kvw}, b, true);
+            b.resize((size_t)w.qkv_rows * 4, 0);
+            w.qkv_bias = (float *)s.to_device(b);
+        }
+        w.o = s.tensor(p + "self_attn.o_proj.weight", {H, qw});
+        if (cfg->output_bias) w.o_bias = (float *)s.tensor(p + "self_attn.o_proj.bias", {H}, true);
+        if (cfg->qk_norm) {
+            w.q_norm = (float *)s.tensor(p + "self_attn.q_norm.weight", {hd}, true);
+            w.k_norm = (float *)s.tensor(p + "self_attn.k_norm.weight", {hd}, true);
+        }
+        if (!w.moe) {
+            uint64_t F = m.F;
+            w.gate = s.tensor(p + "mlp.gate_proj.weight", {F, H});
+            w.up = s.tensor(p + "mlp.up_proj.weight", {F, H});
+            w.down = s.tensor(p + "mlp.down_proj.weight", {H, F});
+        } else {
+            uint64_t E = m.E, Fe = m.Fe, Fs = m.Fs;
+            w.router = s.tensor(p + "mlp.gate.weight", {E, H});
+            if (Fs) {
+                w.shared_gate = s.tensor(p + "mlp.shared_expert_gate.weight", {1, H});
+                w.sh_gate = s.tensor(p + "mlp.shared_expert.gate_proj.weight", {Fs, H});
+                w.sh_up = s.tensor(p + "mlp.shared_expert.up_proj.weight", {Fs, H});
+                w.sh_down = s.tensor(p + "mlp.shared_expert.down_proj.weight", {H, Fs});
+            }
+            std::vector<uint8_t> g, u, d;
+            for (uint64_t e = 0; e < E; ++e) {
+                std::string ep = p + "mlp.experts." + std::to_string(e) + ".";
+                s.read(ep + "gate_proj.weight", {Fe, H}, g);
+                s.read(ep + "up_proj.weight", {Fe, H}, u);
+                s.read(ep + "down_proj.weight", {H, Fe}, d);
+            }
+            w.ex_gate = s.to_device(g);
+            w.ex_up = s.to_device(u);
+            w.ex_down = s.to_device(d);
+        }
+    }
+    m.embed = s.tensor("model.embed_tokens.weight", {(uint64_t)m.V, H});
+    m.final_norm = (float *)s.tensor("model.norm.weight", {H}, true);
+    if (s.has("lm_head.weight")) {
+        m.head = s.tensor("lm_head.weight", {(uint64_t)m.V, H});
+    } else if (cfg->tie_word_embeddings) {
+        m.head = m.embed;  // model.rs:167-169 tied head
+    } else {
+        fail(ESP_INVALID_WEIGHTS, "lm_head.weight missing but tie_word_embeddings is false");
+    }
+    refuse_unconsumed(s);
+    stage_rope(m);
+    return mp.release();
+}
+
+// Synthetic model: every projection / embedding N(0, std) from a seeded
+// device generator, norms 1, biases 0 (bench and large-shape tests).
+Model *synthetic_model(const esp_config *cfg, uint64_t seed, float std, uint32_t lora_rank,
+                       uint32_t lora_mask, float lora_a_std, float lora_b_std,
+                       float lora_scale) {
+    if (!cfg) fail(ESP_INVALID_CONFIG, "null config");
+    validate_config(*cfg);
+    if (lora_mask & 8u) fail(ESP_UNSUPPORTED, "adapter o_proj: unmerged LoRA on o_proj is not implemented");
+    std::unique_ptr<Model> mp(new Model());
+    Model &m = *mp;
+    init_model_shape(m, *cfg);
+    uint64_t tensor_id = 0;
+    auto rnd = [&](size_t n, float sd) {
+        void *p = m.alloc(n * dt_size(m.wt));
+        launch_fill_normal(m.wt, p, n, seed * 0x100000001B3ull + (++tensor_id), sd, nullptr);
+        return p;
+    };
+    auto cst = [&](size_t n, float v) {
+        float *p = (float *)m.alloc(n * 4);
+        launch_fill_const(p, n, v, nullptr);
+        return p;
+    };
+    const size_t H = m.H;
+    int rank_t[3] = {0, 0, 0};
+    int lora_total = 0;
+    for (int j = 0; j < 3; ++j)
+        if (lora_mask & (1u << j)) {
+            rank_t[j] = (int)lora_rank;
+            lora_total += (int)lora_rank;
+        }
+    for (int l = 0; l < m.L; ++l) {
+        LayerW &w = m.layers[l];
+        w.in_norm = cst(H, 1.f);
+        w.post_norm = cst(H, 1.f);
+        w.qkv_rows = m.qw + 2 * m.kvw + lora_total;
+        w.qkv = m.alloc((size_t)w.qkv_rows * H * dt_size(m.wt));
+        size_t base_rows = m.qw + 2 * m.kvw;
+        launch_fill_normal(m.wt, w.qkv, base_rows * H, seed * 0x100000001B3ull + (++tensor_id), std,
+                           nullptr);
+        int tcol = (int)base_rows;
+        for (int j = 0; j < 3; ++j) {
+            if (!rank_t[j]) continue;
+            char *a = (char *)w.qkv + (size_t)tcol * H * dt_size(m.wt);
+            launch_fill_normal(m.wt, a, (size_t)rank_t[j] * H, seed * 0x100000001B3ull + (++tensor_id),
+                               lora_a_std, nullptr);
+            size_t outf = j == 0 ? m.qw : m.kvw;
+            w.lora_b[j] = rnd(outf * rank_t[j], lora_b_std);
+            w.lora_rank[j] = rank_t[j];
+            w.lora_t_col[j] = tcol;
+            w.lora_scale[j] = lora_scale;
+            tcol += rank_t[j];
+        }
+        if (cfg->qkv_bias) w.qkv_bias = cst(w.qkv_rows, 0.f);
+        w.o = rnd((size_t)H * m.qw, std);
+        if (cfg->output_bias) w.o_bias = cst(H, 0.f);
+        if (cfg->qk_norm) {
+            w.q_norm = cst(m.hd, 1.f);
+            w.k_norm = cst(m.hd, 1.f);
+        }
+        if (!w.moe) {
+            w.gate = rnd((size_t)m.F * H, std);
+            w.up = rnd((size_t)m.F * H, std);
+            w.down = rnd((size_t)H * m.F, std);
+        } else {
+            w.router = rnd((size_t)m.E * H, std);
+            if (m.Fs) {
+                w.shared_gate = rnd(H, std);
+                w.sh_gate = rnd((size_t)m.Fs * H, std);
+                w.sh_up = rnd((size_t)m.Fs * H, std);
+                w.sh_down = rnd((size_t)H * m.Fs, std);
+            }
+            w.ex_gate = rnd((size_t)m.E * m.Fe * H, std);
+            w.ex_up = rnd((size_t)m.E * m.Fe * H, std);
+            w.ex_down = rnd((size_t)m.E * H * m.Fe, std);
+        }
+    }
+    m.embed = rnd((size_t)m.V * H, std);
+    m.head = cfg->tie_word_embeddings ? m.embed : rnd((size_t)m.V * H, std);
+    m.final_norm = cst(H, 1.f);
+    stage_rope(m);
+    ESP_HIP(hipDeviceSynchronize());
+    return mp.release();
+}
+
+// ------------------------------------------------------------------- KV
+
+Kv *create_kv(Model *m, uint32_t batch, uint32_t max_ctx) {
+    if (!m) fail(ESP_MODEL_NOT_LOADED, "model not loaded");
+    if (!batch || !max_ctx || max_ctx > m->cfg.max_position_embeddings)
+        fail(ESP_INVALID_REQUEST, "kv: batch must be positive and max_ctx within "
+                                  "max_position_embeddings");
+    std::unique_ptr<Kv> kv(new Kv());
+    kv->model = m;
+    kv->batch = (int)batch;
+    kv->max_ctx = (int)max_ctx;
+    kv->dt = DT_F32;  // keys/values keep f32 precision in every format
+    kv->head_stride = (long long)max_ctx * m->hd;
+    kv->half_stride = kv->head_stride * m->nkv;
+    kv->layer_stride = kv->half_stride * 2;
+    kv->seq_stride = kv->layer_stride * m->L;
+    kv->cache.alloc((size_t)kv->seq_stride * batch * dt_size(kv->dt));
+    kv->pos.assign(batch, 0);
+    ESP_HIP(hipStreamCreateWithFlags(&kv->stream, hipStreamNonBlocking));
+    return kv.release();
+}
+
+// ---------------------------------------------------------------- forward
+
+static const int kMaxRows = 4096;  // token rows per pass through the layers
+
+static void ensure_pinned(Kv &kv, size_t bytes) {
+    if (kv.pinned_bytes >= bytes) return;
+    if (kv.pinned) ESP_HIP(hipHostFree(kv.pinned));
+    kv.pinned = nullptr;
+    kv.pinned_bytes = 0;
+    ESP_HIP(hipHostMalloc(&kv.pinned, bytes, hipHostMallocDefault));
+    kv.pinned_bytes = bytes;
+}
+
+struct Plan {
+    int n_split, split_len;
+};
+
+static Plan attn_plan(const Model &m, int rows, int max_t) {
+    int base = rows * m.nkv;
+    int want = (2048 + base - 1) / base;  // aim for >= 2048 blocks
+    int max_split = (max_t + 63) / 64;
+    int ns = std::max(1, std::min(want, max_split));
+    int sl = (max_t + ns - 1) / ns;
+    sl = (sl + 31) / 32 * 32;
+    ns = (max_t + sl - 1) / sl;
+    return Plan{ns, sl};
+}
+
+// One pass of `Mc` rows (already on the device at `rows`) through all layers.
+// `x_is_gemv` selects the single-row decode kernels.
+static void run_layers(Model &m, Kv &kv, const Rows &rows, int Mc, int max_t) {
+    hipStream_t s = kv.stream;
+    const bool single = Mc == 1;
+    const Dt act = DT_F32;  // activations stay f32; weights carry the format
+    const int H = m.H;
+    Plan plan = attn_plan(m, Mc, max_t);
+    kv.part.ensure((size_t)Mc * m.nq * plan.n_split * (m.hd + 2) * 4);
+    for (int l = 0; l < m.L; ++l) {
+        LayerW &w = m.layers[l];
+        // ---- attention block (layer.rs:120-131)
+        if (single) {
+            GemvArgs g{};
+            g.w = w.qkv;
+            g.x = kv.h.as<float>();
+            g.gamma = w.in_norm;
+            g.eps = m.cfg.rms_norm_eps;
+            g.bias = w.qkv_bias;
+            g.y = kv.qkv.as<float>();
+            g.N = w.qkv_rows;
+            g.K = H;
+            Prof p("gemv", s);
+            launch_gemv(m.wt, GEMV_STORE, g, s);
+        } else {
+            {
+                Prof p("rmsnorm", s);
+                launch_rmsnorm(kv.h.as<float>(), w.in_norm, m.cfg.rms_norm_eps, Mc, H, act,
+                               kv.xn.p, nullptr, s);
+            }
+            GemmArgs g{};
+            g.a = kv.xn.p;
+            g.w = w.qkv;
+            g.bias = w.qkv_bias;
+            g.c = kv.qkv.p;
+            g.M = Mc;
+            g.N = w.qkv_rows;
+            g.K = H;
+            g.ldc = w.qkv_rows;
+            Prof p("gemm", s);
+            launch_gemm(m.wt, GEMM_STORE, g, s);
+        }
+        {
+            RopeKvArgs r{};
+            r.qkv = kv.qkv.as<float>();
+            r.ldq = w.qkv_rows;
+            r.q_out = kv.q.as<float>();
+            r.rope_cos = m.rope_cos;
+            r.rope_sin = m.rope_sin;
+            r.q_norm = w.q_norm;
+            r.k_norm = w.k_norm;
+            r.eps = m.cfg.rms_norm_eps;
+            for (int j = 0; j < 3; ++j) {
+                r.lora_b[j] = w.lora_b[j];
+                r.lora_t_col[j] = w.lora_t_col[j];
+                r.lora_rank[j] = w.lora_rank[j];
+                r.lora_scale[j] = w.lora_scale[j];
+            }
+            r.rows = rows;
+            r.kv = (char *)kv.cache.p + (size_t)l * kv.layer_stride * dt_size(kv.dt);
+            r.seq_stride = kv.seq_stride;
+            r.layer_stride = kv.layer_stride;
+            r.kv_half_stride = kv.half_stride;
+            r.head_stride = kv.head_stride;
+            r.nq = m.nq;
+            r.nkv = m.nkv;
+            r.hd = m.hd;
+            Prof p("rope_kv", s);
+            launch_rope_kv(m.wt, kv.dt, r, s);
+        }
+        {
+            AttnArgs a{};
+            a.q = kv.q.as<float>();
+            a.kv = (char *)kv.cache.p + (size_t)l * kv.layer_stride * dt_size(kv.dt);
+            a.seq_stride = kv.seq_stride;
+            a.layer_stride = kv.layer_stride;
+            a.kv_half_stride = kv.half_stride;
+            a.head_stride = kv.head_stride;
+            a.rows = rows;
+            a.nq = m.nq;
+            a.nkv = m.nkv;
+            a.hd = m.hd;
+            a.window = w.window;
+            a.part = kv.part.as<float>();
+            a.n_split = plan.n_split;
+            a.split_len = plan.split_len;
+            a.out = kv.attn.p;
+            a.out_dt = act;
+            Prof p("attention", s);
+            launch_attention(kv.dt, a, s);
+        }
+        if (single) {
+            GemvArgs g{};
+            g.w = w.o;
+            g.x = kv.attn.as<float>();
+            g.bias = w.o_bias;
+            g.y = kv.h.as<float>();
+            g.N = H;
+            g.K = m.qw;
+            Prof p("gemv", s);
+            launch_gemv(m.wt, GEMV_RESIDUAL, g, s);
+        } else {
+            GemmArgs g{};
+            g.a = kv.attn.p;
+            g.w = w.o;
+            g.bias = w.o_bias;
+            g.c = kv.h.p;
+            g.M = Mc;
+            g.N = H;
+            g.K = m.qw;
+            g.ldc = H;
+            Prof p("gemm", s);
+            launch_gemm(m.wt, GEMM_RESIDUAL, g, s);
+        }
+        // ---- MLP block (layer.rs:147-151)
+        if (w.moe) {
+            moe_block(m, kv, w, Mc, s);
+        } else if (single) {
+            GemvArgs g{};
+            g.w = w.gate;
+            g.w2 = w.up;
+            g.x = kv.h.as<float>();
+            g.gamma = w.post_norm;
+            g.eps = m.cfg.rms_norm_eps;
+            g.y = kv.act.as<float>();
+            g.N = m.F;
+            g.K = H;
+            {
+                Prof p("gemv", s);
+                launch_gemv(m.wt, GEMV_SWIGLU, g, s);
+            }
+            GemvArgs d{};
+            d.w = w.down;
+            d.x = kv.act.as<float>();
+            d.y = kv.h.as<float>();
+            d.N = H;
+            d.K = m.F;
+            Prof p("gemv", s);
+            launch_gemv(m.wt, GEMV_RESIDUAL, d, s);
+        } else {
+            {
+                Prof p("rmsnorm", s);
+                launch_rmsnorm(kv.h.as<float>(), w.post_norm, m.cfg.rms_norm_eps, Mc, H, act,
+                               kv.xn.p, nullptr, s);
+            }
+            GemmArgs g{};
+            g.a = kv.xn.p;
+            g.w = w.gate;
+            g.w2 = w.up;
+            g.c = kv.act.p;
+            g.M = Mc;
+            g.N = m.F;
+            g.K = H;
+            g.ldc = m.F;
+            {
+                Prof p("gemm", s);
+                launch_gemm(m.wt, GEMM_SWIGLU, g, s);
+            }
+            GemmArgs d{};
+            d.a = kv.act.p;
+            d.w = w.down;
+            d.c = kv.h.p;
+            d.M = Mc;
+            d.N = H;
+            d.K = m.F;
+            d.ldc = H;
+            Prof p("gemm", s);
+            launch_gemm(m.wt, GEMM_RESIDUAL, d, s);
+        }
+    }
+}
+
+static void ensure_scratch(Model &m, Kv &kv, int Mc, int n_seqs) {
+    const size_t H = m.H;
+    int qkv_rows = 0;
+    for (auto &w : m.layers) qkv_rows = std::max(qkv_rows, w.qkv_rows);
+    int fmax = std::max(m.F, std::max(m.Fe, m.Fs));
+    kv.h.ensure((size_t)Mc * H * 4);
+    kv.xn.ensure((size_t)Mc * H * 4);
+    kv.qkv.ensure((size_t)Mc * qkv_rows * 4);
+    kv.q.ensure((size_t)Mc * m.qw * 4);
+    kv.attn.ensure((size_t)Mc * m.qw * 4);
+    kv.act.ensure((size_t)Mc * fmax * 4);
+    kv.last_h.ensure((size_t)n_seqs * H * 4);
+    kv.logits.ensure((size_t)std::max(n_seqs, kv.batch) * m.V * 4);
+    kv.rows_dev.ensure((size_t)(3 * kMaxRows + 2 * kv.batch + 64) * 4);
+}
+
+// Head on the last row of each sequence (model.rs:531-538): final RMSNorm
+// then [H] x [V, H]^T into f32 logits rows. `h_src` rows are selected by
+// `row_index` (device, nullable = rows 0..n_seqs-1).
+static void run_head(Model &m, Kv &kv, int n_seqs, const float *h_src, const int32_t *row_index) {
+    hipStream_t s = kv.stream;
+    if (n_seqs == 1) {
+        GemvArgs g{};
+        g.w = m.head;
+        g.x = h_src;
+        g.gamma = m.final_norm;
+        g.eps = m.cfg.rms_norm_eps;
+        g.y = kv.logits.as<float>();
+        g.N = m.V;
+        g.K = m.H;
+        Prof p("gemv", s);
+        launch_gemv(m.wt, GEMV_STORE, g, s);
+        return;
+    }
+    {
+        Prof p("rmsnorm", s);
+        launch_rmsnorm(h_src, m.final_norm, m.cfg.rms_norm_eps, n_seqs, m.H, DT_F32, kv.xn.p,
+                       row_index, s);
+    }
+    GemmArgs g{};
+    g.a = kv.xn.p;
+    g.w = m.head;
+    g.c = kv.logits.p;
+    g.M = n_seqs;
+    g.N = m.V;
+    g.K = m.H;
+    g.ldc = m.V;
+    Prof p("gemm", s);
+    launch_gemm(m.wt, GEMM_STORE, g, s);
+}
+
+void forward(Model &m, Kv &kv, int n_seqs, const uint32_t *seqs, const uint32_t *lens,
+             const int32_t *ids) {
+    if (n_seqs <= 0) fail(ESP_INVALID_REQUEST, "cached input is empty or exceeds the context window");
+    // validate (model.rs:548-556) before touching any state
+    std::vector<int> seen(kv.batch, 0);
+    long long M = 0;
+    for (int i = 0; i < n_seqs; ++i) {
+        if (seqs[i] >= (uint32_t)kv.batch) fail(ESP_INVALID_REQUEST, "sequence index out of range");
+        if (seen[seqs[i]]++) fail(ESP_INVALID_REQUEST, "a sequence appears twice in one batch");
+        long long end = (long long)kv.pos[seqs[i]] + lens[i];
+        if (lens[i] == 0 || end > kv.max_ctx || end > (long long)m.cfg.max_position_embeddings)
+            fail(ESP_INVALID_REQUEST, "cached input is empty or exceeds the context window");
+        M += lens[i];
+    }
+    for (long long r = 0; r < M; ++r)
+        if (ids[r] < 0 || ids[r] >= m.V) fail(ESP_INVALID_REQUEST, "token id outside the vocabulary");
+    ensure_scratch(m, kv, (int)std::min<long long>(M, kMaxRows), n_seqs);
+    // host row descriptors
+    std::vector<int32_t> rseq(M), rpos(M);
+    std::vector<int32_t> last(n_seqs);
+    int max_t = 0;
+    {
+        long long r = 0;
+        for (int i = 0; i < n_seqs; ++i) {
+            for (uint32_t t = 0; t < lens[i]; ++t, ++r) {
+                rseq[r] = (int32_t)seqs[i];
+                rpos[r] = kv.pos[seqs[i]] + (int)t;
+            }
+            last[i] = (int32_t)(r - 1);
+            max_t = std::max(max_t, kv.pos[seqs[i]] + (int)lens[i]);
+        }
+    }
+    hipStream_t s = kv.stream;
+    const int lastoff = 3 * kMaxRows;
+    ensure_pinned(kv, (size_t)(3 * kMaxRows + kv.batch + 64) * 4);
+    int32_t *pin = (int32_t *)kv.pinned;
+    int32_t *dev = kv.rows_dev.as<int32_t>();
+    float *hl = kv.last_h.as<float>();
+    const bool one_chunk = M <= kMaxRows;
+    for (long long c0 = 0; c0 < M; c0 += kMaxRows) {
+        int Mc = (int)std::min<long long>(kMaxRows, M - c0);
+        ESP_HIP(hipStreamSynchronize(s));  // pinned staging buffer reuse
+        memcpy(pin, ids + c0, Mc * 4);
+        memcpy(pin + kMaxRows, rseq.data() + c0, Mc * 4);
+        memcpy(pin + 2 * kMaxRows, rpos.data() + c0, Mc * 4);
+        memcpy(pin + lastoff, last.data(), n_seqs * 4);
+        ESP_HIP(hipMemcpyAsync(dev, pin, (size_t)(lastoff + n_seqs) * 4, hipMemcpyHostToDevice, s));
+        Rows rows{dev, dev + kMaxRows, dev + 2 * kMaxRows, Mc};
+        {
+            Prof p("embed", s);
+            launch_embed(m.wt, m.embed, rows.ids, Mc, m.H, kv.h.as<float>(), s);
+        }
+        run_layers(m, kv, rows, Mc, max_t);
+        if (one_chunk) break;
+        // keep the hidden state of every sequence's last row in this chunk
+        for (int i = 0; i < n_seqs; ++i)
+            if (last[i] >= c0 && last[i] < c0 + Mc)
+                ESP_HIP(hipMemcpyAsync(hl + (size_t)i * m.H, kv.h.as<float>() + (size_t)(last[i] - c0) * m.H,
+                                       (size_t)m.H * 4, hipMemcpyDeviceToDevice, s));
+    }
+    if (one_chunk) {
+        if (n_seqs == 1) run_head(m, kv, 1, kv.h.as<float>() + (size_t)last[0] * m.H, nullptr);
+        else run_head(m, kv, n_seqs, kv.h.as<float>(), dev + lastoff);
+    } else {
+        run_head(m, kv, n_seqs, hl, nullptr);
+    }
+    ESP_HIP(hipStreamSynchronize(s));
+    for (int i = 0; i < n_seqs; ++i) kv.pos[seqs[i]] += (int)lens[i];
+    kv.logits_rows = n_seqs;
+}
+
+}  // namespace esp
+
+namespace esp {
+
+// One greedy decode step whose input token, position and output slot live
+// in device memory (gen layout in k_basic.hip), so the step can be captured
+// once and replayed: generate.rs:154-168 without the host round trip.
+void decode_step_dev(Model &m, Kv &kv, int seq, int max_t, int32_t *gen) {
+    (void)seq;
+    hipStream_t s = kv.stream;
+    ensure_scratch(m, kv, 1, 1);
+    Rows rows{gen, gen + 2, gen + 3, 1};
+    {
+        Prof p("embed", s);
+        launch_embed(m.wt, m.embed, rows.ids, 1, m.H, kv.h.as<float>(), s);
+    }
+    run_layers(m, kv, rows, 1, max_t);
+    run_head(m, kv, 1, kv.h.as<float>(), nullptr);
+    kv.pick_io.ensure(64);
+    PickArgs a{};
+    a.logits = kv.logits.as<float>();
+    a.n = 1;
+    a.V = m.V;
+    a.ids_out = (uint32_t *)kv.pick_io.p;
+    a.flags_out = (uint8_t *)kv.pick_io.p + 16;
+    {
+        Prof p("pick", s);
+        launch_pick(a, s);
+    }
+    launch_gen_step(a.ids_out, gen, s);
+    kv.logits_rows = 1;
+}
+
+// moe.rs:135-256 DecoderMlp::forward (Moe arm) for Mc rows: h += routed
+// experts (+ sigmoid-gated shared expert) of RMSNorm(h).
+void moe_block(Model &m, Kv &kv, LayerW &w, int Mc, hipStream_t s) {
+    const Dt act = DT_F32;
+    const int H = m.H, E = m.E, k = m.topk;
+    {
+        Prof p("rmsnorm", s);
+        launch_rmsnorm(kv.h.as<float>(), w.post_norm, m.cfg.rms_norm_eps, Mc, H, act, kv.xn.p,
+                       nullptr, s);
+    }
+    kv.moe_logits.ensure((size_t)Mc * E * 4);
+    kv.moe_sel.ensure((size_t)Mc * k * 4);
+    kv.moe_w.ensure((size_t)Mc * k * 4);
+    kv.moe_slot.ensure((size_t)Mc * k * 4);
+    kv.moe_offs.ensure((size_t)(E + 2) * 4);
+    kv.moe_perm.ensure((size_t)Mc * k * 4);
+    kv.moe_x.ensure((size_t)Mc * k * H * 4);
+    kv.moe_act.ensure((size_t)Mc * k * m.Fe * 4);
+    kv.moe_y.ensure((size_t)Mc * k * H * 4);
+    GemmArgs r{};
+    r.a = kv.xn.p;
+    r.w = w.router;
+    r.c = kv.moe_logits.p;
+    r.M = Mc;
+    r.N = E;
+    r.K = H;
+    r.ldc = E;
+    {
+        Prof p("gemm", s);
+        launch_gemm(m.wt, GEMM_STORE, r, s);
+    }
+    RouteArgs ra{kv.moe_logits.as<float>(), Mc, E, k, m.norm_topk ? 1 : 0,
+                 kv.moe_sel.as<int32_t>(), kv.moe_w.as<float>(), kv.moe_offs.as<int32_t>(),
+                 kv.moe_perm.as<int32_t>(), kv.moe_slot.as<int32_t>()};
+    {
+        Prof p("moe", s);
+        launch_route(ra, s);
+    }
+    std::vector<int32_t> offs(E + 2);
+    ESP_HIP(hipMemcpyAsync(offs.data(), kv.moe_offs.p, (E + 2) * 4, hipMemcpyDeviceToHost, s));
+    ESP_HIP(hipStreamSynchronize(s));
+    if (offs[E + 1] == 2) fail(ESP_BACKEND, "non-finite expert router");
+    if (offs[E + 1] == 3) fail(ESP_BACKEND, "invalid top-k routing mass");
+    const size_t es = dt_size(act);
+    {
+        Prof p("moe", s);
+        launch_gather_rows(act, kv.xn.p, kv.moe_perm.as<int32_t>(), Mc * k, H, kv.moe_x.p, s);
+    }
+    for (int e = 0; e < E; ++e) {
+        int n = offs[e + 1] - offs[e];
+        if (!n) continue;
+        GemmArgs g{};
+        g.a = (char *)kv.moe_x.p + (size_t)offs[e] * H * es;
+        g.w = (char *)w.ex_gate + (size_t)e * m.Fe * H * dt_size(m.wt);
+        g.w2 = (char *)w.ex_up + (size_t)e * m.Fe * H * dt_size(m.wt);
+        g.c = (char *)kv.moe_act.p + (size_t)offs[e] * m.Fe * es;
+        g.M = n;
+        g.N = m.Fe;
+        g.K = H;
+        g.ldc = m.Fe;
+        {
+            Prof p("gemm", s);
+            launch_gemm(m.wt, GEMM_SWIGLU, g, s);
+        }
+        GemmArgs d{};
+        d.a = g.c;
+        d.w = (char *)w.ex_down + (size_t)e * H * m.Fe * dt_size(m.wt);
+        d.c = kv.moe_y.as<float>() + (size_t)offs[e] * H;
+        d.M = n;
+        d.N = H;
+        d.K = m.Fe;
+        d.ldc = H;
+        Prof p("gemm", s);
+        launch_gemm(m.wt, GEMM_STORE, d, s);
+    }
+    CombineArgs c{};
+    c.y = kv.moe_y.as<float>();
+    c.slot = kv.moe_slot.as<int32_t>();
+    c.w = kv.moe_w.as<float>();
+    c.h = kv.h.as<float>();
+    c.M = Mc;
+    c.k = k;
+    c.H = H;
+    if (m.Fs) {
+        kv.moe_ys.ensure((size_t)Mc * H * 4);
+        kv.moe_sg.ensure((size_t)Mc * 4);
+        GemmArgs g{};
+        g.a = kv.xn.p;
+        g.w = w.sh_gate;
+        g.w2 = w.sh_up;
+        g.c = kv.act.p;
+        g.M = Mc;
+        g.N = m.Fs;
+        g.K = H;
+        g.ldc = m.Fs;
+        GemmArgs d{};
+        d.a = kv.act.p;
+        d.w = w.sh_down;
+        d.c = kv.moe_ys.p;
+        d.M = Mc;
+        d.N = H;
+        d.K = m.Fs;
+        d.ldc = H;
+        GemmArgs sg{};
+        sg.a = kv.xn.p;
+        sg.w = w.shared_gate;
+        sg.c = kv.moe_sg.p;
+        sg.M = Mc;
+        sg.N = 1;
+        sg.K = H;
+        sg.ldc = 1;
+        Prof p("gemm", s);
+        launch_gemm(m.wt, GEMM_SWIGLU, g, s);
+        launch_gemm(m.wt, GEMM_STORE, d, s);
+        launch_gemm(m.wt, GEMM_STORE, sg, s);
+        c.ys = kv.moe_ys.as<float>();
+        c.sg = kv.moe_sg.as<float>();
+    }
+    Prof p("moe", s);
+    launch_combine(c, s);
+}
+
+}  // namespace esp

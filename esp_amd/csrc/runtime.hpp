@@ -1,0 +1,109 @@
+// Host-side runtime objects behind the C ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <map>
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "common.hpp"
+
+namespace esp {
+
+// One device allocation, freed with the owner.
+struct DevMem {
+    void *p = nullptr;
+    size_t bytes = 0;
+    DevMem() = default;
+    explicit DevMem(size_t n) { alloc(n); }
+    DevMem(const DevMem &) = delete;
+    DevMem &operator=(const DevMem &) = delete;
+    ~DevMem() {
+        if (p) (void)hipFree(p);
+    }
+    void alloc(size_t n) {
+        if (p) (void)hipFree(p);
+        p = nullptr;
+        bytes = 0;
+        if (n) ESP_HIP(hipMalloc(&p, n));
+        bytes = n;
+    }
+    // Grow-only reallocation (contents not preserved).
+    void ensure(size_t n) {
+        if (n > bytes) alloc(n);
+    }
+    template <typename T> T *as() const { return (T *)p; }
+};
+
+struct LayerW {
+    float *in_norm = nullptr, *post_norm = nullptr;
+    void *qkv = nullptr;        // [qkv_rows, H]: q | k | v | LoRA-A rows (q, k, v targets)
+    float *qkv_bias = nullptr;  // [qkv_rows] or null
+    int qkv_rows = 0;
+    void *o = nullptr;          // [H, qw]
+    float *o_bias = nullptr;
+    float *q_norm = nullptr, *k_norm = nullptr;
+    void *gate = nullptr, *up = nullptr, *down = nullptr;  // dense
+    bool moe = false;
+    void *router = nullptr;       // [E, H]
+    void *shared_gate = nullptr;  // [1, H]
+    void *sh_gate = nullptr, *sh_up = nullptr, *sh_down = nullptr;
+    void *ex_gate = nullptr, *ex_up = nullptr, *ex_down = nullptr;  // [E][F][H], [E][F][H], [E][H][F]
+    // unmerged LoRA (targets 0 q, 1 k, 2 v): B [out, rank], t at qkv column t_col
+    void *lora_b[3] = {nullptr, nullptr, nullptr};
+    int lora_rank[3] = {0, 0, 0};
+    int lora_t_col[3] = {0, 0, 0};
+    float lora_scale[3] = {0, 0, 0};
+    int window = 0;
+};
+
+struct Model {
+    esp_config cfg{};
+    Dt wt = DT_F32;  // weight (and KV) element type
+    int H = 0, L = 0, nq = 0, nkv = 0, hd = 0, F = 0, V = 0, qw = 0, kvw = 0;
+    int E = 0, topk = 0, Fe = 0, Fs = 0;
+    bool norm_topk = false;
+    std::vector<LayerW> layers;
+    void *embed = nullptr;  // [V, H]
+    void *head = nullptr;   // [V, H] (== embed when tied)
+    float *final_norm = nullptr;
+    float *rope_cos = nullptr, *rope_sin = nullptr;  // [max_pos, hd]
+    std::vector<std::unique_ptr<DevMem>> mem;
+    uint64_t weight_bytes = 0;
+    int device = 0;
+
+    void *alloc(size_t bytes) {
+        mem.emplace_back(new DevMem(bytes));
+        weight_bytes += bytes;
+        return mem.back()->p;
+    }
+};
+
+struct Kv {
+    Model *model = nullptr;
+    int batch = 0, max_ctx = 0;
+    Dt dt = DT_F32;
+    DevMem cache;
+    long long seq_stride = 0, layer_stride = 0, half_stride = 0, head_stride = 0;
+    std::vector<int> pos;  // host mirror of each sequence's position
+    hipStream_t stream = nullptr;
+    // scratch
+    DevMem rows_dev;   // ids | row_seq | row_pos | last_row  (int32)
+    DevMem h, xn, qkv, q, attn, act, part, last_h, logits, pick_scratch, pick_io;
+    DevMem moe_logits, moe_sel, moe_w, moe_slot, moe_offs, moe_perm, moe_x, moe_y, moe_ys, moe_sg,
+        moe_act;
+    int logits_rows = 0;  // rows valid in `logits`
+    void *pinned = nullptr;
+    size_t pinned_bytes = 0;
+    // generation graph
+    hipGraphExec_t gen_exec = nullptr;
+    ~Kv();
+};
+
+// The forward over prepared rows; defined in runtime.cpp.
+void forward(Model &m, Kv &kv, int n_seqs, const uint32_t *seqs, const uint32_t *lens,
+             const int32_t *ids);
+
+}  // namespace esp

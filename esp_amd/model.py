@@ -1,0 +1,249 @@
+"""DecoderModel / KvCache over the HIP library, mirroring esp's model seam.
+
+crates/esp/src/infer/decoder/model.rs: `DecoderModel::{from_loaded,
+new_cache, try_forward_cached_last}` and `KvCache::position`; loader.rs
+`load_decoder_from_bytes`; lora.rs adapters. All compute runs in
+libesp_hip.so; this module converts arguments and errors only.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from typing import List, Optional, Sequence, Tuple
+
+import numpy as np
+
+from . import _lib
+from .config import DecoderConfig
+from .errors import InvalidRequest
+from .sample import Sampler
+
+FORMATS = {"f32": _lib.ESP_FORMAT_F32, "bf16": _lib.ESP_FORMAT_BF16}
+TARGET_BITS = {"q_proj": 1, "k_proj": 2, "v_proj": 4, "o_proj": 8}
+
+
+def esp_config(cfg: DecoderConfig, fmt: str = "f32"):
+    """DecoderConfig -> (EspConfig struct, keep-alive arrays)."""
+    c = _lib.EspConfig()
+    c.vocab_size = cfg.vocab_size
+    c.hidden_size = cfg.hidden_size
+    c.intermediate_size = cfg.intermediate_size
+    c.num_hidden_layers = cfg.num_hidden_layers
+    c.num_attention_heads = cfg.num_attention_heads
+    c.num_key_value_heads = cfg.kv_heads()
+    c.head_dim = cfg.head_dim()
+    c.max_position_embeddings = cfg.max_position_embeddings
+    c.rms_norm_eps = cfg.rms_norm_eps
+    c.rope_theta = cfg.rope_theta
+    rs = cfg.rope_scaling
+    if rs is not None:
+        c.rope_scaling = _lib.ESP_ROPE_LINEAR if rs.kind == "linear" else _lib.ESP_ROPE_LLAMA3
+        c.rope_factor = rs.factor
+        c.rope_low_freq_factor = rs.low_freq_factor
+        c.rope_high_freq_factor = rs.high_freq_factor
+        c.rope_original_max_position_embeddings = rs.original_max_position_embeddings
+    c.tie_word_embeddings = int(cfg.tie_word_embeddings)
+    c.qkv_bias = int(cfg.qkv_bias())
+    c.output_bias = int(cfg.output_bias())
+    c.qk_norm = int(cfg.qk_norm())
+    L = cfg.num_hidden_layers
+    win = (C.c_uint32 * L)(*[cfg.layer_window(i) or 0 for i in range(L)])
+    c.layer_window = C.cast(win, C.POINTER(C.c_uint32))
+    moe = (C.c_uint8 * L)(*[int(cfg.layer_is_moe(i)) for i in range(L)])
+    c.layer_is_moe = C.cast(moe, C.POINTER(C.c_uint8))
+    if cfg.moe is not None:
+        c.num_experts = cfg.moe.num_experts
+        c.num_experts_per_tok = cfg.moe.num_experts_per_tok
+        c.moe_intermediate_size = cfg.moe.moe_intermediate_size
+        c.shared_expert_intermediate_size = cfg.moe.shared_expert_intermediate_size
+        c.norm_topk_prob = int(cfg.moe.norm_topk_prob)
+    c.format = FORMATS[fmt]
+    return c, (win, moe)
+
+
+class LoraAdapter:
+    """One PEFT LoRA adapter (lora.rs:99-217): rank, alpha, selection scale,
+    target modules and the adapter safetensors bytes. Applied unmerged."""
+
+    def __init__(self, rank: int, alpha: float, targets: Sequence[str], weights: bytes,
+                 selection_scale: float = 1.0):
+        for t in targets:
+            if t not in TARGET_BITS:
+                from .errors import InvalidConfig
+                raise InvalidConfig(f"PEFT LoRA target module {t!r} is not supported; expected "
+                                    "llama q/k/v/o projections")
+        self.rank = rank
+        # lora.rs:194: alpha / rank * selection scale, in f32
+        a = np.float32(alpha) / np.float32(rank)
+        self.scale = float(np.float32(a * np.float32(selection_scale)))
+        self.mask = sum(TARGET_BITS[t] for t in set(targets))
+        self.weights = bytes(weights)
+
+
+class KvCache:
+    """model.rs:671-681 KvCache for `batch` independent sequences."""
+
+    def __init__(self, model: "DecoderModel", batch: int, max_ctx: int):
+        L = _lib.load()
+        h = C.c_void_p()
+        _lib.check(L.esp_kv_create(model._h, batch, max_ctx, C.byref(h)))
+        self._h = h
+        self.model = model
+        self.batch = batch
+        self.max_ctx = max_ctx
+
+    def position(self, seq: int = 0) -> int:
+        p = C.c_uint32()
+        _lib.check(_lib.load().esp_kv_position(self._h, seq, C.byref(p)))
+        return p.value
+
+    def reset(self, seq: Optional[int] = None) -> None:
+        _lib.check(_lib.load().esp_kv_reset(self._h, 0xFFFFFFFF if seq is None else seq))
+
+    def stream(self) -> int:
+        s = C.c_void_p()
+        _lib.check(_lib.load().esp_kv_stream(self._h, C.byref(s)))
+        return s.value or 0
+
+    def close(self) -> None:
+        if getattr(self, "_h", None):
+            _lib.load().esp_kv_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        self.close()
+
+
+class DecoderModel:
+    """model.rs:151-667 DecoderModel, weights resident in HBM."""
+
+    def __init__(self, handle, config: DecoderConfig, fmt: str):
+        self._h = handle
+        self.config = config
+        self.format = fmt
+
+    @staticmethod
+    def from_bytes(config: DecoderConfig, weights: bytes, fmt: str = "f32",
+                   adapters: Optional[List[LoraAdapter]] = None) -> "DecoderModel":
+        """loader.rs:573-580 load_decoder_from_bytes (+ lora.rs adapters)."""
+        L = _lib.load()
+        c, keep = esp_config(config, fmt)
+        buf = (C.c_uint8 * len(weights)).from_buffer_copy(weights) if weights else None
+        ads = adapters or []
+        arr = (_lib.EspLora * max(1, len(ads)))()
+        bufs = []
+        for i, a in enumerate(ads):
+            b = (C.c_uint8 * len(a.weights)).from_buffer_copy(a.weights)
+            bufs.append(b)
+            arr[i] = _lib.EspLora(a.rank, a.scale, a.mask, C.cast(b, C.c_void_p), len(a.weights))
+        h = C.c_void_p()
+        _lib.check(L.esp_model_load(C.byref(c), buf, len(weights), arr, len(ads), C.byref(h)))
+        del keep, bufs
+        return DecoderModel(h, config, fmt)
+
+    @staticmethod
+    def synthetic(config: DecoderConfig, seed: int, std: float = 0.02, fmt: str = "bf16",
+                  lora_rank: int = 0, lora_targets: Sequence[str] = (), lora_a_std: float = 0.02,
+                  lora_b_std: float = 0.01, lora_scale: float = 1.0) -> "DecoderModel":
+        L = _lib.load()
+        c, keep = esp_config(config, fmt)
+        mask = sum(TARGET_BITS[t] for t in set(lora_targets))
+        h = C.c_void_p()
+        _lib.check(L.esp_model_create_synthetic(C.byref(c), seed, std, lora_rank, mask, lora_a_std,
+                                                lora_b_std, lora_scale, C.byref(h)))
+        del keep
+        return DecoderModel(h, config, fmt)
+
+    def weight_bytes(self) -> int:
+        n = C.c_uint64()
+        _lib.check(_lib.load().esp_model_weight_bytes(self._h, C.byref(n)))
+        return n.value
+
+    def new_cache(self, batch: int = 1, max_ctx: Optional[int] = None) -> KvCache:
+        """model.rs:476-483"""
+        return KvCache(self, batch, max_ctx or self.config.max_position_embeddings)
+
+    def try_forward_cached_last(self, ids: Sequence[int], cache: KvCache,
+                                seq: int = 0) -> np.ndarray:
+        """model.rs:502-539: logits [vocab] (f32) of the block's last position."""
+        ids = np.ascontiguousarray(ids, dtype=np.int32)
+        out = np.empty(self.config.vocab_size, np.float32)
+        _lib.check(_lib.load().esp_forward_last(
+            self._h, cache._h, seq, ids.ctypes.data_as(C.POINTER(C.c_int32)), len(ids),
+            out.ctypes.data))
+        return out
+
+    def forward_batch(self, cache: KvCache, seqs: Sequence[int],
+                      blocks: Sequence[Sequence[int]], want_logits: bool = True) -> Optional[np.ndarray]:
+        """Several sequences' blocks in one pass; row i = last logits of seqs[i]."""
+        seqs_a = np.ascontiguousarray(seqs, dtype=np.uint32)
+        lens = np.ascontiguousarray([len(b) for b in blocks], dtype=np.uint32)
+        ids = np.ascontiguousarray([t for b in blocks for t in b], dtype=np.int32)
+        out = np.empty((len(seqs_a), self.config.vocab_size), np.float32) if want_logits else None
+        _lib.check(_lib.load().esp_forward_batch(
+            self._h, cache._h, len(seqs_a), seqs_a.ctypes.data_as(C.POINTER(C.c_uint32)),
+            lens.ctypes.data_as(C.POINTER(C.c_uint32)), ids.ctypes.data_as(C.POINTER(C.c_int32)),
+            None if out is None else out.ctypes.data))
+        return out
+
+    def pick(self, cache: KvCache, n_rows: int, allowed_bits: Optional[np.ndarray] = None,
+             samplers: Optional[List[Optional[Sampler]]] = None) -> Tuple[np.ndarray, np.ndarray]:
+        """Token choice over the device-resident logits rows of the last forward
+        (generate.rs:30-44, provider.rs:807-816). Updates sampler RNG state."""
+        ids = np.zeros(n_rows, np.uint32)
+        flags = np.zeros(n_rows, np.uint8)
+        bits = None
+        if allowed_bits is not None:
+            bits = np.ascontiguousarray(allowed_bits, dtype=np.uint32)
+            words = (self.config.vocab_size + 31) // 32
+            if bits.size != n_rows * words:
+                raise InvalidRequest("allowed bitmask has the wrong size")
+        sarr = None
+        if samplers is not None:
+            sarr = (_lib.EspSampler * n_rows)()
+            for i, s in enumerate(samplers):
+                if s is None:
+                    sarr[i] = _lib.EspSampler(0.0, -1.0, 0)
+                else:
+                    sarr[i] = _lib.EspSampler(s.temperature,
+                                              -1.0 if s.top_p is None else s.top_p, s.rng.state)
+        status = _lib.load().esp_pick(
+            cache._h, n_rows, None if bits is None else bits.ctypes.data, sarr,
+            ids.ctypes.data_as(C.POINTER(C.c_uint32)), flags.ctypes.data_as(C.POINTER(C.c_uint8)))
+        if samplers is not None:
+            for i, s in enumerate(samplers):
+                if s is not None:
+                    s.rng.state = sarr[i].state
+        _lib.check(status)
+        return ids, flags
+
+    def generate_greedy_device(self, cache: KvCache, prompt: Sequence[int], max_new: int,
+                               eos: Sequence[int], seq: int = 0) -> List[int]:
+        """generate.rs:134-170 with the greedy picker, run as a device loop."""
+        p = np.ascontiguousarray(prompt, dtype=np.int32)
+        e = np.ascontiguousarray(list(eos) or [0], dtype=np.int32)
+        out = np.zeros(max(1, max_new), np.int32)
+        n = C.c_uint32()
+        P = C.POINTER(C.c_int32)
+        _lib.check(_lib.load().esp_generate_greedy(
+            self._h, cache._h, seq, p.ctypes.data_as(P), len(p), max_new, e.ctypes.data_as(P),
+            len(eos), out.ctypes.data_as(P), C.byref(n)))
+        return [int(x) for x in out[:n.value]]
+
+    def close(self) -> None:
+        if getattr(self, "_h", None):
+            _lib.load().esp_model_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        self.close()
+
+
+def profile_enable(kernel: str, on: bool = True) -> None:
+    _lib.check(_lib.load().esp_profile_enable(kernel.encode(), int(on)))
+
+
+def profile_read(kernel: str) -> Tuple[int, float]:
+    n = C.c_uint64()
+    ms = C.c_double()
+    _lib.check(_lib.load().esp_profile_read(kernel.encode(), C.byref(n), C.byref(ms)))
+    return n.value, ms.value

@@ -1,0 +1,201 @@
+/*
+ * esp_hip.h — C ABI of the MI355X (gfx950) llama-family decoder forward.
+ *
+ * This is the drop-in boundary for esp's model-execution seam. Each entry
+ * point names the reference interface it replaces (paths relative to
+ * merely-made/esp, crates/esp/src/infer/). Plain pointers and sizes only;
+ * no C++ exception crosses the boundary; every call returns an esp_status
+ * whose values are 1:1 with the reference's InferError variants
+ * (provider.rs:160-183), with the message available from esp_last_error.
+ *
+ * Threading: a model is immutable after load and may be shared by threads.
+ * A KV handle binds one HIP stream and is owned by one caller at a time
+ * (the reference's `&mut KvCache`). Calls are synchronous: when one returns,
+ * its outputs are in host memory (or, for device-resident logits, complete
+ * on the KV handle's stream).
+ */
+#ifndef ESP_HIP_H
+#define ESP_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* InferError (provider.rs:160-183) as status codes. */
+typedef enum esp_status {
+    ESP_OK = 0,
+    ESP_PROMPT_TOO_LONG = 1,   /* PromptTooLong { length, limit } */
+    ESP_MODEL_NOT_LOADED = 2,  /* ModelNotLoaded */
+    ESP_INTERRUPTED = 3,       /* Interrupted */
+    ESP_BACKEND = 4,           /* Backend(String): a HIP failure */
+    ESP_STAGE_UNAVAILABLE = 5, /* StageUnavailable(String) */
+    ESP_INVALID_REQUEST = 6,   /* InvalidRequest(String) */
+    ESP_INVALID_CONFIG = 7,    /* InvalidConfig(String) */
+    ESP_INVALID_WEIGHTS = 8,   /* InvalidWeights(String) */
+    ESP_UNSUPPORTED = 9        /* Unsupported { feature, detail }: "feature: detail" */
+} esp_status;
+
+/* Weight storage/compute format (decoder/weight_format.rs:22-32):
+ * F32 widens every checkpoint tensor to f32 (the reference's default
+ * corridor); BF16 keeps bf16 weights in HBM, bf16 MFMA inputs, f32
+ * accumulation and an f32 residual stream; its artifacts must be BF16
+ * (weight_format.rs:283-291). */
+typedef enum esp_format { ESP_FORMAT_F32 = 0, ESP_FORMAT_BF16 = 1 } esp_format;
+
+typedef enum esp_rope_scaling {
+    ESP_ROPE_NONE = 0,
+    ESP_ROPE_LINEAR = 1, /* config.rs:158-160 */
+    ESP_ROPE_LLAMA3 = 2  /* config.rs:161-178 */
+} esp_rope_scaling;
+
+/* Parsed decoder geometry: DecoderConfig (decoder/config.rs:322-363) with
+ * its derived values (config.rs:433-490) already resolved by the host. */
+typedef struct esp_config {
+    uint32_t vocab_size;
+    uint32_t hidden_size;
+    uint32_t intermediate_size;
+    uint32_t num_hidden_layers;
+    uint32_t num_attention_heads;
+    uint32_t num_key_value_heads; /* kv_heads() */
+    uint32_t head_dim;            /* head_dim() */
+    uint32_t max_position_embeddings;
+    float rms_norm_eps;
+    float rope_theta;
+    uint32_t rope_scaling; /* esp_rope_scaling */
+    float rope_factor;
+    float rope_low_freq_factor;
+    float rope_high_freq_factor;
+    uint32_t rope_original_max_position_embeddings;
+    uint32_t tie_word_embeddings;
+    uint32_t qkv_bias;    /* qkv_bias() */
+    uint32_t output_bias; /* output_bias() */
+    uint32_t qk_norm;     /* qk_norm() */
+    const uint32_t *layer_window; /* [layers] layer_window(i), 0 = none; NULL = none */
+    /* Routed experts (MoeConfig, config.rs:37-48); num_experts 0 = dense. */
+    uint32_t num_experts;
+    uint32_t num_experts_per_tok;
+    uint32_t moe_intermediate_size;
+    uint32_t shared_expert_intermediate_size; /* 0 = no shared expert */
+    uint32_t norm_topk_prob;
+    const uint8_t *layer_is_moe; /* [layers] layer_is_moe(i); NULL = none */
+    uint32_t format;             /* esp_format */
+} esp_config;
+
+/* One PEFT LoRA adapter (decoder/lora.rs:99-217), applied unmerged as
+ * y += scale * B (A x) for each targeted attention projection. */
+typedef struct esp_lora {
+    uint32_t rank;
+    float scale;          /* alpha / rank * selection scale (lora.rs:194) */
+    uint32_t target_mask; /* bit 0 q_proj, 1 k_proj, 2 v_proj, 3 o_proj */
+    const uint8_t *safetensors; /* base_model.model.model.layers.{i}.self_attn.{m}.lora_{A,B}.weight */
+    size_t safetensors_len;
+} esp_lora;
+
+/* Sampler state (decoder/sample.rs:56-122). temperature <= 0 selects
+ * greedy (generate.rs:70-79; constrained greedy provider.rs:808-815);
+ * top_p < 0 means None. `state` is the splitmix64 state: seed plus
+ * 0x9E3779B97F4A7C15 * draws (sample.rs:64-69); esp_pick advances it by
+ * one draw for each sampled row. */
+typedef struct esp_sampler {
+    float temperature;
+    float top_p;
+    uint64_t state;
+} esp_sampler;
+
+/* esp_pick per-row flags */
+#define ESP_PICK_NONFINITE 1u   /* the row held NaN/inf logits (provider.rs:219-240) */
+#define ESP_PICK_NO_ELIGIBLE 2u /* no finite allowed token (constraint.rs:292-294) */
+
+typedef struct esp_model esp_model;
+typedef struct esp_kv esp_kv;
+
+/* Thread-local message of the last failing call on this thread. Returns
+ * the full message length; copies at most len-1 bytes plus a NUL. */
+size_t esp_last_error(char *buf, size_t len);
+
+/* decoder/loader.rs:573-580 load_decoder_from_bytes + model.rs:166-194
+ * DecoderModel::from_loaded (+ lora.rs:260-307 when adapters are given).
+ * `safetensors` holds HF-named tensors (loader.rs:36-64); it is borrowed
+ * for the duration of the call only. Unconsumed tensors are refused
+ * (loader.rs:277-308); lm_head.weight may be absent only when tied
+ * (loader.rs:438-446). Weights are staged into HBM on the current device. */
+esp_status esp_model_load(const esp_config *config, const uint8_t *safetensors, size_t len,
+                          const esp_lora *adapters, uint32_t n_adapters, esp_model **out);
+/* Synthetic model of the given geometry (no reference counterpart; used by
+ * benchmarks and large-shape tests): every projection, expert and
+ * embedding is N(0, std) from a seeded device generator, norms are 1 and
+ * biases 0. lora_rank > 0 adds unmerged LoRA on the projections in
+ * lora_mask (bit 0 q, 1 k, 2 v) with A ~ N(0, lora_a_std),
+ * B ~ N(0, lora_b_std) and the given scale. */
+esp_status esp_model_create_synthetic(const esp_config *config, uint64_t seed, float std,
+                                      uint32_t lora_rank, uint32_t lora_mask, float lora_a_std,
+                                      float lora_b_std, float lora_scale, esp_model **out);
+esp_status esp_model_destroy(esp_model *model);
+/* Bytes of HBM the model's weights occupy. */
+esp_status esp_model_weight_bytes(const esp_model *model, uint64_t *bytes);
+
+/* model.rs:476-483 DecoderModel::new_cache, for `batch` independent
+ * sequences of up to `max_ctx` positions each (max_ctx <=
+ * max_position_embeddings). Contiguous per-sequence bf16 (or f32) KV. */
+esp_status esp_kv_create(esp_model *model, uint32_t batch, uint32_t max_ctx, esp_kv **out);
+esp_status esp_kv_destroy(esp_kv *kv);
+/* Forget sequence `seq` (or every sequence when seq == UINT32_MAX). */
+esp_status esp_kv_reset(esp_kv *kv, uint32_t seq);
+/* model.rs:676-681 KvCache::position */
+esp_status esp_kv_position(const esp_kv *kv, uint32_t seq, uint32_t *position);
+/* The HIP stream (hipStream_t) this KV handle's work runs on. */
+esp_status esp_kv_stream(const esp_kv *kv, void **stream);
+
+/* model.rs:502-539 try_forward_cached_last for one sequence: consume `n`
+ * ids at the sequence's position, extend its cache, and leave the
+ * last-position logits (f32, [vocab]) device-resident as row 0 for
+ * esp_pick; also copy them to `logits_out` when it is non-NULL.
+ * Empty, out-of-vocabulary or over-window input -> ESP_INVALID_REQUEST
+ * (model.rs:548-556) and the cache is unchanged. */
+esp_status esp_forward_last(esp_model *model, esp_kv *kv, uint32_t seq, const int32_t *ids,
+                            uint32_t n, float *logits_out);
+
+/* The same forward for several sequences at once: sequence seqs[i]
+ * consumes seq_lens[i] ids (ids concatenated in order). Decode steps are
+ * seq_len 1; grammar-forced spans are short blocks over a warm cache
+ * (provider.rs:865-872). Each sequence's result equals its own
+ * esp_forward_last. Last-position logits land as rows 0..n_seqs-1. */
+esp_status esp_forward_batch(esp_model *model, esp_kv *kv, uint32_t n_seqs, const uint32_t *seqs,
+                             const uint32_t *seq_lens, const int32_t *ids, float *logits_out);
+
+/* Token choice over the device-resident logits rows of the last forward
+ * on this KV handle (generate.rs:30-44 TokenPicker::pick,
+ * provider.rs:807-816). allowed_bits (nullable) holds one bitmask of
+ * ceil(vocab/32) u32 words per row (bit id%32 of word id/32 = allowed);
+ * with a mask, disallowed or non-finite logits become -inf
+ * (constraint.rs:277-297). samplers (nullable = greedy for every row).
+ * ids_out[n_rows]; flags_out[n_rows] (nullable) gets ESP_PICK_* bits.
+ * Returns ESP_INVALID_REQUEST if a masked row has no eligible token. */
+esp_status esp_pick(esp_kv *kv, uint32_t n_rows, const uint32_t *allowed_bits,
+                    esp_sampler *samplers, uint32_t *ids_out, uint8_t *flags_out);
+
+/* generate.rs:134-170 try_generate_ids_with + TokenPicker::Greedy, run on
+ * the device: prefill `prompt`, then up to max_new greedy steps, stopping
+ * at (and excluding) any id in `eos`. Writes generated ids to out_ids
+ * [max_new] and their count to n_out. The per-step token never leaves the
+ * device; decode steps replay one captured HIP graph. */
+esp_status esp_generate_greedy(esp_model *model, esp_kv *kv, uint32_t seq, const int32_t *prompt,
+                               uint32_t n_prompt, uint32_t max_new, const int32_t *eos,
+                               uint32_t n_eos, int32_t *out_ids, uint32_t *n_out);
+
+/* Kernel timing (measurement support, no reference counterpart): while
+ * enabled, every launch of the named kernel family records HIP events on
+ * its stream; read returns launches and total milliseconds since enable. */
+esp_status esp_profile_enable(const char *kernel, int enable);
+esp_status esp_profile_read(const char *kernel, uint64_t *launches, double *total_ms);
+
+/* Library/build identification. */
+const char *esp_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif
