@@ -1,0 +1,52 @@
+// Single-token decode kernels (k_decode.hip).
+#pragma once
+
+#include "common.hpp"
+
+namespace esp {
+
+enum DecodeEpi { DG_STORE = 0, DG_RESID = 1, DG_SWIGLU = 2, DG_QKVROPE = 3, DG_HEAD = 4 };
+constexpr int DG_MAX_PART = 2048;  // argmax partials (blocks) of the head GEMV
+
+struct DecodeGemvArgs {
+    const void *w, *w2;   // [N, K] weight rows (SWIGLU: gate, up)
+    const float *x;       // [K] input row
+    const float *gamma;   // nullable: fused RMSNorm of x
+    float eps;
+    const float *bias;    // nullable
+    float *y;             // STORE/HEAD: out; RESID: +=; SWIGLU: act
+    int N, K;
+    // QKVROPE
+    const float *rope_cos, *rope_sin;
+    const int32_t *row_pos, *row_seq;  // device, one row
+    float *q_out;
+    float *kv;            // layer base of the f32 cache
+    long long seq_stride, kv_half_stride, head_stride;
+    int nq, nkv, hd;
+    // HEAD argmax
+    float *part_v;
+    int32_t *part_i;
+    int32_t *ticket;      // nullable = no argmax
+    uint32_t *picked;
+    int32_t *gen;         // nullable: device-loop token hand-off
+};
+
+bool decode_gemv_ok(int K);
+void launch_decode_gemv(Dt wt, int epi, const DecodeGemvArgs &a, hipStream_t s);
+
+struct AttnDecodeArgs {
+    const float *q;       // [M, nq*hd]
+    const float *kv;      // layer base of the f32 cache
+    long long seq_stride, kv_half_stride, head_stride;
+    const int32_t *row_pos, *row_seq;
+    int M, nq, nkv, hd, window;
+    int n_split, split_len;
+    float *part;          // [M, nq, n_split, hd + 2]
+    int32_t *ticket;      // [M, nkv] zero-initialised
+    float *out;           // [M, nq*hd]
+};
+
+bool attn_decode_ok(int hd, int G);
+void launch_attn_decode(const AttnDecodeArgs &a, hipStream_t s);
+
+}  // namespace esp

@@ -1,0 +1,540 @@
+// Single-token (decode) kernels, built to stream weights at HBM rate with as
+// few dispatches per layer as the data dependencies allow.
+//
+// decode_gemv_k: y = W x for one input row. A block owns RB output rows (or
+// row pairs); its four waves split K into contiguous quarters, each lane
+// keeping its slice of x (optionally RMS-normalised) in registers for the
+// whole grid-stride loop, so x is read once per block while weight rows
+// stream with 16-byte loads. Epilogues fuse what follows the projection:
+//   RESID   h[n] += y (+bias)                      (o_proj, down_proj)
+//   SWIGLU  act[n] = silu(g_n) * u_n               (gate/up pairs)
+//   QKVROPE q/k/v rows in split-half pairs (d, d+hd/2): +bias, RoPE at the
+//           row's position, q -> f32 buffer, k/v appended to the cache
+//   HEAD    logits[n] (+ greedy argmax, lowest id on ties, reduced by the
+//           last block to finish; optionally hands the token to the next
+//           captured step: gen[0] = id, gen[8+step] = id, step++, pos++)
+//
+// attn_decode_k: causal GQA attention for one query row per (kv head, key
+// split), online softmax in registers; the last split to finish for a
+// (row, kv head) merges the partials in split order (deterministic).
+#include "common.hpp"
+#include "dev.hpp"
+#include "decode.hpp"
+
+namespace esp {
+
+constexpr int DG_THREADS = 256;
+constexpr int DG_WAVES = 4;
+constexpr int DG_MAXC = 8;  // max 8-element chunks per lane per row (K <= 4*64*8*8 = 16384)
+
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+// Cross-block hand-off without flushing L2: partials are written with
+// agent-scope (write-through) stores, the writer waits for its stores to
+// complete (s_waitcnt vmcnt(0)) before taking a ticket, and the last block
+// reads the partials with agent-scope loads.
+__device__ __forceinline__ void st_agent(float *p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_agent(int32_t *p, int32_t v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_agent(const float *p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ int32_t ld_agent(const int32_t *p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void wait_stores() { __builtin_amdgcn_s_waitcnt(0x0F70); }  // vmcnt(0)
+
+template <typename WT> struct Chunk;
+template <> struct Chunk<uint16_t> {  // 8 bf16 = 16 bytes
+    u32x4_t v;
+    __device__ __forceinline__ void load(const uint16_t *p) {
+        v = __builtin_nontemporal_load((const u32x4_t *)p);
+    }
+    __device__ __forceinline__ float dot(const float *x) const {
+        float s = 0.f;
+        s += __uint_as_float(v.x << 16) * x[0];
+        s += __uint_as_float(v.x & 0xffff0000u) * x[1];
+        s += __uint_as_float(v.y << 16) * x[2];
+        s += __uint_as_float(v.y & 0xffff0000u) * x[3];
+        s += __uint_as_float(v.z << 16) * x[4];
+        s += __uint_as_float(v.z & 0xffff0000u) * x[5];
+        s += __uint_as_float(v.w << 16) * x[6];
+        s += __uint_as_float(v.w & 0xffff0000u) * x[7];
+        return s;
+    }
+};
+template <> struct Chunk<float> {  // 8 f32 = 2 x 16 bytes
+    f32x4_t a, b;
+    __device__ __forceinline__ void load(const float *p) {
+        a = __builtin_nontemporal_load((const f32x4_t *)p);
+        b = __builtin_nontemporal_load((const f32x4_t *)p + 1);
+    }
+    __device__ __forceinline__ float dot(const float *x) const {
+        float s = 0.f;
+        s += a.x * x[0];
+        s += a.y * x[1];
+        s += a.z * x[2];
+        s += a.w * x[3];
+        s += b.x * x[4];
+        s += b.y * x[5];
+        s += b.z * x[6];
+        s += b.w * x[7];
+        return s;
+    }
+};
+
+// rows handled per unit: SWIGLU and QKVROPE units are row pairs
+template <int EPI> struct RowsPerUnit { static constexpr int v = 1; };
+template <> struct RowsPerUnit<DG_SWIGLU> { static constexpr int v = 2; };
+template <> struct RowsPerUnit<DG_QKVROPE> { static constexpr int v = 2; };
+
+constexpr int DG_MAX_IT = 64;  // grid-stride iterations per block
+
+template <typename WT, int EPI, int RB>
+__global__ void __launch_bounds__(DG_THREADS) decode_gemv_k(DecodeGemvArgs a) {
+    constexpr int RU = RowsPerUnit<EPI>::v;
+    constexpr int R = RB * RU;  // weight rows per block iteration
+    __shared__ float red[DG_MAX_IT][R][DG_WAVES];
+    __shared__ float ssq[DG_WAVES];
+    __shared__ float best_v[DG_WAVES];
+    __shared__ int best_i[DG_WAVES];
+    __shared__ int last;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int K = a.K, kq = K / DG_WAVES, nch = kq / 8;  // chunks in this wave's quarter
+    const int k0 = wave * kq;
+    const WT *W = (const WT *)a.w;
+    const WT *W2 = (const WT *)a.w2;
+    // ---- x slice in registers (+ fused RMSNorm)
+    float xr[DG_MAXC][8];
+    float ss = 0.f;
+#pragma unroll
+    for (int c = 0; c < DG_MAXC; ++c) {
+        int ch = lane + 64 * c;
+        if (ch < nch) {
+            const float *xp = a.x + k0 + ch * 8;
+            f32x4_t p0 = *(const f32x4_t *)xp, p1 = *(const f32x4_t *)(xp + 4);
+            xr[c][0] = p0.x; xr[c][1] = p0.y; xr[c][2] = p0.z; xr[c][3] = p0.w;
+            xr[c][4] = p1.x; xr[c][5] = p1.y; xr[c][6] = p1.z; xr[c][7] = p1.w;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) ss += xr[c][i] * xr[c][i];
+        }
+    }
+    if (a.gamma) {
+        ss = wave_sum(ss);
+        if (lane == 0) ssq[wave] = ss;
+        __syncthreads();
+        float tot = 0.f;
+#pragma unroll
+        for (int w = 0; w < DG_WAVES; ++w) tot += ssq[w];
+        const float rms = sqrtf(tot / (float)K + a.eps);
+#pragma unroll
+        for (int c = 0; c < DG_MAXC; ++c) {
+            int ch = lane + 64 * c;
+            if (ch < nch) {
+                const float *g = a.gamma + k0 + ch * 8;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) xr[c][i] = (xr[c][i] / rms) * g[i];
+            }
+        }
+    }
+    const int units = EPI == DG_QKVROPE ? a.N / 2 : a.N;
+    // ---- stream rows; each wave parks its partial sums in LDS (no barrier)
+    int iters = 0;
+    for (int u0 = blockIdx.x * RB; u0 < units; u0 += gridDim.x * RB, ++iters) {
+        const WT *rp[R];
+#pragma unroll
+        for (int r = 0; r < RB; ++r) {
+            int u = min(u0 + r, units - 1);
+            if (EPI == DG_SWIGLU) {
+                rp[r * 2] = W + (size_t)u * K;
+                rp[r * 2 + 1] = W2 + (size_t)u * K;
+            } else if (EPI == DG_QKVROPE) {
+                int half = a.hd / 2, head = u / half, d = u % half;
+                int row = head * a.hd + d;
+                rp[r * 2] = W + (size_t)row * K;
+                rp[r * 2 + 1] = W + (size_t)(row + half) * K;
+            } else {
+                rp[r] = W + (size_t)u * K;
+            }
+        }
+        float acc[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) acc[r] = 0.f;
+#pragma unroll
+        for (int c = 0; c < DG_MAXC; ++c) {
+            int ch = lane + 64 * c;
+            if (ch < nch) {
+                Chunk<WT> wc[R];
+#pragma unroll
+                for (int r = 0; r < R; ++r) wc[r].load(rp[r] + k0 + ch * 8);
+#pragma unroll
+                for (int r = 0; r < R; ++r) acc[r] += wc[r].dot(xr[c]);
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            float v = wave_sum(acc[r]);
+            if (lane == 0) red[iters][r][wave] = v;
+        }
+    }
+    __syncthreads();
+    // ---- epilogues: thread t handles unit (iteration t / RB, row t % RB)
+    float bv = -INFINITY;
+    int bi = 0x7fffffff;
+    for (int e = tid; e < iters * RB; e += blockDim.x) {
+        const int it = e / RB, r = e % RB;
+        const int u = blockIdx.x * RB + it * gridDim.x * RB + r;
+        if (u >= units) continue;
+        float y[RU];
+#pragma unroll
+        for (int j = 0; j < RU; ++j) {
+            float t = 0.f;
+#pragma unroll
+            for (int w = 0; w < DG_WAVES; ++w) t += red[it][r * RU + j][w];
+            y[j] = t;
+        }
+        if (EPI == DG_RESID) {
+            float v = a.bias ? y[0] + a.bias[u] : y[0];
+            a.y[u] = a.y[u] + v;
+        } else if (EPI == DG_STORE) {
+            a.y[u] = a.bias ? y[0] + a.bias[u] : y[0];
+        } else if (EPI == DG_HEAD) {
+            a.y[u] = y[0];
+            if (y[0] > bv || (y[0] == bv && u < bi)) {
+                bv = y[0];
+                bi = u;
+            }
+        } else if (EPI == DG_SWIGLU) {
+            a.y[u] = silu(y[0]) * y[1];
+        } else {  // DG_QKVROPE
+            const int hd = a.hd, half = hd / 2, head = u / half, d = u % half;
+            const int r0 = head * hd + d, r1 = r0 + half;
+            float v0 = y[0], v1 = y[1];
+            if (a.bias) {
+                v0 = v0 + a.bias[r0];
+                v1 = v1 + a.bias[r1];
+            }
+            const int pos = a.row_pos[0], seq = a.row_seq[0];
+            const float *cs = a.rope_cos + (size_t)pos * hd;
+            const float *sn = a.rope_sin + (size_t)pos * hd;
+            if (head < a.nq + a.nkv) {
+                float o0 = v0 * cs[d] + (-v1) * sn[d];
+                float o1 = v1 * cs[d + half] + v0 * sn[d + half];
+                if (head < a.nq) {
+                    a.q_out[r0] = o0;
+                    a.q_out[r1] = o1;
+                } else {
+                    float *kc = a.kv + (size_t)seq * a.seq_stride +
+                                (size_t)(head - a.nq) * a.head_stride + (size_t)pos * hd;
+                    kc[d] = o0;
+                    kc[d + half] = o1;
+                }
+            } else {
+                float *vc = a.kv + (size_t)seq * a.seq_stride + a.kv_half_stride +
+                            (size_t)(head - a.nq - a.nkv) * a.head_stride + (size_t)pos * hd;
+                vc[d] = v0;
+                vc[d + half] = v1;
+            }
+        }
+    }
+    if (EPI != DG_HEAD || !a.ticket) return;
+    // ---- greedy argmax across blocks: partial per block, last block reduces
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        float ov = __shfl_xor(bv, o, 64);
+        int oi = __shfl_xor(bi, o, 64);
+        if (ov > bv || (ov == bv && oi < bi)) {
+            bv = ov;
+            bi = oi;
+        }
+    }
+    if (lane == 0) {
+        best_v[wave] = bv;
+        best_i[wave] = bi;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        float b = best_v[0];
+        int bj = best_i[0];
+        for (int w = 1; w < DG_WAVES; ++w)
+            if (best_v[w] > b || (best_v[w] == b && best_i[w] < bj)) {
+                b = best_v[w];
+                bj = best_i[w];
+            }
+        st_agent(a.part_v + blockIdx.x, b);
+        st_agent(a.part_i + blockIdx.x, bj);
+        wait_stores();
+        int t = atomicAdd(a.ticket, 1);
+        last = t == (int)gridDim.x - 1;
+    }
+    __syncthreads();
+    if (!last) return;
+    // last block: reduce the partials in block order (deterministic)
+    float b = -INFINITY;
+    int bj = 0x7fffffff;
+    constexpr int PER = DG_MAX_PART / DG_THREADS;
+    float pvs[PER];
+    int pis[PER];
+#pragma unroll
+    for (int q = 0; q < PER; ++q) {  // independent loads, issued together
+        int k = tid + q * DG_THREADS;
+        pvs[q] = k < (int)gridDim.x ? ld_agent(a.part_v + k) : -INFINITY;
+        pis[q] = k < (int)gridDim.x ? ld_agent(a.part_i + k) : 0x7fffffff;
+    }
+#pragma unroll
+    for (int q = 0; q < PER; ++q)
+        if (pvs[q] > b || (pvs[q] == b && pis[q] < bj)) {
+            b = pvs[q];
+            bj = pis[q];
+        }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        float ov = __shfl_xor(b, o, 64);
+        int oi = __shfl_xor(bj, o, 64);
+        if (ov > b || (ov == b && oi < bj)) {
+            b = ov;
+            bj = oi;
+        }
+    }
+    if (lane == 0) {
+        best_v[wave] = b;
+        best_i[wave] = bj;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        b = best_v[0];
+        bj = best_i[0];
+        for (int w = 1; w < DG_WAVES; ++w)
+            if (best_v[w] > b || (best_v[w] == b && best_i[w] < bj)) {
+                b = best_v[w];
+                bj = best_i[w];
+            }
+        if (bj == 0x7fffffff) bj = 0;
+        a.picked[0] = (uint32_t)bj;
+        if (a.gen) {
+            int32_t *g = a.gen;
+            g[0] = bj;
+            g[8 + g[1]] = bj;
+            g[1] += 1;
+            g[3] += 1;
+        }
+        *a.ticket = 0;
+    }
+}
+
+template <typename WT, int EPI, int RB>
+static void dg_launch_rb(const DecodeGemvArgs &a, int cus, hipStream_t s) {
+    const int units = EPI == DG_QKVROPE ? a.N / 2 : a.N;
+    int blocks = (units + RB - 1) / RB;
+    const int cap = cus * 8;
+    if (blocks > cap) blocks = cap;
+    const int need = (units + RB * DG_MAX_IT - 1) / (RB * DG_MAX_IT);  // LDS slots per block
+    if (blocks < need) blocks = need;
+    if (EPI == DG_HEAD && a.ticket && blocks > DG_MAX_PART)
+        fail(ESP_UNSUPPORTED, "decode head: vocabulary above the argmax partial capacity");
+    decode_gemv_k<WT, EPI, RB><<<blocks, DG_THREADS, 0, s>>>(a);
+}
+
+template <typename WT, int EPI>
+static void dg_launch(const DecodeGemvArgs &a, int cus, hipStream_t s) {
+    // Measured on MI355X: two rows per block (more blocks in flight) beats
+    // larger row blocks with more loads per lane at every decode shape.
+    dg_launch_rb<WT, EPI, 2>(a, cus, s);
+}
+
+bool decode_gemv_ok(int K) { return K % 32 == 0 && K / 32 <= 64 * DG_MAXC; }
+
+void launch_decode_gemv(Dt wt, int epi, const DecodeGemvArgs &a, hipStream_t s) {
+    if (!decode_gemv_ok(a.K)) fail(ESP_BACKEND, "decode_gemv: unsupported width");
+    static int cus = 0;
+    if (!cus) {
+        int dev = 0;
+        ESP_HIP(hipGetDevice(&dev));
+        ESP_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+        if (cus <= 0) cus = 256;
+    }
+#define DG_CASE(E)                                                   \
+    case E:                                                          \
+        if (wt == DT_BF16) dg_launch<uint16_t, E>(a, cus, s);        \
+        else dg_launch<float, E>(a, cus, s);                         \
+        break;
+    switch (epi) {
+        DG_CASE(DG_STORE)
+        DG_CASE(DG_RESID)
+        DG_CASE(DG_SWIGLU)
+        DG_CASE(DG_QKVROPE)
+        DG_CASE(DG_HEAD)
+        default: fail(ESP_BACKEND, "decode_gemv: bad epilogue");
+    }
+#undef DG_CASE
+}
+
+// ------------------------------------------------------------ attention
+
+// One block per (key split, kv head, row). Each 16-lane group (hd 64) or
+// 32-lane group (hd 128) owns one key at a time; lanes cover 4 dims each.
+template <int HD>
+__global__ void __launch_bounds__(256) attn_decode_k(AttnDecodeArgs a) {
+    constexpr int LPK = HD / 4;          // lanes per key (4 dims each)
+    constexpr int KPW = 64 / LPK;        // keys per wave per step
+    constexpr int GMAX = 8;              // query heads per kv head
+    __shared__ float wm[4][GMAX], wl[4][GMAX];
+    __shared__ float wacc[4][GMAX][HD];
+    __shared__ int last;
+    const int split = blockIdx.x, g = blockIdx.y, row = blockIdx.z;
+    const int G = a.nq / a.nkv;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int grp = lane / LPK, sub = lane % LPK;
+    const int pos = a.row_pos[row], seq = a.row_seq[row];
+    int lo = a.window > 0 ? max(0, pos - a.window + 1) : 0;
+    int hi = pos + 1;
+    lo = max(lo, split * a.split_len);
+    hi = min(hi, (split + 1) * a.split_len);
+    const float scale = sqrtf((float)HD);
+    // q for the group's heads: this lane's 4 dims
+    float q[GMAX][4];
+    const float *qrow = a.q + (size_t)row * a.nq * HD + (size_t)g * G * HD + sub * 4;
+#pragma unroll
+    for (int j = 0; j < GMAX; ++j)
+        if (j < G) {
+            f32x4_t v = *(const f32x4_t *)(qrow + (size_t)j * HD);
+            q[j][0] = v.x; q[j][1] = v.y; q[j][2] = v.z; q[j][3] = v.w;
+        }
+    float m[GMAX], l[GMAX], acc[GMAX][4];
+#pragma unroll
+    for (int j = 0; j < GMAX; ++j) {
+        m[j] = -INFINITY;
+        l[j] = 0.f;
+        acc[j][0] = acc[j][1] = acc[j][2] = acc[j][3] = 0.f;
+    }
+    const float *kb = a.kv + (size_t)seq * a.seq_stride + (size_t)g * a.head_stride;
+    const float *vb = kb + a.kv_half_stride;
+#pragma unroll 4
+    for (int t = lo + wave * KPW + grp; t < hi; t += 4 * KPW) {
+        f32x4_t kk = *(const f32x4_t *)(kb + (size_t)t * HD + sub * 4);
+        f32x4_t vv = *(const f32x4_t *)(vb + (size_t)t * HD + sub * 4);
+#pragma unroll
+        for (int j = 0; j < GMAX; ++j) {
+            if (j >= G) break;
+            float d = q[j][0] * kk.x + q[j][1] * kk.y + q[j][2] * kk.z + q[j][3] * kk.w;
+#pragma unroll
+            for (int o = LPK / 2; o > 0; o >>= 1) d += __shfl_xor(d, o, 64);
+            float s = d / scale;
+            float mn = fmaxf(m[j], s);
+            float al = __expf(m[j] - mn), p = __expf(s - mn);
+            l[j] = l[j] * al + p;
+            acc[j][0] = acc[j][0] * al + p * vv.x;
+            acc[j][1] = acc[j][1] * al + p * vv.y;
+            acc[j][2] = acc[j][2] * al + p * vv.z;
+            acc[j][3] = acc[j][3] * al + p * vv.w;
+            m[j] = mn;
+        }
+    }
+    // merge the KPW key groups of the wave (lanes with equal `sub`)
+#pragma unroll
+    for (int j = 0; j < GMAX; ++j) {
+        if (j >= G) break;
+#pragma unroll
+        for (int o = LPK; o < 64; o <<= 1) {
+            float om = __shfl_xor(m[j], o, 64), ol = __shfl_xor(l[j], o, 64);
+            float mn = fmaxf(m[j], om);
+            float s1 = mn == -INFINITY ? 0.f : __expf(m[j] - mn);
+            float s2 = mn == -INFINITY ? 0.f : __expf(om - mn);
+            l[j] = l[j] * s1 + ol * s2;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                float oa = __shfl_xor(acc[j][i], o, 64);
+                acc[j][i] = acc[j][i] * s1 + oa * s2;
+            }
+            m[j] = mn;
+        }
+        if (grp == 0) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) wacc[wave][j][sub * 4 + i] = acc[j][i];
+            if (sub == 0) {
+                wm[wave][j] = m[j];
+                wl[wave][j] = l[j];
+            }
+        }
+    }
+    __syncthreads();
+    // merge the 4 waves; write this split's partial (m, l, acc[HD]) per head
+    const size_t stride = (size_t)HD + 2;
+    for (int o = tid; o < G * HD; o += blockDim.x) {
+        int j = o / HD, d = o % HD;
+        float mx = -INFINITY;
+        for (int w = 0; w < 4; ++w) mx = fmaxf(mx, wm[w][j]);
+        float L = 0.f, v = 0.f;
+        for (int w = 0; w < 4; ++w) {
+            float sc = mx == -INFINITY ? 0.f : __expf(wm[w][j] - mx);
+            L += wl[w][j] * sc;
+            v += wacc[w][j][d] * sc;
+        }
+        float *p = a.part + (((size_t)row * a.nq + (size_t)g * G + j) * a.n_split + split) * stride;
+        st_agent(p + 2 + d, v);
+        if (d == 0) {
+            st_agent(p, mx);
+            st_agent(p + 1, L);
+        }
+    }
+    if (a.n_split == 1) {
+        // single split: normalise directly
+        __syncthreads();
+        for (int o = tid; o < G * HD; o += blockDim.x) {
+            int j = o / HD, d = o % HD;
+            const float *p = a.part + (((size_t)row * a.nq + (size_t)g * G + j)) * stride;
+            a.out[(size_t)row * a.nq * HD + (size_t)(g * G + j) * HD + d] =
+                ld_agent(p + 2 + d) / ld_agent(p + 1);
+        }
+        return;
+    }
+    wait_stores();
+    __syncthreads();
+    if (tid == 0) {
+        int *tk = a.ticket + (size_t)row * a.nkv + g;
+        int t = atomicAdd(tk, 1);
+        last = t == a.n_split - 1;
+        if (last) *tk = 0;
+    }
+    __syncthreads();
+    if (!last) return;
+    // stage this (row, kv head)'s partials in LDS with one batch of loads
+    extern __shared__ float stage[];  // [G][n_split][HD + 2]
+    const float *pbase = a.part + ((size_t)row * a.nq + (size_t)g * G) * a.n_split * stride;
+    const int total = G * a.n_split * (int)stride;
+    for (int i = tid; i < total; i += blockDim.x) stage[i] = ld_agent(pbase + i);
+    __syncthreads();
+    for (int o = tid; o < G * HD; o += blockDim.x) {
+        int j = o / HD, d = o % HD;
+        const float *p = stage + (size_t)j * a.n_split * stride;
+        float mx = -INFINITY;
+        for (int sp = 0; sp < a.n_split; ++sp) mx = fmaxf(mx, p[(size_t)sp * stride]);
+        float L = 0.f, v = 0.f;
+        for (int sp = 0; sp < a.n_split; ++sp) {
+            float ms = p[(size_t)sp * stride];
+            if (ms == -INFINITY) continue;
+            float sc = __expf(ms - mx);
+            L += p[(size_t)sp * stride + 1] * sc;
+            v += p[(size_t)sp * stride + 2 + d] * sc;
+        }
+        a.out[(size_t)row * a.nq * HD + (size_t)(g * G + j) * HD + d] = v / L;
+    }
+}
+
+bool attn_decode_ok(int hd, int G) { return (hd == 64 || hd == 128) && G <= 8; }
+
+void launch_attn_decode(const AttnDecodeArgs &a, hipStream_t s) {
+    const int G = a.nq / a.nkv;
+    if (!attn_decode_ok(a.hd, G)) fail(ESP_BACKEND, "attn_decode: unsupported head shape");
+    dim3 grid(a.n_split, a.nkv, a.M);
+    const size_t shm = sizeof(float) * (size_t)G * a.n_split * (a.hd + 2);
+    if (shm > 48 * 1024) fail(ESP_BACKEND, "attn_decode: too many key splits");
+    if (a.hd == 64) attn_decode_k<64><<<grid, 256, shm, s>>>(a);
+    else attn_decode_k<128><<<grid, 256, shm, s>>>(a);
+}
+
+}  // namespace esp

@@ -11,6 +11,7 @@
 #include <mutex>
 #include <set>
 
+#include "decode.hpp"
 #include "kernels_extra.hpp"
 #include "profile.hpp"
 #include "safetensors.hpp"
@@ -489,6 +490,10 @@ Kv *create_kv(Model *m, uint32_t batch, uint32_t max_ctx) {
     kv->cache.alloc((size_t)kv->seq_stride * batch * dt_size(kv->dt));
     kv->pos.assign(batch, 0);
     ESP_HIP(hipStreamCreateWithFlags(&kv->stream, hipStreamNonBlocking));
+    // [0, 4096): attention merge tickets; [4096]: head ticket; then argmax
+    // partials (values, ids) and the picked id
+    kv->tickets.alloc((size_t)(4096 + 8 + 2 * DG_MAX_PART + 8) * 4);
+    ESP_HIP(hipMemset(kv->tickets.p, 0, kv->tickets.bytes));
     return kv.release();
 }
 
@@ -511,13 +516,201 @@ struct Plan {
 
 static Plan attn_plan(const Model &m, int rows, int max_t) {
     int base = rows * m.nkv;
-    int want = (2048 + base - 1) / base;  // aim for >= 2048 blocks
+    int want = (512 + base - 1) / base;  // aim for >= 512 blocks of >= 64 keys
     int max_split = (max_t + 63) / 64;
+    // the decode merge stages G * n_split * (hd + 2) floats in 48 KB of LDS
+    int lds_cap = 48 * 1024 / (4 * (m.nq / m.nkv) * (m.hd + 2));
+    max_split = std::min(max_split, std::max(1, lds_cap));
     int ns = std::max(1, std::min(want, max_split));
     int sl = (max_t + ns - 1) / ns;
     sl = (sl + 31) / 32 * 32;
     ns = (max_t + sl - 1) / sl;
     return Plan{ns, sl};
+}
+
+static int32_t *att_tickets(Kv &kv) { return kv.tickets.as<int32_t>(); }
+
+// One layer for a single token row with the decode kernels: fused
+// QKV+RoPE+KV-append (when the layer has no LoRA or QK norm), split-K
+// attention with in-kernel merge, and norm-fused projections.
+static void run_layer_decode(Model &m, Kv &kv, const Rows &rows, LayerW &w, int l,
+                             const Plan &plan) {
+    hipStream_t s = kv.stream;
+    const int H = m.H;
+    float *kvl = kv.cache.as<float>() + (size_t)l * kv.layer_stride;
+    const bool lora = w.lora_rank[0] || w.lora_rank[1] || w.lora_rank[2];
+    if (!lora && !w.q_norm && decode_gemv_ok(H)) {
+        DecodeGemvArgs g{};
+        g.w = w.qkv;
+        g.x = kv.h.as<float>();
+        g.gamma = w.in_norm;
+        g.eps = m.cfg.rms_norm_eps;
+        g.bias = w.qkv_bias;
+        g.N = m.qw + 2 * m.kvw;
+        g.K = H;
+        g.rope_cos = m.rope_cos;
+        g.rope_sin = m.rope_sin;
+        g.row_pos = rows.row_pos;
+        g.row_seq = rows.row_seq;
+        g.q_out = kv.q.as<float>();
+        g.kv = kvl;
+        g.seq_stride = kv.seq_stride;
+        g.kv_half_stride = kv.half_stride;
+        g.head_stride = kv.head_stride;
+        g.nq = m.nq;
+        g.nkv = m.nkv;
+        g.hd = m.hd;
+        Prof p("gemv", s);
+        launch_decode_gemv(m.wt, DG_QKVROPE, g, s);
+    } else {
+        if (decode_gemv_ok(H)) {
+            DecodeGemvArgs g{};
+            g.w = w.qkv;
+            g.x = kv.h.as<float>();
+            g.gamma = w.in_norm;
+            g.eps = m.cfg.rms_norm_eps;
+            g.bias = w.qkv_bias;
+            g.y = kv.qkv.as<float>();
+            g.N = w.qkv_rows;
+            g.K = H;
+            Prof p("gemv", s);
+            launch_decode_gemv(m.wt, DG_STORE, g, s);
+        } else {
+            GemvArgs g{};
+            g.w = w.qkv;
+            g.x = kv.h.as<float>();
+            g.gamma = w.in_norm;
+            g.eps = m.cfg.rms_norm_eps;
+            g.bias = w.qkv_bias;
+            g.y = kv.qkv.as<float>();
+            g.N = w.qkv_rows;
+            g.K = H;
+            Prof p("gemv", s);
+            launch_gemv(m.wt, GEMV_STORE, g, s);
+        }
+        RopeKvArgs r{};
+        r.qkv = kv.qkv.as<float>();
+        r.ldq = w.qkv_rows;
+        r.q_out = kv.q.as<float>();
+        r.rope_cos = m.rope_cos;
+        r.rope_sin = m.rope_sin;
+        r.q_norm = w.q_norm;
+        r.k_norm = w.k_norm;
+        r.eps = m.cfg.rms_norm_eps;
+        for (int j = 0; j < 3; ++j) {
+            r.lora_b[j] = w.lora_b[j];
+            r.lora_t_col[j] = w.lora_t_col[j];
+            r.lora_rank[j] = w.lora_rank[j];
+            r.lora_scale[j] = w.lora_scale[j];
+        }
+        r.rows = rows;
+        r.kv = kvl;
+        r.seq_stride = kv.seq_stride;
+        r.layer_stride = kv.layer_stride;
+        r.kv_half_stride = kv.half_stride;
+        r.head_stride = kv.head_stride;
+        r.nq = m.nq;
+        r.nkv = m.nkv;
+        r.hd = m.hd;
+        Prof p("rope_kv", s);
+        launch_rope_kv(m.wt, kv.dt, r, s);
+    }
+    if (attn_decode_ok(m.hd, m.nq / m.nkv)) {
+        AttnDecodeArgs a{};
+        a.q = kv.q.as<float>();
+        a.kv = kvl;
+        a.seq_stride = kv.seq_stride;
+        a.kv_half_stride = kv.half_stride;
+        a.head_stride = kv.head_stride;
+        a.row_pos = rows.row_pos;
+        a.row_seq = rows.row_seq;
+        a.M = 1;
+        a.nq = m.nq;
+        a.nkv = m.nkv;
+        a.hd = m.hd;
+        a.window = w.window;
+        a.n_split = plan.n_split;
+        a.split_len = plan.split_len;
+        a.part = kv.part.as<float>();
+        a.ticket = att_tickets(kv);
+        a.out = kv.attn.as<float>();
+        Prof p("attention", s);
+        launch_attn_decode(a, s);
+    } else {
+        AttnArgs a{};
+        a.q = kv.q.as<float>();
+        a.kv = kvl;
+        a.seq_stride = kv.seq_stride;
+        a.layer_stride = kv.layer_stride;
+        a.kv_half_stride = kv.half_stride;
+        a.head_stride = kv.head_stride;
+        a.rows = rows;
+        a.nq = m.nq;
+        a.nkv = m.nkv;
+        a.hd = m.hd;
+        a.window = w.window;
+        a.part = kv.part.as<float>();
+        a.n_split = plan.n_split;
+        a.split_len = plan.split_len;
+        a.out = kv.attn.p;
+        a.out_dt = DT_F32;
+        Prof p("attention", s);
+        launch_attention(kv.dt, a, s);
+    }
+    auto resid = [&](const void *wt, const float *x, const float *bias, int N, int K) {
+        if (decode_gemv_ok(K)) {
+            DecodeGemvArgs g{};
+            g.w = wt;
+            g.x = x;
+            g.bias = bias;
+            g.y = kv.h.as<float>();
+            g.N = N;
+            g.K = K;
+            Prof p("gemv", s);
+            launch_decode_gemv(m.wt, DG_RESID, g, s);
+        } else {
+            GemvArgs g{};
+            g.w = wt;
+            g.x = x;
+            g.bias = bias;
+            g.y = kv.h.as<float>();
+            g.N = N;
+            g.K = K;
+            Prof p("gemv", s);
+            launch_gemv(m.wt, GEMV_RESIDUAL, g, s);
+        }
+    };
+    resid(w.o, kv.attn.as<float>(), w.o_bias, H, m.qw);
+    if (w.moe) {
+        moe_block(m, kv, w, 1, s);
+        return;
+    }
+    if (decode_gemv_ok(H)) {
+        DecodeGemvArgs g{};
+        g.w = w.gate;
+        g.w2 = w.up;
+        g.x = kv.h.as<float>();
+        g.gamma = w.post_norm;
+        g.eps = m.cfg.rms_norm_eps;
+        g.y = kv.act.as<float>();
+        g.N = m.F;
+        g.K = H;
+        Prof p("gemv", s);
+        launch_decode_gemv(m.wt, DG_SWIGLU, g, s);
+    } else {
+        GemvArgs g{};
+        g.w = w.gate;
+        g.w2 = w.up;
+        g.x = kv.h.as<float>();
+        g.gamma = w.post_norm;
+        g.eps = m.cfg.rms_norm_eps;
+        g.y = kv.act.as<float>();
+        g.N = m.F;
+        g.K = H;
+        Prof p("gemv", s);
+        launch_gemv(m.wt, GEMV_SWIGLU, g, s);
+    }
+    resid(w.down, kv.act.as<float>(), nullptr, H, m.F);
 }
 
 // One pass of `Mc` rows (already on the device at `rows`) through all layers.
@@ -531,6 +724,10 @@ static void run_layers(Model &m, Kv &kv, const Rows &rows, int Mc, int max_t) {
     kv.part.ensure((size_t)Mc * m.nq * plan.n_split * (m.hd + 2) * 4);
     for (int l = 0; l < m.L; ++l) {
         LayerW &w = m.layers[l];
+        if (single) {
+            run_layer_decode(m, kv, rows, w, l, plan);
+            continue;
+        }
         // ---- attention block (layer.rs:120-131)
         if (single) {
             GemvArgs g{};
@@ -711,8 +908,28 @@ static void ensure_scratch(Model &m, Kv &kv, int Mc, int n_seqs) {
 // Head on the last row of each sequence (model.rs:531-538): final RMSNorm
 // then [H] x [V, H]^T into f32 logits rows. `h_src` rows are selected by
 // `row_index` (device, nullable = rows 0..n_seqs-1).
-static void run_head(Model &m, Kv &kv, int n_seqs, const float *h_src, const int32_t *row_index) {
+static void run_head(Model &m, Kv &kv, int n_seqs, const float *h_src, const int32_t *row_index,
+                     int32_t *gen = nullptr) {
     hipStream_t s = kv.stream;
+    if (n_seqs == 1 && decode_gemv_ok(m.H)) {
+        int32_t *t = kv.tickets.as<int32_t>();
+        DecodeGemvArgs g{};
+        g.w = m.head;
+        g.x = h_src;
+        g.gamma = m.final_norm;
+        g.eps = m.cfg.rms_norm_eps;
+        g.y = kv.logits.as<float>();
+        g.N = m.V;
+        g.K = m.H;
+        g.ticket = t + 4096;
+        g.part_v = (float *)(t + 4096 + 8);
+        g.part_i = t + 4096 + 8 + DG_MAX_PART;
+        g.picked = (uint32_t *)(t + 4096 + 8 + 2 * DG_MAX_PART);
+        g.gen = gen;
+        Prof p("gemv", s);
+        launch_decode_gemv(m.wt, DG_HEAD, g, s);
+        return;
+    }
     if (n_seqs == 1) {
         GemvArgs g{};
         g.w = m.head;
@@ -831,6 +1048,11 @@ void decode_step_dev(Model &m, Kv &kv, int seq, int max_t, int32_t *gen) {
         launch_embed(m.wt, m.embed, rows.ids, 1, m.H, kv.h.as<float>(), s);
     }
     run_layers(m, kv, rows, 1, max_t);
+    if (decode_gemv_ok(m.H)) {
+        run_head(m, kv, 1, kv.h.as<float>(), nullptr, gen);  // argmax + hand-off fused
+        kv.logits_rows = 1;
+        return;
+    }
     run_head(m, kv, 1, kv.h.as<float>(), nullptr);
     kv.pick_io.ensure(64);
     PickArgs a{};

@@ -181,3 +181,42 @@ def test_pick_mask_and_sampling_match_oracle():
     for i in range(n):
         tok, _ = oracle.sample(logits[i], 1.3, None, states[i])
         assert ids[i] == tok
+
+
+DECODE_VARIANTS = {
+    # name: (extra config, head_dim, heads, kv_heads)
+    "mistral_window": ({"model_type": "mistral", "architectures": ["MistralForCausalLM"],
+                        "sliding_window": 5}, 64, 4, 2),
+    "qwen2_bias_hd128": ({"model_type": "qwen2", "architectures": ["Qwen2ForCausalLM"]}, 128, 4, 1),
+    "qwen3_qknorm": ({"model_type": "qwen3", "architectures": ["Qwen3ForCausalLM"],
+                      "layer_types": ["sliding_attention", "full_attention"],
+                      "sliding_window": 4, "use_sliding_window": True}, 64, 8, 2),
+    "llama_tied": ({"tie_word_embeddings": True}, 64, 4, 4),
+}
+
+
+@pytest.mark.parametrize("variant", sorted(DECODE_VARIANTS))
+def test_decode_kernels_match_oracle(variant):
+    """Single-token decode kernels (fused QKV+RoPE+KV, split-K attention with
+    in-kernel merge, norm-fused projections, head argmax) vs the oracle over
+    a prefill and 10 greedy steps; f32 weights: logits within 1e-4 of scale."""
+    extra, hd, nq, nkv = DECODE_VARIANTS[variant]
+    cfg = synth.llama_config(2, 256, nq, nkv, 320, 777, head_dim=hd, max_pos=96, extra=extra)
+    tensors = synth.make_tensors(cfg, 31, "f32", bias_std=0.05)
+    model = DecoderModel.from_bytes(cfg, st.dump(tensors), "f32")
+    ref = oracle.OracleModel(cfg, tensors)
+    prompt = synth.uniform_ids(17, 9, cfg.vocab_size)
+    kv, rkv = model.new_cache(1, 64), ref.new_cache(64)
+    got = model.try_forward_cached_last(prompt, kv)
+    want = ref.forward_last(rkv, prompt)
+    ids = []
+    for step in range(10):
+        scale = float(np.abs(want).max())
+        assert np.abs(got - want).max() <= 1e-4 * scale, (variant, step)
+        t = oracle.argmax(want)
+        assert int(np.argmax(got)) == t
+        ids.append(t)
+        got = model.try_forward_cached_last([t], kv)
+        want = ref.forward_last(rkv, [t])
+    dev = model.generate_greedy_device(model.new_cache(1, 64), prompt, 10, eos=[])
+    assert dev == ids
