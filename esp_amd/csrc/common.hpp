@@ -78,6 +78,8 @@ struct GemmArgs {
     const float *bias; // nullable [N]
     void *c;           // STORE: f32 [M, ldc]; RESIDUAL: f32 +=; SWIGLU: f32 [M, ldc]
     int M, N, K, ldc;
+    float *ws;         // nullable split-K workspace
+    size_t ws_bytes;
 };
 void launch_gemm(Dt wt, GemmEpi epi, const GemmArgs &a, hipStream_t s);
 

@@ -1,0 +1,276 @@
+// Prefill projection GEMM on the CDNA4 matrix cores:
+//   C[M,N] (f32) = A[M,K] (f32 activations) . W[N,K]^T (bf16 weights)
+// Each activation is split into bf16 hi + lo parts (a = hi + lo + O(2^-17 a))
+// and both parts are multiplied against the same bf16 weight fragment with
+// v_mfma_f32_32x32x16_bf16, accumulating in f32. Every product is exact, so
+// the result keeps f32-level accuracy while running on bf16 MFMA.
+//
+// Block tile 128 x 128 x 32, four waves in a 2 x 2 arrangement, each wave a
+// 64 x 64 output tile of 2 x 2 MFMA blocks. A and W tiles are staged through
+// LDS (double-buffered, rows padded to 80 bytes) from register prefetches
+// issued one k-tile ahead. Epilogues: STORE (+bias), RESIDUAL (+=), SWIGLU
+// (gate and up tiles share the A fragments; out = silu(g) * u).
+#include "common.hpp"
+#include "dev.hpp"
+#include "kernels_extra.hpp"
+
+namespace esp {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef float f32x4v_t __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x4v_t __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2v_t __attribute__((ext_vector_type(2)));
+
+constexpr int MF_BM = 128, MF_BN = 128, MF_BK = 32, MF_LD = MF_BK + 8;
+constexpr int MF_A_ELEMS = MF_BM * MF_LD;  // one A plane (bf16) per buffer
+constexpr int MF_B_ELEMS = MF_BN * MF_LD;
+
+template <int NB> constexpr size_t mfma_lds_bytes() {
+    return (size_t)(2 * MF_A_ELEMS + NB * MF_B_ELEMS) * 2;
+}
+
+// Split-K: blockIdx.z = k-split; each split writes raw f32 sums for its K
+// range to ws[z][M][N] (x NB planes) and mfma_reduce_k adds the splits in
+// order and applies the epilogue, so results do not depend on timing.
+constexpr int MF_PARTIAL = 16;
+
+__device__ __forceinline__ uint32_t pack2(uint16_t lo, uint16_t hi) {
+    return (uint32_t)lo | ((uint32_t)hi << 16);
+}
+
+template <int EPI, int NB>
+__global__ void __launch_bounds__(256, 2) gemm_mfma_k(GemmArgs g, float *ws, int k_per_split) {
+    extern __shared__ uint16_t lds[];
+    uint16_t *sA = lds;                          // [hi/lo][BM*LD]
+    uint16_t *sB = lds + 2 * MF_A_ELEMS;         // [nb][BN*LD]
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int m0 = blockIdx.y * MF_BM, n0 = blockIdx.x * MF_BN;
+    const float *A = (const float *)g.a;
+    const uint16_t *Wm[2] = {(const uint16_t *)g.w, (const uint16_t *)g.w2};
+    const int M = g.M, N = g.N, K = g.K;
+
+    f32x16_t acc[NB][2][2];
+#pragma unroll
+    for (int b = 0; b < NB; ++b)
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) acc[b][i][j][e] = 0.f;
+
+    f32x4v_t ra[4];
+    u32x4v_t rb[NB][2];
+    const int kbeg = blockIdx.z * k_per_split;
+    const int kend = min(K, kbeg + k_per_split);
+    auto load_tile = [&](int kt) {
+        const int kb = kbeg + kt * MF_BK;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            int idx = tid + 256 * i;  // 0..1023 float4 of the 128 x 32 tile
+            int row = idx >> 3, k = kb + (idx & 7) * 4;
+            int gm = m0 + row;
+            if (gm < M && k + 3 < kend) {
+                ra[i] = *(const f32x4v_t *)(A + (size_t)gm * K + k);
+            } else {
+                f32x4v_t v;
+#pragma unroll
+                for (int q = 0; q < 4; ++q) v[q] = (gm < M && k + q < kend) ? A[(size_t)gm * K + k + q] : 0.f;
+                ra[i] = v;
+            }
+        }
+#pragma unroll
+        for (int b = 0; b < NB; ++b)
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                int idx = tid + 256 * i;  // 0..511 chunks of 8 bf16
+                int row = idx >> 2, k = kb + (idx & 3) * 8;
+                int gn = n0 + row;
+                if (gn < N && k + 7 < kend) {
+                    rb[b][i] = __builtin_nontemporal_load(
+                        (const u32x4v_t *)(Wm[b] + (size_t)gn * K + k));
+                } else {
+                    uint16_t e[8];
+#pragma unroll
+                    for (int q = 0; q < 8; ++q) e[q] = (gn < N && k + q < kend) ? Wm[b][(size_t)gn * K + k + q] : 0;
+                    rb[b][i] = u32x4v_t{pack2(e[0], e[1]), pack2(e[2], e[3]), pack2(e[4], e[5]),
+                                        pack2(e[6], e[7])};
+                }
+            }
+    };
+    auto store_tile = [&]() {
+        uint16_t *ah = sA;
+        uint16_t *al = sA + MF_A_ELEMS;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            int idx = tid + 256 * i;
+            int row = idx >> 3, k = (idx & 7) * 4;
+            uint16_t h[4], l[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                float v = ra[i][q];
+                h[q] = f2bf(v);
+                l[q] = f2bf(v - bf2f(h[q]));
+            }
+            *(u32x2v_t *)(ah + row * MF_LD + k) = u32x2v_t{pack2(h[0], h[1]), pack2(h[2], h[3])};
+            *(u32x2v_t *)(al + row * MF_LD + k) = u32x2v_t{pack2(l[0], l[1]), pack2(l[2], l[3])};
+        }
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+            uint16_t *bb = sB + b * MF_B_ELEMS;
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                int idx = tid + 256 * i;
+                int row = idx >> 2, k = (idx & 3) * 8;
+                *(u32x4v_t *)(bb + row * MF_LD + k) = rb[b][i];
+            }
+        }
+    };
+    auto compute = [&]() {
+        const uint16_t *ah = sA;
+        const uint16_t *al = sA + MF_A_ELEMS;
+#pragma unroll
+        for (int ks = 0; ks < MF_BK / 16; ++ks) {
+            const int koff = ks * 16 + (lane >> 5) * 8;
+            bf16x8_t fh[2], fl[2], fb[NB][2];
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                int r = wm * 64 + i * 32 + (lane & 31);
+                fh[i] = *(const bf16x8_t *)(ah + r * MF_LD + koff);
+                fl[i] = *(const bf16x8_t *)(al + r * MF_LD + koff);
+            }
+#pragma unroll
+            for (int b = 0; b < NB; ++b)
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    int r = wn * 64 + j * 32 + (lane & 31);
+                    fb[b][j] = *(const bf16x8_t *)(sB + b * MF_B_ELEMS + r * MF_LD + koff);
+                }
+#pragma unroll
+            for (int b = 0; b < NB; ++b)
+#pragma unroll
+                for (int i = 0; i < 2; ++i)
+#pragma unroll
+                    for (int j = 0; j < 2; ++j) {
+                        acc[b][i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fh[i], fb[b][j], acc[b][i][j], 0, 0, 0);
+                        acc[b][i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fl[i], fb[b][j], acc[b][i][j], 0, 0, 0);
+                    }
+        }
+    };
+
+    // single LDS buffer (more blocks per CU hide latency); the next tile's
+    // global loads are in flight in registers while this tile computes
+    const int KT = (kend - kbeg + MF_BK - 1) / MF_BK;
+    if (KT > 0) load_tile(0);
+    for (int kt = 0; kt < KT; ++kt) {
+        store_tile();
+        __syncthreads();
+        if (kt + 1 < KT) load_tile(kt + 1);
+        compute();
+        __syncthreads();
+    }
+
+    // epilogue: lane holds column (lane & 31) of each 32 x 32 block, rows
+    // (e / 4) * 8 + (lane >> 5) * 4 + e % 4
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int col = n0 + wn * 64 + j * 32 + (lane & 31);
+            if (col >= N) continue;
+            if (EPI == MF_PARTIAL) {
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    const int row = m0 + wm * 64 + i * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3);
+                    if (row >= M) continue;
+#pragma unroll
+                    for (int b = 0; b < NB; ++b)
+                        ws[(((size_t)blockIdx.z * NB + b) * M + row) * N + col] = acc[b][i][j][e];
+                }
+                continue;
+            }
+            const float bias = (EPI != GEMM_SWIGLU && g.bias) ? g.bias[col] : 0.f;
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const int row = m0 + wm * 64 + i * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3);
+                if (row >= M) continue;
+                float *c = (float *)g.c + (size_t)row * g.ldc + col;
+                if (EPI == GEMM_SWIGLU) {
+                    *c = silu(acc[0][i][j][e]) * acc[NB - 1][i][j][e];
+                } else {
+                    float v = g.bias ? acc[0][i][j][e] + bias : acc[0][i][j][e];
+                    if (EPI == GEMM_RESIDUAL) *c = *c + v;
+                    else *c = v;
+                }
+            }
+        }
+}
+
+template <int EPI, int NB>
+__global__ void __launch_bounds__(256) mfma_reduce_k(GemmArgs g, const float *ws, int splits) {
+    const size_t MN = (size_t)g.M * g.N;
+    for (size_t idx = blockIdx.x * (size_t)blockDim.x + threadIdx.x; idx < MN;
+         idx += (size_t)gridDim.x * blockDim.x) {
+        const int row = (int)(idx / g.N), col = (int)(idx % g.N);
+        float v[NB];
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+            float t = 0.f;
+            for (int z = 0; z < splits; ++z) t += ws[((size_t)z * NB + b) * MN + idx];
+            v[b] = t;
+        }
+        float *c = (float *)g.c + (size_t)row * g.ldc + col;
+        if (EPI == GEMM_SWIGLU) {
+            *c = silu(v[0]) * v[NB - 1];
+        } else {
+            float y = g.bias ? v[0] + g.bias[col] : v[0];
+            if (EPI == GEMM_RESIDUAL) *c = *c + y;
+            else *c = y;
+        }
+    }
+}
+
+static int g_cus = 0;
+
+template <int EPI> static void mfma_launch(const GemmArgs &a, float *ws, size_t ws_bytes,
+                                           hipStream_t s) {
+    constexpr int NB = EPI == GEMM_SWIGLU ? 2 : 1;
+    constexpr size_t shm = mfma_lds_bytes<NB>();
+    if (!g_cus) {
+        int dev = 0;
+        ESP_HIP(hipGetDevice(&dev));
+        ESP_HIP(hipDeviceGetAttribute(&g_cus, hipDeviceAttributeMultiprocessorCount, dev));
+        if (g_cus <= 0) g_cus = 256;
+    }
+    const int gx = (a.N + MF_BN - 1) / MF_BN, gy = (a.M + MF_BM - 1) / MF_BM;
+    // split K until the grid covers the chip twice (k-splits stay >= 512)
+    int splits = 1;
+    while (gx * gy * splits < 2 * g_cus && a.K / (splits * 2) >= 512 &&
+           (size_t)(splits * 2) * NB * a.M * a.N * 4 <= ws_bytes)
+        splits *= 2;
+    int kps = (a.K + splits - 1) / splits;
+    kps = (kps + MF_BK - 1) / MF_BK * MF_BK;
+    if (splits == 1) {
+        gemm_mfma_k<EPI, NB><<<dim3(gx, gy, 1), 256, shm, s>>>(a, nullptr, a.K);
+        return;
+    }
+    gemm_mfma_k<MF_PARTIAL, NB><<<dim3(gx, gy, splits), 256, shm, s>>>(a, ws, kps);
+    size_t mn = (size_t)a.M * a.N;
+    int blocks = (int)std::min<size_t>((mn + 255) / 256, (size_t)g_cus * 8);
+    mfma_reduce_k<EPI, NB><<<blocks, 256, 0, s>>>(a, ws, splits);
+}
+
+bool gemm_mfma_ok(Dt wt, const GemmArgs &a) {
+    return wt == DT_BF16 && a.K % 8 == 0 && a.K >= 32 && ((uintptr_t)a.a % 16) == 0 &&
+           ((uintptr_t)a.w % 16) == 0 && (!a.w2 || ((uintptr_t)a.w2 % 16) == 0);
+}
+
+void launch_gemm_mfma(GemmEpi epi, const GemmArgs &a, float *ws, size_t ws_bytes, hipStream_t s) {
+    if (epi == GEMM_STORE) mfma_launch<GEMM_STORE>(a, ws, ws_bytes, s);
+    else if (epi == GEMM_RESIDUAL) mfma_launch<GEMM_RESIDUAL>(a, ws, ws_bytes, s);
+    else mfma_launch<GEMM_SWIGLU>(a, ws, ws_bytes, s);
+}
+
+}  // namespace esp

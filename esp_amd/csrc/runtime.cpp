@@ -12,6 +12,7 @@
 #include <set>
 
 #include "decode.hpp"
+#include "flash.hpp"
 #include "kernels_extra.hpp"
 #include "profile.hpp"
 #include "safetensors.hpp"
@@ -715,7 +716,8 @@ static void run_layer_decode(Model &m, Kv &kv, const Rows &rows, LayerW &w, int 
 
 // One pass of `Mc` rows (already on the device at `rows`) through all layers.
 // `x_is_gemv` selects the single-row decode kernels.
-static void run_layers(Model &m, Kv &kv, const Rows &rows, int Mc, int max_t) {
+static void run_layers(Model &m, Kv &kv, const Rows &rows, int Mc, int max_t, int one_seq = -1,
+                       int p0 = 0) {
     hipStream_t s = kv.stream;
     const bool single = Mc == 1;
     const Dt act = DT_F32;  // activations stay f32; weights carry the format
@@ -748,6 +750,8 @@ static void run_layers(Model &m, Kv &kv, const Rows &rows, int Mc, int max_t) {
                                kv.xn.p, nullptr, s);
             }
             GemmArgs g{};
+            g.ws = kv.gemm_ws.as<float>();
+            g.ws_bytes = kv.gemm_ws.bytes;
             g.a = kv.xn.p;
             g.w = w.qkv;
             g.bias = w.qkv_bias;
@@ -787,7 +791,25 @@ static void run_layers(Model &m, Kv &kv, const Rows &rows, int Mc, int max_t) {
             Prof p("rope_kv", s);
             launch_rope_kv(m.wt, kv.dt, r, s);
         }
-        {
+        if (one_seq >= 0 && Mc >= 16 && m.wt == DT_BF16 && flash_ok(m.hd)) {
+            // rows are consecutive positions of one sequence: tiled MFMA attention
+            FlashArgs f{};
+            f.q = kv.q.as<float>();
+            f.kv = kv.cache.as<float>() + (size_t)l * kv.layer_stride;
+            f.seq_stride = kv.seq_stride;
+            f.kv_half_stride = kv.half_stride;
+            f.head_stride = kv.head_stride;
+            f.seq = one_seq;
+            f.p0 = p0;
+            f.M = Mc;
+            f.nq = m.nq;
+            f.nkv = m.nkv;
+            f.hd = m.hd;
+            f.window = w.window;
+            f.out = kv.attn.as<float>();
+            Prof p("attention", s);
+            launch_flash(f, s);
+        } else {
             AttnArgs a{};
             a.q = kv.q.as<float>();
             a.kv = (char *)kv.cache.p + (size_t)l * kv.layer_stride * dt_size(kv.dt);
@@ -820,6 +842,8 @@ static void run_layers(Model &m, Kv &kv, const Rows &rows, int Mc, int max_t) {
             launch_gemv(m.wt, GEMV_RESIDUAL, g, s);
         } else {
             GemmArgs g{};
+            g.ws = kv.gemm_ws.as<float>();
+            g.ws_bytes = kv.gemm_ws.bytes;
             g.a = kv.attn.p;
             g.w = w.o;
             g.bias = w.o_bias;
@@ -863,6 +887,8 @@ static void run_layers(Model &m, Kv &kv, const Rows &rows, int Mc, int max_t) {
                                kv.xn.p, nullptr, s);
             }
             GemmArgs g{};
+            g.ws = kv.gemm_ws.as<float>();
+            g.ws_bytes = kv.gemm_ws.bytes;
             g.a = kv.xn.p;
             g.w = w.gate;
             g.w2 = w.up;
@@ -876,6 +902,8 @@ static void run_layers(Model &m, Kv &kv, const Rows &rows, int Mc, int max_t) {
                 launch_gemm(m.wt, GEMM_SWIGLU, g, s);
             }
             GemmArgs d{};
+            d.ws = kv.gemm_ws.as<float>();
+            d.ws_bytes = kv.gemm_ws.bytes;
             d.a = kv.act.p;
             d.w = w.down;
             d.c = kv.h.p;
@@ -903,6 +931,7 @@ static void ensure_scratch(Model &m, Kv &kv, int Mc, int n_seqs) {
     kv.last_h.ensure((size_t)n_seqs * H * 4);
     kv.logits.ensure((size_t)std::max(n_seqs, kv.batch) * m.V * 4);
     kv.rows_dev.ensure((size_t)(3 * kMaxRows + 2 * kv.batch + 64) * 4);
+    if (Mc > 1 && m.wt == DT_BF16) kv.gemm_ws.ensure((size_t)256 << 20);  // split-K partials
 }
 
 // Head on the last row of each sequence (model.rs:531-538): final RMSNorm
@@ -949,6 +978,8 @@ static void run_head(Model &m, Kv &kv, int n_seqs, const float *h_src, const int
                        row_index, s);
     }
     GemmArgs g{};
+    g.ws = kv.gemm_ws.as<float>();
+    g.ws_bytes = kv.gemm_ws.bytes;
     g.a = kv.xn.p;
     g.w = m.head;
     g.c = kv.logits.p;
@@ -1012,7 +1043,8 @@ void forward(Model &m, Kv &kv, int n_seqs, const uint32_t *seqs, const uint32_t 
             Prof p("embed", s);
             launch_embed(m.wt, m.embed, rows.ids, Mc, m.H, kv.h.as<float>(), s);
         }
-        run_layers(m, kv, rows, Mc, max_t);
+        if (n_seqs == 1) run_layers(m, kv, rows, Mc, max_t, (int)seqs[0], rpos[c0]);
+        else run_layers(m, kv, rows, Mc, max_t);
         if (one_chunk) break;
         // keep the hidden state of every sequence's last row in this chunk
         for (int i = 0; i < n_seqs; ++i)
@@ -1089,6 +1121,8 @@ void moe_block(Model &m, Kv &kv, LayerW &w, int Mc, hipStream_t s) {
     kv.moe_act.ensure((size_t)Mc * k * m.Fe * 4);
     kv.moe_y.ensure((size_t)Mc * k * H * 4);
     GemmArgs r{};
+    r.ws = kv.gemm_ws.as<float>();
+    r.ws_bytes = kv.gemm_ws.bytes;
     r.a = kv.xn.p;
     r.w = w.router;
     r.c = kv.moe_logits.p;
@@ -1121,6 +1155,8 @@ void moe_block(Model &m, Kv &kv, LayerW &w, int Mc, hipStream_t s) {
         int n = offs[e + 1] - offs[e];
         if (!n) continue;
         GemmArgs g{};
+        g.ws = kv.gemm_ws.as<float>();
+        g.ws_bytes = kv.gemm_ws.bytes;
         g.a = (char *)kv.moe_x.p + (size_t)offs[e] * H * es;
         g.w = (char *)w.ex_gate + (size_t)e * m.Fe * H * dt_size(m.wt);
         g.w2 = (char *)w.ex_up + (size_t)e * m.Fe * H * dt_size(m.wt);
@@ -1134,6 +1170,8 @@ void moe_block(Model &m, Kv &kv, LayerW &w, int Mc, hipStream_t s) {
             launch_gemm(m.wt, GEMM_SWIGLU, g, s);
         }
         GemmArgs d{};
+        d.ws = kv.gemm_ws.as<float>();
+        d.ws_bytes = kv.gemm_ws.bytes;
         d.a = g.c;
         d.w = (char *)w.ex_down + (size_t)e * H * m.Fe * dt_size(m.wt);
         d.c = kv.moe_y.as<float>() + (size_t)offs[e] * H;
@@ -1156,6 +1194,8 @@ void moe_block(Model &m, Kv &kv, LayerW &w, int Mc, hipStream_t s) {
         kv.moe_ys.ensure((size_t)Mc * H * 4);
         kv.moe_sg.ensure((size_t)Mc * 4);
         GemmArgs g{};
+        g.ws = kv.gemm_ws.as<float>();
+        g.ws_bytes = kv.gemm_ws.bytes;
         g.a = kv.xn.p;
         g.w = w.sh_gate;
         g.w2 = w.sh_up;
@@ -1165,6 +1205,8 @@ void moe_block(Model &m, Kv &kv, LayerW &w, int Mc, hipStream_t s) {
         g.K = H;
         g.ldc = m.Fs;
         GemmArgs d{};
+        d.ws = kv.gemm_ws.as<float>();
+        d.ws_bytes = kv.gemm_ws.bytes;
         d.a = kv.act.p;
         d.w = w.sh_down;
         d.c = kv.moe_ys.p;
@@ -1173,6 +1215,8 @@ void moe_block(Model &m, Kv &kv, LayerW &w, int Mc, hipStream_t s) {
         d.K = m.Fs;
         d.ldc = H;
         GemmArgs sg{};
+        sg.ws = kv.gemm_ws.as<float>();
+        sg.ws_bytes = kv.gemm_ws.bytes;
         sg.a = kv.xn.p;
         sg.w = w.shared_gate;
         sg.c = kv.moe_sg.p;

@@ -220,3 +220,50 @@ def test_decode_kernels_match_oracle(variant):
         want = ref.forward_last(rkv, [t])
     dev = model.generate_greedy_device(model.new_cache(1, 64), prompt, 10, eos=[])
     assert dev == ids
+
+
+def test_bf16_prefill_odd_shapes_and_moe():
+    """bf16 MFMA projections at shapes that cross tile edges (150 rows,
+    320 / 200 / 448 widths), a qwen2 bias model and a routed-expert model,
+    prefill + decode vs the oracle within the bf16 tolerance."""
+    for extra, seed in (({"model_type": "qwen2", "architectures": ["Qwen2ForCausalLM"]}, 41),
+                        ({"model_type": "qwen2_moe", "architectures": ["Qwen2MoeForCausalLM"],
+                          "num_experts": 6, "num_experts_per_tok": 2,
+                          "moe_intermediate_size": 96, "shared_expert_intermediate_size": 64,
+                          "norm_topk_prob": True, "decoder_sparse_step": 1}, 43)):
+        cfg = synth.llama_config(2, 320, 5, 1, 200, 1000, head_dim=64, max_pos=256, extra=extra)
+        tensors = synth.make_tensors(cfg, seed, "bf16", bias_std=0.05)
+        model = DecoderModel.from_bytes(cfg, st.dump(tensors), "bf16")
+        ref = oracle.OracleModel(cfg, tensors)
+        prompt = synth.uniform_ids(seed, 150, cfg.vocab_size)
+        kv, rkv = model.new_cache(1, 200), ref.new_cache(200)
+        got = model.try_forward_cached_last(prompt, kv)
+        want = ref.forward_last(rkv, prompt)
+        assert _close_bf16(got, want), (extra.get("model_type"), float(np.abs(got - want).max()))
+        for step in range(3):
+            t = oracle.argmax(want)
+            got = model.try_forward_cached_last([t, (t + 1) % cfg.vocab_size], kv)
+            want = ref.forward_last(rkv, [t, (t + 1) % cfg.vocab_size])
+            assert _close_bf16(got, want), (step, float(np.abs(got - want).max()))
+
+
+@pytest.mark.parametrize("variant", ["llama_hd64", "gqa_hd128", "window_hd64"])
+def test_bf16_flash_prefill_chunks_match_oracle(variant):
+    """MFMA prefill attention (bf16 format): a 140-token prefill, then a
+    45-token block over the warm cache (rows start at position 140), then
+    decode; logits within the bf16 tolerance of the oracle."""
+    extra, hd, nq, nkv = {
+        "llama_hd64": ({}, 64, 4, 2),
+        "gqa_hd128": ({}, 128, 8, 2),
+        "window_hd64": ({"model_type": "mistral", "architectures": ["MistralForCausalLM"],
+                         "sliding_window": 37}, 64, 4, 1),
+    }[variant]
+    cfg = synth.llama_config(2, 256, nq, nkv, 384, 900, head_dim=hd, max_pos=512, extra=extra)
+    tensors = synth.make_tensors(cfg, 51, "bf16")
+    model = DecoderModel.from_bytes(cfg, st.dump(tensors), "bf16")
+    ref = oracle.OracleModel(cfg, tensors)
+    kv, rkv = model.new_cache(1, 256), ref.new_cache(256)
+    for block in (synth.uniform_ids(1, 140, 900), synth.uniform_ids(2, 45, 900), [7], [8]):
+        got = model.try_forward_cached_last(block, kv)
+        want = ref.forward_last(rkv, block)
+        assert _close_bf16(got, want), (variant, len(block), float(np.abs(got - want).max()))
