@@ -32,11 +32,22 @@ def c2_config(max_pos=2048):
                         extra={"tie_word_embeddings": True})
 
 
-def decode_bytes(cfg, ctx: int, kv_bytes_per_elem: int = 4) -> dict:
-    """Algorithmic HBM bytes of one batch-1 decode step at context `ctx`."""
+def c3_config(max_pos=8192):
+    from tests.synth import llama_config
+    return llama_config(32, 4096, 32, 8, 14336, 128256, theta=500000.0, max_pos=max_pos)
+
+
+def decode_bytes(cfg, ctx: int, kv_bytes_per_elem: int = 4, lora_rank: int = 0,
+                 lora_targets=()) -> dict:
+    """Algorithmic HBM bytes of one batch-1 decode step at context `ctx`:
+    every weight once (bf16) + the K/V cache once (f32) + LoRA A/B (bf16)."""
     H, L, F, V = cfg.hidden_size, cfg.num_hidden_layers, cfg.intermediate_size, cfg.vocab_size
     qw, kvw = cfg.query_width(), cfg.kv_heads() * cfg.head_dim()
-    layer_w = (H * (qw + 2 * kvw) + H * qw + 3 * H * F) * 2
+    lora = 0
+    for t in lora_targets:
+        outf = qw if t == "q_proj" else kvw
+        lora += lora_rank * (H + outf) * 2
+    layer_w = (H * (qw + 2 * kvw) + H * qw + 3 * H * F) * 2 + lora
     head_w = V * H * 2
     kv = 2 * L * kvw * ctx * kv_bytes_per_elem
     return {"gemv_weights": L * layer_w + head_w, "kv": kv, "total": L * layer_w + head_w + kv}
@@ -106,6 +117,54 @@ def cpu_baseline(cfg, ctx: int, budget_s: float = 15.0) -> dict:
                       f"burn-ndarray path, OpenMP over {threads} threads"}
 
 
+def c3_bench(steps: int) -> dict:
+    """Llama-3-8B shape bf16 with rank-16 LoRA (alpha 32)
+    on q_proj and v_proj; batch-1 greedy decode at ~4096 context and a
+    separate 2048-token prefill."""
+    from esp_amd import DecoderModel
+    from tests.synth import uniform_ids
+    cfg = c3_config()
+    model = DecoderModel.synthetic(cfg, seed=4321, std=0.02, fmt="bf16", lora_rank=16,
+                                   lora_targets=["q_proj", "v_proj"], lora_a_std=0.02,
+                                   lora_b_std=0.01, lora_scale=2.0)
+    prompt = uniform_ids(7, 4064, cfg.vocab_size)
+    n_dec = 64
+    kv = model.new_cache(1, 4064 + n_dec)
+    pre = uniform_ids(8, 2048, cfg.vocab_size)
+
+    def prefill(ids):
+        kv.reset(0)
+        t0 = time.perf_counter()
+        model.try_forward_cached_last(ids, kv)
+        return time.perf_counter() - t0
+
+    def gen():
+        t0 = time.perf_counter()
+        out = model.generate_greedy_device(kv, prompt, n_dec, eos=[])
+        assert len(out) == n_dec
+        return time.perf_counter() - t0
+
+    gen()
+    prefill(pre)
+    t_gen = sorted(gen() for _ in range(steps))[steps // 2]
+    t_p4 = sorted(prefill(prompt) for _ in range(steps))[steps // 2]
+    t_p2 = sorted(prefill(pre) for _ in range(steps))[steps // 2]
+    t_dec = (t_gen - t_p4) / (n_dec - 1)
+    db = decode_bytes(cfg, 4064 + n_dec // 2, lora_rank=16, lora_targets=["q_proj", "v_proj"])
+    fl = prefill_flops(cfg, 2048) + 2.0 * 2048 * 32 * 16 * (4096 + 4096 + 4096 + 1024)  # + LoRA
+    res = {"workload": "C3: Llama-3-8B shape bf16, LoRA r16 on q/v; decode at 4064-4128 "
+                       "context, separate 2048-token prefill (BASELINE configs[2])",
+           "decode_tokens_per_s": round(1.0 / t_dec, 2),
+           "decode_ms_per_token": round(t_dec * 1e3, 4),
+           "decode_hbm_frac": round(db["total"] / t_dec / 1e9 / HBM_PEAK_GBS, 4),
+           "decode_bytes_per_token": db["total"],
+           "prefill_2048_tokens_per_s": round(2048 / t_p2, 1),
+           "prefill_2048_ms": round(t_p2 * 1e3, 3),
+           "prefill_mfma_frac": round(fl / t_p2 / 1e12 / BF16_PEAK_TFLOPS, 4)}
+    model.close()
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -114,6 +173,7 @@ def main():
     ap.add_argument("--prompt", type=int, default=512)
     ap.add_argument("--decode", type=int, default=256)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-c3", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 "
@@ -201,6 +261,11 @@ def main():
     }
     print(f"gpu: decode {dec_tps:.1f} tok/s, prefill {pre_tps:.1f} tok/s, gemv {gemv_gbs:.0f} GB/s",
           file=sys.stderr, flush=True)
+    if not args.no_c3:
+        del kv, kv2
+        model.close()
+        result["c3"] = c3_bench(max(1, args.steps))
+        print(f"c3: {result['c3']}", file=sys.stderr, flush=True)
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(cfg, int(avg_ctx))
     print(json.dumps(result), flush=True)

@@ -267,3 +267,59 @@ def test_bf16_flash_prefill_chunks_match_oracle(variant):
         got = model.try_forward_cached_last(block, kv)
         want = ref.forward_last(rkv, block)
         assert _close_bf16(got, want), (variant, len(block), float(np.abs(got - want).max()))
+
+
+def _adapter(cfg, rank, targets, seed, fmt):
+    """PEFT LoRA tensors base_model.model.model.layers.{i}.self_attn.{m}.lora_{A,B}.weight,
+    A ~ N(0, 0.02), B ~ N(0, 0.01)."""
+    H, qw, kvw = cfg.hidden_size, cfg.query_width(), cfg.kv_heads() * cfg.head_dim()
+    out = {}
+    for l in range(cfg.num_hidden_layers):
+        for t in targets:
+            pre = f"base_model.model.model.layers.{l}.self_attn.{t}"
+            outf = qw if t == "q_proj" else kvw
+            a = synth.normal(synth.tensor_seed(seed, pre + "A"), rank * H, 0.02).reshape(rank, H)
+            b = synth.normal(synth.tensor_seed(seed, pre + "B"), outf * rank, 0.01).reshape(outf, rank)
+            if fmt == "bf16":
+                out[pre + ".lora_A.weight"] = (st.bf16_round(a), "BF16")
+                out[pre + ".lora_B.weight"] = (st.bf16_round(b), "BF16")
+            else:
+                out[pre + ".lora_A.weight"] = (a, "F32")
+                out[pre + ".lora_B.weight"] = (b, "F32")
+    return out
+
+
+@pytest.mark.parametrize("fmt", ["f32", "bf16"])
+def test_lora_unmerged_matches_merged_oracle(fmt):
+    """lora.rs:99-217: rank-16 alpha-32 adapters on q_proj and v_proj, applied
+    unmerged on the GPU (y += s B (A x)) vs the oracle's merged W + s B A;
+    plus a second adapter stacked on q_proj."""
+    from esp_amd.model import LoraAdapter
+    cfg = synth.llama_config(2, 256, 4, 2, 320, 500, head_dim=64, max_pos=128)
+    tensors = synth.make_tensors(cfg, 61, fmt, std=0.05)
+    ad1 = _adapter(cfg, 16, ["q_proj", "v_proj"], 1, fmt)
+    ad2 = _adapter(cfg, 8, ["q_proj"], 2, fmt)
+    model = DecoderModel.from_bytes(
+        cfg, st.dump(tensors), fmt,
+        adapters=[LoraAdapter(16, 32.0, ["q_proj", "v_proj"], st.dump(ad1)),
+                  LoraAdapter(8, 16.0, ["q_proj"], st.dump(ad2))])
+    merged = oracle.apply_lora(cfg, tensors, {"rank": 16, "alpha": 32.0, "targets": ["q_proj", "v_proj"],
+                                              "tensors": ad1})
+    merged = oracle.apply_lora(cfg, merged, {"rank": 8, "alpha": 16.0, "targets": ["q_proj"],
+                                             "tensors": ad2})
+    ref = oracle.OracleModel(cfg, merged)
+    plain = oracle.OracleModel(cfg, tensors)
+    prompt = synth.uniform_ids(8, 40, cfg.vocab_size)
+    kv, rkv = model.new_cache(1, 64), ref.new_cache(64)
+    got = model.try_forward_cached_last(prompt, kv)
+    want = ref.forward_last(rkv, prompt)
+    base = plain.forward_last(plain.new_cache(64), prompt)
+    assert np.abs(want - base).max() > 1e-3  # the adapters matter
+    for step in range(4):
+        if fmt == "f32":
+            assert np.abs(got - want).max() <= 1e-4 * float(np.abs(want).max()), step
+        else:
+            assert _close_bf16(got, want), (step, float(np.abs(got - want).max()))
+        t = oracle.argmax(want)
+        got = model.try_forward_cached_last([t], kv)
+        want = ref.forward_last(rkv, [t])
