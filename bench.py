@@ -174,6 +174,7 @@ def main():
     ap.add_argument("--decode", type=int, default=256)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-c3", action="store_true")
+    ap.add_argument("--only-c3", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 "
@@ -183,6 +184,9 @@ def main():
     from esp_amd.model import profile_enable, profile_read
     from tests.synth import uniform_ids
 
+    if args.only_c3:
+        print(json.dumps({"c3": c3_bench(max(1, args.steps))}), flush=True)
+        return
     cfg = c2_config()
     model = DecoderModel.synthetic(cfg, seed=1234, std=0.02, fmt="bf16")
     prompt = uniform_ids(42, args.prompt, cfg.vocab_size)

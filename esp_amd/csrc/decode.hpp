@@ -47,6 +47,7 @@ struct AttnDecodeArgs {
 };
 
 bool attn_decode_ok(int hd, int G);
+int attn_decode_splits(int hd, int max_t);
 void launch_attn_decode(const AttnDecodeArgs &a, hipStream_t s);
 
 }  // namespace esp

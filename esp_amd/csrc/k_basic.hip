@@ -52,7 +52,7 @@ void launch_rmsnorm(const float *x, const float *gamma, float eps, int M, int H,
 // attention.rs:306-326: q/k/v projections (+bias, + unmerged LoRA as in
 // lora.rs:93-97), optional QK RMSNorm over head_dim (:312-319), split-half
 // RoPE at the row's absolute position (:99-123), then K/V appended to the
-// cache (:126-148). One block per token row.
+// cache (:126-148). One block per (token row, group of heads).
 template <typename WT, typename KT>
 __global__ void __launch_bounds__(256) rope_kv_k(RopeKvArgs a) {
     extern __shared__ float sh[];  // [heads_per_iter][hd]
@@ -67,7 +67,8 @@ __global__ void __launch_bounds__(256) rope_kv_k(RopeKvArgs a) {
     const int total = a.nq + 2 * a.nkv;
     const int qw = a.nq * hd, kvw = a.nkv * hd;
     KT *cache = (KT *)a.kv;
-    for (int base = 0; base < total; base += hpi) {
+    {
+        const int base = blockIdx.y * hpi;  // one head group per block
         const int lh = threadIdx.x / hd;
         const int head = base + lh;
         const bool active = lh < hpi && head < total;
@@ -128,7 +129,6 @@ __global__ void __launch_bounds__(256) rope_kv_k(RopeKvArgs a) {
                 st(cache, off, x);
             }
         }
-        __syncthreads();
     }
 }
 
@@ -137,12 +137,14 @@ void launch_rope_kv(Dt wt, Dt kvdt, const RopeKvArgs &a, hipStream_t s) {
     int threads = a.hd > 256 ? 0 : 256;
     if (!threads) fail(ESP_UNSUPPORTED, "head_dim: values above 256 are not implemented");
     size_t shm = sizeof(float) * hpi * a.hd;
+    const int groups = (a.nq + 2 * a.nkv + hpi - 1) / hpi;
+    dim3 grid(a.rows.M, groups);
     if (wt == DT_BF16 && kvdt == DT_BF16)
-        rope_kv_k<uint16_t, uint16_t><<<a.rows.M, threads, shm, s>>>(a);
+        rope_kv_k<uint16_t, uint16_t><<<grid, threads, shm, s>>>(a);
     else if (wt == DT_BF16 && kvdt == DT_F32)
-        rope_kv_k<uint16_t, float><<<a.rows.M, threads, shm, s>>>(a);
+        rope_kv_k<uint16_t, float><<<grid, threads, shm, s>>>(a);
     else if (wt == DT_F32 && kvdt == DT_F32)
-        rope_kv_k<float, float><<<a.rows.M, threads, shm, s>>>(a);
+        rope_kv_k<float, float><<<grid, threads, shm, s>>>(a);
     else
         fail(ESP_BACKEND, "rope_kv: unsupported dtype pair");
 }

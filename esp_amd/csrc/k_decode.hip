@@ -375,6 +375,8 @@ void launch_decode_gemv(Dt wt, int epi, const DecodeGemvArgs &a, hipStream_t s) 
 
 // ------------------------------------------------------------ attention
 
+constexpr int ATT_MAX_SPLIT = 128;
+
 // One block per (key split, kv head, row). Each 16-lane group (hd 64) or
 // 32-lane group (hd 128) owns one key at a time; lanes cover 4 dims each.
 template <int HD>
@@ -502,39 +504,63 @@ __global__ void __launch_bounds__(256) attn_decode_k(AttnDecodeArgs a) {
     }
     __syncthreads();
     if (!last) return;
-    // stage this (row, kv head)'s partials in LDS with one batch of loads
-    extern __shared__ float stage[];  // [G][n_split][HD + 2]
-    const float *pbase = a.part + ((size_t)row * a.nq + (size_t)g * G) * a.n_split * stride;
-    const int total = G * a.n_split * (int)stride;
-    for (int i = tid; i < total; i += blockDim.x) stage[i] = ld_agent(pbase + i);
+    // merge: split maxima / sums staged in LDS, then per output one batch of
+    // independent partial loads weighted in split order (deterministic)
+    __shared__ float mm[GMAX][ATT_MAX_SPLIT], ww[GMAX][ATT_MAX_SPLIT], LL[GMAX];
+    const int ns = a.n_split;
+    const float *pb = a.part + ((size_t)row * a.nq + (size_t)g * G) * ns * stride;
+    for (int i = tid; i < G * ns; i += blockDim.x) {
+        const int j = i / ns, sp = i % ns;
+        mm[j][sp] = ld_agent(pb + ((size_t)j * ns + sp) * stride);
+        ww[j][sp] = ld_agent(pb + ((size_t)j * ns + sp) * stride + 1);
+    }
+    __syncthreads();
+    if (tid < G) {
+        float mx = -INFINITY;
+        for (int sp = 0; sp < ns; ++sp) mx = fmaxf(mx, mm[tid][sp]);
+        float L = 0.f;
+        for (int sp = 0; sp < ns; ++sp) {
+            float w = mm[tid][sp] == -INFINITY ? 0.f : __expf(mm[tid][sp] - mx);
+            L += ww[tid][sp] * w;
+            ww[tid][sp] = w;
+        }
+        LL[tid] = L;
+    }
     __syncthreads();
     for (int o = tid; o < G * HD; o += blockDim.x) {
-        int j = o / HD, d = o % HD;
-        const float *p = stage + (size_t)j * a.n_split * stride;
-        float mx = -INFINITY;
-        for (int sp = 0; sp < a.n_split; ++sp) mx = fmaxf(mx, p[(size_t)sp * stride]);
-        float L = 0.f, v = 0.f;
-        for (int sp = 0; sp < a.n_split; ++sp) {
-            float ms = p[(size_t)sp * stride];
-            if (ms == -INFINITY) continue;
-            float sc = __expf(ms - mx);
-            L += p[(size_t)sp * stride + 1] * sc;
-            v += p[(size_t)sp * stride + 2 + d] * sc;
+        const int j = o / HD, d = o % HD;
+        const float *p = pb + (size_t)j * ns * stride + 2 + d;
+        float v = 0.f;
+        int sp = 0;
+        for (; sp + 8 <= ns; sp += 8) {
+            float t[8];
+#pragma unroll
+            for (int q = 0; q < 8; ++q) t[q] = ld_agent(p + (size_t)(sp + q) * stride);
+#pragma unroll
+            for (int q = 0; q < 8; ++q) v += t[q] * ww[j][sp + q];
         }
-        a.out[(size_t)row * a.nq * HD + (size_t)(g * G + j) * HD + d] = v / L;
+        for (; sp < ns; ++sp) v += ld_agent(p + (size_t)sp * stride) * ww[j][sp];
+        a.out[(size_t)row * a.nq * HD + (size_t)(g * G + j) * HD + d] = v / LL[j];
     }
 }
 
 bool attn_decode_ok(int hd, int G) { return (hd == 64 || hd == 128) && G <= 8; }
 
+// Key splits for one decode row: ~32 keys per block, capped so the merge
+// re-reads at most a few percent of the keys' bytes.
+int attn_decode_splits(int hd, int max_t) {
+    int cap = hd == 64 ? ATT_MAX_SPLIT : ATT_MAX_SPLIT / 2;
+    int ns = (max_t + 31) / 32;
+    return ns < 1 ? 1 : (ns > cap ? cap : ns);
+}
+
 void launch_attn_decode(const AttnDecodeArgs &a, hipStream_t s) {
     const int G = a.nq / a.nkv;
     if (!attn_decode_ok(a.hd, G)) fail(ESP_BACKEND, "attn_decode: unsupported head shape");
     dim3 grid(a.n_split, a.nkv, a.M);
-    const size_t shm = sizeof(float) * (size_t)G * a.n_split * (a.hd + 2);
-    if (shm > 48 * 1024) fail(ESP_BACKEND, "attn_decode: too many key splits");
-    if (a.hd == 64) attn_decode_k<64><<<grid, 256, shm, s>>>(a);
-    else attn_decode_k<128><<<grid, 256, shm, s>>>(a);
+    if (a.n_split > ATT_MAX_SPLIT) fail(ESP_BACKEND, "attn_decode: too many key splits");
+    if (a.hd == 64) attn_decode_k<64><<<grid, 256, 0, s>>>(a);
+    else attn_decode_k<128><<<grid, 256, 0, s>>>(a);
 }
 
 }  // namespace esp

@@ -519,9 +519,6 @@ static Plan attn_plan(const Model &m, int rows, int max_t) {
     int base = rows * m.nkv;
     int want = (512 + base - 1) / base;  // aim for >= 512 blocks of >= 64 keys
     int max_split = (max_t + 63) / 64;
-    // the decode merge stages G * n_split * (hd + 2) floats in 48 KB of LDS
-    int lds_cap = 48 * 1024 / (4 * (m.nq / m.nkv) * (m.hd + 2));
-    max_split = std::min(max_split, std::max(1, lds_cap));
     int ns = std::max(1, std::min(want, max_split));
     int sl = (max_t + ns - 1) / ns;
     sl = (sl + 31) / 32 * 32;
@@ -723,6 +720,10 @@ static void run_layers(Model &m, Kv &kv, const Rows &rows, int Mc, int max_t, in
     const Dt act = DT_F32;  // activations stay f32; weights carry the format
     const int H = m.H;
     Plan plan = attn_plan(m, Mc, max_t);
+    if (single && attn_decode_ok(m.hd, m.nq / m.nkv)) {
+        plan.n_split = attn_decode_splits(m.hd, max_t);
+        plan.split_len = (max_t + plan.n_split - 1) / plan.n_split;
+    }
     kv.part.ensure((size_t)Mc * m.nq * plan.n_split * (m.hd + 2) * 4);
     for (int l = 0; l < m.L; ++l) {
         LayerW &w = m.layers[l];
