@@ -26,10 +26,12 @@ struct Error {
 
 typedef uint16_t bf16_t;  // raw bf16 bits in host code
 
-// Activation/weight element kinds used to instantiate kernels.
-enum Dt { DT_F32 = 0, DT_BF16 = 1 };
+// Element kinds. DT_SPLIT is an f32 activation matrix stored as two bf16
+// planes of the same shape, hi = bf16(x) then lo = bf16(x - hi), so matrix
+// cores can consume it exactly (R x C matrix: hi[r*C+c], lo[R*C + r*C+c]).
+enum Dt { DT_F32 = 0, DT_BF16 = 1, DT_SPLIT = 2 };
 
-inline size_t dt_size(Dt d) { return d == DT_F32 ? 4 : 2; }
+inline size_t dt_size(Dt d) { return d == DT_BF16 ? 2 : 4; }
 
 // ---------------------------------------------------------------------------
 // Kernel launch interfaces (implemented in the .hip files). Every launcher
@@ -72,11 +74,13 @@ void launch_gemv(Dt wt, GemvEpi epi, const GemvArgs &a, hipStream_t s);
 // A, weights W in the model format, f32 accumulation.
 enum GemmEpi { GEMM_STORE = 0, GEMM_RESIDUAL = 1, GEMM_SWIGLU = 2 };
 struct GemmArgs {
-    const void *a;     // [M, K] act
+    const void *a;     // [M, K] act: f32, or the hi plane of a split matrix
+    const void *a_lo;  // lo plane of a split A (nullable = A is f32)
     const void *w;     // [N, K] wt
     const void *w2;    // SWIGLU up rows
     const float *bias; // nullable [N]
-    void *c;           // STORE: f32 [M, ldc]; RESIDUAL: f32 +=; SWIGLU: f32 [M, ldc]
+    void *c;           // STORE: f32 [M, ldc]; RESIDUAL: f32 +=; SWIGLU: f32 [M, ldc] or hi plane
+    void *c_lo;        // SWIGLU only: lo plane of a split output (nullable = f32 out)
     int M, N, K, ldc;
     float *ws;         // nullable split-K workspace
     size_t ws_bytes;
@@ -113,7 +117,7 @@ struct AttnArgs {
     int nq, nkv, hd, window;  // window 0 = none
     float *part;        // scratch partials
     int n_split, split_len;
-    void *out;          // [M, nq*hd] out dt
+    void *out;          // [M, nq*hd] out dt (DT_SPLIT: planes of M rows)
     Dt out_dt;
 };
 void launch_attention(Dt kvdt, const AttnArgs &a, hipStream_t s);

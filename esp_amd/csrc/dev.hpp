@@ -28,6 +28,13 @@ template <> __device__ __forceinline__ void st<uint16_t>(uint16_t *p, size_t i, 
     p[i] = f2bf(v);
 }
 
+// Store x into a split (hi/lo bf16 planes) matrix; `plane` = elements per plane.
+__device__ __forceinline__ void st_split(uint16_t *base, size_t plane, size_t i, float x) {
+    uint16_t h = f2bf(x);
+    base[i] = h;
+    base[plane + i] = f2bf(x - bf2f(h));
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);

@@ -11,7 +11,8 @@ struct FlashArgs {
     long long seq_stride, kv_half_stride, head_stride;
     int seq, p0;       // the rows are positions p0 .. p0+M-1 of sequence `seq`
     int M, nq, nkv, hd, window;
-    float *out;        // [M, nq*hd]
+    float *out;        // [M, nq*hd] f32, or the hi plane when out_lo is set
+    uint16_t *out_lo;  // nullable: lo plane of a split output
 };
 
 bool flash_ok(int hd);

@@ -25,7 +25,7 @@ void launch_embed(Dt wt, const void *embed, const int32_t *ids, int M, int H, fl
 
 // ---------------------------------------------------------------- rmsnorm
 // burn-nn RmsNorm (built at layer.rs:27-33): y = x / sqrt(mean(x^2) + eps) * gamma.
-template <typename OT>
+template <typename OT, bool SPLIT>
 __global__ void __launch_bounds__(256) rmsnorm_k(const float *x, const float *gamma, float eps,
                                                  int H, OT *out, const int32_t *row_index) {
     __shared__ float red[16];
@@ -36,16 +36,22 @@ __global__ void __launch_bounds__(256) rmsnorm_k(const float *x, const float *ga
     for (int j = threadIdx.x; j < H; j += blockDim.x) ss += xr[j] * xr[j];
     ss = block_sum(ss, red);
     float rms = sqrtf(ss / (float)H + eps);
-    for (int j = threadIdx.x; j < H; j += blockDim.x)
-        st(out, (size_t)m * H + j, (xr[j] / rms) * gamma[j]);
+    const size_t plane = (size_t)gridDim.x * H;
+    for (int j = threadIdx.x; j < H; j += blockDim.x) {
+        float y = (xr[j] / rms) * gamma[j];
+        if (SPLIT) st_split((uint16_t *)out, plane, (size_t)m * H + j, y);
+        else st(out, (size_t)m * H + j, y);
+    }
 }
 
 void launch_rmsnorm(const float *x, const float *gamma, float eps, int M, int H, Dt out_dt,
                     void *out, const int32_t *row_index, hipStream_t s) {
-    if (out_dt == DT_BF16)
-        rmsnorm_k<uint16_t><<<M, 256, 0, s>>>(x, gamma, eps, H, (uint16_t *)out, row_index);
+    if (out_dt == DT_SPLIT)
+        rmsnorm_k<uint16_t, true><<<M, 256, 0, s>>>(x, gamma, eps, H, (uint16_t *)out, row_index);
+    else if (out_dt == DT_BF16)
+        rmsnorm_k<uint16_t, false><<<M, 256, 0, s>>>(x, gamma, eps, H, (uint16_t *)out, row_index);
     else
-        rmsnorm_k<float><<<M, 256, 0, s>>>(x, gamma, eps, H, (float *)out, row_index);
+        rmsnorm_k<float, false><<<M, 256, 0, s>>>(x, gamma, eps, H, (float *)out, row_index);
 }
 
 // ----------------------------------------------------------------- rope_kv
@@ -261,7 +267,7 @@ __global__ void __launch_bounds__(256) attn_split_k(AttnArgs a) {
     }
 }
 
-template <typename OT>
+template <typename OT, bool SPLIT>
 __global__ void __launch_bounds__(256) attn_reduce_k(AttnArgs a, OT *out) {
     const int qh = blockIdx.x, row = blockIdx.y;
     const int hd = a.hd;
@@ -279,7 +285,9 @@ __global__ void __launch_bounds__(256) attn_reduce_k(AttnArgs a, OT *out) {
             float ms = p[(size_t)s * (hd + 2)];
             if (ms != -INFINITY) v += p[(size_t)s * (hd + 2) + 2 + d] * __expf(ms - mx);
         }
-        st(out, (size_t)row * a.nq * hd + (size_t)qh * hd + d, v / l);
+        const size_t i = (size_t)row * a.nq * hd + (size_t)qh * hd + d;
+        if (SPLIT) st_split((uint16_t *)out, (size_t)a.rows.M * a.nq * hd, i, v / l);
+        else st(out, i, v / l);
     }
 }
 
@@ -306,10 +314,12 @@ void launch_attention(Dt kvdt, const AttnArgs &a, hipStream_t s) {
     dim3 g2(a.nq, a.rows.M);
     int th = a.hd >= 64 ? 64 * ((a.hd + 63) / 64) : 64;
     if (th > 256) th = 256;
-    if (a.out_dt == DT_BF16)
-        attn_reduce_k<uint16_t><<<g2, th, 0, s>>>(a, (uint16_t *)a.out);
+    if (a.out_dt == DT_SPLIT)
+        attn_reduce_k<uint16_t, true><<<g2, th, 0, s>>>(a, (uint16_t *)a.out);
+    else if (a.out_dt == DT_BF16)
+        attn_reduce_k<uint16_t, false><<<g2, th, 0, s>>>(a, (uint16_t *)a.out);
     else
-        attn_reduce_k<float><<<g2, th, 0, s>>>(a, (float *)a.out);
+        attn_reduce_k<float, false><<<g2, th, 0, s>>>(a, (float *)a.out);
 }
 
 // ------------------------------------------------------------ generation

@@ -198,8 +198,17 @@ __global__ void __launch_bounds__(256) flash_attn_k(FlashArgs a) {
         if (r >= a.M) continue;
         const float inv_l = lsum[i];
 #pragma unroll
-        for (int t = 0; t < NDT; ++t)
-            a.out[(size_t)r * a.nq * HD + (size_t)qh * HD + t * 32 + col] = o[t][i] / inv_l;
+        for (int t = 0; t < NDT; ++t) {
+            const size_t idx = (size_t)r * a.nq * HD + (size_t)qh * HD + t * 32 + col;
+            const float v = o[t][i] / inv_l;
+            if (a.out_lo) {
+                uint16_t h = f2bf(v);
+                ((uint16_t *)a.out)[idx] = h;
+                a.out_lo[idx] = f2bf(v - bf2f(h));
+            } else {
+                a.out[idx] = v;
+            }
+        }
     }
 }
 

@@ -1,14 +1,15 @@
 // Prefill projection GEMM on the CDNA4 matrix cores:
 //   C[M,N] (f32) = A[M,K] (f32 activations) . W[N,K]^T (bf16 weights)
-// Each activation is split into bf16 hi + lo parts (a = hi + lo + O(2^-17 a))
-// and both parts are multiplied against the same bf16 weight fragment with
-// v_mfma_f32_32x32x16_bf16, accumulating in f32. Every product is exact, so
-// the result keeps f32-level accuracy while running on bf16 MFMA.
+// The activations arrive split into two bf16 planes, hi = bf16(a) and
+// lo = bf16(a - hi) (a = hi + lo + O(2^-17 a)), written that way by the
+// kernel that produced them; both parts are multiplied against the same bf16
+// weight fragment with v_mfma_f32_32x32x16_bf16, accumulating in f32. Every
+// product is exact, so the result keeps f32-level accuracy on bf16 MFMA.
 //
 // Block tile 128 x 128 x 32, four waves in a 2 x 2 arrangement, each wave a
 // 64 x 64 output tile of 2 x 2 MFMA blocks. A and W tiles are staged through
-// LDS (double-buffered, rows padded to 80 bytes) from register prefetches
-// issued one k-tile ahead. Epilogues: STORE (+bias), RESIDUAL (+=), SWIGLU
+// LDS (rows padded to 80 bytes) from register prefetches issued one k-tile
+// ahead. Epilogues: STORE (+bias), RESIDUAL (+=), SWIGLU
 // (gate and up tiles share the A fragments; out = silu(g) * u).
 #include "common.hpp"
 #include "dev.hpp"
@@ -39,15 +40,26 @@ __device__ __forceinline__ uint32_t pack2(uint16_t lo, uint16_t hi) {
     return (uint32_t)lo | ((uint32_t)hi << 16);
 }
 
+// XCD-aware tile order: workgroups are dispatched round-robin over the 8
+// XCDs (linear id % 8), so XCD x is given the contiguous tile range
+// [x*per, (x+1)*per) of a column-major tile order (row tiles fastest). Each
+// weight tile is then fetched into one XCD's L2 and reused by every row tile
+// that XCD runs, instead of being pulled into all eight L2s.
+constexpr int MF_XCDS = 8;
+
 template <int EPI, int NB>
-__global__ void __launch_bounds__(256, 2) gemm_mfma_k(GemmArgs g, float *ws, int k_per_split) {
+__global__ void __launch_bounds__(256, 2) gemm_mfma_k(GemmArgs g, float *ws, int k_per_split,
+                                                     int mt, int nt) {
     extern __shared__ uint16_t lds[];
     uint16_t *sA = lds;                          // [hi/lo][BM*LD]
     uint16_t *sB = lds + 2 * MF_A_ELEMS;         // [nb][BN*LD]
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int wm = wave >> 1, wn = wave & 1;
-    const int m0 = blockIdx.y * MF_BM, n0 = blockIdx.x * MF_BN;
-    const float *A = (const float *)g.a;
+    const int total = mt * nt, per = (total + MF_XCDS - 1) / MF_XCDS;
+    const int tile = (blockIdx.x % MF_XCDS) * per + blockIdx.x / MF_XCDS;
+    if (tile >= total) return;
+    const int m0 = (tile % mt) * MF_BM, n0 = (tile / mt) * MF_BN;
+    const uint16_t *Ah = (const uint16_t *)g.a, *Al = (const uint16_t *)g.a_lo;
     const uint16_t *Wm[2] = {(const uint16_t *)g.w, (const uint16_t *)g.w2};
     const int M = g.M, N = g.N, K = g.K;
 
@@ -61,26 +73,30 @@ __global__ void __launch_bounds__(256, 2) gemm_mfma_k(GemmArgs g, float *ws, int
 #pragma unroll
                 for (int e = 0; e < 16; ++e) acc[b][i][j][e] = 0.f;
 
-    f32x4v_t ra[4];
+    u32x4v_t ra[2][2];  // [hi/lo][chunk]
     u32x4v_t rb[NB][2];
     const int kbeg = blockIdx.z * k_per_split;
     const int kend = min(K, kbeg + k_per_split);
     auto load_tile = [&](int kt) {
         const int kb = kbeg + kt * MF_BK;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            int idx = tid + 256 * i;  // 0..1023 float4 of the 128 x 32 tile
-            int row = idx >> 3, k = kb + (idx & 7) * 4;
-            int gm = m0 + row;
-            if (gm < M && k + 3 < kend) {
-                ra[i] = *(const f32x4v_t *)(A + (size_t)gm * K + k);
-            } else {
-                f32x4v_t v;
+        for (int p = 0; p < 2; ++p)
 #pragma unroll
-                for (int q = 0; q < 4; ++q) v[q] = (gm < M && k + q < kend) ? A[(size_t)gm * K + k + q] : 0.f;
-                ra[i] = v;
+            for (int i = 0; i < 2; ++i) {
+                int idx = tid + 256 * i;  // 0..511 chunks of 8 bf16 (128 x 32 tile)
+                int row = idx >> 2, k = kb + (idx & 3) * 8;
+                int gm = m0 + row;
+                const uint16_t *src = p ? Al : Ah;
+                if (gm < M && k + 7 < kend) {
+                    ra[p][i] = *(const u32x4v_t *)(src + (size_t)gm * K + k);
+                } else {
+                    uint16_t e[8];
+#pragma unroll
+                    for (int q = 0; q < 8; ++q) e[q] = (gm < M && k + q < kend) ? src[(size_t)gm * K + k + q] : 0;
+                    ra[p][i] = u32x4v_t{pack2(e[0], e[1]), pack2(e[2], e[3]), pack2(e[4], e[5]),
+                                        pack2(e[6], e[7])};
+                }
             }
-        }
 #pragma unroll
         for (int b = 0; b < NB; ++b)
 #pragma unroll
@@ -104,19 +120,13 @@ __global__ void __launch_bounds__(256, 2) gemm_mfma_k(GemmArgs g, float *ws, int
         uint16_t *ah = sA;
         uint16_t *al = sA + MF_A_ELEMS;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            int idx = tid + 256 * i;
-            int row = idx >> 3, k = (idx & 7) * 4;
-            uint16_t h[4], l[4];
+        for (int p = 0; p < 2; ++p)
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                float v = ra[i][q];
-                h[q] = f2bf(v);
-                l[q] = f2bf(v - bf2f(h[q]));
+            for (int i = 0; i < 2; ++i) {
+                int idx = tid + 256 * i;
+                int row = idx >> 2, k = (idx & 3) * 8;
+                *(u32x4v_t *)((p ? al : ah) + row * MF_LD + k) = ra[p][i];
             }
-            *(u32x2v_t *)(ah + row * MF_LD + k) = u32x2v_t{pack2(h[0], h[1]), pack2(h[2], h[3])};
-            *(u32x2v_t *)(al + row * MF_LD + k) = u32x2v_t{pack2(l[0], l[1]), pack2(l[2], l[3])};
-        }
 #pragma unroll
         for (int b = 0; b < NB; ++b) {
             uint16_t *bb = sB + b * MF_B_ELEMS;
@@ -198,7 +208,15 @@ __global__ void __launch_bounds__(256, 2) gemm_mfma_k(GemmArgs g, float *ws, int
                 if (row >= M) continue;
                 float *c = (float *)g.c + (size_t)row * g.ldc + col;
                 if (EPI == GEMM_SWIGLU) {
-                    *c = silu(acc[0][i][j][e]) * acc[NB - 1][i][j][e];
+                    const float y = silu(acc[0][i][j][e]) * acc[NB - 1][i][j][e];
+                    if (g.c_lo) {
+                        const size_t ci = (size_t)row * g.ldc + col;
+                        uint16_t h = f2bf(y);
+                        ((uint16_t *)g.c)[ci] = h;
+                        ((uint16_t *)g.c_lo)[ci] = f2bf(y - bf2f(h));
+                    } else {
+                        *c = y;
+                    }
                 } else {
                     float v = g.bias ? acc[0][i][j][e] + bias : acc[0][i][j][e];
                     if (EPI == GEMM_RESIDUAL) *c = *c + v;
@@ -223,7 +241,15 @@ __global__ void __launch_bounds__(256) mfma_reduce_k(GemmArgs g, const float *ws
         }
         float *c = (float *)g.c + (size_t)row * g.ldc + col;
         if (EPI == GEMM_SWIGLU) {
-            *c = silu(v[0]) * v[NB - 1];
+            const float y = silu(v[0]) * v[NB - 1];
+            if (g.c_lo) {
+                const size_t ci = (size_t)row * g.ldc + col;
+                uint16_t h = f2bf(y);
+                ((uint16_t *)g.c)[ci] = h;
+                ((uint16_t *)g.c_lo)[ci] = f2bf(y - bf2f(h));
+            } else {
+                *c = y;
+            }
         } else {
             float y = g.bias ? v[0] + g.bias[col] : v[0];
             if (EPI == GEMM_RESIDUAL) *c = *c + y;
@@ -245,6 +271,7 @@ template <int EPI> static void mfma_launch(const GemmArgs &a, float *ws, size_t 
         if (g_cus <= 0) g_cus = 256;
     }
     const int gx = (a.N + MF_BN - 1) / MF_BN, gy = (a.M + MF_BM - 1) / MF_BM;
+    const int blocks = MF_XCDS * ((gx * gy + MF_XCDS - 1) / MF_XCDS);
     // split K until the grid covers the chip twice (k-splits stay >= 512)
     int splits = 1;
     while (gx * gy * splits < 2 * g_cus && a.K / (splits * 2) >= 512 &&
@@ -253,18 +280,19 @@ template <int EPI> static void mfma_launch(const GemmArgs &a, float *ws, size_t 
     int kps = (a.K + splits - 1) / splits;
     kps = (kps + MF_BK - 1) / MF_BK * MF_BK;
     if (splits == 1) {
-        gemm_mfma_k<EPI, NB><<<dim3(gx, gy, 1), 256, shm, s>>>(a, nullptr, a.K);
+        gemm_mfma_k<EPI, NB><<<dim3(blocks, 1, 1), 256, shm, s>>>(a, nullptr, a.K, gy, gx);
         return;
     }
-    gemm_mfma_k<MF_PARTIAL, NB><<<dim3(gx, gy, splits), 256, shm, s>>>(a, ws, kps);
+    gemm_mfma_k<MF_PARTIAL, NB><<<dim3(blocks, 1, splits), 256, shm, s>>>(a, ws, kps, gy, gx);
     size_t mn = (size_t)a.M * a.N;
-    int blocks = (int)std::min<size_t>((mn + 255) / 256, (size_t)g_cus * 8);
-    mfma_reduce_k<EPI, NB><<<blocks, 256, 0, s>>>(a, ws, splits);
+    const int rblocks = (int)std::min<size_t>((mn + 255) / 256, (size_t)g_cus * 8);
+    mfma_reduce_k<EPI, NB><<<rblocks, 256, 0, s>>>(a, ws, splits);
 }
 
 bool gemm_mfma_ok(Dt wt, const GemmArgs &a) {
-    return wt == DT_BF16 && a.K % 8 == 0 && a.K >= 32 && ((uintptr_t)a.a % 16) == 0 &&
-           ((uintptr_t)a.w % 16) == 0 && (!a.w2 || ((uintptr_t)a.w2 % 16) == 0);
+    return wt == DT_BF16 && a.a_lo && a.K % 8 == 0 && a.K >= 32 && ((uintptr_t)a.a % 16) == 0 &&
+           ((uintptr_t)a.a_lo % 16) == 0 && ((uintptr_t)a.w % 16) == 0 &&
+           (!a.w2 || ((uintptr_t)a.w2 % 16) == 0);
 }
 
 void launch_gemm_mfma(GemmEpi epi, const GemmArgs &a, float *ws, size_t ws_bytes, hipStream_t s) {

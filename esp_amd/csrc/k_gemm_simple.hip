@@ -31,7 +31,13 @@ __global__ void __launch_bounds__(256) gemm_simple_k(GemmArgs a) {
             int e = tid + i * 256;  // 0..1023
             int r = e / SG_BK, kk = e % SG_BK;
             int gm = m0 + r, gk = k0 + kk;
-            As[kk][r] = (gm < a.M && gk < a.K) ? ld(A, (size_t)gm * a.K + gk) : 0.f;
+            float av = 0.f;
+            if (gm < a.M && gk < a.K) {
+                size_t ai = (size_t)gm * a.K + gk;
+                av = a.a_lo ? bf2f(((const uint16_t *)a.a)[ai]) + bf2f(((const uint16_t *)a.a_lo)[ai])
+                            : ld(A, ai);
+            }
+            As[kk][r] = av;
 #pragma unroll
             for (int w = 0; w < NW; ++w) {
                 int gn = n0 + r;
@@ -66,7 +72,15 @@ __global__ void __launch_bounds__(256) gemm_simple_k(GemmArgs a) {
             int gn = n0 + tx * 4 + j;
             if (gn >= a.N) continue;
             if (EPI == GEMM_SWIGLU) {
-                st((AT *)a.c, (size_t)gm * a.ldc + gn, silu(acc[0][i][j]) * acc[NW - 1][i][j]);
+                float y = silu(acc[0][i][j]) * acc[NW - 1][i][j];
+                size_t ci = (size_t)gm * a.ldc + gn;
+                if (a.c_lo) {
+                    uint16_t h = f2bf(y);
+                    ((uint16_t *)a.c)[ci] = h;
+                    ((uint16_t *)a.c_lo)[ci] = f2bf(y - bf2f(h));
+                } else {
+                    st((AT *)a.c, ci, y);
+                }
             } else {
                 float v = a.bias ? acc[0][i][j] + a.bias[gn] : acc[0][i][j];
                 float *c = (float *)a.c + (size_t)gm * a.ldc + gn;

@@ -528,6 +528,11 @@ static Plan attn_plan(const Model &m, int rows, int max_t) {
 
 static int32_t *att_tickets(Kv &kv) { return kv.tickets.as<int32_t>(); }
 
+// lo plane of a split activation buffer holding rows x cols (nullptr for f32)
+static void *lo_plane(Dt act, const DevMem &b, int rows, int cols) {
+    return act == DT_SPLIT ? (void *)((uint16_t *)b.p + (size_t)rows * cols) : nullptr;
+}
+
 // One layer for a single token row with the decode kernels: fused
 // QKV+RoPE+KV-append (when the layer has no LoRA or QK norm), split-K
 // attention with in-kernel merge, and norm-fused projections.
@@ -717,7 +722,9 @@ static void run_layers(Model &m, Kv &kv, const Rows &rows, int Mc, int max_t, in
                        int p0 = 0) {
     hipStream_t s = kv.stream;
     const bool single = Mc == 1;
-    const Dt act = DT_F32;  // activations stay f32; weights carry the format
+    // activations keep f32 precision; bf16 models hand them to the matrix
+    // cores as split hi/lo bf16 planes, f32 models as plain f32
+    const Dt act = m.wt == DT_BF16 ? DT_SPLIT : DT_F32;
     const int H = m.H;
     Plan plan = attn_plan(m, Mc, max_t);
     if (single && attn_decode_ok(m.hd, m.nq / m.nkv)) {
@@ -754,6 +761,7 @@ static void run_layers(Model &m, Kv &kv, const Rows &rows, int Mc, int max_t, in
             g.ws = kv.gemm_ws.as<float>();
             g.ws_bytes = kv.gemm_ws.bytes;
             g.a = kv.xn.p;
+            g.a_lo = lo_plane(act, kv.xn, Mc, H);
             g.w = w.qkv;
             g.bias = w.qkv_bias;
             g.c = kv.qkv.p;
@@ -808,6 +816,7 @@ static void run_layers(Model &m, Kv &kv, const Rows &rows, int Mc, int max_t, in
             f.hd = m.hd;
             f.window = w.window;
             f.out = kv.attn.as<float>();
+            f.out_lo = (uint16_t *)lo_plane(act, kv.attn, Mc, m.qw);
             Prof p("attention", s);
             launch_flash(f, s);
         } else {
@@ -846,6 +855,7 @@ static void run_layers(Model &m, Kv &kv, const Rows &rows, int Mc, int max_t, in
             g.ws = kv.gemm_ws.as<float>();
             g.ws_bytes = kv.gemm_ws.bytes;
             g.a = kv.attn.p;
+            g.a_lo = lo_plane(act, kv.attn, Mc, m.qw);
             g.w = w.o;
             g.bias = w.o_bias;
             g.c = kv.h.p;
@@ -891,9 +901,11 @@ static void run_layers(Model &m, Kv &kv, const Rows &rows, int Mc, int max_t, in
             g.ws = kv.gemm_ws.as<float>();
             g.ws_bytes = kv.gemm_ws.bytes;
             g.a = kv.xn.p;
+            g.a_lo = lo_plane(act, kv.xn, Mc, H);
             g.w = w.gate;
             g.w2 = w.up;
             g.c = kv.act.p;
+            g.c_lo = lo_plane(act, kv.act, Mc, m.F);
             g.M = Mc;
             g.N = m.F;
             g.K = H;
@@ -906,6 +918,7 @@ static void run_layers(Model &m, Kv &kv, const Rows &rows, int Mc, int max_t, in
             d.ws = kv.gemm_ws.as<float>();
             d.ws_bytes = kv.gemm_ws.bytes;
             d.a = kv.act.p;
+            d.a_lo = lo_plane(act, kv.act, Mc, m.F);
             d.w = w.down;
             d.c = kv.h.p;
             d.M = Mc;
@@ -975,13 +988,14 @@ static void run_head(Model &m, Kv &kv, int n_seqs, const float *h_src, const int
     }
     {
         Prof p("rmsnorm", s);
-        launch_rmsnorm(h_src, m.final_norm, m.cfg.rms_norm_eps, n_seqs, m.H, DT_F32, kv.xn.p,
-                       row_index, s);
+        launch_rmsnorm(h_src, m.final_norm, m.cfg.rms_norm_eps, n_seqs, m.H,
+                       m.wt == DT_BF16 ? DT_SPLIT : DT_F32, kv.xn.p, row_index, s);
     }
     GemmArgs g{};
     g.ws = kv.gemm_ws.as<float>();
     g.ws_bytes = kv.gemm_ws.bytes;
     g.a = kv.xn.p;
+    g.a_lo = lo_plane(m.wt == DT_BF16 ? DT_SPLIT : DT_F32, kv.xn, n_seqs, m.H);
     g.w = m.head;
     g.c = kv.logits.p;
     g.M = n_seqs;
@@ -1103,28 +1117,30 @@ void decode_step_dev(Model &m, Kv &kv, int seq, int max_t, int32_t *gen) {
 }
 
 // moe.rs:135-256 DecoderMlp::forward (Moe arm) for Mc rows: h += routed
-// experts (+ sigmoid-gated shared expert) of RMSNorm(h).
+// experts (+ sigmoid-gated shared expert) of RMSNorm(h). Routing and the
+// combine run on the device; the per-expert row counts come back to the host
+// to size the per-expert GEMMs.
 void moe_block(Model &m, Kv &kv, LayerW &w, int Mc, hipStream_t s) {
-    const Dt act = DT_F32;
-    const int H = m.H, E = m.E, k = m.topk;
+    const Dt act = m.wt == DT_BF16 ? DT_SPLIT : DT_F32;
+    const bool split = act == DT_SPLIT;
+    const int H = m.H, E = m.E, k = m.topk, R = Mc * k;
     {
         Prof p("rmsnorm", s);
         launch_rmsnorm(kv.h.as<float>(), w.post_norm, m.cfg.rms_norm_eps, Mc, H, act, kv.xn.p,
                        nullptr, s);
     }
     kv.moe_logits.ensure((size_t)Mc * E * 4);
-    kv.moe_sel.ensure((size_t)Mc * k * 4);
-    kv.moe_w.ensure((size_t)Mc * k * 4);
-    kv.moe_slot.ensure((size_t)Mc * k * 4);
+    kv.moe_sel.ensure((size_t)R * 4);
+    kv.moe_w.ensure((size_t)R * 4);
+    kv.moe_slot.ensure((size_t)R * 4);
     kv.moe_offs.ensure((size_t)(E + 2) * 4);
-    kv.moe_perm.ensure((size_t)Mc * k * 4);
-    kv.moe_x.ensure((size_t)Mc * k * H * 4);
-    kv.moe_act.ensure((size_t)Mc * k * m.Fe * 4);
-    kv.moe_y.ensure((size_t)Mc * k * H * 4);
+    kv.moe_perm.ensure((size_t)R * 4);
+    kv.moe_x.ensure((size_t)R * H * 4);
+    kv.moe_act.ensure((size_t)R * m.Fe * 4);
+    kv.moe_y.ensure((size_t)R * H * 4);
     GemmArgs r{};
-    r.ws = kv.gemm_ws.as<float>();
-    r.ws_bytes = kv.gemm_ws.bytes;
     r.a = kv.xn.p;
+    r.a_lo = lo_plane(act, kv.xn, Mc, H);
     r.w = w.router;
     r.c = kv.moe_logits.p;
     r.M = Mc;
@@ -1147,21 +1163,34 @@ void moe_block(Model &m, Kv &kv, LayerW &w, int Mc, hipStream_t s) {
     ESP_HIP(hipStreamSynchronize(s));
     if (offs[E + 1] == 2) fail(ESP_BACKEND, "non-finite expert router");
     if (offs[E + 1] == 3) fail(ESP_BACKEND, "invalid top-k routing mass");
-    const size_t es = dt_size(act);
     {
         Prof p("moe", s);
-        launch_gather_rows(act, kv.xn.p, kv.moe_perm.as<int32_t>(), Mc * k, H, kv.moe_x.p, s);
+        if (split) {
+            const uint16_t *xs = kv.xn.as<uint16_t>();
+            uint16_t *xd = kv.moe_x.as<uint16_t>();
+            launch_gather_rows(DT_BF16, xs, kv.moe_perm.as<int32_t>(), R, H, xd, s);
+            launch_gather_rows(DT_BF16, xs + (size_t)Mc * H, kv.moe_perm.as<int32_t>(), R, H,
+                               xd + (size_t)R * H, s);
+        } else {
+            launch_gather_rows(DT_F32, kv.xn.p, kv.moe_perm.as<int32_t>(), R, H, kv.moe_x.p, s);
+        }
     }
+    const size_t es = split ? 2 : 4;             // bytes per element of one plane
+    const size_t wes = dt_size(m.wt);
+    char *xh = (char *)kv.moe_x.p, *xl = split ? xh + (size_t)R * H * 2 : nullptr;
+    char *ah = (char *)kv.moe_act.p, *al = split ? ah + (size_t)R * m.Fe * 2 : nullptr;
     for (int e = 0; e < E; ++e) {
         int n = offs[e + 1] - offs[e];
         if (!n) continue;
         GemmArgs g{};
         g.ws = kv.gemm_ws.as<float>();
         g.ws_bytes = kv.gemm_ws.bytes;
-        g.a = (char *)kv.moe_x.p + (size_t)offs[e] * H * es;
-        g.w = (char *)w.ex_gate + (size_t)e * m.Fe * H * dt_size(m.wt);
-        g.w2 = (char *)w.ex_up + (size_t)e * m.Fe * H * dt_size(m.wt);
-        g.c = (char *)kv.moe_act.p + (size_t)offs[e] * m.Fe * es;
+        g.a = xh + (size_t)offs[e] * H * es;
+        g.a_lo = split ? xl + (size_t)offs[e] * H * es : nullptr;
+        g.w = (char *)w.ex_gate + (size_t)e * m.Fe * H * wes;
+        g.w2 = (char *)w.ex_up + (size_t)e * m.Fe * H * wes;
+        g.c = ah + (size_t)offs[e] * m.Fe * es;
+        g.c_lo = split ? al + (size_t)offs[e] * m.Fe * es : nullptr;
         g.M = n;
         g.N = m.Fe;
         g.K = H;
@@ -1174,7 +1203,8 @@ void moe_block(Model &m, Kv &kv, LayerW &w, int Mc, hipStream_t s) {
         d.ws = kv.gemm_ws.as<float>();
         d.ws_bytes = kv.gemm_ws.bytes;
         d.a = g.c;
-        d.w = (char *)w.ex_down + (size_t)e * H * m.Fe * dt_size(m.wt);
+        d.a_lo = g.c_lo;
+        d.w = (char *)w.ex_down + (size_t)e * H * m.Fe * wes;
         d.c = kv.moe_y.as<float>() + (size_t)offs[e] * H;
         d.M = n;
         d.N = H;
@@ -1198,9 +1228,11 @@ void moe_block(Model &m, Kv &kv, LayerW &w, int Mc, hipStream_t s) {
         g.ws = kv.gemm_ws.as<float>();
         g.ws_bytes = kv.gemm_ws.bytes;
         g.a = kv.xn.p;
+        g.a_lo = lo_plane(act, kv.xn, Mc, H);
         g.w = w.sh_gate;
         g.w2 = w.sh_up;
         g.c = kv.act.p;
+        g.c_lo = lo_plane(act, kv.act, Mc, m.Fs);
         g.M = Mc;
         g.N = m.Fs;
         g.K = H;
@@ -1209,6 +1241,7 @@ void moe_block(Model &m, Kv &kv, LayerW &w, int Mc, hipStream_t s) {
         d.ws = kv.gemm_ws.as<float>();
         d.ws_bytes = kv.gemm_ws.bytes;
         d.a = kv.act.p;
+        d.a_lo = g.c_lo;
         d.w = w.sh_down;
         d.c = kv.moe_ys.p;
         d.M = Mc;
@@ -1219,6 +1252,7 @@ void moe_block(Model &m, Kv &kv, LayerW &w, int Mc, hipStream_t s) {
         sg.ws = kv.gemm_ws.as<float>();
         sg.ws_bytes = kv.gemm_ws.bytes;
         sg.a = kv.xn.p;
+        sg.a_lo = g.a_lo;
         sg.w = w.shared_gate;
         sg.c = kv.moe_sg.p;
         sg.M = Mc;
