@@ -58,99 +58,143 @@ void launch_rmsnorm(const float *x, const float *gamma, float eps, int M, int H,
 // attention.rs:306-326: q/k/v projections (+bias, + unmerged LoRA as in
 // lora.rs:93-97), optional QK RMSNorm over head_dim (:312-319), split-half
 // RoPE at the row's absolute position (:99-123), then K/V appended to the
-// cache (:126-148). One block per (token row, group of heads).
+// cache (:126-148). A block owns a group of heads (one thread per head
+// element) and up to ROPE_ROWS consecutive token rows: every row's loads
+// are issued before any is used, each thread's LoRA-B row (first ROPE_BREG
+// ranks) is loaded once into registers, and the rows' LoRA t values are
+// staged in LDS.
+constexpr int ROPE_BREG = 32, ROPE_ROWS = 16;
+
 template <typename WT, typename KT>
-__global__ void __launch_bounds__(256) rope_kv_k(RopeKvArgs a) {
-    extern __shared__ float sh[];  // [heads_per_iter][hd]
-    const int m = blockIdx.x;
+__global__ void __launch_bounds__(256) rope_kv_k(RopeKvArgs a, int rows_per_block, int t_lo, int t_n) {
+    extern __shared__ float sh[];  // [rows][heads_per_block * hd] values, then [rows][t_n] LoRA t
     const int hd = a.hd, half = hd / 2;
-    const int pos = a.rows.row_pos[m];
-    const int seq = a.rows.row_seq[m];
-    const float *row = a.qkv + (size_t)m * a.ldq;
-    const float *cs = a.rope_cos + (size_t)pos * hd;
-    const float *sn = a.rope_sin + (size_t)pos * hd;
-    const int hpi = blockDim.x / hd > 0 ? blockDim.x / hd : 1;
+    const int hpi = blockDim.x / hd, bw = hpi * hd;
+    float *tsh = sh + (size_t)rows_per_block * bw;
     const int total = a.nq + 2 * a.nkv;
     const int qw = a.nq * hd, kvw = a.nkv * hd;
     KT *cache = (KT *)a.kv;
-    {
-        const int base = blockIdx.y * hpi;  // one head group per block
-        const int lh = threadIdx.x / hd;
-        const int head = base + lh;
-        const bool active = lh < hpi && head < total;
-        float x = 0.f;
-        int target = 0, col = 0, d = threadIdx.x % hd;
-        if (active) {
-            if (head < a.nq) {
-                target = 0;
-                col = head * hd + d;
-            } else if (head < a.nq + a.nkv) {
-                target = 1;
-                col = qw + (head - a.nq) * hd + d;
-            } else {
-                target = 2;
-                col = qw + kvw + (head - a.nq - a.nkv) * hd + d;
-            }
-            x = row[col];
-            if (a.lora_b[target]) {
-                const WT *B = (const WT *)a.lora_b[target];
-                int r = a.lora_rank[target];
-                int o = col - (target == 0 ? 0 : (target == 1 ? qw : qw + kvw));
-                const float *t = row + a.lora_t_col[target];
-                float acc = 0.f;
-                for (int i = 0; i < r; ++i) acc += ld(B, (size_t)o * r + i) * t[i];
-                x = x + acc * a.lora_scale[target];
-            }
-            sh[lh * hd + d] = x;
+    const int lh = threadIdx.x / hd, head = blockIdx.y * hpi + lh, d = threadIdx.x % hd;
+    const bool active = lh < hpi && head < total;
+    int target = 0, col = 0, off = 0;
+    if (active) {
+        target = head < a.nq ? 0 : (head < a.nq + a.nkv ? 1 : 2);
+        off = target == 0 ? 0 : (target == 1 ? qw : qw + kvw);
+        col = off + (head - (target == 0 ? 0 : (target == 1 ? a.nq : a.nq + a.nkv))) * hd + d;
+    }
+    const int m0 = blockIdx.x * rows_per_block;
+    const int nr = min(a.rows.M - m0, rows_per_block);
+
+    // issue every load of the block's rows
+    for (int i = threadIdx.x; i < nr * t_n; i += blockDim.x)
+        tsh[i] = a.qkv[(size_t)(m0 + i / t_n) * a.ldq + t_lo + i % t_n];
+    float x[ROPE_ROWS];
+#pragma unroll
+    for (int r = 0; r < ROPE_ROWS; ++r)
+        x[r] = active && r < nr ? a.qkv[(size_t)(m0 + r) * a.ldq + col] : 0.f;
+    const WT *B = active ? (const WT *)a.lora_b[target] : nullptr;
+    const int rank = B ? a.lora_rank[target] : 0;
+    float breg[ROPE_BREG];
+#pragma unroll
+    for (int i = 0; i < ROPE_BREG; ++i) breg[i] = i < rank ? ld(B, (size_t)(col - off) * rank + i) : 0.f;
+    __syncthreads();
+
+    // LoRA: x += scale * B t
+    if (rank) {
+        const int tcol = a.lora_t_col[target] - t_lo;
+        const float sc = a.lora_scale[target];
+#pragma unroll
+        for (int r = 0; r < ROPE_ROWS; ++r) {
+            if (r >= nr) break;
+            const float *t = tsh + r * t_n + tcol;
+            float acc = 0.f;
+#pragma unroll
+            for (int i = 0; i < ROPE_BREG; ++i)
+                if (i < rank) acc += breg[i] * t[i];
+            for (int i = ROPE_BREG; i < rank; ++i) acc += ld(B, (size_t)(col - off) * rank + i) * t[i];
+            x[r] = x[r] + acc * sc;
         }
+    }
+    if (active) {
+#pragma unroll
+        for (int r = 0; r < ROPE_ROWS; ++r)
+            if (r < nr) sh[r * bw + lh * hd + d] = x[r];
+    }
+    // QK RMSNorm over each head's hd values
+    const float *g = active && target < 2 ? (target == 0 ? a.q_norm : a.k_norm) : nullptr;
+    if (a.q_norm || a.k_norm) {
         __syncthreads();
-        if (active && target < 2) {
-            const float *g = target == 0 ? a.q_norm : a.k_norm;
-            if (g) {
+        if (g) {
+#pragma unroll
+            for (int r = 0; r < ROPE_ROWS; ++r) {
+                if (r >= nr) break;
+                const float *v = sh + r * bw + lh * hd;
                 float ss = 0.f;
-                for (int i = 0; i < hd; ++i) ss += sh[lh * hd + i] * sh[lh * hd + i];
-                float rms = sqrtf(ss / (float)hd + a.eps);
-                x = (x / rms) * g[d];
+                for (int i = 0; i < hd; ++i) ss += v[i] * v[i];
+                const float rms = sqrtf(ss / (float)hd + a.eps);
+                x[r] = (x[r] / rms) * g[d];
             }
         }
         __syncthreads();
-        if (active && target < 2) sh[lh * hd + d] = x;
-        __syncthreads();
-        if (active) {
-            if (target < 2) {
-                float rot = d < half ? -sh[lh * hd + d + half] : sh[lh * hd + d - half];
-                float y = x * cs[d] + rot * sn[d];
-                if (target == 0) {
-                    a.q_out[(size_t)m * qw + head * hd + d] = y;
-                } else {
-                    int kh = head - a.nq;
-                    size_t off = (size_t)seq * a.seq_stride + (size_t)kh * a.head_stride +
-                                 (size_t)pos * hd + d;
-                    st(cache, off, y);
-                }
+        if (g) {
+#pragma unroll
+            for (int r = 0; r < ROPE_ROWS; ++r)
+                if (r < nr) sh[r * bw + lh * hd + d] = x[r];
+        }
+    }
+    __syncthreads();
+    if (!active) return;
+#pragma unroll
+    for (int r = 0; r < ROPE_ROWS; ++r) {
+        if (r >= nr) break;
+        const int m = m0 + r;
+        const int pos = a.rows.row_pos[m];
+        const int seq = a.rows.row_seq[m];
+        if (target < 2) {
+            const float *v = sh + r * bw + lh * hd;
+            const float rot = d < half ? -v[d + half] : v[d - half];
+            const float y = x[r] * a.rope_cos[(size_t)pos * hd + d] + rot * a.rope_sin[(size_t)pos * hd + d];
+            if (target == 0) {
+                a.q_out[(size_t)m * qw + head * hd + d] = y;
             } else {
-                int vh = head - a.nq - a.nkv;
-                size_t off = (size_t)seq * a.seq_stride + a.kv_half_stride +
-                             (size_t)vh * a.head_stride + (size_t)pos * hd + d;
-                st(cache, off, x);
+                const int kh = head - a.nq;
+                st(cache, (size_t)seq * a.seq_stride + (size_t)kh * a.head_stride + (size_t)pos * hd + d, y);
             }
+        } else {
+            const int vh = head - a.nq - a.nkv;
+            st(cache, (size_t)seq * a.seq_stride + a.kv_half_stride + (size_t)vh * a.head_stride +
+                          (size_t)pos * hd + d, x[r]);
         }
     }
 }
 
 void launch_rope_kv(Dt wt, Dt kvdt, const RopeKvArgs &a, hipStream_t s) {
-    int hpi = 256 / a.hd > 0 ? 256 / a.hd : 1;
-    int threads = a.hd > 256 ? 0 : 256;
-    if (!threads) fail(ESP_UNSUPPORTED, "head_dim: values above 256 are not implemented");
-    size_t shm = sizeof(float) * hpi * a.hd;
-    const int groups = (a.nq + 2 * a.nkv + hpi - 1) / hpi;
-    dim3 grid(a.rows.M, groups);
+    if (a.hd > 256) fail(ESP_UNSUPPORTED, "head_dim: values above 256 are not implemented");
+    const int hpi = 256 / a.hd;
+    // contiguous span of LoRA t columns read by this layer
+    int t_lo = 0, t_hi = 0;
+    bool any = false;
+    for (int j = 0; j < 3; ++j) {
+        if (!a.lora_b[j] || !a.lora_rank[j]) continue;
+        const int c0 = a.lora_t_col[j], c1 = c0 + a.lora_rank[j];
+        t_lo = any ? std::min(t_lo, c0) : c0;
+        t_hi = any ? std::max(t_hi, c1) : c1;
+        any = true;
+    }
+    const int t_n = t_hi - t_lo;
+    const size_t per_row = sizeof(float) * ((size_t)hpi * a.hd + t_n);
+    const size_t lds_cap = 64 * 1024;
+    if (per_row > lds_cap) fail(ESP_UNSUPPORTED, "lora: total adapter rank too large for one layer");
+    int rpb = a.rows.M >= 1024 ? ROPE_ROWS : (a.rows.M >= 128 ? 4 : 1);
+    while (rpb > 1 && rpb * per_row > lds_cap) rpb /= 2;
+    const size_t shm = rpb * per_row;
+    dim3 grid((a.rows.M + rpb - 1) / rpb, (a.nq + 2 * a.nkv + hpi - 1) / hpi);
     if (wt == DT_BF16 && kvdt == DT_BF16)
-        rope_kv_k<uint16_t, uint16_t><<<grid, threads, shm, s>>>(a);
+        rope_kv_k<uint16_t, uint16_t><<<grid, 256, shm, s>>>(a, rpb, t_lo, t_n);
     else if (wt == DT_BF16 && kvdt == DT_F32)
-        rope_kv_k<uint16_t, float><<<grid, threads, shm, s>>>(a);
+        rope_kv_k<uint16_t, float><<<grid, 256, shm, s>>>(a, rpb, t_lo, t_n);
     else if (wt == DT_F32 && kvdt == DT_F32)
-        rope_kv_k<float, float><<<grid, threads, shm, s>>>(a);
+        rope_kv_k<float, float><<<grid, 256, shm, s>>>(a, rpb, t_lo, t_n);
     else
         fail(ESP_BACKEND, "rope_kv: unsupported dtype pair");
 }
