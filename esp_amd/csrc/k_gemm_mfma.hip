@@ -6,11 +6,15 @@
 // weight fragment with v_mfma_f32_32x32x16_bf16, accumulating in f32. Every
 // product is exact, so the result keeps f32-level accuracy on bf16 MFMA.
 //
-// Block tile 128 x 128 x 32, four waves in a 2 x 2 arrangement, each wave a
-// 64 x 64 output tile of 2 x 2 MFMA blocks. A and W tiles are staged through
-// LDS (rows padded to 80 bytes) from register prefetches issued one k-tile
-// ahead. Epilogues: STORE (+bias), RESIDUAL (+=), SWIGLU
-// (gate and up tiles share the A fragments; out = silu(g) * u).
+// Block tile 128 x (NB x BN) x 32, four waves in a 2 x 2 arrangement; each
+// wave owns 64 rows x NB*BN/2 weight columns. The wide form has 128 columns
+// per wave (2 x 4 MFMA blocks of 32 x 32): BN = 256 for one weight matrix,
+// or BN = 128 each for the gate and up matrices of SWIGLU, whose tiles share
+// the A fragments; it keeps LDS reads at 512 bytes per MFMA (A costs 4 bytes
+// per element as two planes). Grids too small to fill the chip with it use
+// the narrow form (half the columns per block). A and W tiles are staged through LDS (rows padded to
+// 80 bytes) from register prefetches issued one k-tile ahead. Epilogues:
+// STORE (+bias), RESIDUAL (+=), SWIGLU (out = silu(g) * u).
 #include "common.hpp"
 #include "dev.hpp"
 #include "kernels_extra.hpp"
@@ -23,12 +27,13 @@ typedef float f32x4v_t __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x4v_t __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x2v_t __attribute__((ext_vector_type(2)));
 
-constexpr int MF_BM = 128, MF_BN = 128, MF_BK = 32, MF_LD = MF_BK + 8;
+constexpr int MF_BM = 128, MF_BK = 32, MF_LD = MF_BK + 8;
 constexpr int MF_A_ELEMS = MF_BM * MF_LD;  // one A plane (bf16) per buffer
-constexpr int MF_B_ELEMS = MF_BN * MF_LD;
+// NJ = 32-column MFMA blocks per wave and weight matrix; BN = 64 * NJ
+template <int NJ> constexpr int mf_b_elems() { return 64 * NJ * MF_LD; }
 
-template <int NB> constexpr size_t mfma_lds_bytes() {
-    return (size_t)(2 * MF_A_ELEMS + NB * MF_B_ELEMS) * 2;
+template <int NB, int NJ> constexpr size_t mfma_lds_bytes() {
+    return (size_t)(2 * MF_A_ELEMS + NB * mf_b_elems<NJ>()) * 2;
 }
 
 // Split-K: blockIdx.z = k-split; each split writes raw f32 sums for its K
@@ -47,9 +52,10 @@ __device__ __forceinline__ uint32_t pack2(uint16_t lo, uint16_t hi) {
 // that XCD runs, instead of being pulled into all eight L2s.
 constexpr int MF_XCDS = 8;
 
-template <int EPI, int NB>
+template <int EPI, int NB, int NJ>
 __global__ void __launch_bounds__(256, 2) gemm_mfma_k(GemmArgs g, float *ws, int k_per_split,
                                                      int mt, int nt) {
+    constexpr int BN = 64 * NJ, B_ELEMS = mf_b_elems<NJ>();
     extern __shared__ uint16_t lds[];
     uint16_t *sA = lds;                          // [hi/lo][BM*LD]
     uint16_t *sB = lds + 2 * MF_A_ELEMS;         // [nb][BN*LD]
@@ -58,23 +64,23 @@ __global__ void __launch_bounds__(256, 2) gemm_mfma_k(GemmArgs g, float *ws, int
     const int total = mt * nt, per = (total + MF_XCDS - 1) / MF_XCDS;
     const int tile = (blockIdx.x % MF_XCDS) * per + blockIdx.x / MF_XCDS;
     if (tile >= total) return;
-    const int m0 = (tile % mt) * MF_BM, n0 = (tile / mt) * MF_BN;
+    const int m0 = (tile % mt) * MF_BM, n0 = (tile / mt) * BN;
     const uint16_t *Ah = (const uint16_t *)g.a, *Al = (const uint16_t *)g.a_lo;
     const uint16_t *Wm[2] = {(const uint16_t *)g.w, (const uint16_t *)g.w2};
     const int M = g.M, N = g.N, K = g.K;
 
-    f32x16_t acc[NB][2][2];
+    f32x16_t acc[NB][2][NJ];
 #pragma unroll
     for (int b = 0; b < NB; ++b)
 #pragma unroll
         for (int i = 0; i < 2; ++i)
 #pragma unroll
-            for (int j = 0; j < 2; ++j)
+            for (int j = 0; j < NJ; ++j)
 #pragma unroll
                 for (int e = 0; e < 16; ++e) acc[b][i][j][e] = 0.f;
 
     u32x4v_t ra[2][2];  // [hi/lo][chunk]
-    u32x4v_t rb[NB][2];
+    u32x4v_t rb[NB][NJ];
     const int kbeg = blockIdx.z * k_per_split;
     const int kend = min(K, kbeg + k_per_split);
     auto load_tile = [&](int kt) {
@@ -100,8 +106,8 @@ __global__ void __launch_bounds__(256, 2) gemm_mfma_k(GemmArgs g, float *ws, int
 #pragma unroll
         for (int b = 0; b < NB; ++b)
 #pragma unroll
-            for (int i = 0; i < 2; ++i) {
-                int idx = tid + 256 * i;  // 0..511 chunks of 8 bf16
+            for (int i = 0; i < NJ; ++i) {
+                int idx = tid + 256 * i;  // chunks of 8 bf16 (BN x 32 tile)
                 int row = idx >> 2, k = kb + (idx & 3) * 8;
                 int gn = n0 + row;
                 if (gn < N && k + 7 < kend) {
@@ -129,9 +135,9 @@ __global__ void __launch_bounds__(256, 2) gemm_mfma_k(GemmArgs g, float *ws, int
             }
 #pragma unroll
         for (int b = 0; b < NB; ++b) {
-            uint16_t *bb = sB + b * MF_B_ELEMS;
+            uint16_t *bb = sB + b * B_ELEMS;
 #pragma unroll
-            for (int i = 0; i < 2; ++i) {
+            for (int i = 0; i < NJ; ++i) {
                 int idx = tid + 256 * i;
                 int row = idx >> 2, k = (idx & 3) * 8;
                 *(u32x4v_t *)(bb + row * MF_LD + k) = rb[b][i];
@@ -144,7 +150,7 @@ __global__ void __launch_bounds__(256, 2) gemm_mfma_k(GemmArgs g, float *ws, int
 #pragma unroll
         for (int ks = 0; ks < MF_BK / 16; ++ks) {
             const int koff = ks * 16 + (lane >> 5) * 8;
-            bf16x8_t fh[2], fl[2], fb[NB][2];
+            bf16x8_t fh[2], fl[2], fb[NB][NJ];
 #pragma unroll
             for (int i = 0; i < 2; ++i) {
                 int r = wm * 64 + i * 32 + (lane & 31);
@@ -154,16 +160,16 @@ __global__ void __launch_bounds__(256, 2) gemm_mfma_k(GemmArgs g, float *ws, int
 #pragma unroll
             for (int b = 0; b < NB; ++b)
 #pragma unroll
-                for (int j = 0; j < 2; ++j) {
-                    int r = wn * 64 + j * 32 + (lane & 31);
-                    fb[b][j] = *(const bf16x8_t *)(sB + b * MF_B_ELEMS + r * MF_LD + koff);
+                for (int j = 0; j < NJ; ++j) {
+                    int r = wn * (BN / 2) + j * 32 + (lane & 31);
+                    fb[b][j] = *(const bf16x8_t *)(sB + b * B_ELEMS + r * MF_LD + koff);
                 }
 #pragma unroll
             for (int b = 0; b < NB; ++b)
 #pragma unroll
                 for (int i = 0; i < 2; ++i)
 #pragma unroll
-                    for (int j = 0; j < 2; ++j) {
+                    for (int j = 0; j < NJ; ++j) {
                         acc[b][i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fh[i], fb[b][j], acc[b][i][j], 0, 0, 0);
                         acc[b][i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fl[i], fb[b][j], acc[b][i][j], 0, 0, 0);
                     }
@@ -187,8 +193,8 @@ __global__ void __launch_bounds__(256, 2) gemm_mfma_k(GemmArgs g, float *ws, int
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const int col = n0 + wn * 64 + j * 32 + (lane & 31);
+        for (int j = 0; j < NJ; ++j) {
+            const int col = n0 + wn * (BN / 2) + j * 32 + (lane & 31);
             if (col >= N) continue;
             if (EPI == MF_PARTIAL) {
 #pragma unroll
@@ -260,17 +266,11 @@ __global__ void __launch_bounds__(256) mfma_reduce_k(GemmArgs g, const float *ws
 
 static int g_cus = 0;
 
-template <int EPI> static void mfma_launch(const GemmArgs &a, float *ws, size_t ws_bytes,
-                                           hipStream_t s) {
-    constexpr int NB = EPI == GEMM_SWIGLU ? 2 : 1;
-    constexpr size_t shm = mfma_lds_bytes<NB>();
-    if (!g_cus) {
-        int dev = 0;
-        ESP_HIP(hipGetDevice(&dev));
-        ESP_HIP(hipDeviceGetAttribute(&g_cus, hipDeviceAttributeMultiprocessorCount, dev));
-        if (g_cus <= 0) g_cus = 256;
-    }
-    const int gx = (a.N + MF_BN - 1) / MF_BN, gy = (a.M + MF_BM - 1) / MF_BM;
+template <int EPI, int NB, int NJ>
+static void mfma_launch_nj(const GemmArgs &a, float *ws, size_t ws_bytes, hipStream_t s) {
+    constexpr size_t shm = mfma_lds_bytes<NB, NJ>();
+    constexpr int BN = 64 * NJ;
+    const int gx = (a.N + BN - 1) / BN, gy = (a.M + MF_BM - 1) / MF_BM;
     const int blocks = MF_XCDS * ((gx * gy + MF_XCDS - 1) / MF_XCDS);
     // split K until the grid covers the chip twice (k-splits stay >= 512)
     int splits = 1;
@@ -280,13 +280,28 @@ template <int EPI> static void mfma_launch(const GemmArgs &a, float *ws, size_t 
     int kps = (a.K + splits - 1) / splits;
     kps = (kps + MF_BK - 1) / MF_BK * MF_BK;
     if (splits == 1) {
-        gemm_mfma_k<EPI, NB><<<dim3(blocks, 1, 1), 256, shm, s>>>(a, nullptr, a.K, gy, gx);
+        gemm_mfma_k<EPI, NB, NJ><<<dim3(blocks, 1, 1), 256, shm, s>>>(a, nullptr, a.K, gy, gx);
         return;
     }
-    gemm_mfma_k<MF_PARTIAL, NB><<<dim3(blocks, 1, splits), 256, shm, s>>>(a, ws, kps, gy, gx);
+    gemm_mfma_k<MF_PARTIAL, NB, NJ><<<dim3(blocks, 1, splits), 256, shm, s>>>(a, ws, kps, gy, gx);
     size_t mn = (size_t)a.M * a.N;
     const int rblocks = (int)std::min<size_t>((mn + 255) / 256, (size_t)g_cus * 8);
     mfma_reduce_k<EPI, NB><<<rblocks, 256, 0, s>>>(a, ws, splits);
+}
+
+template <int EPI> static void mfma_launch(const GemmArgs &a, float *ws, size_t ws_bytes,
+                                           hipStream_t s) {
+    constexpr int NB = EPI == GEMM_SWIGLU ? 2 : 1;
+    constexpr int NJW = 4 / NB;  // wide form: 128 weight columns per wave
+    if (!g_cus) {
+        int dev = 0;
+        ESP_HIP(hipGetDevice(&dev));
+        ESP_HIP(hipDeviceGetAttribute(&g_cus, hipDeviceAttributeMultiprocessorCount, dev));
+        if (g_cus <= 0) g_cus = 256;
+    }
+    const long long wide_tiles = (long long)((a.N + 64 * NJW - 1) / (64 * NJW)) * ((a.M + MF_BM - 1) / MF_BM);
+    if (wide_tiles >= g_cus) mfma_launch_nj<EPI, NB, NJW>(a, ws, ws_bytes, s);
+    else mfma_launch_nj<EPI, NB, NJW / 2>(a, ws, ws_bytes, s);
 }
 
 bool gemm_mfma_ok(Dt wt, const GemmArgs &a) {
