@@ -41,13 +41,15 @@ struct AttnDecodeArgs {
     const int32_t *row_pos, *row_seq;
     int M, nq, nkv, hd, window;
     int n_split, split_len;
-    float *part;          // [M, nq, n_split, hd + 2]
+    float *part;          // [M, nq, n_split, hd + 4]
     int32_t *ticket;      // [M, nkv] zero-initialised
     float *out;           // [M, nq*hd]
 };
 
 bool attn_decode_ok(int hd, int G);
-int attn_decode_splits(int hd, int max_t);
+// key splits and keys per split for a decode row over max_t cached keys
+int attn_decode_splits(int hd, int max_t, int *split_len);
+constexpr int ATT_PART_PAD = 4;  // partial row = hd + ATT_PART_PAD floats
 void launch_attn_decode(const AttnDecodeArgs &a, hipStream_t s);
 
 }  // namespace esp

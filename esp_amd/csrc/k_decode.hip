@@ -376,14 +376,35 @@ void launch_decode_gemv(Dt wt, int epi, const DecodeGemvArgs &a, hipStream_t s) 
 // ------------------------------------------------------------ attention
 
 constexpr int ATT_MAX_SPLIT = 128;
+constexpr int ATT_CHUNK = 64;  // keys whose K/V loads a block issues at once
+constexpr int ATT_PSTRIDE_PAD = ATT_PART_PAD;  // partial row: m, l, 2 pad, acc[hd]
 
-// One block per (key split, kv head, row). Each 16-lane group (hd 64) or
-// 32-lane group (hd 128) owns one key at a time; lanes cover 4 dims each.
-template <int HD>
+// Sum over aligned groups of N lanes (N = 8 or 16) with DPP lane swaps:
+// quad xor 1, quad xor 2, half-row mirror (8 lanes), row mirror (16 lanes).
+template <int N> __device__ __forceinline__ float group_sum(float v) {
+    static_assert(N == 8 || N == 16, "group_sum: 8 or 16 lanes");
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x141, 0xF, 0xF, false));
+    if (N == 16)
+        v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x140, 0xF, 0xF, false));
+    return v;
+}
+
+// One block per (key split, kv head, row). A key is covered by a group of
+// hd/8 lanes (8 dims each), so a wave scores 64*8/hd keys per step and a
+// dot product is finished with DPP swaps inside the group. A chunk of
+// ATT_CHUNK keys has all its K/V loads issued before any score is formed,
+// and the softmax update is done once per chunk (one exp per key). GM is
+// the largest query-head group the instance serves (4 or 8).
+template <int HD, int GM>
 __global__ void __launch_bounds__(256) attn_decode_k(AttnDecodeArgs a) {
-    constexpr int LPK = HD / 4;          // lanes per key (4 dims each)
+    constexpr int DPL = 8;               // dims per lane
+    constexpr int LPK = HD / DPL;        // lanes per key
     constexpr int KPW = 64 / LPK;        // keys per wave per step
-    constexpr int GMAX = 8;              // query heads per kv head
+    constexpr int NS = ATT_CHUNK / (4 * KPW);  // steps per chunk
+    constexpr int GMAX = GM;
+    constexpr int STRIDE = HD + ATT_PSTRIDE_PAD;
     __shared__ float wm[4][GMAX], wl[4][GMAX];
     __shared__ float wacc[4][GMAX][HD];
     __shared__ int last;
@@ -396,44 +417,73 @@ __global__ void __launch_bounds__(256) attn_decode_k(AttnDecodeArgs a) {
     int hi = pos + 1;
     lo = max(lo, split * a.split_len);
     hi = min(hi, (split + 1) * a.split_len);
-    const float scale = sqrtf((float)HD);
-    // q for the group's heads: this lane's 4 dims
-    float q[GMAX][4];
-    const float *qrow = a.q + (size_t)row * a.nq * HD + (size_t)g * G * HD + sub * 4;
+    const float inv_scale = 1.f / sqrtf((float)HD);
+    // q for the group's heads: this lane's 8 dims
+    float q[GMAX][DPL];
+    const float *qrow = a.q + (size_t)row * a.nq * HD + (size_t)g * G * HD + sub * DPL;
 #pragma unroll
     for (int j = 0; j < GMAX; ++j)
         if (j < G) {
-            f32x4_t v = *(const f32x4_t *)(qrow + (size_t)j * HD);
-            q[j][0] = v.x; q[j][1] = v.y; q[j][2] = v.z; q[j][3] = v.w;
+            const f32x4_t v0 = *(const f32x4_t *)(qrow + (size_t)j * HD);
+            const f32x4_t v1 = *(const f32x4_t *)(qrow + (size_t)j * HD + 4);
+            q[j][0] = v0.x; q[j][1] = v0.y; q[j][2] = v0.z; q[j][3] = v0.w;
+            q[j][4] = v1.x; q[j][5] = v1.y; q[j][6] = v1.z; q[j][7] = v1.w;
         }
-    float m[GMAX], l[GMAX], acc[GMAX][4];
+    float m[GMAX], l[GMAX], acc[GMAX][DPL];
 #pragma unroll
     for (int j = 0; j < GMAX; ++j) {
         m[j] = -INFINITY;
         l[j] = 0.f;
-        acc[j][0] = acc[j][1] = acc[j][2] = acc[j][3] = 0.f;
+#pragma unroll
+        for (int e = 0; e < DPL; ++e) acc[j][e] = 0.f;
     }
-    const float *kb = a.kv + (size_t)seq * a.seq_stride + (size_t)g * a.head_stride;
+    const float *kb = a.kv + (size_t)seq * a.seq_stride + (size_t)g * a.head_stride + sub * DPL;
     const float *vb = kb + a.kv_half_stride;
-#pragma unroll 4
-    for (int t = lo + wave * KPW + grp; t < hi; t += 4 * KPW) {
-        f32x4_t kk = *(const f32x4_t *)(kb + (size_t)t * HD + sub * 4);
-        f32x4_t vv = *(const f32x4_t *)(vb + (size_t)t * HD + sub * 4);
+    for (int c0 = lo; c0 < hi; c0 += ATT_CHUNK) {
+        f32x4_t kk[NS][2], vv[NS][2];
+#pragma unroll
+        for (int st = 0; st < NS; ++st) {
+            const int t = c0 + st * 4 * KPW + wave * KPW + grp;
+            kk[st][0] = kk[st][1] = vv[st][0] = vv[st][1] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+            if (t < hi) {
+                kk[st][0] = *(const f32x4_t *)(kb + (size_t)t * HD);
+                kk[st][1] = *(const f32x4_t *)(kb + (size_t)t * HD + 4);
+                vv[st][0] = *(const f32x4_t *)(vb + (size_t)t * HD);
+                vv[st][1] = *(const f32x4_t *)(vb + (size_t)t * HD + 4);
+            }
+        }
 #pragma unroll
         for (int j = 0; j < GMAX; ++j) {
             if (j >= G) break;
-            float d = q[j][0] * kk.x + q[j][1] * kk.y + q[j][2] * kk.z + q[j][3] * kk.w;
+            float sc[NS];
+            float mx = m[j];
 #pragma unroll
-            for (int o = LPK / 2; o > 0; o >>= 1) d += __shfl_xor(d, o, 64);
-            float s = d / scale;
-            float mn = fmaxf(m[j], s);
-            float al = __expf(m[j] - mn), p = __expf(s - mn);
-            l[j] = l[j] * al + p;
-            acc[j][0] = acc[j][0] * al + p * vv.x;
-            acc[j][1] = acc[j][1] * al + p * vv.y;
-            acc[j][2] = acc[j][2] * al + p * vv.z;
-            acc[j][3] = acc[j][3] * al + p * vv.w;
-            m[j] = mn;
+            for (int st = 0; st < NS; ++st) {
+                float d = 0.f;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) d += q[j][e] * kk[st][0][e];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) d += q[j][4 + e] * kk[st][1][e];
+                d = group_sum<LPK>(d);
+                const int t = c0 + st * 4 * KPW + wave * KPW + grp;
+                sc[st] = t < hi ? d * inv_scale : -INFINITY;
+                mx = fmaxf(mx, sc[st]);
+            }
+            if (mx == -INFINITY) continue;  // no key of this lane's group in the chunk yet
+            const float al = __expf(m[j] - mx);
+            l[j] *= al;
+#pragma unroll
+            for (int e = 0; e < DPL; ++e) acc[j][e] *= al;
+#pragma unroll
+            for (int st = 0; st < NS; ++st) {
+                const float p = __expf(sc[st] - mx);
+                l[j] += p;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) acc[j][e] += p * vv[st][0][e];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) acc[j][4 + e] += p * vv[st][1][e];
+            }
+            m[j] = mx;
         }
     }
     // merge the KPW key groups of the wave (lanes with equal `sub`)
@@ -448,7 +498,7 @@ __global__ void __launch_bounds__(256) attn_decode_k(AttnDecodeArgs a) {
             float s2 = mn == -INFINITY ? 0.f : __expf(om - mn);
             l[j] = l[j] * s1 + ol * s2;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
+            for (int i = 0; i < DPL; ++i) {
                 float oa = __shfl_xor(acc[j][i], o, 64);
                 acc[j][i] = acc[j][i] * s1 + oa * s2;
             }
@@ -456,7 +506,7 @@ __global__ void __launch_bounds__(256) attn_decode_k(AttnDecodeArgs a) {
         }
         if (grp == 0) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) wacc[wave][j][sub * 4 + i] = acc[j][i];
+            for (int i = 0; i < DPL; ++i) wacc[wave][j][sub * DPL + i] = acc[j][i];
             if (sub == 0) {
                 wm[wave][j] = m[j];
                 wl[wave][j] = l[j];
@@ -464,8 +514,7 @@ __global__ void __launch_bounds__(256) attn_decode_k(AttnDecodeArgs a) {
         }
     }
     __syncthreads();
-    // merge the 4 waves; write this split's partial (m, l, acc[HD]) per head
-    const size_t stride = (size_t)HD + 2;
+    // merge the 4 waves; write this split's partial (m, l, -, -, acc[HD]) per head
     for (int o = tid; o < G * HD; o += blockDim.x) {
         int j = o / HD, d = o % HD;
         float mx = -INFINITY;
@@ -476,24 +525,18 @@ __global__ void __launch_bounds__(256) attn_decode_k(AttnDecodeArgs a) {
             L += wl[w][j] * sc;
             v += wacc[w][j][d] * sc;
         }
-        float *p = a.part + (((size_t)row * a.nq + (size_t)g * G + j) * a.n_split + split) * stride;
-        st_agent(p + 2 + d, v);
+        if (a.n_split == 1) {  // single split: normalise directly
+            a.out[(size_t)row * a.nq * HD + (size_t)(g * G + j) * HD + d] = v / L;
+            continue;
+        }
+        float *p = a.part + (((size_t)row * a.nq + (size_t)g * G + j) * a.n_split + split) * STRIDE;
+        st_agent(p + ATT_PSTRIDE_PAD + d, v);
         if (d == 0) {
             st_agent(p, mx);
             st_agent(p + 1, L);
         }
     }
-    if (a.n_split == 1) {
-        // single split: normalise directly
-        __syncthreads();
-        for (int o = tid; o < G * HD; o += blockDim.x) {
-            int j = o / HD, d = o % HD;
-            const float *p = a.part + (((size_t)row * a.nq + (size_t)g * G + j)) * stride;
-            a.out[(size_t)row * a.nq * HD + (size_t)(g * G + j) * HD + d] =
-                ld_agent(p + 2 + d) / ld_agent(p + 1);
-        }
-        return;
-    }
+    if (a.n_split == 1) return;
     wait_stores();
     __syncthreads();
     if (tid == 0) {
@@ -504,54 +547,73 @@ __global__ void __launch_bounds__(256) attn_decode_k(AttnDecodeArgs a) {
     }
     __syncthreads();
     if (!last) return;
-    // merge: split maxima / sums staged in LDS, then per output one batch of
-    // independent partial loads weighted in split order (deterministic)
+    // Merge in the last block. Split maxima / sums go to LDS; each head's
+    // weights exp(m_s - max) and total are reduced across one wave; then
+    // every thread issues its partial loads (up to 32 splits x 2 outputs)
+    // at once and weights them in split order, so the result is
+    // deterministic.
     __shared__ float mm[GMAX][ATT_MAX_SPLIT], ww[GMAX][ATT_MAX_SPLIT], LL[GMAX];
     const int ns = a.n_split;
-    const float *pb = a.part + ((size_t)row * a.nq + (size_t)g * G) * ns * stride;
+    const float *pb = a.part + ((size_t)row * a.nq + (size_t)g * G) * ns * STRIDE;
     for (int i = tid; i < G * ns; i += blockDim.x) {
         const int j = i / ns, sp = i % ns;
-        mm[j][sp] = ld_agent(pb + ((size_t)j * ns + sp) * stride);
-        ww[j][sp] = ld_agent(pb + ((size_t)j * ns + sp) * stride + 1);
+        mm[j][sp] = ld_agent(pb + ((size_t)j * ns + sp) * STRIDE);
+        ww[j][sp] = ld_agent(pb + ((size_t)j * ns + sp) * STRIDE + 1);
     }
     __syncthreads();
-    if (tid < G) {
-        float mx = -INFINITY;
-        for (int sp = 0; sp < ns; ++sp) mx = fmaxf(mx, mm[tid][sp]);
-        float L = 0.f;
-        for (int sp = 0; sp < ns; ++sp) {
-            float w = mm[tid][sp] == -INFINITY ? 0.f : __expf(mm[tid][sp] - mx);
-            L += ww[tid][sp] * w;
-            ww[tid][sp] = w;
-        }
-        LL[tid] = L;
+    for (int j = wave; j < G; j += 4) {
+        const int s0 = lane, s1 = lane + 64;  // ns <= 128
+        const float m0 = s0 < ns ? mm[j][s0] : -INFINITY, m1 = s1 < ns ? mm[j][s1] : -INFINITY;
+        const float mx = wave_max(fmaxf(m0, m1));
+        const float w0 = m0 == -INFINITY ? 0.f : __expf(m0 - mx);
+        const float w1 = m1 == -INFINITY ? 0.f : __expf(m1 - mx);
+        const float L = wave_sum((s0 < ns ? ww[j][s0] * w0 : 0.f) + (s1 < ns ? ww[j][s1] * w1 : 0.f));
+        if (s0 < ns) ww[j][s0] = w0;
+        if (s1 < ns) ww[j][s1] = w1;
+        if (lane == 0) LL[j] = L;
     }
     __syncthreads();
-    for (int o = tid; o < G * HD; o += blockDim.x) {
-        const int j = o / HD, d = o % HD;
-        const float *p = pb + (size_t)j * ns * stride + 2 + d;
-        float v = 0.f;
-        int sp = 0;
-        for (; sp + 8 <= ns; sp += 8) {
-            float t[8];
+    constexpr int MB = 32;  // splits per load batch
+    for (int o0 = tid; o0 < G * HD; o0 += 2 * blockDim.x) {
+        const int o1 = o0 + blockDim.x;
+        const bool has1 = o1 < G * HD;
+        const int j0 = o0 / HD, d0 = o0 % HD, j1 = has1 ? o1 / HD : j0, d1 = has1 ? o1 % HD : d0;
+        const float *p0 = pb + (size_t)j0 * ns * STRIDE + ATT_PSTRIDE_PAD + d0;
+        const float *p1 = pb + (size_t)j1 * ns * STRIDE + ATT_PSTRIDE_PAD + d1;
+        float v0 = 0.f, v1 = 0.f;
+        for (int sp0 = 0; sp0 < ns; sp0 += MB) {
+            float t0[MB], t1[MB];
 #pragma unroll
-            for (int q = 0; q < 8; ++q) t[q] = ld_agent(p + (size_t)(sp + q) * stride);
+            for (int q = 0; q < MB; ++q) {
+                t0[q] = sp0 + q < ns ? ld_agent(p0 + (size_t)(sp0 + q) * STRIDE) : 0.f;
+                t1[q] = has1 && sp0 + q < ns ? ld_agent(p1 + (size_t)(sp0 + q) * STRIDE) : 0.f;
+            }
 #pragma unroll
-            for (int q = 0; q < 8; ++q) v += t[q] * ww[j][sp + q];
+            for (int q = 0; q < MB; ++q) {
+                if (sp0 + q < ns) {
+                    v0 += t0[q] * ww[j0][sp0 + q];
+                    v1 += t1[q] * ww[j1][sp0 + q];
+                }
+            }
         }
-        for (; sp < ns; ++sp) v += ld_agent(p + (size_t)sp * stride) * ww[j][sp];
-        a.out[(size_t)row * a.nq * HD + (size_t)(g * G + j) * HD + d] = v / LL[j];
+        a.out[(size_t)row * a.nq * HD + (size_t)(g * G + j0) * HD + d0] = v0 / LL[j0];
+        if (has1) a.out[(size_t)row * a.nq * HD + (size_t)(g * G + j1) * HD + d1] = v1 / LL[j1];
     }
 }
 
 bool attn_decode_ok(int hd, int G) { return (hd == 64 || hd == 128) && G <= 8; }
 
-// Key splits for one decode row: ~32 keys per block, capped so the merge
-// re-reads at most a few percent of the keys' bytes.
-int attn_decode_splits(int hd, int max_t) {
-    int cap = hd == 64 ? ATT_MAX_SPLIT : ATT_MAX_SPLIT / 2;
-    int ns = (max_t + 31) / 32;
-    return ns < 1 ? 1 : (ns > cap ? cap : ns);
+// Key splits for one decode row: splits of a multiple of 32 keys, as many
+// as the cap allows (64 for hd 128, 128 for hd 64: the merge re-reads
+// every split's partial); longer splits are walked in ATT_CHUNK-key chunks.
+int attn_decode_splits(int hd, int max_t, int *split_len) {
+    const int cap = hd == 64 ? ATT_MAX_SPLIT : ATT_MAX_SPLIT / 2;
+    int len = (max_t + cap - 1) / cap;
+    len = len < 32 ? 32 : (len + 31) / 32 * 32;
+    int ns = (max_t + len - 1) / len;
+    if (ns < 1) ns = 1;
+    *split_len = len;
+    return ns;
 }
 
 void launch_attn_decode(const AttnDecodeArgs &a, hipStream_t s) {
@@ -559,8 +621,13 @@ void launch_attn_decode(const AttnDecodeArgs &a, hipStream_t s) {
     if (!attn_decode_ok(a.hd, G)) fail(ESP_BACKEND, "attn_decode: unsupported head shape");
     dim3 grid(a.n_split, a.nkv, a.M);
     if (a.n_split > ATT_MAX_SPLIT) fail(ESP_BACKEND, "attn_decode: too many key splits");
-    if (a.hd == 64) attn_decode_k<64><<<grid, 256, 0, s>>>(a);
-    else attn_decode_k<128><<<grid, 256, 0, s>>>(a);
+    if (a.hd == 64) {
+        if (G <= 4) attn_decode_k<64, 4><<<grid, 256, 0, s>>>(a);
+        else attn_decode_k<64, 8><<<grid, 256, 0, s>>>(a);
+    } else {
+        if (G <= 4) attn_decode_k<128, 4><<<grid, 256, 0, s>>>(a);
+        else attn_decode_k<128, 8><<<grid, 256, 0, s>>>(a);
+    }
 }
 
 }  // namespace esp

@@ -285,6 +285,26 @@ def test_bf16_long_prefill_wide_gemm_tiles():
         assert _close_bf16(got, want), (len(block), float(np.abs(got - want).max()))
 
 
+def test_bf16_long_context_decode_splits():
+    """Decode over 8.3k cached keys (hd 128, 4 query heads on one kv head):
+    the key range is cut into 52 splits of 160 keys (two load chunks each)
+    whose partials the last block merges; logits within the bf16 tolerance
+    of the oracle for three teacher-forced steps."""
+    cfg = synth.llama_config(1, 256, 4, 1, 256, 500, head_dim=128, max_pos=8400)
+    tensors = synth.make_tensors(cfg, 71, "bf16")
+    model = DecoderModel.from_bytes(cfg, st.dump(tensors), "bf16")
+    ref = oracle.OracleModel(cfg, tensors)
+    kv, rkv = model.new_cache(1, 8320), ref.new_cache(8320)
+    got = model.try_forward_cached_last(synth.uniform_ids(4, 8300, 500), kv)
+    want = ref.forward_last(rkv, synth.uniform_ids(4, 8300, 500))
+    assert _close_bf16(got, want), float(np.abs(got - want).max())
+    for step in range(3):
+        t = oracle.argmax(want)
+        got = model.try_forward_cached_last([t], kv)
+        want = ref.forward_last(rkv, [t])
+        assert _close_bf16(got, want), (step, float(np.abs(got - want).max()))
+
+
 def _adapter(cfg, rank, targets, seed, fmt):
     """PEFT LoRA tensors base_model.model.model.layers.{i}.self_attn.{m}.lora_{A,B}.weight,
     A ~ N(0, 0.02), B ~ N(0, 0.01)."""
