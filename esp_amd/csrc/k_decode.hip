@@ -376,7 +376,8 @@ void launch_decode_gemv(Dt wt, int epi, const DecodeGemvArgs &a, hipStream_t s) 
 // ------------------------------------------------------------ attention
 
 constexpr int ATT_MAX_SPLIT = 128;
-constexpr int ATT_CHUNK = 64;  // keys whose K/V loads a block issues at once
+constexpr int ATT_WAVES = 8;     // waves per attention block
+constexpr int ATT_CHUNK = 128;  // keys whose K/V loads a block issues at once
 constexpr int ATT_PSTRIDE_PAD = ATT_PART_PAD;  // partial row: m, l, 2 pad, acc[hd]
 
 // Sum over aligned groups of N lanes (N = 8 or 16) with DPP lane swaps:
@@ -398,15 +399,16 @@ template <int N> __device__ __forceinline__ float group_sum(float v) {
 // and the softmax update is done once per chunk (one exp per key). GM is
 // the largest query-head group the instance serves (4 or 8).
 template <int HD, int GM>
-__global__ void __launch_bounds__(256) attn_decode_k(AttnDecodeArgs a) {
+__global__ void __launch_bounds__(ATT_WAVES * 64) attn_decode_k(AttnDecodeArgs a) {
+    constexpr int NW = ATT_WAVES;
     constexpr int DPL = 8;               // dims per lane
     constexpr int LPK = HD / DPL;        // lanes per key
     constexpr int KPW = 64 / LPK;        // keys per wave per step
-    constexpr int NS = ATT_CHUNK / (4 * KPW);  // steps per chunk
+    constexpr int NS = ATT_CHUNK / (NW * KPW);  // steps per chunk
     constexpr int GMAX = GM;
     constexpr int STRIDE = HD + ATT_PSTRIDE_PAD;
-    __shared__ float wm[4][GMAX], wl[4][GMAX];
-    __shared__ float wacc[4][GMAX][HD];
+    __shared__ float wm[NW][GMAX], wl[NW][GMAX];
+    __shared__ float wacc[NW][GMAX][HD];
     __shared__ int last;
     const int split = blockIdx.x, g = blockIdx.y, row = blockIdx.z;
     const int G = a.nq / a.nkv;
@@ -443,7 +445,7 @@ __global__ void __launch_bounds__(256) attn_decode_k(AttnDecodeArgs a) {
         f32x4_t kk[NS][2], vv[NS][2];
 #pragma unroll
         for (int st = 0; st < NS; ++st) {
-            const int t = c0 + st * 4 * KPW + wave * KPW + grp;
+            const int t = c0 + st * NW * KPW + wave * KPW + grp;
             kk[st][0] = kk[st][1] = vv[st][0] = vv[st][1] = f32x4_t{0.f, 0.f, 0.f, 0.f};
             if (t < hi) {
                 kk[st][0] = *(const f32x4_t *)(kb + (size_t)t * HD);
@@ -465,7 +467,7 @@ __global__ void __launch_bounds__(256) attn_decode_k(AttnDecodeArgs a) {
 #pragma unroll
                 for (int e = 0; e < 4; ++e) d += q[j][4 + e] * kk[st][1][e];
                 d = group_sum<LPK>(d);
-                const int t = c0 + st * 4 * KPW + wave * KPW + grp;
+                const int t = c0 + st * NW * KPW + wave * KPW + grp;
                 sc[st] = t < hi ? d * inv_scale : -INFINITY;
                 mx = fmaxf(mx, sc[st]);
             }
@@ -514,13 +516,13 @@ __global__ void __launch_bounds__(256) attn_decode_k(AttnDecodeArgs a) {
         }
     }
     __syncthreads();
-    // merge the 4 waves; write this split's partial (m, l, -, -, acc[HD]) per head
+    // merge the waves; write this split's partial (m, l, -, -, acc[HD]) per head
     for (int o = tid; o < G * HD; o += blockDim.x) {
         int j = o / HD, d = o % HD;
         float mx = -INFINITY;
-        for (int w = 0; w < 4; ++w) mx = fmaxf(mx, wm[w][j]);
+        for (int w = 0; w < NW; ++w) mx = fmaxf(mx, wm[w][j]);
         float L = 0.f, v = 0.f;
-        for (int w = 0; w < 4; ++w) {
+        for (int w = 0; w < NW; ++w) {
             float sc = mx == -INFINITY ? 0.f : __expf(wm[w][j] - mx);
             L += wl[w][j] * sc;
             v += wacc[w][j][d] * sc;
@@ -561,7 +563,7 @@ __global__ void __launch_bounds__(256) attn_decode_k(AttnDecodeArgs a) {
         ww[j][sp] = ld_agent(pb + ((size_t)j * ns + sp) * STRIDE + 1);
     }
     __syncthreads();
-    for (int j = wave; j < G; j += 4) {
+    for (int j = wave; j < G; j += NW) {
         const int s0 = lane, s1 = lane + 64;  // ns <= 128
         const float m0 = s0 < ns ? mm[j][s0] : -INFINITY, m1 = s1 < ns ? mm[j][s1] : -INFINITY;
         const float mx = wave_max(fmaxf(m0, m1));
@@ -603,13 +605,13 @@ __global__ void __launch_bounds__(256) attn_decode_k(AttnDecodeArgs a) {
 
 bool attn_decode_ok(int hd, int G) { return (hd == 64 || hd == 128) && G <= 8; }
 
-// Key splits for one decode row: splits of a multiple of 32 keys, as many
-// as the cap allows (64 for hd 128, 128 for hd 64: the merge re-reads
-// every split's partial); longer splits are walked in ATT_CHUNK-key chunks.
+// Key splits for one decode row: splits of a multiple of ATT_CHUNK keys
+// (one round of loads per chunk), at most 64 (hd 128) or 128 (hd 64) of
+// them since the merge re-reads every split's partial.
 int attn_decode_splits(int hd, int max_t, int *split_len) {
     const int cap = hd == 64 ? ATT_MAX_SPLIT : ATT_MAX_SPLIT / 2;
     int len = (max_t + cap - 1) / cap;
-    len = len < 32 ? 32 : (len + 31) / 32 * 32;
+    len = len < ATT_CHUNK ? ATT_CHUNK : (len + ATT_CHUNK - 1) / ATT_CHUNK * ATT_CHUNK;
     int ns = (max_t + len - 1) / len;
     if (ns < 1) ns = 1;
     *split_len = len;
@@ -622,11 +624,11 @@ void launch_attn_decode(const AttnDecodeArgs &a, hipStream_t s) {
     dim3 grid(a.n_split, a.nkv, a.M);
     if (a.n_split > ATT_MAX_SPLIT) fail(ESP_BACKEND, "attn_decode: too many key splits");
     if (a.hd == 64) {
-        if (G <= 4) attn_decode_k<64, 4><<<grid, 256, 0, s>>>(a);
-        else attn_decode_k<64, 8><<<grid, 256, 0, s>>>(a);
+        if (G <= 4) attn_decode_k<64, 4><<<grid, ATT_WAVES * 64, 0, s>>>(a);
+        else attn_decode_k<64, 8><<<grid, ATT_WAVES * 64, 0, s>>>(a);
     } else {
-        if (G <= 4) attn_decode_k<128, 4><<<grid, 256, 0, s>>>(a);
-        else attn_decode_k<128, 8><<<grid, 256, 0, s>>>(a);
+        if (G <= 4) attn_decode_k<128, 4><<<grid, ATT_WAVES * 64, 0, s>>>(a);
+        else attn_decode_k<128, 8><<<grid, ATT_WAVES * 64, 0, s>>>(a);
     }
 }
 
