@@ -94,7 +94,25 @@ template <> struct RowsPerUnit<DG_QKVROPE> { static constexpr int v = 2; };
 
 constexpr int DG_MAX_IT = 64;  // grid-stride iterations per block
 
-template <typename WT, int EPI, int RB>
+// Sum over all 64 lanes, returned wave-uniform: DPP sums inside each
+// 16-lane row, then the four row sums read out in a fixed order.
+__device__ __forceinline__ float wave_sum_uniform(float v) {
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x141, 0xF, 0xF, false));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x140, 0xF, 0xF, false));
+    const int b = __builtin_bit_cast(int, v);
+    return ((__builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 0)) +
+             __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 16))) +
+            __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 32))) +
+           __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 48));
+}
+
+// NCH = 8-element chunks per lane and row in this wave's quarter of K
+// (K <= 4 * 64 * 8 * NCH). The first iteration's weight loads are issued
+// before x is read and normalised, and each iteration issues the next
+// one's loads before reducing its own sums.
+template <typename WT, int EPI, int RB, int NCH>
 __global__ void __launch_bounds__(DG_THREADS) decode_gemv_k(DecodeGemvArgs a) {
     constexpr int RU = RowsPerUnit<EPI>::v;
     constexpr int R = RB * RU;  // weight rows per block iteration
@@ -108,11 +126,42 @@ __global__ void __launch_bounds__(DG_THREADS) decode_gemv_k(DecodeGemvArgs a) {
     const int k0 = wave * kq;
     const WT *W = (const WT *)a.w;
     const WT *W2 = (const WT *)a.w2;
+    const int units = EPI == DG_QKVROPE ? a.N / 2 : a.N;
+
+    Chunk<WT> wc[R][NCH];
+    auto load_rows = [&](int u0) {
+        const WT *rp[R];
+#pragma unroll
+        for (int r = 0; r < RB; ++r) {
+            int u = min(u0 + r, units - 1);
+            if (EPI == DG_SWIGLU) {
+                rp[r * 2] = W + (size_t)u * K;
+                rp[r * 2 + 1] = W2 + (size_t)u * K;
+            } else if (EPI == DG_QKVROPE) {
+                int half = a.hd / 2, head = u / half, d = u % half;
+                int row = head * a.hd + d;
+                rp[r * 2] = W + (size_t)row * K;
+                rp[r * 2 + 1] = W + (size_t)(row + half) * K;
+            } else {
+                rp[r] = W + (size_t)u * K;
+            }
+        }
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) {
+            const int ch = lane + 64 * c;
+            if (ch < nch) {
+#pragma unroll
+                for (int r = 0; r < R; ++r) wc[r][c].load(rp[r] + k0 + ch * 8);
+            }
+        }
+    };
+    if ((int)blockIdx.x * RB < units) load_rows(blockIdx.x * RB);
+
     // ---- x slice in registers (+ fused RMSNorm)
-    float xr[DG_MAXC][8];
+    float xr[NCH][8];
     float ss = 0.f;
 #pragma unroll
-    for (int c = 0; c < DG_MAXC; ++c) {
+    for (int c = 0; c < NCH; ++c) {
         int ch = lane + 64 * c;
         if (ch < nch) {
             const float *xp = a.x + k0 + ch * 8;
@@ -132,7 +181,7 @@ __global__ void __launch_bounds__(DG_THREADS) decode_gemv_k(DecodeGemvArgs a) {
         for (int w = 0; w < DG_WAVES; ++w) tot += ssq[w];
         const float rms = sqrtf(tot / (float)K + a.eps);
 #pragma unroll
-        for (int c = 0; c < DG_MAXC; ++c) {
+        for (int c = 0; c < NCH; ++c) {
             int ch = lane + 64 * c;
             if (ch < nch) {
                 const float *g = a.gamma + k0 + ch * 8;
@@ -141,43 +190,24 @@ __global__ void __launch_bounds__(DG_THREADS) decode_gemv_k(DecodeGemvArgs a) {
             }
         }
     }
-    const int units = EPI == DG_QKVROPE ? a.N / 2 : a.N;
-    // ---- stream rows; each wave parks its partial sums in LDS (no barrier)
+    // ---- stream rows; each wave parks its sums in LDS (no barrier)
     int iters = 0;
     for (int u0 = blockIdx.x * RB; u0 < units; u0 += gridDim.x * RB, ++iters) {
-        const WT *rp[R];
-#pragma unroll
-        for (int r = 0; r < RB; ++r) {
-            int u = min(u0 + r, units - 1);
-            if (EPI == DG_SWIGLU) {
-                rp[r * 2] = W + (size_t)u * K;
-                rp[r * 2 + 1] = W2 + (size_t)u * K;
-            } else if (EPI == DG_QKVROPE) {
-                int half = a.hd / 2, head = u / half, d = u % half;
-                int row = head * a.hd + d;
-                rp[r * 2] = W + (size_t)row * K;
-                rp[r * 2 + 1] = W + (size_t)(row + half) * K;
-            } else {
-                rp[r] = W + (size_t)u * K;
-            }
-        }
         float acc[R];
 #pragma unroll
         for (int r = 0; r < R; ++r) acc[r] = 0.f;
 #pragma unroll
-        for (int c = 0; c < DG_MAXC; ++c) {
+        for (int c = 0; c < NCH; ++c) {
             int ch = lane + 64 * c;
             if (ch < nch) {
-                Chunk<WT> wc[R];
 #pragma unroll
-                for (int r = 0; r < R; ++r) wc[r].load(rp[r] + k0 + ch * 8);
-#pragma unroll
-                for (int r = 0; r < R; ++r) acc[r] += wc[r].dot(xr[c]);
+                for (int r = 0; r < R; ++r) acc[r] += wc[r][c].dot(xr[c]);
             }
         }
+        if (u0 + gridDim.x * RB < units) load_rows(u0 + gridDim.x * RB);
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-            float v = wave_sum(acc[r]);
+            const float v = wave_sum_uniform(acc[r]);
             if (lane == 0) red[iters][r][wave] = v;
         }
     }
@@ -326,24 +356,37 @@ __global__ void __launch_bounds__(DG_THREADS) decode_gemv_k(DecodeGemvArgs a) {
     }
 }
 
-template <typename WT, int EPI, int RB>
-static void dg_launch_rb(const DecodeGemvArgs &a, int cus, hipStream_t s) {
+template <typename WT, int EPI, int RB, int NCH>
+static void dg_launch_nch(const DecodeGemvArgs &a, int cus, hipStream_t s) {
+    static int per_cu = 0;  // resident blocks per CU for this instance
+    if (!per_cu) {
+        ESP_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(
+            &per_cu, reinterpret_cast<const void *>(decode_gemv_k<WT, EPI, RB, NCH>), DG_THREADS, 0));
+        if (per_cu <= 0) per_cu = 1;
+    }
     const int units = EPI == DG_QKVROPE ? a.N / 2 : a.N;
-    int blocks = (units + RB - 1) / RB;
-    const int cap = cus * 8;
-    if (blocks > cap) blocks = cap;
-    const int need = (units + RB * DG_MAX_IT - 1) / (RB * DG_MAX_IT);  // LDS slots per block
+    const int groups = (units + RB - 1) / RB;
+    // one round of resident blocks, every block doing the same number of
+    // iterations
+    const int cap = cus * per_cu;
+    int iters = (groups + cap - 1) / cap;
+    const int need = (groups + DG_MAX_IT - 1) / DG_MAX_IT;  // LDS slots per block
+    int blocks = (groups + iters - 1) / iters;
     if (blocks < need) blocks = need;
     if (EPI == DG_HEAD && a.ticket && blocks > DG_MAX_PART)
         fail(ESP_UNSUPPORTED, "decode head: vocabulary above the argmax partial capacity");
-    decode_gemv_k<WT, EPI, RB><<<blocks, DG_THREADS, 0, s>>>(a);
+    decode_gemv_k<WT, EPI, RB, NCH><<<blocks, DG_THREADS, 0, s>>>(a);
 }
 
 template <typename WT, int EPI>
 static void dg_launch(const DecodeGemvArgs &a, int cus, hipStream_t s) {
     // Measured on MI355X: two rows per block (more blocks in flight) beats
     // larger row blocks with more loads per lane at every decode shape.
-    dg_launch_rb<WT, EPI, 2>(a, cus, s);
+    const int nch = (a.K / DG_WAVES / 8 + 63) / 64;  // chunks per lane and row
+    if (nch <= 1) dg_launch_nch<WT, EPI, 2, 1>(a, cus, s);
+    else if (nch <= 2) dg_launch_nch<WT, EPI, 2, 2>(a, cus, s);
+    else if (nch <= 4) dg_launch_nch<WT, EPI, 2, 4>(a, cus, s);
+    else dg_launch_nch<WT, EPI, 2, DG_MAXC>(a, cus, s);
 }
 
 bool decode_gemv_ok(int K) { return K % 32 == 0 && K / 32 <= 64 * DG_MAXC; }
