@@ -48,7 +48,7 @@ struct AttnDecodeArgs {
 
 bool attn_decode_ok(int hd, int G);
 // key splits and keys per split for a decode row over max_t cached keys
-int attn_decode_splits(int hd, int max_t, int *split_len);
+int attn_decode_splits(int hd, int nkv, int G, int max_t, int *split_len);
 constexpr int ATT_PART_PAD = 4;  // partial row = hd + ATT_PART_PAD floats
 void launch_attn_decode(const AttnDecodeArgs &a, hipStream_t s);
 

@@ -419,7 +419,7 @@ void launch_decode_gemv(Dt wt, int epi, const DecodeGemvArgs &a, hipStream_t s) 
 // ------------------------------------------------------------ attention
 
 constexpr int ATT_MAX_SPLIT = 128;
-constexpr int ATT_WAVES = 8;     // waves per attention block
+constexpr int ATT_WAVES = 4;     // waves per attention block
 constexpr int ATT_CHUNK = 128;  // keys whose K/V loads a block issues at once
 constexpr int ATT_PSTRIDE_PAD = ATT_PART_PAD;  // partial row: m, l, 2 pad, acc[hd]
 
@@ -648,14 +648,37 @@ __global__ void __launch_bounds__(ATT_WAVES * 64) attn_decode_k(AttnDecodeArgs a
 
 bool attn_decode_ok(int hd, int G) { return (hd == 64 || hd == 128) && G <= 8; }
 
-// Key splits for one decode row: splits of a multiple of ATT_CHUNK keys
-// (one round of loads per chunk), at most 64 (hd 128) or 128 (hd 64) of
-// them since the merge re-reads every split's partial.
-int attn_decode_splits(int hd, int max_t, int *split_len) {
+template <int HD, int GM> static int attn_resident_blocks() {
+    static int per_cu = 0;
+    if (!per_cu) {
+        ESP_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(
+            &per_cu, reinterpret_cast<const void *>(attn_decode_k<HD, GM>), ATT_WAVES * 64, 0));
+        if (per_cu <= 0) per_cu = 1;
+    }
+    static int cus = 0;
+    if (!cus) {
+        int dev = 0;
+        ESP_HIP(hipGetDevice(&dev));
+        ESP_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+        if (cus <= 0) cus = 256;
+    }
+    return per_cu * cus;
+}
+
+// Key splits for one decode row: as many splits as keep every (split, kv
+// head) block resident at once (one round of blocks), at most 64 (hd 128)
+// or 128 (hd 64) since the merge re-reads every split's partial; split
+// lengths are multiples of 32 keys, and a split up to ATT_CHUNK keys is
+// read in one round of loads.
+int attn_decode_splits(int hd, int nkv, int G, int max_t, int *split_len) {
+    int slots = hd == 64 ? (G <= 4 ? attn_resident_blocks<64, 4>() : attn_resident_blocks<64, 8>())
+                         : (G <= 4 ? attn_resident_blocks<128, 4>() : attn_resident_blocks<128, 8>());
     const int cap = hd == 64 ? ATT_MAX_SPLIT : ATT_MAX_SPLIT / 2;
-    int len = (max_t + cap - 1) / cap;
-    len = len < ATT_CHUNK ? ATT_CHUNK : (len + ATT_CHUNK - 1) / ATT_CHUNK * ATT_CHUNK;
-    int ns = (max_t + len - 1) / len;
+    int ns = slots / (nkv > 0 ? nkv : 1);
+    ns = ns < 1 ? 1 : (ns > cap ? cap : ns);
+    int len = (max_t + ns - 1) / ns;
+    len = len < 32 ? 32 : (len + 31) / 32 * 32;
+    ns = (max_t + len - 1) / len;
     if (ns < 1) ns = 1;
     *split_len = len;
     return ns;

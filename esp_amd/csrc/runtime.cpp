@@ -728,7 +728,7 @@ static void run_layers(Model &m, Kv &kv, const Rows &rows, int Mc, int max_t, in
     const int H = m.H;
     Plan plan = attn_plan(m, Mc, max_t);
     if (single && attn_decode_ok(m.hd, m.nq / m.nkv)) {
-        plan.n_split = attn_decode_splits(m.hd, max_t, &plan.split_len);
+        plan.n_split = attn_decode_splits(m.hd, m.nkv, m.nq / m.nkv, max_t, &plan.split_len);
     }
     kv.part.ensure((size_t)Mc * m.nq * plan.n_split * (m.hd + ATT_PART_PAD) * 4);
     for (int l = 0; l < m.L; ++l) {
