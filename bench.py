@@ -221,21 +221,31 @@ def main():
     pre_tps = args.prompt / tp
     avg_ctx = args.prompt + args.decode / 2
     db = decode_bytes(cfg, int(avg_ctx))
-    # profiled pass: per-launch HIP events on the KV stream for the GEMV family
-    profile_enable("gemv", True)
+    # profiled pass: per-launch HIP events on the KV stream. The dominant
+    # kernel is the persistent decode step (one launch = embedding, every
+    # layer and the head for one token: all weights + the K/V cache read
+    # once); with ESP_STEP=0 it is the GEMV family of the per-kernel path.
+    for fam in ("step", "gemv"):
+        profile_enable(fam, True)
     gen_eager_steps = 16
     kv2 = model.new_cache(1, ctx)
     kv2.reset(0)
     model.try_forward_cached_last(prompt, kv2)
-    n0, ms0 = profile_read("gemv")
+    before = {fam: profile_read(fam) for fam in ("step", "gemv")}
     for i in range(gen_eager_steps):
         model.try_forward_cached_last([i + 1], kv2)
-    n1, ms1 = profile_read("gemv")
-    profile_enable("gemv", False)
-    gemv_launches = n1 - n0
-    gemv_ms = ms1 - ms0
-    gemv_bytes = db["gemv_weights"] * gen_eager_steps
-    gemv_gbs = gemv_bytes / (gemv_ms / 1e3) / 1e9
+    after = {fam: profile_read(fam) for fam in ("step", "gemv")}
+    for fam in ("step", "gemv"):
+        profile_enable(fam, False)
+    if after["step"][0] > before["step"][0]:
+        fam, kname = "step", "step_k (persistent decode step: all layers + head)"
+        fam_bytes = sum(decode_bytes(cfg, args.prompt + i + 1)["total"] for i in range(gen_eager_steps))
+    else:
+        fam, kname = "gemv", "gemv (decode projections + head)"
+        fam_bytes = db["gemv_weights"] * gen_eager_steps
+    gemv_launches = after[fam][0] - before[fam][0]
+    gemv_ms = after[fam][1] - before[fam][1]
+    gemv_gbs = fam_bytes / (gemv_ms / 1e3) / 1e9
     result = {
         "metric": "decode & prefill tokens/s on 1 MI355X; % of HBM / bf16-MFMA roofline",
         "value": round(dec_tps, 2),
@@ -257,13 +267,13 @@ def main():
         "prefill_mfma_frac": round(prefill_flops(cfg, args.prompt) / tp / 1e12 / BF16_PEAK_TFLOPS, 4),
         "decode_ms_per_token": round(t_dec / n_dec * 1e3, 4),
         "decode_hbm_frac": round(db["total"] / (t_dec / n_dec) / 1e9 / HBM_PEAK_GBS, 4),
-        "roofline": {"bound": "hbm", "kernel": "gemv (decode projections + head)",
+        "roofline": {"bound": "hbm", "kernel": kname,
                      "achieved": round(gemv_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gemv_gbs / HBM_PEAK_GBS, 4), "traffic": None,
                      "launches": gemv_launches,
                      "avg_launch_us": round(gemv_ms / max(1, gemv_launches) * 1e3, 3)},
     }
-    print(f"gpu: decode {dec_tps:.1f} tok/s, prefill {pre_tps:.1f} tok/s, gemv {gemv_gbs:.0f} GB/s",
+    print(f"gpu: decode {dec_tps:.1f} tok/s, prefill {pre_tps:.1f} tok/s, {fam} {gemv_gbs:.0f} GB/s",
           file=sys.stderr, flush=True)
     if not args.no_c3:
         del kv, kv2

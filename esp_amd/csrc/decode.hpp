@@ -23,6 +23,12 @@ struct DecodeGemvArgs {
     float *kv;            // layer base of the f32 cache
     long long seq_stride, kv_half_stride, head_stride;
     int nq, nkv, hd;
+    // QKVROPE unmerged LoRA (targets 0 q, 1 k, 2 v): row o of target j gets
+    // + lora_scale[j] * B_j[o, :] . t_j with t_j at lora_t + lora_t_col[j]
+    const float *lora_t;  // nullable = no LoRA
+    const void *lora_b[3];
+    int lora_rank[3], lora_t_col[3];
+    float lora_scale[3];
     // HEAD argmax
     float *part_v;
     int32_t *part_i;

@@ -1,0 +1,107 @@
+// Device helpers shared by the single-token kernels (k_decode.hip) and the
+// persistent decode-step kernel (k_step.hip).
+#pragma once
+
+#include "common.hpp"
+#include "dev.hpp"
+
+namespace esp {
+
+constexpr int DG_THREADS = 256;
+constexpr int DG_WAVES = 4;
+constexpr int DG_MAXC = 8;  // max 8-element chunks per lane per row (K <= 4*64*8*8 = 16384)
+
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+// Cross-block hand-off without flushing L2: partials are written with
+// agent-scope (write-through) stores, the writer waits for its stores to
+// complete (s_waitcnt vmcnt(0)) before taking a ticket, and the last block
+// reads the partials with agent-scope loads.
+__device__ __forceinline__ void st_agent(float *p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_agent(int32_t *p, int32_t v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_agent(const float *p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ int32_t ld_agent(const int32_t *p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void wait_stores() { __builtin_amdgcn_s_waitcnt(0x0F70); }  // vmcnt(0)
+
+template <typename WT> struct Chunk;
+template <> struct Chunk<uint16_t> {  // 8 bf16 = 16 bytes
+    u32x4_t v;
+    __device__ __forceinline__ void load(const uint16_t *p) {
+        v = __builtin_nontemporal_load((const u32x4_t *)p);
+    }
+    __device__ __forceinline__ float dot(const float *x) const {
+        float s = 0.f;
+        s += __uint_as_float(v.x << 16) * x[0];
+        s += __uint_as_float(v.x & 0xffff0000u) * x[1];
+        s += __uint_as_float(v.y << 16) * x[2];
+        s += __uint_as_float(v.y & 0xffff0000u) * x[3];
+        s += __uint_as_float(v.z << 16) * x[4];
+        s += __uint_as_float(v.z & 0xffff0000u) * x[5];
+        s += __uint_as_float(v.w << 16) * x[6];
+        s += __uint_as_float(v.w & 0xffff0000u) * x[7];
+        return s;
+    }
+};
+template <> struct Chunk<float> {  // 8 f32 = 2 x 16 bytes
+    f32x4_t a, b;
+    __device__ __forceinline__ void load(const float *p) {
+        a = __builtin_nontemporal_load((const f32x4_t *)p);
+        b = __builtin_nontemporal_load((const f32x4_t *)p + 1);
+    }
+    __device__ __forceinline__ float dot(const float *x) const {
+        float s = 0.f;
+        s += a.x * x[0];
+        s += a.y * x[1];
+        s += a.z * x[2];
+        s += a.w * x[3];
+        s += b.x * x[4];
+        s += b.y * x[5];
+        s += b.z * x[6];
+        s += b.w * x[7];
+        return s;
+    }
+};
+
+// rows handled per unit: SWIGLU and QKVROPE units are row pairs
+template <int EPI> struct RowsPerUnit { static constexpr int v = 1; };
+template <> struct RowsPerUnit<DG_SWIGLU> { static constexpr int v = 2; };
+template <> struct RowsPerUnit<DG_QKVROPE> { static constexpr int v = 2; };
+
+constexpr int DG_MAX_IT = 64;  // grid-stride iterations per block
+
+// Sum over all 64 lanes, returned wave-uniform: DPP sums inside each
+// 16-lane row, then the four row sums read out in a fixed order.
+__device__ __forceinline__ float wave_sum_uniform(float v) {
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x141, 0xF, 0xF, false));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x140, 0xF, 0xF, false));
+    const int b = __builtin_bit_cast(int, v);
+    return ((__builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 0)) +
+             __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 16))) +
+            __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 32))) +
+           __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 48));
+}
+
+// Sum over aligned groups of N lanes (N = 8 or 16) with DPP lane swaps:
+// quad xor 1, quad xor 2, half-row mirror (8 lanes), row mirror (16 lanes).
+template <int N> __device__ __forceinline__ float group_sum(float v) {
+    static_assert(N == 8 || N == 16, "group_sum: 8 or 16 lanes");
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x141, 0xF, 0xF, false));
+    if (N == 16)
+        v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x140, 0xF, 0xF, false));
+    return v;
+}
+
+}  // namespace esp

@@ -105,7 +105,7 @@ __global__ void __launch_bounds__(256) rope_kv_k(RopeKvArgs a, int rows_per_bloc
         const float sc = a.lora_scale[target];
 #pragma unroll
         for (int r = 0; r < ROPE_ROWS; ++r) {
-            if (r >= nr) break;
+            if (r >= nr) continue;
             const float *t = tsh + r * t_n + tcol;
             float acc = 0.f;
 #pragma unroll
@@ -127,7 +127,7 @@ __global__ void __launch_bounds__(256) rope_kv_k(RopeKvArgs a, int rows_per_bloc
         if (g) {
 #pragma unroll
             for (int r = 0; r < ROPE_ROWS; ++r) {
-                if (r >= nr) break;
+                if (r >= nr) continue;
                 const float *v = sh + r * bw + lh * hd;
                 float ss = 0.f;
                 for (int i = 0; i < hd; ++i) ss += v[i] * v[i];
@@ -146,7 +146,7 @@ __global__ void __launch_bounds__(256) rope_kv_k(RopeKvArgs a, int rows_per_bloc
     if (!active) return;
 #pragma unroll
     for (int r = 0; r < ROPE_ROWS; ++r) {
-        if (r >= nr) break;
+        if (r >= nr) continue;
         const int m = m0 + r;
         const int pos = a.rows.row_pos[m];
         const int seq = a.rows.row_seq[m];

@@ -20,93 +20,9 @@
 #include "common.hpp"
 #include "dev.hpp"
 #include "decode.hpp"
+#include "decode_dev.hpp"
 
 namespace esp {
-
-constexpr int DG_THREADS = 256;
-constexpr int DG_WAVES = 4;
-constexpr int DG_MAXC = 8;  // max 8-element chunks per lane per row (K <= 4*64*8*8 = 16384)
-
-typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
-typedef float f32x4_t __attribute__((ext_vector_type(4)));
-
-// Cross-block hand-off without flushing L2: partials are written with
-// agent-scope (write-through) stores, the writer waits for its stores to
-// complete (s_waitcnt vmcnt(0)) before taking a ticket, and the last block
-// reads the partials with agent-scope loads.
-__device__ __forceinline__ void st_agent(float *p, float v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void st_agent(int32_t *p, int32_t v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ float ld_agent(const float *p) {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ int32_t ld_agent(const int32_t *p) {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void wait_stores() { __builtin_amdgcn_s_waitcnt(0x0F70); }  // vmcnt(0)
-
-template <typename WT> struct Chunk;
-template <> struct Chunk<uint16_t> {  // 8 bf16 = 16 bytes
-    u32x4_t v;
-    __device__ __forceinline__ void load(const uint16_t *p) {
-        v = __builtin_nontemporal_load((const u32x4_t *)p);
-    }
-    __device__ __forceinline__ float dot(const float *x) const {
-        float s = 0.f;
-        s += __uint_as_float(v.x << 16) * x[0];
-        s += __uint_as_float(v.x & 0xffff0000u) * x[1];
-        s += __uint_as_float(v.y << 16) * x[2];
-        s += __uint_as_float(v.y & 0xffff0000u) * x[3];
-        s += __uint_as_float(v.z << 16) * x[4];
-        s += __uint_as_float(v.z & 0xffff0000u) * x[5];
-        s += __uint_as_float(v.w << 16) * x[6];
-        s += __uint_as_float(v.w & 0xffff0000u) * x[7];
-        return s;
-    }
-};
-template <> struct Chunk<float> {  // 8 f32 = 2 x 16 bytes
-    f32x4_t a, b;
-    __device__ __forceinline__ void load(const float *p) {
-        a = __builtin_nontemporal_load((const f32x4_t *)p);
-        b = __builtin_nontemporal_load((const f32x4_t *)p + 1);
-    }
-    __device__ __forceinline__ float dot(const float *x) const {
-        float s = 0.f;
-        s += a.x * x[0];
-        s += a.y * x[1];
-        s += a.z * x[2];
-        s += a.w * x[3];
-        s += b.x * x[4];
-        s += b.y * x[5];
-        s += b.z * x[6];
-        s += b.w * x[7];
-        return s;
-    }
-};
-
-// rows handled per unit: SWIGLU and QKVROPE units are row pairs
-template <int EPI> struct RowsPerUnit { static constexpr int v = 1; };
-template <> struct RowsPerUnit<DG_SWIGLU> { static constexpr int v = 2; };
-template <> struct RowsPerUnit<DG_QKVROPE> { static constexpr int v = 2; };
-
-constexpr int DG_MAX_IT = 64;  // grid-stride iterations per block
-
-// Sum over all 64 lanes, returned wave-uniform: DPP sums inside each
-// 16-lane row, then the four row sums read out in a fixed order.
-__device__ __forceinline__ float wave_sum_uniform(float v) {
-    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));
-    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));
-    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x141, 0xF, 0xF, false));
-    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x140, 0xF, 0xF, false));
-    const int b = __builtin_bit_cast(int, v);
-    return ((__builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 0)) +
-             __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 16))) +
-            __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 32))) +
-           __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 48));
-}
 
 // NCH = 8-element chunks per lane and row in this wave's quarter of K
 // (K <= 4 * 64 * 8 * NCH). The first iteration's weight loads are issued
@@ -247,6 +163,22 @@ __global__ void __launch_bounds__(DG_THREADS) decode_gemv_k(DecodeGemvArgs a) {
             if (a.bias) {
                 v0 = v0 + a.bias[r0];
                 v1 = v1 + a.bias[r1];
+            }
+            if (a.lora_t) {  // unmerged LoRA, before RoPE (lora.rs:93-97)
+                const int j = head < a.nq ? 0 : (head < a.nq + a.nkv ? 1 : 2);
+                if (a.lora_b[j]) {
+                    const WT *B = (const WT *)a.lora_b[j];
+                    const int rank = a.lora_rank[j];
+                    const int off = j == 0 ? 0 : (j == 1 ? a.nq * hd : (a.nq + a.nkv) * hd);
+                    const float *t = a.lora_t + a.lora_t_col[j];
+                    float c0 = 0.f, c1 = 0.f;
+                    for (int i = 0; i < rank; ++i) {
+                        c0 += ld(B, (size_t)(r0 - off) * rank + i) * t[i];
+                        c1 += ld(B, (size_t)(r1 - off) * rank + i) * t[i];
+                    }
+                    v0 = v0 + c0 * a.lora_scale[j];
+                    v1 = v1 + c1 * a.lora_scale[j];
+                }
             }
             const int pos = a.row_pos[0], seq = a.row_seq[0];
             const float *cs = a.rope_cos + (size_t)pos * hd;
@@ -422,18 +354,6 @@ constexpr int ATT_MAX_SPLIT = 128;
 constexpr int ATT_WAVES = 4;     // waves per attention block
 constexpr int ATT_CHUNK = 128;  // keys whose K/V loads a block issues at once
 constexpr int ATT_PSTRIDE_PAD = ATT_PART_PAD;  // partial row: m, l, 2 pad, acc[hd]
-
-// Sum over aligned groups of N lanes (N = 8 or 16) with DPP lane swaps:
-// quad xor 1, quad xor 2, half-row mirror (8 lanes), row mirror (16 lanes).
-template <int N> __device__ __forceinline__ float group_sum(float v) {
-    static_assert(N == 8 || N == 16, "group_sum: 8 or 16 lanes");
-    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));
-    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));
-    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x141, 0xF, 0xF, false));
-    if (N == 16)
-        v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x140, 0xF, 0xF, false));
-    return v;
-}
 
 // One block per (key split, kv head, row). A key is covered by a group of
 // hd/8 lanes (8 dims each), so a wave scores 64*8/hd keys per step and a

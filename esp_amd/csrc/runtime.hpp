@@ -73,6 +73,9 @@ struct Model {
     std::vector<std::unique_ptr<DevMem>> mem;
     uint64_t weight_bytes = 0;
     int device = 0;
+    // persistent decode-step kernel: -1 not decided, 0 not usable, 1 usable
+    int step_mode = -1;
+    std::unique_ptr<DevMem> step_layers;  // StepLayer[L]
 
     void *alloc(size_t bytes) {
         mem.emplace_back(new DevMem(bytes));
