@@ -53,6 +53,49 @@ def decode_bytes(cfg, ctx: int, kv_bytes_per_elem: int = 4, lora_rank: int = 0,
     return {"gemv_weights": L * layer_w + head_w, "kv": kv, "total": L * layer_w + head_w + kv}
 
 
+def mlp_gemv_bytes(cfg) -> int:
+    """Algorithmic bytes of one decode SwiGLU GEMV launch: gate and up rows
+    (bf16, F x H each), the input row and RMSNorm weight (f32, H each), the
+    activation row written (f32, F)."""
+    H, F = cfg.hidden_size, cfg.intermediate_size
+    return 2 * F * H * 2 + 2 * H * 4 + F * 4
+
+
+def measured_traffic(name: str = "decode_gemv_mlp_c2_traffic.md"):
+    """HBM bytes per launch of the roofline kernel from the committed
+    FETCH_SIZE / WRITE_SIZE counter summary (profiles/), or None."""
+    path = os.path.join(ROOT, "profiles", name)
+    try:
+        for line in open(path):
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(line.split(":")[1])
+    except OSError:
+        pass
+    return None
+
+
+def traffic_run(steps: int = 8) -> None:
+    """Workload for the FETCH_SIZE / WRITE_SIZE counter passes: one plain
+    device-to-device copy of known size (the calibration dispatch), then a
+    C2 prefill and `steps` eager decode steps (the SwiGLU GEMV dispatches)."""
+    import torch
+    from esp_amd import DecoderModel
+    from tests.synth import uniform_ids
+    n = 64 << 20
+    src = torch.ones(n, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    cfg = c2_config()
+    model = DecoderModel.synthetic(cfg, seed=1234, std=0.02, fmt="bf16")
+    kv = model.new_cache(1, 600)
+    model.try_forward_cached_last(uniform_ids(42, 512, cfg.vocab_size), kv)
+    for i in range(steps):
+        model.try_forward_cached_last([i + 1], kv)
+    print(json.dumps({"copy_bytes": n * 4, "mlp_gemv_bytes": mlp_gemv_bytes(cfg),
+                      "decode_steps": steps}), flush=True)
+
+
 def prefill_flops(cfg, S: int) -> float:
     H, L, F, V = cfg.hidden_size, cfg.num_hidden_layers, cfg.intermediate_size, cfg.vocab_size
     qw, kvw, hd, nq = cfg.query_width(), cfg.kv_heads() * cfg.head_dim(), cfg.head_dim(), \
@@ -175,6 +218,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-c3", action="store_true")
     ap.add_argument("--only-c3", action="store_true")
+    ap.add_argument("--traffic", action="store_true",
+                    help="run only the workload of the HBM-traffic counter passes")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 "
@@ -184,6 +229,9 @@ def main():
     from esp_amd.model import profile_enable, profile_read
     from tests.synth import uniform_ids
 
+    if args.traffic:
+        traffic_run()
+        return
     if args.only_c3:
         print(json.dumps({"c3": c3_bench(max(1, args.steps))}), flush=True)
         return
@@ -222,27 +270,28 @@ def main():
     avg_ctx = args.prompt + args.decode / 2
     db = decode_bytes(cfg, int(avg_ctx))
     # profiled pass: per-launch HIP events on the KV stream. The dominant
-    # kernel is the persistent decode step (one launch = embedding, every
-    # layer and the head for one token: all weights + the K/V cache read
-    # once); with ESP_STEP=0 it is the GEMV family of the per-kernel path.
-    for fam in ("step", "gemv"):
+    # decode kernel is the SwiGLU GEMV (decode_gemv_k, gate+up: the largest
+    # per-layer weight stream); with ESP_STEP=1 it is the persistent step
+    # kernel (one launch = all layers + head: every weight + the K/V once).
+    fams = ("step", "gemv_mlp")
+    for fam in fams:
         profile_enable(fam, True)
     gen_eager_steps = 16
     kv2 = model.new_cache(1, ctx)
     kv2.reset(0)
     model.try_forward_cached_last(prompt, kv2)
-    before = {fam: profile_read(fam) for fam in ("step", "gemv")}
+    before = {fam: profile_read(fam) for fam in fams}
     for i in range(gen_eager_steps):
         model.try_forward_cached_last([i + 1], kv2)
-    after = {fam: profile_read(fam) for fam in ("step", "gemv")}
-    for fam in ("step", "gemv"):
+    after = {fam: profile_read(fam) for fam in fams}
+    for fam in fams:
         profile_enable(fam, False)
     if after["step"][0] > before["step"][0]:
         fam, kname = "step", "step_k (persistent decode step: all layers + head)"
         fam_bytes = sum(decode_bytes(cfg, args.prompt + i + 1)["total"] for i in range(gen_eager_steps))
     else:
-        fam, kname = "gemv", "gemv (decode projections + head)"
-        fam_bytes = db["gemv_weights"] * gen_eager_steps
+        fam, kname = "gemv_mlp", "decode_gemv_k<bf16, SWIGLU> (gate+up projections, fused RMSNorm)"
+        fam_bytes = mlp_gemv_bytes(cfg) * (after[fam][0] - before[fam][0])
     gemv_launches = after[fam][0] - before[fam][0]
     gemv_ms = after[fam][1] - before[fam][1]
     gemv_gbs = fam_bytes / (gemv_ms / 1e3) / 1e9
@@ -269,7 +318,8 @@ def main():
         "decode_hbm_frac": round(db["total"] / (t_dec / n_dec) / 1e9 / HBM_PEAK_GBS, 4),
         "roofline": {"bound": "hbm", "kernel": kname,
                      "achieved": round(gemv_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gemv_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(gemv_gbs / HBM_PEAK_GBS, 4),
+                     "traffic": measured_traffic() if fam == "gemv_mlp" else None,
                      "launches": gemv_launches,
                      "avg_launch_us": round(gemv_ms / max(1, gemv_launches) * 1e3, 3)},
     }

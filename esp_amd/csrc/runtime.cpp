@@ -564,7 +564,7 @@ static void run_layer_decode(Model &m, Kv &kv, const Rows &rows, LayerW &w, int 
             t.y = kv.qkv.as<float>() + qkv_n;
             t.N = w.qkv_rows - qkv_n;
             t.K = H;
-            Prof p("gemv", s);
+            Prof p("gemv_lora", s);
             launch_decode_gemv(m.wt, DG_STORE, t, s);
         }
         DecodeGemvArgs g{};
@@ -596,7 +596,7 @@ static void run_layer_decode(Model &m, Kv &kv, const Rows &rows, LayerW &w, int 
                 g.lora_scale[j] = w.lora_scale[j];
             }
         }
-        Prof p("gemv", s);
+        Prof p("gemv_qkv", s);
         launch_decode_gemv(m.wt, DG_QKVROPE, g, s);
     } else {
         if (decode_gemv_ok(H)) {
@@ -609,7 +609,7 @@ static void run_layer_decode(Model &m, Kv &kv, const Rows &rows, LayerW &w, int 
             g.y = kv.qkv.as<float>();
             g.N = w.qkv_rows;
             g.K = H;
-            Prof p("gemv", s);
+            Prof p("gemv_qkv", s);
             launch_decode_gemv(m.wt, DG_STORE, g, s);
         } else {
             GemvArgs g{};
@@ -693,7 +693,7 @@ static void run_layer_decode(Model &m, Kv &kv, const Rows &rows, LayerW &w, int 
         Prof p("attention", s);
         launch_attention(kv.dt, a, s);
     }
-    auto resid = [&](const void *wt, const float *x, const float *bias, int N, int K) {
+    auto resid = [&](const char *fam, const void *wt, const float *x, const float *bias, int N, int K) {
         if (decode_gemv_ok(K)) {
             DecodeGemvArgs g{};
             g.w = wt;
@@ -702,7 +702,7 @@ static void run_layer_decode(Model &m, Kv &kv, const Rows &rows, LayerW &w, int 
             g.y = kv.h.as<float>();
             g.N = N;
             g.K = K;
-            Prof p("gemv", s);
+            Prof p(fam, s);
             launch_decode_gemv(m.wt, DG_RESID, g, s);
         } else {
             GemvArgs g{};
@@ -712,11 +712,11 @@ static void run_layer_decode(Model &m, Kv &kv, const Rows &rows, LayerW &w, int 
             g.y = kv.h.as<float>();
             g.N = N;
             g.K = K;
-            Prof p("gemv", s);
+            Prof p(fam, s);
             launch_gemv(m.wt, GEMV_RESIDUAL, g, s);
         }
     };
-    resid(w.o, kv.attn.as<float>(), w.o_bias, H, m.qw);
+    resid("gemv_o", w.o, kv.attn.as<float>(), w.o_bias, H, m.qw);
     if (w.moe) {
         moe_block(m, kv, w, 1, s);
         return;
@@ -731,7 +731,7 @@ static void run_layer_decode(Model &m, Kv &kv, const Rows &rows, LayerW &w, int 
         g.y = kv.act.as<float>();
         g.N = m.F;
         g.K = H;
-        Prof p("gemv", s);
+        Prof p("gemv_mlp", s);
         launch_decode_gemv(m.wt, DG_SWIGLU, g, s);
     } else {
         GemvArgs g{};
@@ -743,10 +743,10 @@ static void run_layer_decode(Model &m, Kv &kv, const Rows &rows, LayerW &w, int 
         g.y = kv.act.as<float>();
         g.N = m.F;
         g.K = H;
-        Prof p("gemv", s);
+        Prof p("gemv_mlp", s);
         launch_gemv(m.wt, GEMV_SWIGLU, g, s);
     }
-    resid(w.down, kv.act.as<float>(), nullptr, H, m.F);
+    resid("gemv_down", w.down, kv.act.as<float>(), nullptr, H, m.F);
 }
 
 // One pass of `Mc` rows (already on the device at `rows`) through all layers.
@@ -1001,7 +1001,7 @@ static void run_head(Model &m, Kv &kv, int n_seqs, const float *h_src, const int
         g.part_i = t + 4096 + 8 + DG_MAX_PART;
         g.picked = (uint32_t *)(t + 4096 + 8 + 2 * DG_MAX_PART);
         g.gen = gen;
-        Prof p("gemv", s);
+        Prof p("gemv_head", s);
         launch_decode_gemv(m.wt, DG_HEAD, g, s);
         return;
     }
