@@ -44,6 +44,7 @@ struct Rows {
     const int32_t *row_seq;  // [M]
     const int32_t *row_pos;  // [M]
     int M;
+    int seq1 = -1;           // >= 0: every row belongs to this sequence
 };
 
 // h[M,H] (f32) = embed[ids[m]] (wt)

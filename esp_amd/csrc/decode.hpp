@@ -45,17 +45,25 @@ struct AttnDecodeArgs {
     const float *kv;      // layer base of the f32 cache
     long long seq_stride, kv_half_stride, head_stride;
     const int32_t *row_pos, *row_seq;
+    int seq1;             // >= 0: every row belongs to this sequence (row_seq unread)
     int M, nq, nkv, hd, window;
+    int max_t;            // plan bound: every row's position is below it
     int n_split, split_len;
     float *part;          // [M, nq, n_split, hd + 4]
     int32_t *ticket;      // [M, nkv] zero-initialised
-    float *out;           // [M, nq*hd]
+    float *out;           // [M, nq*hd] f32, or the bf16 hi plane when out_lo is set
+    uint16_t *out_lo;     // nullable: bf16 lo plane (split activation output)
+    int xcd_nx;           // set by the launcher: merge protocol (0 = agent scope)
 };
 
 bool attn_decode_ok(int hd, int G);
-// key splits and keys per split for a decode row over max_t cached keys
-int attn_decode_splits(int hd, int nkv, int G, int max_t, int *split_len);
+// key splits and keys per split for M decode rows over max_t cached keys
+int attn_decode_splits(int hd, int nkv, int G, int M, int max_t, int *split_len);
+constexpr int ATT_MAX_TICKETS = 4096;  // (row, kv head) merge tickets at the start of Kv::tickets
 constexpr int ATT_PART_PAD = 4;  // partial row = hd + ATT_PART_PAD floats
 void launch_attn_decode(const AttnDecodeArgs &a, hipStream_t s);
+// XCD count of the XCD-local split merge, or 0 for the agent-scope merge
+// (probed once per process; environment ESP_ATT_XCD=0 forces 0)
+int attn_xcd_mode();
 
 }  // namespace esp

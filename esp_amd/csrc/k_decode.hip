@@ -17,6 +17,10 @@
 // attn_decode_k: causal GQA attention for one query row per (kv head, key
 // split), online softmax in registers; the last split to finish for a
 // (row, kv head) merges the partials in split order (deterministic).
+#include <algorithm>
+#include <cstdlib>
+#include <vector>
+
 #include "common.hpp"
 #include "dev.hpp"
 #include "decode.hpp"
@@ -351,87 +355,194 @@ void launch_decode_gemv(Dt wt, int epi, const DecodeGemvArgs &a, hipStream_t s) 
 // ------------------------------------------------------------ attention
 
 constexpr int ATT_MAX_SPLIT = 128;
-constexpr int ATT_WAVES = 4;     // waves per attention block
-constexpr int ATT_CHUNK = 128;  // keys whose K/V loads a block issues at once
-constexpr int ATT_PSTRIDE_PAD = ATT_PART_PAD;  // partial row: m, l, 2 pad, acc[hd]
+constexpr int ATT_WAVES = 8;      // waves per attention block (two per SIMD)
+constexpr int ATT_MB = 32;        // splits whose partials one merge batch loads at once
 
-// One block per (key split, kv head, row). A key is covered by a group of
-// hd/8 lanes (8 dims each), so a wave scores 64*8/hd keys per step and a
-// dot product is finished with DPP swaps inside the group. A chunk of
-// ATT_CHUNK keys has all its K/V loads issued before any score is formed,
-// and the softmax update is done once per chunk (one exp per key). GM is
-// the largest query-head group the instance serves (4 or 8).
-template <int HD, int GM>
+// Steps (of ATT_WAVES * 64 * 8 / HD keys) whose K/V loads a block keeps in
+// flight together: 16 VGPRs per step and lane.
+template <int GM> struct AttSteps { static constexpr int v = GM <= 4 ? 5 : 3; };
+
+// Both values of the lane pair (lane, lane ^ X), lower lane first, in every
+// lane of the pair: X = 32 and 16 with the gfx950 permlane swaps, X = 8 with
+// a DPP rotate by 8 inside each 16-lane row.
+template <int X> __device__ __forceinline__ void lane_pair(float v, float &lo, float &hi) {
+    if constexpr (X == 32) {
+        const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+        lo = __uint_as_float(r[0]);
+        hi = __uint_as_float(r[1]);
+    } else if constexpr (X == 16) {
+        const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+        lo = __uint_as_float(r[0]);
+        hi = __uint_as_float(r[1]);
+    } else {
+        static_assert(X == 8, "lane_pair: X = 8, 16 or 32");
+        const float o = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x128, 0xF, 0xF, false));
+        const bool low = (threadIdx.x & 8) == 0;
+        lo = low ? v : o;
+        hi = low ? o : v;
+    }
+}
+
+// Merges the online-softmax states (m, l, acc[8]) of lane pairs (lane, lane ^ X).
+template <int X, int GM>
+__device__ __forceinline__ void att_pair_merge(int G, float (&m)[GM], float (&l)[GM], float (&acc)[GM][8]) {
+#pragma unroll
+    for (int j = 0; j < GM; ++j) {
+        if (j >= G) break;
+        float m0, m1, l0, l1;
+        lane_pair<X>(m[j], m0, m1);
+        lane_pair<X>(l[j], l0, l1);
+        const float mn = fmaxf(m0, m1);
+        const float w0 = mn == -INFINITY ? 0.f : __expf(m0 - mn);
+        const float w1 = mn == -INFINITY ? 0.f : __expf(m1 - mn);
+        l[j] = l0 * w0 + l1 * w1;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            float a0, a1;
+            lane_pair<X>(acc[j][i], a0, a1);
+            acc[j][i] = a0 * w0 + a1 * w1;
+        }
+        m[j] = mn;
+    }
+}
+
+__device__ __forceinline__ void att_store(const AttnDecodeArgs &a, size_t i, float v) {
+    if (a.out_lo) {
+        const uint16_t h = f2bf(v);
+        ((uint16_t *)a.out)[i] = h;
+        a.out_lo[i] = f2bf(v - bf2f(h));
+    } else {
+        a.out[i] = v;
+    }
+}
+
+// One block of ATT_WAVES waves per (key split, kv head, row): a 1-D grid
+// whose block -> work mapping depends on the merge protocol (below). A key
+// is covered by a group of hd/8 lanes; lane `sub` of the group holds dims
+// [4 sub, 4 sub + 4) and [hd/2 + 4 sub, hd/2 + 4 sub + 4), so each 16-byte
+// load of the group covers a contiguous hd/2 * 4 bytes of the key row, and
+// a dot product is finished with DPP swaps inside the group. The loads of
+// the first chunk of the split (up to AttSteps steps) are issued before the
+// row's position is known: they cover the split's planned range (clamped to
+// max_t, the plan's key bound; lanes past the range load nothing) and keys
+// past the position are masked afterwards, so the position read and the K/V
+// stream overlap. The softmax update runs once per chunk (one exp per key).
+// The key groups of a wave merge through lane-pair swaps, the waves through
+// LDS; the last split to finish for a (row, kv head) merges the partials in
+// split order (deterministic), each thread one output with every partial
+// load of a batch in flight at once.
+//
+// Merge protocol. With xcd_nx > 0, the splits of one (row, kv head) are
+// blocks whose linear ids share the residue mod xcd_nx; the dispatcher deals
+// the blocks of a launch to the XCDs round-robin (from a rotating first
+// XCD), so they all run on one XCD and exchange partials through its L2:
+// plain stores, then L1-bypassing loads in the merging block. With
+// xcd_nx == 0 the partials go through agent-scope (write-through) stores and
+// loads instead, which any placement tolerates.
+template <int HD, int GM, bool XCD>
 __global__ void __launch_bounds__(ATT_WAVES * 64) attn_decode_k(AttnDecodeArgs a) {
     constexpr int NW = ATT_WAVES;
+    constexpr int NT = NW * 64;
     constexpr int DPL = 8;               // dims per lane
     constexpr int LPK = HD / DPL;        // lanes per key
     constexpr int KPW = 64 / LPK;        // keys per wave per step
-    constexpr int NS = ATT_CHUNK / (NW * KPW);  // steps per chunk
-    constexpr int GMAX = GM;
-    constexpr int STRIDE = HD + ATT_PSTRIDE_PAD;
-    __shared__ float wm[NW][GMAX], wl[NW][GMAX];
-    __shared__ float wacc[NW][GMAX][HD];
+    constexpr int STEP = NW * KPW;       // keys per block step
+    constexpr int NS = AttSteps<GM>::v;  // steps per chunk
+    constexpr int CH = NS * STEP;        // keys per chunk
+    constexpr int HALF = HD / 2;
+    constexpr int STRIDE = HD + ATT_PART_PAD;
+    __shared__ float wm[NW][GM], wl[NW][GM];
+    __shared__ __attribute__((aligned(16))) float wacc[NW][GM][HD];
     __shared__ int last;
-    const int split = blockIdx.x, g = blockIdx.y, row = blockIdx.z;
+    const int ns = a.n_split, U = a.M * a.nkv;
+    int unit, split;
+    {
+        const int b = blockIdx.x;
+        if (XCD) {
+            const int x = b % a.xcd_nx, i = b / a.xcd_nx;
+            unit = x + a.xcd_nx * (i / ns);
+            split = i % ns;
+            if (unit >= U) return;  // padding block of a short residue class
+        } else {
+            unit = b / ns;
+            split = b % ns;
+        }
+    }
+    const int g = unit % a.nkv, row = unit / a.nkv;
     const int G = a.nq / a.nkv;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int grp = lane / LPK, sub = lane % LPK;
-    const int pos = a.row_pos[row], seq = a.row_seq[row];
-    int lo = a.window > 0 ? max(0, pos - a.window + 1) : 0;
-    int hi = pos + 1;
-    lo = max(lo, split * a.split_len);
-    hi = min(hi, (split + 1) * a.split_len);
-    const float inv_scale = 1.f / sqrtf((float)HD);
-    // q for the group's heads: this lane's 8 dims
-    float q[GMAX][DPL];
-    const float *qrow = a.q + (size_t)row * a.nq * HD + (size_t)g * G * HD + sub * DPL;
+    const int seq = a.seq1 >= 0 ? a.seq1 : a.row_seq[row];
+    const int s0 = split * a.split_len;
+    const int s1 = min(s0 + a.split_len, a.max_t);
+    const float *kb = a.kv + (size_t)seq * a.seq_stride + (size_t)g * a.head_stride + sub * 4;
+    const float *vb = kb + a.kv_half_stride;
+    f32x4_t kk[NS][2], vv[NS][2];
+    // lanes past the chunk end re-read its last key (masked later)
+    auto issue = [&](int c0, int c1) {
 #pragma unroll
-    for (int j = 0; j < GMAX; ++j)
+        for (int st = 0; st < NS; ++st) {
+            if (c0 + st * STEP < c1) {  // block-uniform
+                const int t = min(c0 + st * STEP + wave * KPW + grp, c1 - 1);
+                kk[st][0] = __builtin_nontemporal_load((const f32x4_t *)(kb + (size_t)t * HD));
+                kk[st][1] = __builtin_nontemporal_load((const f32x4_t *)(kb + (size_t)t * HD + HALF));
+                vv[st][0] = __builtin_nontemporal_load((const f32x4_t *)(vb + (size_t)t * HD));
+                vv[st][1] = __builtin_nontemporal_load((const f32x4_t *)(vb + (size_t)t * HD + HALF));
+            }
+        }
+    };
+    issue(s0, min(s0 + CH, s1));
+    // q for the group's heads: this lane's 8 dims
+    float q[GM][DPL];
+    const float *qrow = a.q + (size_t)row * a.nq * HD + (size_t)g * G * HD + sub * 4;
+#pragma unroll
+    for (int j = 0; j < GM; ++j)
         if (j < G) {
             const f32x4_t v0 = *(const f32x4_t *)(qrow + (size_t)j * HD);
-            const f32x4_t v1 = *(const f32x4_t *)(qrow + (size_t)j * HD + 4);
+            const f32x4_t v1 = *(const f32x4_t *)(qrow + (size_t)j * HD + HALF);
             q[j][0] = v0.x; q[j][1] = v0.y; q[j][2] = v0.z; q[j][3] = v0.w;
             q[j][4] = v1.x; q[j][5] = v1.y; q[j][6] = v1.z; q[j][7] = v1.w;
         }
-    float m[GMAX], l[GMAX], acc[GMAX][DPL];
+    const int pos = a.row_pos[row];
+    int lo = a.window > 0 ? max(0, pos - a.window + 1) : 0;
+    int hi = min(pos + 1, a.max_t);
+    lo = max(lo, s0);
+    hi = min(hi, s1);
+    const float inv_scale = 1.f / sqrtf((float)HD);
+    float m[GM], l[GM], acc[GM][DPL];
 #pragma unroll
-    for (int j = 0; j < GMAX; ++j) {
+    for (int j = 0; j < GM; ++j) {
         m[j] = -INFINITY;
         l[j] = 0.f;
 #pragma unroll
         for (int e = 0; e < DPL; ++e) acc[j][e] = 0.f;
     }
-    const float *kb = a.kv + (size_t)seq * a.seq_stride + (size_t)g * a.head_stride + sub * DPL;
-    const float *vb = kb + a.kv_half_stride;
-    for (int c0 = lo; c0 < hi; c0 += ATT_CHUNK) {
-        f32x4_t kk[NS][2], vv[NS][2];
+    for (int c0 = s0; c0 < hi; c0 += CH) {
+        const int c1 = min(c0 + CH, hi);
+        if (c0 > s0) issue(c0, c1);
+        bool ok[NS];
 #pragma unroll
         for (int st = 0; st < NS; ++st) {
-            const int t = c0 + st * NW * KPW + wave * KPW + grp;
-            kk[st][0] = kk[st][1] = vv[st][0] = vv[st][1] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-            if (t < hi) {
-                kk[st][0] = *(const f32x4_t *)(kb + (size_t)t * HD);
-                kk[st][1] = *(const f32x4_t *)(kb + (size_t)t * HD + 4);
-                vv[st][0] = *(const f32x4_t *)(vb + (size_t)t * HD);
-                vv[st][1] = *(const f32x4_t *)(vb + (size_t)t * HD + 4);
-            }
+            const int t = c0 + st * STEP + wave * KPW + grp;
+            ok[st] = t >= lo && t < c1;
+            if (!ok[st]) vv[st][0] = vv[st][1] = f32x4_t{0.f, 0.f, 0.f, 0.f};  // unread or unwritten rows
         }
 #pragma unroll
-        for (int j = 0; j < GMAX; ++j) {
+        for (int j = 0; j < GM; ++j) {
             if (j >= G) break;
             float sc[NS];
             float mx = m[j];
 #pragma unroll
             for (int st = 0; st < NS; ++st) {
                 float d = 0.f;
-#pragma unroll
-                for (int e = 0; e < 4; ++e) d += q[j][e] * kk[st][0][e];
-#pragma unroll
-                for (int e = 0; e < 4; ++e) d += q[j][4 + e] * kk[st][1][e];
-                d = group_sum<LPK>(d);
-                const int t = c0 + st * NW * KPW + wave * KPW + grp;
-                sc[st] = t < hi ? d * inv_scale : -INFINITY;
+                if (c0 + st * STEP < c1) {  // block-uniform
+                    const float d0 = q[j][0] * kk[st][0][0] + q[j][1] * kk[st][0][1];
+                    const float d1 = q[j][2] * kk[st][0][2] + q[j][3] * kk[st][0][3];
+                    const float d2 = q[j][4] * kk[st][1][0] + q[j][5] * kk[st][1][1];
+                    const float d3 = q[j][6] * kk[st][1][2] + q[j][7] * kk[st][1][3];
+                    d = group_sum<LPK>((d0 + d1) + (d2 + d3));
+                }
+                sc[st] = ok[st] ? d * inv_scale : -INFINITY;
                 mx = fmaxf(mx, sc[st]);
             }
             if (mx == -INFINITY) continue;  // no key of this lane's group in the chunk yet
@@ -441,37 +552,28 @@ __global__ void __launch_bounds__(ATT_WAVES * 64) attn_decode_k(AttnDecodeArgs a
             for (int e = 0; e < DPL; ++e) acc[j][e] *= al;
 #pragma unroll
             for (int st = 0; st < NS; ++st) {
-                const float p = __expf(sc[st] - mx);
-                l[j] += p;
+                if (c0 + st * STEP < c1) {
+                    const float p = __expf(sc[st] - mx);
+                    l[j] += p;
 #pragma unroll
-                for (int e = 0; e < 4; ++e) acc[j][e] += p * vv[st][0][e];
+                    for (int e = 0; e < 4; ++e) acc[j][e] += p * vv[st][0][e];
 #pragma unroll
-                for (int e = 0; e < 4; ++e) acc[j][4 + e] += p * vv[st][1][e];
+                    for (int e = 0; e < 4; ++e) acc[j][4 + e] += p * vv[st][1][e];
+                }
             }
             m[j] = mx;
         }
     }
-    // merge the KPW key groups of the wave (lanes with equal `sub`)
+    // merge the KPW key groups of the wave: lane pairs at distance LPK .. 32
+    if constexpr (LPK <= 8) att_pair_merge<8, GM>(G, m, l, acc);
+    if constexpr (LPK <= 16) att_pair_merge<16, GM>(G, m, l, acc);
+    att_pair_merge<32, GM>(G, m, l, acc);
+    if (grp == 0) {
 #pragma unroll
-    for (int j = 0; j < GMAX; ++j) {
-        if (j >= G) break;
-#pragma unroll
-        for (int o = LPK; o < 64; o <<= 1) {
-            float om = __shfl_xor(m[j], o, 64), ol = __shfl_xor(l[j], o, 64);
-            float mn = fmaxf(m[j], om);
-            float s1 = mn == -INFINITY ? 0.f : __expf(m[j] - mn);
-            float s2 = mn == -INFINITY ? 0.f : __expf(om - mn);
-            l[j] = l[j] * s1 + ol * s2;
-#pragma unroll
-            for (int i = 0; i < DPL; ++i) {
-                float oa = __shfl_xor(acc[j][i], o, 64);
-                acc[j][i] = acc[j][i] * s1 + oa * s2;
-            }
-            m[j] = mn;
-        }
-        if (grp == 0) {
-#pragma unroll
-            for (int i = 0; i < DPL; ++i) wacc[wave][j][sub * DPL + i] = acc[j][i];
+        for (int j = 0; j < GM; ++j) {
+            if (j >= G) break;
+            *(f32x4_t *)&wacc[wave][j][sub * 4] = f32x4_t{acc[j][0], acc[j][1], acc[j][2], acc[j][3]};
+            *(f32x4_t *)&wacc[wave][j][HALF + sub * 4] = f32x4_t{acc[j][4], acc[j][5], acc[j][6], acc[j][7]};
             if (sub == 0) {
                 wm[wave][j] = m[j];
                 wl[wave][j] = l[j];
@@ -480,101 +582,124 @@ __global__ void __launch_bounds__(ATT_WAVES * 64) attn_decode_k(AttnDecodeArgs a
     }
     __syncthreads();
     // merge the waves; write this split's partial (m, l, -, -, acc[HD]) per head
-    for (int o = tid; o < G * HD; o += blockDim.x) {
-        int j = o / HD, d = o % HD;
+    for (int o = tid; o < G * HD; o += NT) {
+        const int j = o / HD, d = o % HD;
         float mx = -INFINITY;
+#pragma unroll
         for (int w = 0; w < NW; ++w) mx = fmaxf(mx, wm[w][j]);
         float L = 0.f, v = 0.f;
+#pragma unroll
         for (int w = 0; w < NW; ++w) {
-            float sc = mx == -INFINITY ? 0.f : __expf(wm[w][j] - mx);
+            const float sc = mx == -INFINITY ? 0.f : __expf(wm[w][j] - mx);
             L += wl[w][j] * sc;
             v += wacc[w][j][d] * sc;
         }
-        if (a.n_split == 1) {  // single split: normalise directly
-            a.out[(size_t)row * a.nq * HD + (size_t)(g * G + j) * HD + d] = v / L;
+        if (ns == 1) {  // single split: normalise directly
+            att_store(a, (size_t)row * a.nq * HD + (size_t)(g * G + j) * HD + d, v / L);
             continue;
         }
-        float *p = a.part + (((size_t)row * a.nq + (size_t)g * G + j) * a.n_split + split) * STRIDE;
-        st_agent(p + ATT_PSTRIDE_PAD + d, v);
-        if (d == 0) {
-            st_agent(p, mx);
-            st_agent(p + 1, L);
+        float *p = a.part + (((size_t)row * a.nq + (size_t)g * G + j) * ns + split) * STRIDE;
+        if (XCD) {
+            p[ATT_PART_PAD + d] = v;
+            if (d == 0) {
+                p[0] = mx;
+                p[1] = L;
+            }
+        } else {
+            st_agent(p + ATT_PART_PAD + d, v);
+            if (d == 0) {
+                st_agent(p, mx);
+                st_agent(p + 1, L);
+            }
         }
     }
-    if (a.n_split == 1) return;
+    if (ns == 1) return;
     wait_stores();
     __syncthreads();
     if (tid == 0) {
-        int *tk = a.ticket + (size_t)row * a.nkv + g;
-        int t = atomicAdd(tk, 1);
-        last = t == a.n_split - 1;
+        int *tk = a.ticket + unit;
+        const int t = atomicAdd(tk, 1);
+        last = t == ns - 1;
         if (last) *tk = 0;
     }
     __syncthreads();
     if (!last) return;
-    // Merge in the last block. Split maxima / sums go to LDS; each head's
-    // weights exp(m_s - max) and total are reduced across one wave; then
-    // every thread issues its partial loads (up to 32 splits x 2 outputs)
-    // at once and weights them in split order, so the result is
-    // deterministic.
-    __shared__ float mm[GMAX][ATT_MAX_SPLIT], ww[GMAX][ATT_MAX_SPLIT], LL[GMAX];
-    const int ns = a.n_split;
+    // Merge in the last block, splits in batches of ATT_MB: each thread owns
+    // four consecutive outputs of one head and issues its 16-byte partial
+    // loads of the batch first; the batch's (m, l) pairs are read once into
+    // LDS meanwhile. A running maximum carries across batches; splits are
+    // summed in order (deterministic). Offsets past the last split are
+    // clamped (their weight is zero), so the loads carry no predicates.
+    __shared__ float bm_[GM][ATT_MB], bl_[GM][ATT_MB];
     const float *pb = a.part + ((size_t)row * a.nq + (size_t)g * G) * ns * STRIDE;
-    for (int i = tid; i < G * ns; i += blockDim.x) {
-        const int j = i / ns, sp = i % ns;
-        mm[j][sp] = ld_agent(pb + ((size_t)j * ns + sp) * STRIDE);
-        ww[j][sp] = ld_agent(pb + ((size_t)j * ns + sp) * STRIDE + 1);
-    }
-    __syncthreads();
-    for (int j = wave; j < G; j += NW) {
-        const int s0 = lane, s1 = lane + 64;  // ns <= 128
-        const float m0 = s0 < ns ? mm[j][s0] : -INFINITY, m1 = s1 < ns ? mm[j][s1] : -INFINITY;
-        const float mx = wave_max(fmaxf(m0, m1));
-        const float w0 = m0 == -INFINITY ? 0.f : __expf(m0 - mx);
-        const float w1 = m1 == -INFINITY ? 0.f : __expf(m1 - mx);
-        const float L = wave_sum((s0 < ns ? ww[j][s0] * w0 : 0.f) + (s1 < ns ? ww[j][s1] * w1 : 0.f));
-        if (s0 < ns) ww[j][s0] = w0;
-        if (s1 < ns) ww[j][s1] = w1;
-        if (lane == 0) LL[j] = L;
-    }
-    __syncthreads();
-    constexpr int MB = 32;  // splits per load batch
-    for (int o0 = tid; o0 < G * HD; o0 += 2 * blockDim.x) {
-        const int o1 = o0 + blockDim.x;
-        const bool has1 = o1 < G * HD;
-        const int j0 = o0 / HD, d0 = o0 % HD, j1 = has1 ? o1 / HD : j0, d1 = has1 ? o1 % HD : d0;
-        const float *p0 = pb + (size_t)j0 * ns * STRIDE + ATT_PSTRIDE_PAD + d0;
-        const float *p1 = pb + (size_t)j1 * ns * STRIDE + ATT_PSTRIDE_PAD + d1;
-        float v0 = 0.f, v1 = 0.f;
-        for (int sp0 = 0; sp0 < ns; sp0 += MB) {
-            float t0[MB], t1[MB];
-#pragma unroll
-            for (int q = 0; q < MB; ++q) {
-                t0[q] = sp0 + q < ns ? ld_agent(p0 + (size_t)(sp0 + q) * STRIDE) : 0.f;
-                t1[q] = has1 && sp0 + q < ns ? ld_agent(p1 + (size_t)(sp0 + q) * STRIDE) : 0.f;
-            }
-#pragma unroll
-            for (int q = 0; q < MB; ++q) {
-                if (sp0 + q < ns) {
-                    v0 += t0[q] * ww[j0][sp0 + q];
-                    v1 += t1[q] * ww[j1][sp0 + q];
-                }
-            }
+    const int o4 = tid * 4;
+    const bool own = o4 < G * HD;  // wave-uniform
+    const int j = own ? o4 / HD : 0, d = own ? o4 % HD : 0;
+    // L1-bypassing (sc0) loads of this unit's partial rows
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)pb, (short)0, G * ns * STRIDE * (int)sizeof(float), 0x00020000);
+    auto ld4 = [&](int off) -> f32x4_t {
+        if (XCD) return __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rs, off * 4, 0, 1));
+        const float *pp = pb + off;
+        return f32x4_t{ld_agent(pp), ld_agent(pp + 1), ld_agent(pp + 2), ld_agent(pp + 3)};
+    };
+    auto ld2 = [&](int off, float &x, float &y) {
+        if (XCD) {
+            const auto r = __builtin_amdgcn_raw_buffer_load_b64(rs, off * 4, 0, 1);
+            x = __uint_as_float(r[0]);
+            y = __uint_as_float(r[1]);
+        } else {
+            x = ld_agent(pb + off);
+            y = ld_agent(pb + off + 1);
         }
-        a.out[(size_t)row * a.nq * HD + (size_t)(g * G + j0) * HD + d0] = v0 / LL[j0];
-        if (has1) a.out[(size_t)row * a.nq * HD + (size_t)(g * G + j1) * HD + d1] = v1 / LL[j1];
+    };
+    float M = -INFINITY, L = 0.f;
+    f32x4_t V = {0.f, 0.f, 0.f, 0.f};
+    for (int sp0 = 0; sp0 < ns; sp0 += ATT_MB) {
+        f32x4_t tv[ATT_MB];
+        if (own) {
+#pragma unroll
+            for (int q = 0; q < ATT_MB; ++q)
+                tv[q] = ld4((j * ns + min(sp0 + q, ns - 1)) * STRIDE + ATT_PART_PAD + d);
+        }
+        __syncthreads();  // previous batch's (m, l) reads are done
+        if (tid < G * ATT_MB) {
+            const int jj = tid / ATT_MB, q = tid % ATT_MB;
+            float mv, lv;
+            ld2((jj * ns + min(sp0 + q, ns - 1)) * STRIDE, mv, lv);
+            bm_[jj][q] = sp0 + q < ns ? mv : -INFINITY;
+            bl_[jj][q] = lv;
+        }
+        __syncthreads();
+        if (!own) continue;
+        float bmax = M;
+#pragma unroll
+        for (int q = 0; q < ATT_MB; ++q) bmax = fmaxf(bmax, bm_[j][q]);
+        if (bmax == -INFINITY) continue;
+        const float r = __expf(M - bmax);
+        L *= r;
+        V *= r;
+#pragma unroll
+        for (int q = 0; q < ATT_MB; ++q) {
+            const float w = __expf(bm_[j][q] - bmax);
+            L += bl_[j][q] * w;
+            V += tv[q] * w;
+        }
+        M = bmax;
+    }
+    if (own) {
+        const size_t oi = (size_t)row * a.nq * HD + (size_t)g * G * HD + o4;
+        const float inv = 1.f / L;
+        att_store(a, oi, V.x * inv);
+        att_store(a, oi + 1, V.y * inv);
+        att_store(a, oi + 2, V.z * inv);
+        att_store(a, oi + 3, V.w * inv);
     }
 }
 
 bool attn_decode_ok(int hd, int G) { return (hd == 64 || hd == 128) && G <= 8; }
 
-template <int HD, int GM> static int attn_resident_blocks() {
-    static int per_cu = 0;
-    if (!per_cu) {
-        ESP_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(
-            &per_cu, reinterpret_cast<const void *>(attn_decode_k<HD, GM>), ATT_WAVES * 64, 0));
-        if (per_cu <= 0) per_cu = 1;
-    }
+static int device_cus() {
     static int cus = 0;
     if (!cus) {
         int dev = 0;
@@ -582,40 +707,97 @@ template <int HD, int GM> static int attn_resident_blocks() {
         ESP_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
         if (cus <= 0) cus = 256;
     }
-    return per_cu * cus;
+    return cus;
 }
 
-// Key splits for one decode row: as many splits as keep every (split, kv
-// head) block resident at once (one round of blocks), at most 64 (hd 128)
-// or 128 (hd 64) since the merge re-reads every split's partial; split
-// lengths are multiples of 32 keys, and a split up to ATT_CHUNK keys is
-// read in one round of loads.
-int attn_decode_splits(int hd, int nkv, int G, int max_t, int *split_len) {
-    int slots = hd == 64 ? (G <= 4 ? attn_resident_blocks<64, 4>() : attn_resident_blocks<64, 8>())
-                         : (G <= 4 ? attn_resident_blocks<128, 4>() : attn_resident_blocks<128, 8>());
-    const int cap = hd == 64 ? ATT_MAX_SPLIT : ATT_MAX_SPLIT / 2;
-    int ns = slots / (nkv > 0 ? nkv : 1);
-    ns = ns < 1 ? 1 : (ns > cap ? cap : ns);
+// Key splits for M decode rows over max_t cached keys: about one block per
+// CU in total (rows x kv heads x splits), but no split shorter than one block
+// step while the rows alone do not fill the chip; split lengths are
+// multiples of the keys one wave covers per step; at most ATT_MAX_SPLIT
+// splits.
+int attn_decode_splits(int hd, int nkv, int G, int M, int max_t, int *split_len) {
+    (void)G;
+    const int kpw = 64 * 8 / hd, step = ATT_WAVES * kpw;
+    const int target = device_cus();
+    const long long base = (long long)M * (nkv > 0 ? nkv : 1);
+    int ns = (int)((target + base - 1) / base);
+    ns = std::min(ns, (max_t + step - 1) / step);
+    ns = std::max(1, std::min(ns, ATT_MAX_SPLIT));
     int len = (max_t + ns - 1) / ns;
-    len = len < 32 ? 32 : (len + 31) / 32 * 32;
+    len = std::max(kpw, (len + kpw - 1) / kpw * kpw);
     ns = (max_t + len - 1) / len;
     if (ns < 1) ns = 1;
     *split_len = len;
     return ns;
 }
 
-void launch_attn_decode(const AttnDecodeArgs &a, hipStream_t s) {
+// Probe of the dispatch order the XCD-local merge relies on: in every
+// launch, blocks whose linear ids share a residue mod the XCD count run on
+// one XCD. Checked once per process on the current device over launches of
+// several sizes; any mismatch selects the agent-scope merge.
+__global__ void xcc_probe_k(int32_t *out) {
+    const unsigned x = __builtin_amdgcn_s_getreg((3 << 11) | (0 << 6) | 20);  // HW_REG_XCC_ID[3:0]
+    if (threadIdx.x == 0) out[blockIdx.x] = (int32_t)x;
+}
+
+int attn_xcd_mode() {
+    static int mode = -1;
+    if (mode < 0) {
+        int dev = 0, nx = 0;
+        ESP_HIP(hipGetDevice(&dev));
+        if (hipDeviceGetAttribute(&nx, hipDeviceAttributeNumberOfXccs, dev) != hipSuccess || nx < 1) nx = 0;
+        mode = 0;
+        if (nx == 1) {
+            mode = 1;
+        } else if (nx > 1) {
+            const int sizes[4] = {7, 256, 1000, 4099};
+            int32_t *d = nullptr;
+            ESP_HIP(hipMalloc(&d, 4099 * sizeof(int32_t)));
+            std::vector<int32_t> h(4099);
+            bool ok = true;
+            for (int rep = 0; rep < 16 && ok; ++rep) {
+                const int nb = sizes[rep % 4];
+                xcc_probe_k<<<nb, 64>>>(d);
+                ESP_HIP(hipMemcpy(h.data(), d, nb * sizeof(int32_t), hipMemcpyDeviceToHost));
+                for (int b = nx; b < nb && ok; ++b) ok = h[b] == h[b % nx];
+            }
+            ESP_HIP(hipFree(d));
+            mode = ok ? nx : 0;
+        }
+    }
+    const char *e = getenv("ESP_ATT_XCD");
+    if (e && e[0] == '0') return 0;
+    return mode;
+}
+
+void launch_attn_decode(const AttnDecodeArgs &a0, hipStream_t s) {
+    AttnDecodeArgs a = a0;
     const int G = a.nq / a.nkv;
     if (!attn_decode_ok(a.hd, G)) fail(ESP_BACKEND, "attn_decode: unsupported head shape");
-    dim3 grid(a.n_split, a.nkv, a.M);
     if (a.n_split > ATT_MAX_SPLIT) fail(ESP_BACKEND, "attn_decode: too many key splits");
+    if (a.max_t < 1 || (long long)a.n_split * a.split_len < a.max_t)
+        fail(ESP_BACKEND, "attn_decode: key splits do not cover max_t");
+    const long long U = (long long)a.M * a.nkv;
+    if (a.n_split > 1 && U > ATT_MAX_TICKETS)
+        fail(ESP_BACKEND, "attn_decode: too many (row, kv head) merges");
+    a.xcd_nx = a.n_split > 1 ? attn_xcd_mode() : 0;
+    long long nb = a.xcd_nx > 0 ? (long long)a.xcd_nx * ((U + a.xcd_nx - 1) / a.xcd_nx) * a.n_split
+                                : U * a.n_split;
+    if (nb > 0x7fffffffLL) fail(ESP_BACKEND, "attn_decode: grid too large");
+    dim3 grid((unsigned)nb);
+#define ATT_LAUNCH(HD_, GM_)                                                              \
+    do {                                                                              \
+        if (a.xcd_nx > 0) attn_decode_k<HD_, GM_, true><<<grid, ATT_WAVES * 64, 0, s>>>(a);  \
+        else attn_decode_k<HD_, GM_, false><<<grid, ATT_WAVES * 64, 0, s>>>(a);             \
+    } while (0)
     if (a.hd == 64) {
-        if (G <= 4) attn_decode_k<64, 4><<<grid, ATT_WAVES * 64, 0, s>>>(a);
-        else attn_decode_k<64, 8><<<grid, ATT_WAVES * 64, 0, s>>>(a);
+        if (G <= 4) ATT_LAUNCH(64, 4);
+        else ATT_LAUNCH(64, 8);
     } else {
-        if (G <= 4) attn_decode_k<128, 4><<<grid, ATT_WAVES * 64, 0, s>>>(a);
-        else attn_decode_k<128, 8><<<grid, ATT_WAVES * 64, 0, s>>>(a);
+        if (G <= 4) ATT_LAUNCH(128, 4);
+        else ATT_LAUNCH(128, 8);
     }
+#undef ATT_LAUNCH
 }
 
 }  // namespace esp

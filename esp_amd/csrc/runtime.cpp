@@ -505,6 +505,7 @@ Kv *create_kv(Model *m, uint32_t batch, uint32_t max_ctx) {
     // barrier words
     kv->tickets.alloc((size_t)(kStepBarOff + STEP_BAR_WORDS) * 4);
     ESP_HIP(hipMemset(kv->tickets.p, 0, kv->tickets.bytes));
+    (void)attn_xcd_mode();  // one-time dispatch probe, outside any graph capture
     return kv.release();
 }
 
@@ -523,6 +524,7 @@ static void ensure_pinned(Kv &kv, size_t bytes) {
 
 struct Plan {
     int n_split, split_len;
+    int max_t = 0;
 };
 
 static Plan attn_plan(const Model &m, int rows, int max_t) {
@@ -541,6 +543,40 @@ static int32_t *att_tickets(Kv &kv) { return kv.tickets.as<int32_t>(); }
 // lo plane of a split activation buffer holding rows x cols (nullptr for f32)
 static void *lo_plane(Dt act, const DevMem &b, int rows, int cols) {
     return act == DT_SPLIT ? (void *)((uint16_t *)b.p + (size_t)rows * cols) : nullptr;
+}
+
+// Split-K decode attention of Mc rows (each row its own query position)
+// into kv.attn (f32), with the plan from attn_decode_splits.
+static void attn_decode_rows(Model &m, Kv &kv, const Rows &rows, int Mc, int l, const LayerW &w,
+                             const Plan &plan, Dt out_dt = DT_F32) {
+    AttnDecodeArgs a{};
+    a.q = kv.q.as<float>();
+    a.kv = kv.cache.as<float>() + (size_t)l * kv.layer_stride;
+    a.seq_stride = kv.seq_stride;
+    a.kv_half_stride = kv.half_stride;
+    a.head_stride = kv.head_stride;
+    a.row_pos = rows.row_pos;
+    a.row_seq = rows.row_seq;
+    a.seq1 = rows.seq1;
+    a.M = Mc;
+    a.nq = m.nq;
+    a.nkv = m.nkv;
+    a.hd = m.hd;
+    a.window = w.window;
+    a.max_t = plan.max_t;
+    a.n_split = plan.n_split;
+    a.split_len = plan.split_len;
+    a.part = kv.part.as<float>();
+    a.ticket = att_tickets(kv);
+    a.out = kv.attn.as<float>();
+    a.out_lo = (uint16_t *)lo_plane(out_dt, kv.attn, Mc, m.qw);
+    launch_attn_decode(a, kv.stream);
+}
+
+// Whether Mc rows take the split-K decode attention kernel.
+static bool use_attn_decode(const Model &m, const Kv &kv, int Mc) {
+    return kv.dt == DT_F32 && attn_decode_ok(m.hd, m.nq / m.nkv) &&
+           (long long)Mc * m.nkv <= ATT_MAX_TICKETS;
 }
 
 // One layer for a single token row with the decode kernels: fused
@@ -652,26 +688,8 @@ static void run_layer_decode(Model &m, Kv &kv, const Rows &rows, LayerW &w, int 
         launch_rope_kv(m.wt, kv.dt, r, s);
     }
     if (attn_decode_ok(m.hd, m.nq / m.nkv)) {
-        AttnDecodeArgs a{};
-        a.q = kv.q.as<float>();
-        a.kv = kvl;
-        a.seq_stride = kv.seq_stride;
-        a.kv_half_stride = kv.half_stride;
-        a.head_stride = kv.head_stride;
-        a.row_pos = rows.row_pos;
-        a.row_seq = rows.row_seq;
-        a.M = 1;
-        a.nq = m.nq;
-        a.nkv = m.nkv;
-        a.hd = m.hd;
-        a.window = w.window;
-        a.n_split = plan.n_split;
-        a.split_len = plan.split_len;
-        a.part = kv.part.as<float>();
-        a.ticket = att_tickets(kv);
-        a.out = kv.attn.as<float>();
         Prof p("attention", s);
-        launch_attn_decode(a, s);
+        attn_decode_rows(m, kv, rows, 1, l, w, plan);
     } else {
         AttnArgs a{};
         a.q = kv.q.as<float>();
@@ -759,10 +777,11 @@ static void run_layers(Model &m, Kv &kv, const Rows &rows, int Mc, int max_t, in
     // cores as split hi/lo bf16 planes, f32 models as plain f32
     const Dt act = m.wt == DT_BF16 ? DT_SPLIT : DT_F32;
     const int H = m.H;
+    const bool dec_attn = use_attn_decode(m, kv, Mc);
     Plan plan = attn_plan(m, Mc, max_t);
-    if (single && attn_decode_ok(m.hd, m.nq / m.nkv)) {
-        plan.n_split = attn_decode_splits(m.hd, m.nkv, m.nq / m.nkv, max_t, &plan.split_len);
-    }
+    if (dec_attn)
+        plan.n_split = attn_decode_splits(m.hd, m.nkv, m.nq / m.nkv, Mc, max_t, &plan.split_len);
+    plan.max_t = max_t;
     kv.part.ensure((size_t)Mc * m.nq * plan.n_split * (m.hd + ATT_PART_PAD) * 4);
     for (int l = 0; l < m.L; ++l) {
         LayerW &w = m.layers[l];
@@ -851,6 +870,9 @@ static void run_layers(Model &m, Kv &kv, const Rows &rows, int Mc, int max_t, in
             f.out_lo = (uint16_t *)lo_plane(act, kv.attn, Mc, m.qw);
             Prof p("attention", s);
             launch_flash(f, s);
+        } else if (dec_attn) {
+            Prof p("attention", s);
+            attn_decode_rows(m, kv, rows, Mc, l, w, plan, act);
         } else {
             AttnArgs a{};
             a.q = kv.q.as<float>();
@@ -1085,7 +1107,7 @@ void forward(Model &m, Kv &kv, int n_seqs, const uint32_t *seqs, const uint32_t 
         memcpy(pin + 2 * kMaxRows, rpos.data() + c0, Mc * 4);
         memcpy(pin + lastoff, last.data(), n_seqs * 4);
         ESP_HIP(hipMemcpyAsync(dev, pin, (size_t)(lastoff + n_seqs) * 4, hipMemcpyHostToDevice, s));
-        Rows rows{dev, dev + kMaxRows, dev + 2 * kMaxRows, Mc};
+        Rows rows{dev, dev + kMaxRows, dev + 2 * kMaxRows, Mc, n_seqs == 1 ? (int)seqs[0] : -1};
         if (M == 1 && step_usable(m)) {  // one decode row: the persistent step kernel
             run_step(m, kv, rows, max_t, nullptr);
             ESP_HIP(hipStreamSynchronize(s));
@@ -1233,10 +1255,9 @@ void check_step_barrier(Kv &kv) {
 }
 
 void decode_step_dev(Model &m, Kv &kv, int seq, int max_t, int32_t *gen) {
-    (void)seq;
     hipStream_t s = kv.stream;
     ensure_scratch(m, kv, 1, 1);
-    Rows rows{gen, gen + 2, gen + 3, 1};
+    Rows rows{gen, gen + 2, gen + 3, 1, seq};
     if (step_usable(m)) {
         run_step(m, kv, rows, max_t, gen);
         kv.logits_rows = 1;

@@ -287,9 +287,10 @@ def test_bf16_long_prefill_wide_gemm_tiles():
 
 def test_bf16_long_context_decode_splits():
     """Decode over 8.3k cached keys (hd 128, 4 query heads on one kv head):
-    the key range is cut into 52 splits of 160 keys (two load chunks each)
-    whose partials the last block merges; logits within the bf16 tolerance
-    of the oracle for three teacher-forced steps."""
+    the key range is cut into one split per CU (up to 128 splits of at least
+    65 keys; past 160 keys a split takes two load chunks) whose partials the last block merges;
+    logits within the bf16 tolerance of the oracle for three teacher-forced
+    steps."""
     cfg = synth.llama_config(1, 256, 4, 1, 256, 500, head_dim=128, max_pos=8400)
     tensors = synth.make_tensors(cfg, 71, "bf16")
     model = DecoderModel.from_bytes(cfg, st.dump(tensors), "bf16")
@@ -415,3 +416,53 @@ def test_step_kernel_opt_in_matches_oracle(variant, monkeypatch):
         ids.append(int(np.argmax(logits)))
         logits = model.try_forward_cached_last([ids[-1]], kv2)
     assert model.generate_greedy_device(model.new_cache(1, 64), prompt, 6, eos=[]) == ids
+
+
+@pytest.mark.parametrize("protocol", ["xcd", "agent"])
+def test_decode_attention_merge_protocols(protocol, monkeypatch):
+    """Split-K decode attention with either cross-block merge: partials
+    exchanged inside one XCD's L2 (blocks of a (row, kv head) share a
+    dispatch residue) or through agent-scope stores and loads
+    (ESP_ATT_XCD=0). 1.5k cached keys over 2 kv heads (hd 64, 4 query heads
+    each) give many splits per head; logits within 1e-4 of the f32 oracle
+    for a prefill and four greedy steps."""
+    if protocol == "agent":
+        monkeypatch.setenv("ESP_ATT_XCD", "0")
+    else:
+        monkeypatch.delenv("ESP_ATT_XCD", raising=False)
+    cfg = synth.llama_config(2, 256, 8, 2, 320, 300, head_dim=64, max_pos=1600)
+    tensors = synth.make_tensors(cfg, 53, "f32")
+    model = DecoderModel.from_bytes(cfg, st.dump(tensors), "f32")
+    ref = oracle.OracleModel(cfg, tensors)
+    prompt = synth.uniform_ids(6, 1500, cfg.vocab_size)
+    kv, rkv = model.new_cache(1, 1540), ref.new_cache(1540)
+    got = model.try_forward_cached_last(prompt, kv)
+    want = ref.forward_last(rkv, prompt)
+    for step in range(4):
+        scale = float(np.abs(want).max())
+        assert np.abs(got - want).max() <= 1e-4 * scale, (protocol, step)
+        t = oracle.argmax(want)
+        got = model.try_forward_cached_last([t], kv)
+        want = ref.forward_last(rkv, [t])
+
+
+def test_bf16_batch_decode_rows_match_oracle():
+    """Multi-sequence rows (decode rows of six sequences + an 8-token forced
+    block of a seventh) through the split-K decode attention with split
+    (hi/lo bf16) output feeding the MFMA projections; each sequence's logits
+    within the bf16 tolerance of the oracle run alone."""
+    cfg = synth.llama_config(2, 256, 8, 2, 512, 400, head_dim=64, max_pos=512)
+    tensors = synth.make_tensors(cfg, 23, "bf16")
+    model = DecoderModel.from_bytes(cfg, st.dump(tensors), "bf16")
+    ref = oracle.OracleModel(cfg, tensors)
+    n = 7
+    prompts = [synth.uniform_ids(300 + i, 40 + 37 * i, cfg.vocab_size) for i in range(n)]
+    kv = model.new_cache(n, 400)
+    model.forward_batch(kv, list(range(n)), prompts, want_logits=False)
+    blocks = [[(5 * i + 1) % cfg.vocab_size] for i in range(n - 1)] + [[3, 1, 4, 1, 5, 9, 2, 6]]
+    got = model.forward_batch(kv, list(range(n)), blocks)
+    for i in range(n):
+        rkv = ref.new_cache(400)
+        ref.forward_last(rkv, prompts[i])
+        want = ref.forward_last(rkv, blocks[i])
+        assert _close_bf16(got[i], want), (i, float(np.abs(got[i] - want).max()))
