@@ -15,6 +15,8 @@
 // the narrow form (half the columns per block). A and W tiles are staged through LDS (rows padded to
 // 80 bytes) from register prefetches issued one k-tile ahead. Epilogues:
 // STORE (+bias), RESIDUAL (+=), SWIGLU (out = silu(g) * u).
+#include <cstdlib>
+
 #include "common.hpp"
 #include "dev.hpp"
 #include "kernels_extra.hpp"
@@ -28,6 +30,7 @@ typedef unsigned int u32x4v_t __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x2v_t __attribute__((ext_vector_type(2)));
 
 constexpr int MF_BM = 128, MF_BK = 32, MF_LD = MF_BK + 8;
+constexpr int MF_CPR = MF_BK / 8;  // 16-byte chunks per tile row
 constexpr int MF_A_ELEMS = MF_BM * MF_LD;  // one A plane (bf16) per buffer
 // NJ = 32-column MFMA blocks per wave and weight matrix; BN = 64 * NJ
 template <int NJ> constexpr int mf_b_elems() { return 64 * NJ * MF_LD; }
@@ -79,8 +82,9 @@ __global__ void __launch_bounds__(256, 2) gemm_mfma_k(GemmArgs g, float *ws, int
 #pragma unroll
                 for (int e = 0; e < 16; ++e) acc[b][i][j][e] = 0.f;
 
-    u32x4v_t ra[2][2];  // [hi/lo][chunk]
-    u32x4v_t rb[NB][NJ];
+    constexpr int ACH = MF_BM * MF_CPR / 256, BCH = BN * MF_CPR / 256;  // chunks per thread
+    u32x4v_t ra[2][ACH];  // [hi/lo][chunk]
+    u32x4v_t rb[NB][BCH];
     const int kbeg = blockIdx.z * k_per_split;
     const int kend = min(K, kbeg + k_per_split);
     auto load_tile = [&](int kt) {
@@ -88,9 +92,9 @@ __global__ void __launch_bounds__(256, 2) gemm_mfma_k(GemmArgs g, float *ws, int
 #pragma unroll
         for (int p = 0; p < 2; ++p)
 #pragma unroll
-            for (int i = 0; i < 2; ++i) {
-                int idx = tid + 256 * i;  // 0..511 chunks of 8 bf16 (128 x 32 tile)
-                int row = idx >> 2, k = kb + (idx & 3) * 8;
+            for (int i = 0; i < ACH; ++i) {
+                int idx = tid + 256 * i;  // chunks of 8 bf16 (128 x BK tile)
+                int row = idx / MF_CPR, k = kb + (idx % MF_CPR) * 8;
                 int gm = m0 + row;
                 const uint16_t *src = p ? Al : Ah;
                 if (gm < M && k + 7 < kend) {
@@ -106,9 +110,9 @@ __global__ void __launch_bounds__(256, 2) gemm_mfma_k(GemmArgs g, float *ws, int
 #pragma unroll
         for (int b = 0; b < NB; ++b)
 #pragma unroll
-            for (int i = 0; i < NJ; ++i) {
-                int idx = tid + 256 * i;  // chunks of 8 bf16 (BN x 32 tile)
-                int row = idx >> 2, k = kb + (idx & 3) * 8;
+            for (int i = 0; i < BCH; ++i) {
+                int idx = tid + 256 * i;  // chunks of 8 bf16 (BN x BK tile)
+                int row = idx / MF_CPR, k = kb + (idx % MF_CPR) * 8;
                 int gn = n0 + row;
                 if (gn < N && k + 7 < kend) {
                     rb[b][i] = __builtin_nontemporal_load(
@@ -128,18 +132,18 @@ __global__ void __launch_bounds__(256, 2) gemm_mfma_k(GemmArgs g, float *ws, int
 #pragma unroll
         for (int p = 0; p < 2; ++p)
 #pragma unroll
-            for (int i = 0; i < 2; ++i) {
+            for (int i = 0; i < ACH; ++i) {
                 int idx = tid + 256 * i;
-                int row = idx >> 2, k = (idx & 3) * 8;
+                int row = idx / MF_CPR, k = (idx % MF_CPR) * 8;
                 *(u32x4v_t *)((p ? al : ah) + row * MF_LD + k) = ra[p][i];
             }
 #pragma unroll
         for (int b = 0; b < NB; ++b) {
             uint16_t *bb = sB + b * B_ELEMS;
 #pragma unroll
-            for (int i = 0; i < NJ; ++i) {
+            for (int i = 0; i < BCH; ++i) {
                 int idx = tid + 256 * i;
-                int row = idx >> 2, k = (idx & 3) * 8;
+                int row = idx / MF_CPR, k = (idx % MF_CPR) * 8;
                 *(u32x4v_t *)(bb + row * MF_LD + k) = rb[b][i];
             }
         }
@@ -264,6 +268,193 @@ __global__ void __launch_bounds__(256) mfma_reduce_k(GemmArgs g, const float *ws
     }
 }
 
+// ---------------------------------------------------------------------------
+// Streamed form (K a multiple of 32): the same 128 x 256 block tile, but the
+// A planes and weight rows go global -> LDS directly (global_load_lds, 16
+// bytes per lane) through a ring of LDS_STAGES stages of 32 keys, issued
+// LDS_STAGES - 1 stages ahead, so no registers stage the tiles and global
+// latency is covered by three stages of MFMA work. One barrier per stage.
+// Each tile row is 64 bytes (four 16-byte chunks); chunk c of row r sits at
+// slot c ^ ((r >> 2) & 3). ds_read_b128 serves 16 lanes per cycle from 64
+// four-byte banks, so the 16 rows a quarter-wave reads (same chunk) must
+// land on 16 distinct 16-byte slots mod 256 bytes; rows r, r+4, r+8, r+12
+// share r & 3 and the XOR separates them (measured: no bank conflicts). Rows past M or N re-read the
+// last valid row (their results are dropped by the epilogue).
+constexpr int LS_BK = 32;
+constexpr int LS_ROWB = LS_BK * 2;                 // bytes per tile row
+constexpr int LS_BROWS = 256;                      // weight rows per stage (all matrices)
+
+// BMW waves along M (block rows 64 * BMW) x 2 along N; stages per form:
+// 128-row blocks keep two stages (64 KB) so two blocks share a CU, 256-row
+// blocks (eight waves) keep three (144 KB).
+template <int BMW> struct LsForm {
+    static constexpr int BM = 64 * BMW, NT = 128 * BMW;
+    static constexpr int A = BM * LS_ROWB;                       // one A plane per stage
+    static constexpr int STAGE = 2 * A + LS_BROWS * LS_ROWB;
+    static constexpr int STAGES = BMW == 2 ? 2 : 3;
+    static constexpr size_t LDS = (size_t)STAGES * STAGE;
+    static constexpr int QB = 8 / BMW;                           // weight loads per wave and stage
+    static constexpr int LPS = 4 + QB;                           // loads per wave and stage
+};
+
+// s_waitcnt immediate for vmcnt(n) (n & 15 in bits 3:0, n >> 4 in bits 15:14)
+constexpr int vm_imm(int n) { return (n & 15) | (7 << 4) | (15 << 8) | ((n >> 4) << 14); }
+
+__device__ __forceinline__ int ls_swz(int r) { return (r >> 2) & 3; }
+
+typedef const void __attribute__((address_space(1))) *gptr_t;
+typedef void __attribute__((address_space(3))) *lptr_t;
+
+template <int EPI, int NB, int BMW>
+__global__ void __launch_bounds__(128 * BMW, 2 / (BMW / 2)) gemm_lds_k(GemmArgs g, float *ws,
+                                                                      int k_per_split, int mt, int nt) {
+    using F = LsForm<BMW>;
+    constexpr int BN = LS_BROWS / NB;  // weight columns per matrix
+    constexpr int NJ = BN / 64;        // 32-column MFMA blocks per wave and matrix
+    constexpr int STAGES = F::STAGES;
+    extern __shared__ __attribute__((aligned(16))) char lds_s[];
+    // wave index in an SGPR: the LDS bases of the direct loads (M0) stay scalar
+    const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int total = mt * nt, per = (total + MF_XCDS - 1) / MF_XCDS;
+    const int tile = (blockIdx.x % MF_XCDS) * per + blockIdx.x / MF_XCDS;
+    if (tile >= total) return;
+    const int m0 = (tile % mt) * F::BM, n0 = (tile / mt) * BN;
+    const int M = g.M, N = g.N, K = g.K;
+    const int kbeg = blockIdx.z * k_per_split;
+    const int KT = (min(K, kbeg + k_per_split) - kbeg) / LS_BK;
+
+    // this lane's global sources: A plane p, wave-instruction q covers LDS
+    // slots (wave*2+q)*64 + lane; weights: (wave*QB+q)*64 + lane
+    const uint16_t *asrc[2][2], *bsrc[F::QB];
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+        const int sl = (wave * 2 + q) * 64 + lane, r = sl >> 2, kc = (sl & 3) ^ ls_swz(r);
+        const size_t off = (size_t)min(m0 + r, M - 1) * K + kbeg + kc * 8;
+        asrc[0][q] = (const uint16_t *)g.a + off;
+        asrc[1][q] = (const uint16_t *)g.a_lo + off;
+    }
+#pragma unroll
+    for (int q = 0; q < F::QB; ++q) {
+        const int sl = (wave * F::QB + q) * 64 + lane, r = sl >> 2, kc = (sl & 3) ^ ls_swz(r);
+        const int b = r / BN, n = min(n0 + r % BN, N - 1);
+        bsrc[q] = (const uint16_t *)(b ? g.w2 : g.w) + (size_t)n * K + kbeg + kc * 8;
+    }
+    auto issue = [&](int kt) {
+        char *base = lds_s + (kt % STAGES) * F::STAGE;
+        const int ko = kt * LS_BK;
+#pragma unroll
+        for (int p = 0; p < 2; ++p)
+#pragma unroll
+            for (int q = 0; q < 2; ++q)
+                __builtin_amdgcn_global_load_lds((gptr_t)(asrc[p][q] + ko),
+                                                 (lptr_t)(base + p * F::A + (wave * 2 + q) * 1024), 16, 0, 0);
+#pragma unroll
+        for (int q = 0; q < F::QB; ++q)
+            __builtin_amdgcn_global_load_lds((gptr_t)(bsrc[q] + ko),
+                                             (lptr_t)(base + 2 * F::A + (wave * F::QB + q) * 1024), 16, 0, 0);
+    };
+
+    f32x16_t acc[NB][2][NJ];
+#pragma unroll
+    for (int b = 0; b < NB; ++b)
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < NJ; ++j)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) acc[b][i][j][e] = 0.f;
+
+#pragma unroll
+    for (int st = 0; st < STAGES - 1; ++st)
+        if (st < KT) issue(st);
+    for (int kt = 0; kt < KT; ++kt) {
+        // this stage's loads are done once at most (later stages issued) x LPS remain
+        const int later = min(STAGES - 2, KT - 1 - kt);
+        static_assert(STAGES <= 3 && 2 * F::LPS < 64, "vmcnt waits below cover up to 2 later stages");
+        if (later >= 2) __builtin_amdgcn_s_waitcnt(vm_imm(2 * F::LPS));
+        else if (later == 1) __builtin_amdgcn_s_waitcnt(vm_imm(F::LPS));
+        else __builtin_amdgcn_s_waitcnt(vm_imm(0));
+        // every wave's loads of stage kt landed; stage kt-1 is free. A bare
+        // s_barrier: a fenced __syncthreads would wait for every stage in flight
+        __builtin_amdgcn_s_barrier();
+        if (kt + STAGES - 1 < KT) issue(kt + STAGES - 1);
+        const char *base = lds_s + (kt % STAGES) * F::STAGE;
+        const char *ah = base, *al = base + F::A, *bb = base + 2 * F::A;
+#pragma unroll
+        for (int ks = 0; ks < LS_BK / 16; ++ks) {
+            const int c = 2 * ks + (lane >> 5);
+            bf16x8_t fh[2], fl[2], fb[NB][NJ];
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const int r = wm * 64 + i * 32 + (lane & 31);
+                const int off = r * LS_ROWB + ((c ^ ls_swz(r)) << 4);
+                fh[i] = *(const bf16x8_t *)(ah + off);
+                fl[i] = *(const bf16x8_t *)(al + off);
+            }
+#pragma unroll
+            for (int b = 0; b < NB; ++b)
+#pragma unroll
+                for (int j = 0; j < NJ; ++j) {
+                    const int r = b * BN + wn * (BN / 2) + j * 32 + (lane & 31);
+                    fb[b][j] = *(const bf16x8_t *)(bb + r * LS_ROWB + ((c ^ ls_swz(r)) << 4));
+                }
+#pragma unroll
+            for (int b = 0; b < NB; ++b)
+#pragma unroll
+                for (int i = 0; i < 2; ++i)
+#pragma unroll
+                    for (int j = 0; j < NJ; ++j) {
+                        acc[b][i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fh[i], fb[b][j], acc[b][i][j], 0, 0, 0);
+                        acc[b][i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fl[i], fb[b][j], acc[b][i][j], 0, 0, 0);
+                    }
+        }
+    }
+
+    // epilogue: lane holds column (lane & 31) of each 32 x 32 block, rows
+    // (e / 4) * 8 + (lane >> 5) * 4 + e % 4
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+            const int col = n0 + wn * (BN / 2) + j * 32 + (lane & 31);
+            if (col >= N) continue;
+            if (EPI == MF_PARTIAL) {
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    const int row = m0 + wm * 64 + i * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3);
+                    if (row >= M) continue;
+#pragma unroll
+                    for (int b = 0; b < NB; ++b)
+                        ws[(((size_t)blockIdx.z * NB + b) * M + row) * N + col] = acc[b][i][j][e];
+                }
+                continue;
+            }
+            const float bias = (EPI != GEMM_SWIGLU && g.bias) ? g.bias[col] : 0.f;
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const int row = m0 + wm * 64 + i * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3);
+                if (row >= M) continue;
+                float *c = (float *)g.c + (size_t)row * g.ldc + col;
+                if (EPI == GEMM_SWIGLU) {
+                    const float y = silu(acc[0][i][j][e]) * acc[NB - 1][i][j][e];
+                    if (g.c_lo) {
+                        const size_t ci = (size_t)row * g.ldc + col;
+                        uint16_t h = f2bf(y);
+                        ((uint16_t *)g.c)[ci] = h;
+                        ((uint16_t *)g.c_lo)[ci] = f2bf(y - bf2f(h));
+                    } else {
+                        *c = y;
+                    }
+                } else {
+                    float v = g.bias ? acc[0][i][j][e] + bias : acc[0][i][j][e];
+                    if (EPI == GEMM_RESIDUAL) *c = *c + v;
+                    else *c = v;
+                }
+            }
+        }
+}
+
 static int g_cus = 0;
 
 template <int EPI, int NB, int NJ>
@@ -289,6 +480,38 @@ static void mfma_launch_nj(const GemmArgs &a, float *ws, size_t ws_bytes, hipStr
     mfma_reduce_k<EPI, NB><<<rblocks, 256, 0, s>>>(a, ws, splits);
 }
 
+template <int EPI, int NB, int BMW>
+static void lds_launch(const GemmArgs &a, float *ws, size_t ws_bytes, hipStream_t s) {
+    using F = LsForm<BMW>;
+    constexpr int BN = LS_BROWS / NB;
+    static bool attr = false;
+    if (!attr) {
+        ESP_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(gemm_lds_k<EPI, NB, BMW>),
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, (int)F::LDS));
+        ESP_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(gemm_lds_k<MF_PARTIAL, NB, BMW>),
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, (int)F::LDS));
+        attr = true;
+    }
+    const int gx = (a.N + BN - 1) / BN, gy = (a.M + F::BM - 1) / F::BM;
+    const int blocks = MF_XCDS * ((gx * gy + MF_XCDS - 1) / MF_XCDS);
+    // split K until every CU holds two blocks' worth of waves (k-splits stay >= 512)
+    const int want = BMW == 2 ? 2 * g_cus : g_cus;
+    int splits = 1;
+    while (gx * gy * splits < want && a.K / (splits * 2) >= 512 &&
+           (size_t)(splits * 2) * NB * a.M * a.N * 4 <= ws_bytes)
+        splits *= 2;
+    int kps = (a.K + splits - 1) / splits;
+    kps = (kps + LS_BK - 1) / LS_BK * LS_BK;
+    if (splits == 1) {
+        gemm_lds_k<EPI, NB, BMW><<<dim3(blocks, 1, 1), F::NT, F::LDS, s>>>(a, nullptr, a.K, gy, gx);
+        return;
+    }
+    gemm_lds_k<MF_PARTIAL, NB, BMW><<<dim3(blocks, 1, splits), F::NT, F::LDS, s>>>(a, ws, kps, gy, gx);
+    size_t mn = (size_t)a.M * a.N;
+    const int rblocks = (int)std::min<size_t>((mn + 255) / 256, (size_t)g_cus * 8);
+    mfma_reduce_k<EPI, NB><<<rblocks, 256, 0, s>>>(a, ws, splits);
+}
+
 template <int EPI> static void mfma_launch(const GemmArgs &a, float *ws, size_t ws_bytes,
                                            hipStream_t s) {
     constexpr int NB = EPI == GEMM_SWIGLU ? 2 : 1;
@@ -300,6 +523,13 @@ template <int EPI> static void mfma_launch(const GemmArgs &a, float *ws, size_t 
         if (g_cus <= 0) g_cus = 256;
     }
     const long long wide_tiles = (long long)((a.N + 64 * NJW - 1) / (64 * NJW)) * ((a.M + MF_BM - 1) / MF_BM);
+    // long row counts (prefill of >= 1024 tokens) take the LDS-streamed form:
+    // 256-row blocks for one weight matrix, 128-row blocks for gate/up pairs
+    if (a.K % LS_BK == 0 && a.M >= 1024) {
+        if (NB == 1) lds_launch<EPI, NB, 4>(a, ws, ws_bytes, s);
+        else lds_launch<EPI, NB, 2>(a, ws, ws_bytes, s);
+        return;
+    }
     if (wide_tiles >= g_cus) mfma_launch_nj<EPI, NB, NJW>(a, ws, ws_bytes, s);
     else mfma_launch_nj<EPI, NB, NJW / 2>(a, ws, ws_bytes, s);
 }

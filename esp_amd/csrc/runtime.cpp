@@ -820,7 +820,7 @@ static void run_layers(Model &m, Kv &kv, const Rows &rows, int Mc, int max_t, in
             g.N = w.qkv_rows;
             g.K = H;
             g.ldc = w.qkv_rows;
-            Prof p("gemm", s);
+            Prof p("gemm_qkv", s);
             launch_gemm(m.wt, GEMM_STORE, g, s);
         }
         {
@@ -917,7 +917,7 @@ static void run_layers(Model &m, Kv &kv, const Rows &rows, int Mc, int max_t, in
             g.N = H;
             g.K = m.qw;
             g.ldc = H;
-            Prof p("gemm", s);
+            Prof p("gemm_o", s);
             launch_gemm(m.wt, GEMM_RESIDUAL, g, s);
         }
         // ---- MLP block (layer.rs:147-151)
@@ -965,7 +965,7 @@ static void run_layers(Model &m, Kv &kv, const Rows &rows, int Mc, int max_t, in
             g.K = H;
             g.ldc = m.F;
             {
-                Prof p("gemm", s);
+                Prof p("gemm_mlp", s);
                 launch_gemm(m.wt, GEMM_SWIGLU, g, s);
             }
             GemmArgs d{};
@@ -979,7 +979,7 @@ static void run_layers(Model &m, Kv &kv, const Rows &rows, int Mc, int max_t, in
             d.N = H;
             d.K = m.F;
             d.ldc = H;
-            Prof p("gemm", s);
+            Prof p("gemm_down", s);
             launch_gemm(m.wt, GEMM_RESIDUAL, d, s);
         }
     }

@@ -270,16 +270,17 @@ def test_bf16_flash_prefill_chunks_match_oracle(variant):
 
 
 def test_bf16_long_prefill_wide_gemm_tiles():
-    """1024-row prefill whose projections are large enough for the wide GEMM
-    tiles (q/k/v: 1024 x 8192 outputs, gate/up: 1024 x 4096 each -> 256 wide
-    tiles), then a 2-token block and a decode step; logits within the bf16
-    tolerance of the oracle."""
+    """1100-row prefill (not a multiple of the 256-row block: the last row
+    tile re-reads its last valid row) through the LDS-streamed GEMM (q/k/v
+    1100 x 8192, gate/up 1100 x 4096 each, o_proj split over K), then a
+    2-token block and a decode step on the register-staged GEMM; logits
+    within the bf16 tolerance of the oracle."""
     cfg = synth.llama_config(2, 256, 48, 8, 4096, 1000, head_dim=128, max_pos=1200)
     tensors = synth.make_tensors(cfg, 61, "bf16")
     model = DecoderModel.from_bytes(cfg, st.dump(tensors), "bf16")
     ref = oracle.OracleModel(cfg, tensors)
-    kv, rkv = model.new_cache(1, 1100), ref.new_cache(1100)
-    for block in (synth.uniform_ids(3, 1024, 1000), [5, 6], [7]):
+    kv, rkv = model.new_cache(1, 1110), ref.new_cache(1110)
+    for block in (synth.uniform_ids(3, 1100, 1000), [5, 6], [7]):
         got = model.try_forward_cached_last(block, kv)
         want = ref.forward_last(rkv, block)
         assert _close_bf16(got, want), (len(block), float(np.abs(got - want).max()))
