@@ -208,6 +208,157 @@ def c3_bench(steps: int) -> dict:
     return res
 
 
+def c4_config(max_pos=4096):
+    from esp_amd.config import DecoderConfig
+    return DecoderConfig.mixtral_style(vocab_size=32000, hidden_size=4096, intermediate_size=14336,
+                                       num_hidden_layers=4, num_attention_heads=32,
+                                       num_key_value_heads=8, max_position_embeddings=max_pos,
+                                       rope_theta=1000000.0, num_experts=8, num_experts_per_tok=2,
+                                       moe_intermediate_size=14336)
+
+
+def moe_decode_bytes(cfg, ctx: int) -> int:
+    """Algorithmic HBM bytes of one batch-1 MoE decode step: attention
+    weights, router and the top-k experts' gate/up/down rows of every layer
+    (bf16), the head (bf16) and the K/V cache (f32) once."""
+    H, L, V = cfg.hidden_size, cfg.num_hidden_layers, cfg.vocab_size
+    qw, kvw = cfg.query_width(), cfg.kv_heads() * cfg.head_dim()
+    m = cfg.moe
+    layer = (H * (qw + 2 * kvw) + H * qw + m.num_experts * H
+             + m.num_experts_per_tok * 3 * H * m.moe_intermediate_size) * 2
+    return L * layer + V * H * 2 + 2 * L * kvw * ctx * 4
+
+
+def moe_prefill_flops(cfg, S: int) -> float:
+    """Useful FLOPs of an S-token MoE prefill: projections, router, the top-k
+    experts each token is routed to, causal attention, last-position head."""
+    H, L, V = cfg.hidden_size, cfg.num_hidden_layers, cfg.vocab_size
+    qw, kvw, hd, nq = cfg.query_width(), cfg.kv_heads() * cfg.head_dim(), cfg.head_dim(), \
+        cfg.num_attention_heads
+    m = cfg.moe
+    per_tok = H * (qw + 2 * kvw) + H * qw + m.num_experts * H + \
+        m.num_experts_per_tok * 3 * H * m.moe_intermediate_size
+    return 2.0 * S * L * per_tok + 2.0 * 2.0 * L * nq * hd * S * (S + 1) / 2 + 2.0 * H * V
+
+
+def c4_bench(steps: int) -> dict:
+    """Mixtral-style MoE stack (4 layers, hidden 4096,
+    8 experts of SwiGLU 14336, top-2 softmax router, vocab 32000), bf16,
+    synthetic N(0, 0.02) weights: a 2048-token uniform-random prefill, then
+    batch-1 greedy decode at ~2048 context (device loop, captured step)."""
+    from esp_amd import DecoderModel
+    from tests.synth import uniform_ids
+    cfg = c4_config()
+    model = DecoderModel.synthetic(cfg, seed=777, std=0.02, fmt="bf16")
+    prompt = uniform_ids(17, 2048, cfg.vocab_size)
+    n_dec = 64
+    kv = model.new_cache(1, 2048 + n_dec)
+
+    def prefill():
+        kv.reset(0)
+        t0 = time.perf_counter()
+        model.try_forward_cached_last(prompt, kv)
+        return time.perf_counter() - t0
+
+    def gen():
+        t0 = time.perf_counter()
+        out = model.generate_greedy_device(kv, prompt, n_dec, eos=[])
+        assert len(out) == n_dec
+        return time.perf_counter() - t0
+
+    gen()
+    prefill()
+    t_gen = sorted(gen() for _ in range(steps))[steps // 2]
+    t_pre = sorted(prefill() for _ in range(steps))[steps // 2]
+    t_dec = (t_gen - t_pre) / (n_dec - 1)
+    db = moe_decode_bytes(cfg, 2048 + n_dec // 2)
+    fl = moe_prefill_flops(cfg, 2048)
+    res = {"workload": "C4: Mixtral-style MoE (4 layers, hidden 4096, 8 experts x SwiGLU 14336, "
+                       "top-2), bf16; 2048-token prefill, batch-1 decode at 2048-2112 context "
+                       "(BASELINE configs[3])",
+           "decode_tokens_per_s": round(1.0 / t_dec, 2),
+           "decode_ms_per_token": round(t_dec * 1e3, 4),
+           "decode_hbm_frac": round(db / t_dec / 1e9 / HBM_PEAK_GBS, 4),
+           "decode_bytes_per_token": db,
+           "prefill_2048_tokens_per_s": round(2048 / t_pre, 1),
+           "prefill_2048_ms": round(t_pre * 1e3, 3),
+           "prefill_mfma_frac": round(fl / t_pre / 1e12 / BF16_PEAK_TFLOPS, 4)}
+    model.close()
+    return res
+
+
+def c5_bench(steps: int, warmup: int = 2) -> dict:
+    """constrained decode on the 1B shape, 64 concurrent
+    sequences at ~1024 context. Each step: every sequence whose index is
+    congruent to the step mod 8 evaluates a forced 8-token block (a causal
+    mini-prefill over its warm cache), the other 56 one decode token; then
+    one esp_pick over the 64 last-position logits rows applies a
+    per-sequence allowed-token bitmask (Bernoulli 0.05 from the seed, at
+    least one token allowed) and seeded temperature 0.8 / top-p 0.9
+    sampling (sample.rs:83-121). Sequences are prefilled with 1024
+    uniform-random ids before timing."""
+    import numpy as np
+    from esp_amd import DecoderModel, Sampler
+    from tests.synth import uniform_ids
+    cfg = c2_config(max_pos=2048)
+    B, ctx0, V = 64, 1024, cfg.vocab_size
+    total = warmup + steps
+    model = DecoderModel.synthetic(cfg, seed=1234, std=0.02, fmt="bf16")
+    kv = model.new_cache(B, ctx0 + 8 * total + 8)
+    model.forward_batch(kv, list(range(B)), [uniform_ids(5000 + i, ctx0, V) for i in range(B)],
+                        want_logits=False)
+    words = (V + 31) // 32
+    rng = np.random.default_rng(20261201)
+    masks = []
+    for st in range(total):
+        allow = rng.random((B, words * 32), dtype=np.float32) < 0.05
+        allow[:, V:] = False
+        allow[np.arange(B), rng.integers(0, V, B)] = True  # at least one allowed
+        masks.append(np.packbits(allow, axis=1, bitorder="little").view(np.uint32).copy())
+    forced = [[uniform_ids(9000 + 100 * st + i, 8, V) for i in range(B)] for st in range(total)]
+    samplers = [Sampler(0.8, 0.9, 0xC5C5 + i) for i in range(B)]
+    last = [int(x) for x in rng.integers(0, V, B)]
+    seqs = list(range(B))
+    rows = 0
+
+    def step(st):
+        nonlocal rows
+        blocks = []
+        for i in range(B):
+            if (i + st) % 8 == 0:
+                blocks.append(forced[st][i])
+                samplers[i].skip_draws(8)  # forced tokens consume one draw each
+            else:
+                blocks.append([last[i]])
+        rows += sum(len(b) for b in blocks)
+        model.forward_batch(kv, seqs, blocks, want_logits=False)
+        ids, flags = model.pick(kv, B, masks[st], samplers)
+        for i in range(B):
+            last[i] = int(ids[i])
+
+    for st in range(warmup):
+        step(st)
+    rows = 0
+    t0 = time.perf_counter()
+    for st in range(warmup, total):
+        step(st)
+    el = time.perf_counter() - t0
+    ctx_mid = ctx0 + 8 * total // 2
+    qkv_kv = 2 * cfg.num_hidden_layers * cfg.kv_heads() * cfg.head_dim() * 4
+    step_bytes = decode_bytes(cfg, 0)["gemv_weights"] + B * ctx_mid * qkv_kv + 2 * B * V * 4 + B * words * 4
+    res = {"workload": "C5: 1B shape bf16, 64 sequences at 1024-1200 context; per step 56 decode "
+                       "rows + 8 forced 8-token blocks, allowed-token bitmask (5%) + seeded "
+                       "temperature 0.8 / top-p 0.9 sampling (BASELINE configs[4])",
+           "sequence_tokens_per_s": round(B * steps / el, 1),
+           "rows_per_s": round(rows / el, 1),
+           "ms_per_step": round(el / steps * 1e3, 3),
+           "step_hbm_frac": round(step_bytes / (el / steps) / 1e9 / HBM_PEAK_GBS, 4),
+           "step_bytes": step_bytes,
+           "steps": steps}
+    model.close()
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -218,6 +369,10 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-c3", action="store_true")
     ap.add_argument("--only-c3", action="store_true")
+    ap.add_argument("--no-c4", action="store_true")
+    ap.add_argument("--only-c4", action="store_true")
+    ap.add_argument("--no-c5", action="store_true")
+    ap.add_argument("--only-c5", action="store_true")
     ap.add_argument("--traffic", action="store_true",
                     help="run only the workload of the HBM-traffic counter passes")
     args = ap.parse_args()
@@ -234,6 +389,12 @@ def main():
         return
     if args.only_c3:
         print(json.dumps({"c3": c3_bench(max(1, args.steps))}), flush=True)
+        return
+    if args.only_c4:
+        print(json.dumps({"c4": c4_bench(max(1, args.steps))}), flush=True)
+        return
+    if args.only_c5:
+        print(json.dumps({"c5": c5_bench(16)}), flush=True)
         return
     cfg = c2_config()
     model = DecoderModel.synthetic(cfg, seed=1234, std=0.02, fmt="bf16")
@@ -330,6 +491,12 @@ def main():
         model.close()
         result["c3"] = c3_bench(max(1, args.steps))
         print(f"c3: {result['c3']}", file=sys.stderr, flush=True)
+    if not args.no_c4:
+        result["c4"] = c4_bench(max(1, args.steps))
+        print(f"c4: {result['c4']}", file=sys.stderr, flush=True)
+    if not args.no_c5:
+        result["c5"] = c5_bench(16)
+        print(f"c5: {result['c5']}", file=sys.stderr, flush=True)
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(cfg, int(avg_ctx))
     print(json.dumps(result), flush=True)

@@ -29,6 +29,15 @@ struct DecodeGemvArgs {
     const void *lora_b[3];
     int lora_rank[3], lora_t_col[3];
     float lora_scale[3];
+    // routed experts (moe.rs:135-256, one row): with ex_sel set, SWIGLU
+    // units are (slot, row) pairs, slot = unit / ex_rows, reading expert
+    // ex_sel[slot] (clamped to [0, ex_count)) of the [E][rows][K] tensors;
+    // RESID reads expert ex_sel[ex_slot] and scales by ex_w[ex_slot].
+    const int32_t *ex_sel;
+    const float *ex_w;
+    long long ex_stride;   // elements between consecutive experts
+    int ex_rows, ex_slot, ex_count;
+    const float *sig_scale;  // nullable (RESID): y *= sigmoid(*sig_scale)
     // HEAD argmax
     float *part_v;
     int32_t *part_i;

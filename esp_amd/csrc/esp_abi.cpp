@@ -265,12 +265,14 @@ esp_status esp_generate_greedy(esp_model *model, esp_kv *kv, uint32_t seq, const
         launch_pick(a, s);
         launch_gen_step(a.ids_out, g, s);
         const int max_t = (int)last_pos;
-        // MoE layers read their expert row counts back to the host, which a
-        // captured graph cannot do; ESP_GRAPHS=0 replays eagerly (profilers).
+        // Multi-row MoE layers read their expert row counts back to the
+        // host, which a captured graph cannot do; single-row decode routes on
+        // the device when the expert shapes fit the decode GEMV. ESP_GRAPHS=0
+        // replays eagerly (profilers).
         const char *env = getenv("ESP_GRAPHS");
-        const bool capturable = std::none_of(m.layers.begin(), m.layers.end(),
-                                             [](const LayerW &w) { return w.moe; }) &&
-                                !(env && env[0] == '0');
+        const bool has_moe = std::any_of(m.layers.begin(), m.layers.end(),
+                                         [](const LayerW &w) { return w.moe; });
+        const bool capturable = (!has_moe || moe_decode_ok(m)) && !(env && env[0] == '0');
         uint32_t steps = max_new - 1;
         if (steps) {
             decode_step_dev(m, k, (int)seq, max_t, g);  // eager: sizes every scratch buffer

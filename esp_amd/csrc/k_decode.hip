@@ -46,6 +46,8 @@ __global__ void __launch_bounds__(DG_THREADS) decode_gemv_k(DecodeGemvArgs a) {
     const int k0 = wave * kq;
     const WT *W = (const WT *)a.w;
     const WT *W2 = (const WT *)a.w2;
+    if (EPI == DG_RESID && a.ex_sel)  // one routed expert's rows
+        W += (size_t)min(max(a.ex_sel[a.ex_slot], 0), a.ex_count - 1) * a.ex_stride;
     const int units = EPI == DG_QKVROPE ? a.N / 2 : a.N;
 
     Chunk<WT> wc[R][NCH];
@@ -55,8 +57,13 @@ __global__ void __launch_bounds__(DG_THREADS) decode_gemv_k(DecodeGemvArgs a) {
         for (int r = 0; r < RB; ++r) {
             int u = min(u0 + r, units - 1);
             if (EPI == DG_SWIGLU) {
-                rp[r * 2] = W + (size_t)u * K;
-                rp[r * 2 + 1] = W2 + (size_t)u * K;
+                size_t off = (size_t)u * K;
+                if (a.ex_sel) {  // (slot, row) of a routed expert
+                    const int j = u / a.ex_rows, e = min(max(a.ex_sel[j], 0), a.ex_count - 1);
+                    off = (size_t)e * a.ex_stride + (size_t)(u - j * a.ex_rows) * K;
+                }
+                rp[r * 2] = W + off;
+                rp[r * 2 + 1] = W2 + off;
             } else if (EPI == DG_QKVROPE) {
                 int half = a.hd / 2, head = u / half, d = u % half;
                 int row = head * a.hd + d;
@@ -149,6 +156,8 @@ __global__ void __launch_bounds__(DG_THREADS) decode_gemv_k(DecodeGemvArgs a) {
         }
         if (EPI == DG_RESID) {
             float v = a.bias ? y[0] + a.bias[u] : y[0];
+            if (a.ex_w) v = v * a.ex_w[a.ex_slot];
+            if (a.sig_scale) v = v * (1.f / (1.f + expf(-a.sig_scale[0])));
             a.y[u] = a.y[u] + v;
         } else if (EPI == DG_STORE) {
             a.y[u] = a.bias ? y[0] + a.bias[u] : y[0];

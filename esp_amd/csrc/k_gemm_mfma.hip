@@ -457,15 +457,19 @@ __global__ void __launch_bounds__(128 * BMW, 2 / (BMW / 2)) gemm_lds_k(GemmArgs 
 
 static int g_cus = 0;
 
+// min_ks: smallest k range a split may get (the weight tile each block
+// streams shrinks with it, so skinny row counts use short splits to put the
+// weight stream on every CU)
 template <int EPI, int NB, int NJ>
-static void mfma_launch_nj(const GemmArgs &a, float *ws, size_t ws_bytes, hipStream_t s) {
+static void mfma_launch_nj(const GemmArgs &a, float *ws, size_t ws_bytes, hipStream_t s,
+                           int min_ks = 512) {
     constexpr size_t shm = mfma_lds_bytes<NB, NJ>();
     constexpr int BN = 64 * NJ;
     const int gx = (a.N + BN - 1) / BN, gy = (a.M + MF_BM - 1) / MF_BM;
     const int blocks = MF_XCDS * ((gx * gy + MF_XCDS - 1) / MF_XCDS);
-    // split K until the grid covers the chip twice (k-splits stay >= 512)
+    // split K until the grid covers the chip twice
     int splits = 1;
-    while (gx * gy * splits < 2 * g_cus && a.K / (splits * 2) >= 512 &&
+    while (gx * gy * splits < 2 * g_cus && a.K / (splits * 2) >= min_ks &&
            (size_t)(splits * 2) * NB * a.M * a.N * 4 <= ws_bytes)
         splits *= 2;
     int kps = (a.K + splits - 1) / splits;
@@ -528,6 +532,12 @@ template <int EPI> static void mfma_launch(const GemmArgs &a, float *ws, size_t 
     if (a.K % LS_BK == 0 && a.M >= 1024) {
         if (NB == 1) lds_launch<EPI, NB, 4>(a, ws, ws_bytes, s);
         else lds_launch<EPI, NB, 2>(a, ws, ws_bytes, s);
+        return;
+    }
+    if (a.M <= MF_BM) {
+        // one row tile (decode batches, forced blocks): 64-column weight
+        // tiles and k splits down to 128 keep hundreds of blocks streaming
+        mfma_launch_nj<EPI, NB, 1>(a, ws, ws_bytes, s, 128);
         return;
     }
     if (wide_tiles >= g_cus) mfma_launch_nj<EPI, NB, NJW>(a, ws, ws_bytes, s);

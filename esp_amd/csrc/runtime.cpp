@@ -736,7 +736,8 @@ static void run_layer_decode(Model &m, Kv &kv, const Rows &rows, LayerW &w, int 
     };
     resid("gemv_o", w.o, kv.attn.as<float>(), w.o_bias, H, m.qw);
     if (w.moe) {
-        moe_block(m, kv, w, 1, s);
+        if (moe_decode_ok(m)) moe_decode(m, kv, w, s);
+        else moe_block(m, kv, w, 1, s);
         return;
     }
     if (decode_gemv_ok(H)) {
@@ -1287,6 +1288,109 @@ void decode_step_dev(Model &m, Kv &kv, int seq, int max_t, int32_t *gen) {
     }
     launch_gen_step(a.ids_out, gen, s);
     kv.logits_rows = 1;
+}
+
+// Whether single-row MoE layers take the device-only decode path.
+bool moe_decode_ok(const Model &m) {
+    return decode_gemv_ok(m.H) && decode_gemv_ok(m.Fe) && (!m.Fs || decode_gemv_ok(m.Fs)) &&
+           m.E <= 256 && m.topk <= 8;
+}
+
+// moe.rs:135-256 for one decode row, entirely on the device (capturable):
+// router GEMV over RMSNorm(h), device top-k routing, one SwiGLU GEMV over
+// the k selected experts' gate/up rows (expert ids read on the device), then
+// per slot in ascending expert order a down GEMV that adds w_slot * y into
+// h, then the sigmoid-gated shared expert.
+void moe_decode(Model &m, Kv &kv, LayerW &w, hipStream_t s) {
+    const int H = m.H, E = m.E, k = m.topk;
+    kv.moe_logits.ensure((size_t)E * 4);
+    kv.moe_sel.ensure((size_t)k * 4);
+    kv.moe_w.ensure((size_t)k * 4);
+    kv.moe_slot.ensure((size_t)k * 4);
+    kv.moe_offs.ensure((size_t)(E + 2) * 4);
+    kv.moe_perm.ensure((size_t)k * 4);
+    kv.moe_act.ensure((size_t)k * std::max(m.Fe, m.Fs) * 4);
+    kv.moe_sg.ensure(64);
+    const size_t wes = dt_size(m.wt);
+    {
+        DecodeGemvArgs r{};
+        r.w = w.router;
+        r.x = kv.h.as<float>();
+        r.gamma = w.post_norm;
+        r.eps = m.cfg.rms_norm_eps;
+        r.y = kv.moe_logits.as<float>();
+        r.N = E;
+        r.K = H;
+        Prof p("moe", s);
+        launch_decode_gemv(m.wt, DG_STORE, r, s);
+        RouteArgs ra{kv.moe_logits.as<float>(), 1, E, k, m.norm_topk ? 1 : 0,
+                     kv.moe_sel.as<int32_t>(), kv.moe_w.as<float>(), kv.moe_offs.as<int32_t>(),
+                     kv.moe_perm.as<int32_t>(), kv.moe_slot.as<int32_t>()};
+        launch_route(ra, s);
+    }
+    {
+        DecodeGemvArgs g{};
+        g.w = w.ex_gate;
+        g.w2 = w.ex_up;
+        g.x = kv.h.as<float>();
+        g.gamma = w.post_norm;
+        g.eps = m.cfg.rms_norm_eps;
+        g.y = kv.moe_act.as<float>();
+        g.N = k * m.Fe;
+        g.K = H;
+        g.ex_sel = kv.moe_sel.as<int32_t>();
+        g.ex_stride = (long long)m.Fe * H;
+        g.ex_rows = m.Fe;
+        g.ex_count = E;
+        Prof p("gemv_mlp", s);
+        launch_decode_gemv(m.wt, DG_SWIGLU, g, s);
+    }
+    for (int j = 0; j < k; ++j) {
+        DecodeGemvArgs d{};
+        d.w = w.ex_down;
+        d.x = kv.moe_act.as<float>() + (size_t)j * m.Fe;
+        d.y = kv.h.as<float>();
+        d.N = H;
+        d.K = m.Fe;
+        d.ex_sel = kv.moe_sel.as<int32_t>();
+        d.ex_w = kv.moe_w.as<float>();
+        d.ex_stride = (long long)H * m.Fe;
+        d.ex_slot = j;
+        d.ex_count = E;
+        Prof p("gemv_down", s);
+        launch_decode_gemv(m.wt, DG_RESID, d, s);
+    }
+    (void)wes;
+    if (m.Fs) {
+        DecodeGemvArgs sg{};
+        sg.w = w.shared_gate;
+        sg.x = kv.h.as<float>();
+        sg.gamma = w.post_norm;
+        sg.eps = m.cfg.rms_norm_eps;
+        sg.y = kv.moe_sg.as<float>();
+        sg.N = 1;
+        sg.K = H;
+        DecodeGemvArgs g{};
+        g.w = w.sh_gate;
+        g.w2 = w.sh_up;
+        g.x = kv.h.as<float>();
+        g.gamma = w.post_norm;
+        g.eps = m.cfg.rms_norm_eps;
+        g.y = kv.moe_act.as<float>();
+        g.N = m.Fs;
+        g.K = H;
+        DecodeGemvArgs d{};
+        d.w = w.sh_down;
+        d.x = kv.moe_act.as<float>();
+        d.y = kv.h.as<float>();
+        d.N = H;
+        d.K = m.Fs;
+        d.sig_scale = kv.moe_sg.as<float>();
+        Prof p("moe", s);
+        launch_decode_gemv(m.wt, DG_STORE, sg, s);
+        launch_decode_gemv(m.wt, DG_SWIGLU, g, s);
+        launch_decode_gemv(m.wt, DG_RESID, d, s);
+    }
 }
 
 // moe.rs:135-256 DecoderMlp::forward (Moe arm) for Mc rows: h += routed
