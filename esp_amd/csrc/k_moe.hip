@@ -69,6 +69,55 @@ __global__ void __launch_bounds__(256) route_k(RouteArgs a) {
         }
         return;
     }
+    // Stable grouping: selection i = t*k + j (token-major) gets the rank of
+    // i among the selections of its expert. Each thread counts a contiguous
+    // range of selections per expert, an exclusive scan over threads (one
+    // expert per scanning thread) gives every range its start, and the ranges
+    // are then placed in parallel: rows of an expert stay in token order.
+    constexpr int EMAX = 32;  // experts handled by the parallel form
+    __shared__ int tc[EMAX][257];
+    __shared__ int eoff[257];
+    const int R = a.M * k;
+    const int nt = blockDim.x, tid = threadIdx.x;
+    if (E <= EMAX) {
+        const int per = (R + nt - 1) / nt, b0 = min(R, tid * per), b1 = min(R, b0 + per);
+        for (int e = 0; e < E; ++e) tc[e][tid] = 0;
+        for (int i = b0; i < b1; ++i) tc[a.sel[i]][tid] += 1;
+        __syncthreads();
+        if (tid < E) {  // exclusive scan of expert tid's counts over threads
+            int acc = 0;
+            for (int t = 0; t < nt; ++t) {
+                const int c = tc[tid][t];
+                tc[tid][t] = acc;
+                acc += c;
+            }
+            eoff[tid] = acc;  // expert total
+        }
+        __syncthreads();
+        if (tid == 0) {
+            int acc = 0;
+            for (int e = 0; e < E; ++e) {
+                const int c = eoff[e];
+                eoff[e] = acc;
+                a.offs[e] = acc;
+                acc += c;
+            }
+            a.offs[E] = acc;
+            a.offs[E + 1] = 0;
+        }
+        __syncthreads();
+        int run[EMAX];
+        for (int e = 0; e < E; ++e) run[e] = eoff[e] + tc[e][tid];
+        for (int i = b0; i < b1; ++i) {
+            const int e = a.sel[i];
+            int c = 0;
+            for (int q = 0; q < E; ++q)
+                if (q == e) c = run[q]++;
+            a.perm[c] = i / k;
+            a.slot[i] = c;
+        }
+        return;
+    }
     __shared__ int cnt[257];
     for (int e = threadIdx.x; e < E; e += blockDim.x) {
         int c = 0;
