@@ -326,8 +326,14 @@ static void dg_launch_nch(const DecodeGemvArgs &a, int cus, hipStream_t s) {
 template <typename WT, int EPI>
 static void dg_launch(const DecodeGemvArgs &a, int cus, hipStream_t s) {
     // Measured on MI355X: two rows per block (more blocks in flight) beats
-    // larger row blocks with more loads per lane at every decode shape.
+    // one or four rows per block at the projection shapes.
     const int nch = (a.K / DG_WAVES / 8 + 63) / 64;  // chunks per lane and row
+    // the head over a short K (one chunk per lane) streams best with four
+    // rows per block (measured at H 2048: 90.6 vs 97.4 us for 128256 rows)
+    if (EPI == DG_HEAD && nch <= 1) {
+        dg_launch_nch<WT, EPI, 4, 1>(a, cus, s);
+        return;
+    }
     if (nch <= 1) dg_launch_nch<WT, EPI, 2, 1>(a, cus, s);
     else if (nch <= 2) dg_launch_nch<WT, EPI, 2, 2>(a, cus, s);
     else if (nch <= 4) dg_launch_nch<WT, EPI, 2, 4>(a, cus, s);

@@ -245,8 +245,22 @@ __global__ void __launch_bounds__(256) mfma_reduce_k(GemmArgs g, const float *ws
         float v[NB];
 #pragma unroll
         for (int b = 0; b < NB; ++b) {
+            // up to eight split partials in flight per batch, summed in split order
             float t = 0.f;
-            for (int z = 0; z < splits; ++z) t += ws[((size_t)z * NB + b) * MN + idx];
+            if (splits <= 4) {
+                for (int z = 0; z < splits; ++z) t += ws[((size_t)z * NB + b) * MN + idx];
+                v[b] = t;
+                continue;
+            }
+            for (int z0 = 0; z0 < splits; z0 += 8) {
+                float pz[8];
+#pragma unroll
+                for (int q = 0; q < 8; ++q)
+                    pz[q] = z0 + q < splits ? ws[((size_t)(z0 + q) * NB + b) * MN + idx] : 0.f;
+#pragma unroll
+                for (int q = 0; q < 8; ++q)
+                    if (z0 + q < splits) t += pz[q];
+            }
             v[b] = t;
         }
         float *c = (float *)g.c + (size_t)row * g.ldc + col;
@@ -282,19 +296,22 @@ __global__ void __launch_bounds__(256) mfma_reduce_k(GemmArgs g, const float *ws
 // last valid row (their results are dropped by the epilogue).
 constexpr int LS_BK = 32;
 constexpr int LS_ROWB = LS_BK * 2;                 // bytes per tile row
-constexpr int LS_BROWS = 256;                      // weight rows per stage (all matrices)
 
-// BMW waves along M (block rows 64 * BMW) x 2 along N; stages per form:
-// 128-row blocks keep two stages (64 KB) so two blocks share a CU, 256-row
-// blocks (eight waves) keep three (144 KB).
-template <int BMW> struct LsForm {
+// BMW waves along M (block rows 64 * BMW) x 2 along N, BROWS weight rows
+// per stage (all matrices), STG stages: 128-row blocks with 256 weight rows
+// keep two stages (64 KB) so two blocks share a CU; 256-row blocks (eight
+// waves) keep three (144 KB); skinny row counts (M <= 128) use 64 weight
+// rows per matrix and six stages in flight (one block per CU), since their
+// time is the latency of the weight stream, not the matrix cores.
+template <int BMW, int BROWS = 256, int STG = (BMW == 2 ? 2 : 3)> struct LsForm {
     static constexpr int BM = 64 * BMW, NT = 128 * BMW;
     static constexpr int A = BM * LS_ROWB;                       // one A plane per stage
-    static constexpr int STAGE = 2 * A + LS_BROWS * LS_ROWB;
-    static constexpr int STAGES = BMW == 2 ? 2 : 3;
+    static constexpr int STAGE = 2 * A + BROWS * LS_ROWB;
+    static constexpr int STAGES = STG;
     static constexpr size_t LDS = (size_t)STAGES * STAGE;
-    static constexpr int QB = 8 / BMW;                           // weight loads per wave and stage
+    static constexpr int QB = BROWS / (32 * BMW);                // weight loads per wave and stage
     static constexpr int LPS = 4 + QB;                           // loads per wave and stage
+    static_assert(QB >= 1 && QB * 32 * BMW == BROWS, "weight rows must split over the waves");
 };
 
 // s_waitcnt immediate for vmcnt(n) (n & 15 in bits 3:0, n >> 4 in bits 15:14)
@@ -305,11 +322,11 @@ __device__ __forceinline__ int ls_swz(int r) { return (r >> 2) & 3; }
 typedef const void __attribute__((address_space(1))) *gptr_t;
 typedef void __attribute__((address_space(3))) *lptr_t;
 
-template <int EPI, int NB, int BMW>
-__global__ void __launch_bounds__(128 * BMW, 2 / (BMW / 2)) gemm_lds_k(GemmArgs g, float *ws,
-                                                                      int k_per_split, int mt, int nt) {
-    using F = LsForm<BMW>;
-    constexpr int BN = LS_BROWS / NB;  // weight columns per matrix
+template <int EPI, int NB, int BMW, int BROWS = 256, int STG = (BMW == 2 ? 2 : 3)>
+__global__ void __launch_bounds__(128 * BMW, (BMW == 2 && STG == 2) ? 2 : 1)
+    gemm_lds_k(GemmArgs g, float *ws, int k_per_split, int mt, int nt) {
+    using F = LsForm<BMW, BROWS, STG>;
+    constexpr int BN = BROWS / NB;     // weight columns per matrix
     constexpr int NJ = BN / 64;        // 32-column MFMA blocks per wave and matrix
     constexpr int STAGES = F::STAGES;
     extern __shared__ __attribute__((aligned(16))) char lds_s[];
@@ -371,8 +388,10 @@ __global__ void __launch_bounds__(128 * BMW, 2 / (BMW / 2)) gemm_lds_k(GemmArgs 
     for (int kt = 0; kt < KT; ++kt) {
         // this stage's loads are done once at most (later stages issued) x LPS remain
         const int later = min(STAGES - 2, KT - 1 - kt);
-        static_assert(STAGES <= 3 && 2 * F::LPS < 64, "vmcnt waits below cover up to 2 later stages");
-        if (later >= 2) __builtin_amdgcn_s_waitcnt(vm_imm(2 * F::LPS));
+        static_assert(STAGES <= 6 && 4 * F::LPS < 64, "vmcnt waits below cover up to 4 later stages");
+        if (later >= 4) __builtin_amdgcn_s_waitcnt(vm_imm(4 * F::LPS));
+        else if (later == 3) __builtin_amdgcn_s_waitcnt(vm_imm(3 * F::LPS));
+        else if (later == 2) __builtin_amdgcn_s_waitcnt(vm_imm(2 * F::LPS));
         else if (later == 1) __builtin_amdgcn_s_waitcnt(vm_imm(F::LPS));
         else __builtin_amdgcn_s_waitcnt(vm_imm(0));
         // every wave's loads of stage kt landed; stage kt-1 is free. A bare
@@ -484,33 +503,32 @@ static void mfma_launch_nj(const GemmArgs &a, float *ws, size_t ws_bytes, hipStr
     mfma_reduce_k<EPI, NB><<<rblocks, 256, 0, s>>>(a, ws, splits);
 }
 
-template <int EPI, int NB, int BMW>
-static void lds_launch(const GemmArgs &a, float *ws, size_t ws_bytes, hipStream_t s) {
-    using F = LsForm<BMW>;
-    constexpr int BN = LS_BROWS / NB;
+template <int EPI, int NB, int BMW, int BROWS = 256, int STG = (BMW == 2 ? 2 : 3)>
+static void lds_launch(const GemmArgs &a, float *ws, size_t ws_bytes, hipStream_t s,
+                       int want_blocks, int min_ks = 512) {
+    using F = LsForm<BMW, BROWS, STG>;
+    constexpr int BN = BROWS / NB;
     static bool attr = false;
     if (!attr) {
-        ESP_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(gemm_lds_k<EPI, NB, BMW>),
+        ESP_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(gemm_lds_k<EPI, NB, BMW, BROWS, STG>),
                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)F::LDS));
-        ESP_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(gemm_lds_k<MF_PARTIAL, NB, BMW>),
+        ESP_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(gemm_lds_k<MF_PARTIAL, NB, BMW, BROWS, STG>),
                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)F::LDS));
         attr = true;
     }
     const int gx = (a.N + BN - 1) / BN, gy = (a.M + F::BM - 1) / F::BM;
     const int blocks = MF_XCDS * ((gx * gy + MF_XCDS - 1) / MF_XCDS);
-    // split K until every CU holds two blocks' worth of waves (k-splits stay >= 512)
-    const int want = BMW == 2 ? 2 * g_cus : g_cus;
     int splits = 1;
-    while (gx * gy * splits < want && a.K / (splits * 2) >= 512 &&
+    while (gx * gy * splits < want_blocks && a.K / (splits * 2) >= min_ks &&
            (size_t)(splits * 2) * NB * a.M * a.N * 4 <= ws_bytes)
         splits *= 2;
     int kps = (a.K + splits - 1) / splits;
     kps = (kps + LS_BK - 1) / LS_BK * LS_BK;
     if (splits == 1) {
-        gemm_lds_k<EPI, NB, BMW><<<dim3(blocks, 1, 1), F::NT, F::LDS, s>>>(a, nullptr, a.K, gy, gx);
+        gemm_lds_k<EPI, NB, BMW, BROWS, STG><<<dim3(blocks, 1, 1), F::NT, F::LDS, s>>>(a, nullptr, a.K, gy, gx);
         return;
     }
-    gemm_lds_k<MF_PARTIAL, NB, BMW><<<dim3(blocks, 1, splits), F::NT, F::LDS, s>>>(a, ws, kps, gy, gx);
+    gemm_lds_k<MF_PARTIAL, NB, BMW, BROWS, STG><<<dim3(blocks, 1, splits), F::NT, F::LDS, s>>>(a, ws, kps, gy, gx);
     size_t mn = (size_t)a.M * a.N;
     const int rblocks = (int)std::min<size_t>((mn + 255) / 256, (size_t)g_cus * 8);
     mfma_reduce_k<EPI, NB><<<rblocks, 256, 0, s>>>(a, ws, splits);
@@ -530,13 +548,18 @@ template <int EPI> static void mfma_launch(const GemmArgs &a, float *ws, size_t 
     // long row counts (prefill of >= 1024 tokens) take the LDS-streamed form:
     // 256-row blocks for one weight matrix, 128-row blocks for gate/up pairs
     if (a.K % LS_BK == 0 && a.M >= 1024) {
-        if (NB == 1) lds_launch<EPI, NB, 4>(a, ws, ws_bytes, s);
-        else lds_launch<EPI, NB, 2>(a, ws, ws_bytes, s);
+        if (NB == 1) lds_launch<EPI, NB, 4>(a, ws, ws_bytes, s, g_cus);
+        else lds_launch<EPI, NB, 2>(a, ws, ws_bytes, s, 2 * g_cus);
+        return;
+    }
+    if (a.K % LS_BK == 0 && a.M <= MF_BM && !getenv("ESP_SKINNY_REG")) {
+        // one row tile (decode batches, forced blocks): 64 weight columns per
+        // matrix, six stages in flight, k splits down to 256 keys
+        lds_launch<EPI, NB, 2, 64 * NB, 6>(a, ws, ws_bytes, s, g_cus, 256);
         return;
     }
     if (a.M <= MF_BM) {
-        // one row tile (decode batches, forced blocks): 64-column weight
-        // tiles and k splits down to 128 keep hundreds of blocks streaming
+        // 64-column register-staged tiles, k splits down to 128 keys
         mfma_launch_nj<EPI, NB, 1>(a, ws, ws_bytes, s, 128);
         return;
     }
