@@ -454,9 +454,8 @@ __device__ __forceinline__ void att_store(const AttnDecodeArgs &a, size_t i, flo
 // plain stores, then L1-bypassing loads in the merging block. With
 // xcd_nx == 0 the partials go through agent-scope (write-through) stores and
 // loads instead, which any placement tolerates.
-template <int HD, int GM, bool XCD>
-__global__ void __launch_bounds__(ATT_WAVES * 64) attn_decode_k(AttnDecodeArgs a) {
-    constexpr int NW = ATT_WAVES;
+template <int HD, int GM, bool XCD, int NW = ATT_WAVES>
+__global__ void __launch_bounds__(NW * 64) attn_decode_k(AttnDecodeArgs a) {
     constexpr int NT = NW * 64;
     constexpr int DPL = 8;               // dims per lane
     constexpr int LPK = HD / DPL;        // lanes per key
@@ -800,10 +799,20 @@ void launch_attn_decode(const AttnDecodeArgs &a0, hipStream_t s) {
                                 : U * a.n_split;
     if (nb > 0x7fffffffLL) fail(ESP_BACKEND, "attn_decode: grid too large");
     dim3 grid((unsigned)nb);
-#define ATT_LAUNCH(HD_, GM_)                                                              \
-    do {                                                                              \
-        if (a.xcd_nx > 0) attn_decode_k<HD_, GM_, true><<<grid, ATT_WAVES * 64, 0, s>>>(a);  \
-        else attn_decode_k<HD_, GM_, false><<<grid, ATT_WAVES * 64, 0, s>>>(a);             \
+    // Many rows (batched decode) already fill the chip without key splits:
+    // four-wave blocks then let two blocks share a CU, so one block's loads
+    // overlap the other's scores across the chunks of a long split.
+    const bool narrow = U >= device_cus() && a.split_len > 2 * ATT_WAVES * 64 * 8 / a.hd;
+#define ATT_LAUNCH(HD_, GM_)                                                                   \
+    do {                                                                                   \
+        if (narrow) {                                                                      \
+            if (a.xcd_nx > 0) attn_decode_k<HD_, GM_, true, 4><<<grid, 4 * 64, 0, s>>>(a);   \
+            else attn_decode_k<HD_, GM_, false, 4><<<grid, 4 * 64, 0, s>>>(a);              \
+        } else if (a.xcd_nx > 0) {                                                         \
+            attn_decode_k<HD_, GM_, true><<<grid, ATT_WAVES * 64, 0, s>>>(a);                \
+        } else {                                                                           \
+            attn_decode_k<HD_, GM_, false><<<grid, ATT_WAVES * 64, 0, s>>>(a);               \
+        }                                                                                  \
     } while (0)
     if (a.hd == 64) {
         if (G <= 4) ATT_LAUNCH(64, 4);
