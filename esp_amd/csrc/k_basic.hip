@@ -6,6 +6,8 @@
 
 namespace esp {
 
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
 // ------------------------------------------------------------------ embed
 // model.rs:57-62 TokenEmbedding::forward — gather rows of [V, H].
 template <typename WT>
@@ -44,8 +46,78 @@ __global__ void __launch_bounds__(256) rmsnorm_k(const float *x, const float *ga
     }
 }
 
+// One wave per row for rows up to 4096 wide: the row and the norm weights
+// stay in registers (NQ four-element pieces per lane, 16-byte loads issued
+// together), the sum of squares is a wave reduction, and the output goes out
+// four elements per store.
+template <typename OT, bool SPLIT, int NQ>
+__global__ void __launch_bounds__(256) rmsnorm_wave_k(const float *x, const float *gamma, float eps, int M,
+                                                      int H, OT *out, const int32_t *row_index) {
+    const int lane = threadIdx.x & 63;
+    const int m = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (m >= M) return;
+    const int src = row_index ? row_index[m] : m;
+    const float *xr = x + (size_t)src * H;
+    f32x4 v[NQ], gv[NQ];  // the row and the norm weights, loaded together
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < NQ; ++i) {
+        const int j = (lane + 64 * i) * 4;
+        v[i] = j < H ? *(const f32x4 *)(xr + j) : f32x4{0.f, 0.f, 0.f, 0.f};
+        gv[i] = j < H ? *(const f32x4 *)(gamma + j) : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+#pragma unroll
+    for (int i = 0; i < NQ; ++i) ss += v[i][0] * v[i][0] + v[i][1] * v[i][1] + v[i][2] * v[i][2] + v[i][3] * v[i][3];
+    ss = wave_sum(ss);
+    const float rms = sqrtf(ss / (float)H + eps);
+    const size_t plane = (size_t)M * H;
+#pragma unroll
+    for (int i = 0; i < NQ; ++i) {
+        const int j = (lane + 64 * i) * 4;
+        if (j >= H) continue;
+        float y[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) y[e] = (v[i][e] / rms) * gv[i][e];
+        const size_t o = (size_t)m * H + j;
+        if (SPLIT) {
+            uint16_t hi[4], lo[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                hi[e] = f2bf(y[e]);
+                lo[e] = f2bf(y[e] - bf2f(hi[e]));
+            }
+            *(uint2 *)((uint16_t *)out + o) = make_uint2(hi[0] | ((uint32_t)hi[1] << 16), hi[2] | ((uint32_t)hi[3] << 16));
+            *(uint2 *)((uint16_t *)out + plane + o) =
+                make_uint2(lo[0] | ((uint32_t)lo[1] << 16), lo[2] | ((uint32_t)lo[3] << 16));
+        } else if (sizeof(OT) == 2) {
+            uint16_t b[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) b[e] = f2bf(y[e]);
+            *(uint2 *)((uint16_t *)out + o) = make_uint2(b[0] | ((uint32_t)b[1] << 16), b[2] | ((uint32_t)b[3] << 16));
+        } else {
+            *(f32x4 *)((float *)out + o) = f32x4{y[0], y[1], y[2], y[3]};
+        }
+    }
+}
+
+template <typename OT, bool SPLIT>
+static bool rmsnorm_wave(const float *x, const float *gamma, float eps, int M, int H, OT *out,
+                         const int32_t *row_index, hipStream_t s) {
+    if (H % 4 || H > 4096) return false;
+    const int nq = (H / 4 + 63) / 64;
+    const int blocks = (M + 3) / 4;
+    if (nq <= 2) rmsnorm_wave_k<OT, SPLIT, 2><<<blocks, 256, 0, s>>>(x, gamma, eps, M, H, out, row_index);
+    else if (nq <= 4) rmsnorm_wave_k<OT, SPLIT, 4><<<blocks, 256, 0, s>>>(x, gamma, eps, M, H, out, row_index);
+    else if (nq <= 8) rmsnorm_wave_k<OT, SPLIT, 8><<<blocks, 256, 0, s>>>(x, gamma, eps, M, H, out, row_index);
+    else rmsnorm_wave_k<OT, SPLIT, 16><<<blocks, 256, 0, s>>>(x, gamma, eps, M, H, out, row_index);
+    return true;
+}
+
 void launch_rmsnorm(const float *x, const float *gamma, float eps, int M, int H, Dt out_dt,
                     void *out, const int32_t *row_index, hipStream_t s) {
+    if (out_dt == DT_SPLIT && rmsnorm_wave<uint16_t, true>(x, gamma, eps, M, H, (uint16_t *)out, row_index, s)) return;
+    if (out_dt == DT_BF16 && rmsnorm_wave<uint16_t, false>(x, gamma, eps, M, H, (uint16_t *)out, row_index, s)) return;
+    if (out_dt == DT_F32 && rmsnorm_wave<float, false>(x, gamma, eps, M, H, (float *)out, row_index, s)) return;
     if (out_dt == DT_SPLIT)
         rmsnorm_k<uint16_t, true><<<M, 256, 0, s>>>(x, gamma, eps, H, (uint16_t *)out, row_index);
     else if (out_dt == DT_BF16)
