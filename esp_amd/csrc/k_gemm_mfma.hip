@@ -322,13 +322,19 @@ __device__ __forceinline__ int ls_swz(int r) { return (r >> 2) & 3; }
 typedef const void __attribute__((address_space(1))) *gptr_t;
 typedef void __attribute__((address_space(3))) *lptr_t;
 
-template <int EPI, int NB, int BMW, int BROWS = 256, int STG = (BMW == 2 ? 2 : 3)>
-__global__ void __launch_bounds__(128 * BMW, (BMW == 2 && STG == 2) ? 2 : 1)
+// PROD: one more wave per block issues every direct load of the tiles (the
+// 2 x BMW MFMA waves issue no vector memory instructions): it waits for a
+// stage's loads, meets the MFMA waves at the stage barrier and issues the
+// stage that reuses the slot just freed.
+template <int EPI, int NB, int BMW, int BROWS = 256, int STG = (BMW == 2 ? 2 : 3), bool PROD = false>
+__global__ void __launch_bounds__(128 * BMW + (PROD ? 64 : 0), (BMW == 2 && STG == 2) ? 2 : 1)
     gemm_lds_k(GemmArgs g, float *ws, int k_per_split, int mt, int nt) {
     using F = LsForm<BMW, BROWS, STG>;
     constexpr int BN = BROWS / NB;     // weight columns per matrix
     constexpr int NJ = BN / 64;        // 32-column MFMA blocks per wave and matrix
     constexpr int STAGES = F::STAGES;
+    constexpr int NMW = 2 * BMW;       // MFMA waves
+    static_assert(!PROD || (BN % 16) == 0, "a producer instruction's 16 weight rows share a matrix");
     extern __shared__ __attribute__((aligned(16))) char lds_s[];
     // wave index in an SGPR: the LDS bases of the direct loads (M0) stay scalar
     const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
@@ -372,6 +378,52 @@ __global__ void __launch_bounds__(128 * BMW, (BMW == 2 && STG == 2) ? 2 : 1)
                                              (lptr_t)(base + 2 * F::A + (wave * F::QB + q) * 1024), 16, 0, 0);
     };
 
+    if constexpr (PROD) {
+        if (wave == NMW) {  // the producer wave: every slot of every stage
+            constexpr int AQ = 2 * NMW, BQ = F::QB * NMW;  // instructions per A plane / for B
+            constexpr int LP = 2 * AQ + BQ;                 // loads per stage
+            static_assert(LP < 64, "one stage's loads must fit the vmcnt counter");
+            int aoff[AQ], boff[BQ];
+#pragma unroll
+            for (int q = 0; q < AQ; ++q) {
+                const int sl = q * 64 + lane, r = sl >> 2, kc = (sl & 3) ^ ls_swz(r);
+                aoff[q] = (int)((size_t)min(m0 + r, M - 1) * K + kbeg + kc * 8);
+            }
+#pragma unroll
+            for (int q = 0; q < BQ; ++q) {
+                const int sl = q * 64 + lane, r = sl >> 2, kc = (sl & 3) ^ ls_swz(r);
+                boff[q] = (int)((size_t)min(n0 + r % BN, N - 1) * K + kbeg + kc * 8);
+            }
+            const uint16_t *pa = (const uint16_t *)g.a, *pl = (const uint16_t *)g.a_lo;
+            auto pissue = [&](int kt) {
+                char *base = lds_s + (kt % STAGES) * F::STAGE;
+                const int ko = kt * LS_BK;
+#pragma unroll
+                for (int q = 0; q < AQ; ++q) {
+                    __builtin_amdgcn_global_load_lds((gptr_t)(pa + aoff[q] + ko), (lptr_t)(base + q * 1024), 16, 0, 0);
+                    __builtin_amdgcn_global_load_lds((gptr_t)(pl + aoff[q] + ko), (lptr_t)(base + F::A + q * 1024), 16, 0, 0);
+                }
+#pragma unroll
+                for (int q = 0; q < BQ; ++q) {  // rows [16 q, 16 q + 16): gate rows, then up rows
+                    const uint16_t *pw = (const uint16_t *)(q * 16 < BN ? g.w : g.w2);
+                    __builtin_amdgcn_global_load_lds((gptr_t)(pw + boff[q] + ko), (lptr_t)(base + 2 * F::A + q * 1024), 16, 0, 0);
+                }
+            };
+#pragma unroll
+            for (int st = 0; st < STAGES - 1; ++st)
+                if (st < KT) pissue(st);
+            for (int kt = 0; kt < KT; ++kt) {
+                const int later = min(STAGES - 2, KT - 1 - kt);
+                static_assert(STAGES == 3, "the producer keeps one later stage in flight");
+                if (later >= 1) __builtin_amdgcn_s_waitcnt(vm_imm(LP));
+                else __builtin_amdgcn_s_waitcnt(vm_imm(0));
+                __builtin_amdgcn_s_barrier();
+                if (kt + STAGES - 1 < KT) pissue(kt + STAGES - 1);
+            }
+            return;
+        }
+    }
+
     f32x16_t acc[NB][2][NJ];
 #pragma unroll
     for (int b = 0; b < NB; ++b)
@@ -382,22 +434,28 @@ __global__ void __launch_bounds__(128 * BMW, (BMW == 2 && STG == 2) ? 2 : 1)
 #pragma unroll
                 for (int e = 0; e < 16; ++e) acc[b][i][j][e] = 0.f;
 
+    if constexpr (!PROD) {
 #pragma unroll
-    for (int st = 0; st < STAGES - 1; ++st)
-        if (st < KT) issue(st);
+        for (int st = 0; st < STAGES - 1; ++st)
+            if (st < KT) issue(st);
+    }
     for (int kt = 0; kt < KT; ++kt) {
         // this stage's loads are done once at most (later stages issued) x LPS remain
-        const int later = min(STAGES - 2, KT - 1 - kt);
-        static_assert(STAGES <= 6 && 4 * F::LPS < 64, "vmcnt waits below cover up to 4 later stages");
-        if (later >= 4) __builtin_amdgcn_s_waitcnt(vm_imm(4 * F::LPS));
-        else if (later == 3) __builtin_amdgcn_s_waitcnt(vm_imm(3 * F::LPS));
-        else if (later == 2) __builtin_amdgcn_s_waitcnt(vm_imm(2 * F::LPS));
-        else if (later == 1) __builtin_amdgcn_s_waitcnt(vm_imm(F::LPS));
-        else __builtin_amdgcn_s_waitcnt(vm_imm(0));
+        if constexpr (!PROD) {
+            const int later = min(STAGES - 2, KT - 1 - kt);
+            static_assert(STAGES <= 6 && 4 * F::LPS < 64, "vmcnt waits below cover up to 4 later stages");
+            if (later >= 4) __builtin_amdgcn_s_waitcnt(vm_imm(4 * F::LPS));
+            else if (later == 3) __builtin_amdgcn_s_waitcnt(vm_imm(3 * F::LPS));
+            else if (later == 2) __builtin_amdgcn_s_waitcnt(vm_imm(2 * F::LPS));
+            else if (later == 1) __builtin_amdgcn_s_waitcnt(vm_imm(F::LPS));
+            else __builtin_amdgcn_s_waitcnt(vm_imm(0));
+        }
         // every wave's loads of stage kt landed; stage kt-1 is free. A bare
         // s_barrier: a fenced __syncthreads would wait for every stage in flight
         __builtin_amdgcn_s_barrier();
-        if (kt + STAGES - 1 < KT) issue(kt + STAGES - 1);
+        if constexpr (!PROD) {
+            if (kt + STAGES - 1 < KT) issue(kt + STAGES - 1);
+        }
         const char *base = lds_s + (kt % STAGES) * F::STAGE;
         const char *ah = base, *al = base + F::A, *bb = base + 2 * F::A;
 #pragma unroll
@@ -524,6 +582,31 @@ static void lds_launch(const GemmArgs &a, float *ws, size_t ws_bytes, hipStream_
         splits *= 2;
     int kps = (a.K + splits - 1) / splits;
     kps = (kps + LS_BK - 1) / LS_BK * LS_BK;
+    // 256-row tiles of one weight matrix take the producer form (measured on
+    // MI355X at the 8B prefill shapes: down 522 -> 502 us, o 159 -> 152 us;
+    // gate/up pairs showed no gain and keep 128-row blocks)
+    constexpr bool prod = BMW == 4 && NB == 1 && BROWS == 256 && STG == 3;
+    if constexpr (prod) {
+        {
+            static bool pattr = false;
+            if (!pattr) {
+                ESP_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(gemm_lds_k<EPI, NB, BMW, BROWS, STG, true>),
+                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)F::LDS));
+                ESP_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(gemm_lds_k<MF_PARTIAL, NB, BMW, BROWS, STG, true>),
+                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)F::LDS));
+                pattr = true;
+            }
+            if (splits == 1) {
+                gemm_lds_k<EPI, NB, BMW, BROWS, STG, true><<<dim3(blocks, 1, 1), F::NT + 64, F::LDS, s>>>(a, nullptr, a.K, gy, gx);
+                return;
+            }
+            gemm_lds_k<MF_PARTIAL, NB, BMW, BROWS, STG, true><<<dim3(blocks, 1, splits), F::NT + 64, F::LDS, s>>>(a, ws, kps, gy, gx);
+            size_t mn = (size_t)a.M * a.N;
+            const int rblocks = (int)std::min<size_t>((mn + 255) / 256, (size_t)g_cus * 8);
+            mfma_reduce_k<EPI, NB><<<rblocks, 256, 0, s>>>(a, ws, splits);
+            return;
+        }
+    }
     if (splits == 1) {
         gemm_lds_k<EPI, NB, BMW, BROWS, STG><<<dim3(blocks, 1, 1), F::NT, F::LDS, s>>>(a, nullptr, a.K, gy, gx);
         return;
