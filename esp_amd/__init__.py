@@ -9,5 +9,7 @@ from .errors import (Backend, InferError, Interrupted, InvalidConfig, InvalidReq
                      InvalidWeights, ModelNotLoaded, PromptTooLong, StageUnavailable, Unsupported)
 from .config import DecoderConfig, MoeConfig, RopeScaling  # noqa: F401
 from .model import DecoderModel, KvCache  # noqa: F401
-from .generate import TokenPicker, generate_ids, generate_ids_with  # noqa: F401
+from .generate import (TokenPicker, generate_constrained, generate_ids,  # noqa: F401
+                       generate_ids_with)
 from .sample import Sampler  # noqa: F401
+from .constraint import Constraint, Vocabulary  # noqa: F401

@@ -9,6 +9,7 @@
 
 #include "kernels_extra.hpp"
 #include "profile.hpp"
+#include "constraint.hpp"
 #include "runtime.hpp"
 
 namespace esp {
@@ -172,61 +173,202 @@ esp_status esp_forward_batch(esp_model *model, esp_kv *kv, uint32_t n_seqs, cons
     });
 }
 
+}  // extern "C"
+
+// esp_pick and esp_pick_constrained: masks come from the host
+// (allowed_bits) or are computed on the device from constraints (cs).
+static void pick_rows(Kv &k, uint32_t n_rows, const uint32_t *allowed_bits,
+                      esp_constraint *const *cs, esp_sampler *samplers, uint32_t *ids_out,
+                      uint8_t *flags_out) {
+    if (!n_rows || (int)n_rows > k.logits_rows)
+        fail(ESP_INVALID_REQUEST, "pick: rows exceed the logits of the last forward");
+    if (!ids_out) fail(ESP_INVALID_REQUEST, "pick: null ids_out");
+    const int V = k.model->V, words = (V + 31) / 32;
+    std::vector<Constraint *> rows_c, con;
+    std::vector<uint32_t *> con_mask;
+    if (cs) {
+        for (uint32_t i = 0; i < n_rows; ++i) {
+            Constraint *c = (Constraint *)cs[i];
+            if (c && (int)c->vocab->n != V)
+                fail(ESP_INVALID_REQUEST, "constraint vocabulary does not match the model");
+            rows_c.push_back(c);
+        }
+    }
+    const bool masked = allowed_bits || cs;
+    const size_t mask_b = masked ? (size_t)n_rows * words * 4 : 0;
+    const size_t smp_b = samplers ? (size_t)n_rows * sizeof(esp_sampler) : 0;
+    const size_t out_b = (size_t)n_rows * (4 + 1 + 8) + 64;
+    size_t off_mask = 0, off_smp = (mask_b + 255) / 256 * 256,
+           off_out = off_smp + (smp_b + 255) / 256 * 256;
+    k.pick_io.ensure(off_out + out_b);
+    char *io = (char *)k.pick_io.p;
+    hipStream_t s = k.stream;
+    if (allowed_bits)
+        ESP_HIP(hipMemcpyAsync(io + off_mask, allowed_bits, mask_b, hipMemcpyHostToDevice, s));
+    if (cs) {
+        uint32_t *m = (uint32_t *)(io + off_mask);
+        for (uint32_t i = 0; i < n_rows; ++i) {
+            if (rows_c[i]) {
+                con.push_back(rows_c[i]);
+                con_mask.push_back(m + (size_t)i * words);
+            } else {
+                ESP_HIP(hipMemsetAsync(m + (size_t)i * words, 0xff, (size_t)words * 4, s));
+            }
+        }
+        if (!k.cmask) k.cmask = std::make_shared<MaskCtx>();
+        Prof p("cmask", s);
+        run_cmask(*k.cmask, con.data(), con_mask.data(), (int)con.size(), s);
+    }
+    if (smp_b) ESP_HIP(hipMemcpyAsync(io + off_smp, samplers, smp_b, hipMemcpyHostToDevice, s));
+    bool any_sampled = false;
+    for (uint32_t i = 0; samplers && i < n_rows; ++i) any_sampled |= samplers[i].temperature > 0.f;
+    size_t scr = any_sampled ? pick_scratch_bytes((int)n_rows, V) : 0;
+    k.pick_scratch.ensure(scr ? scr : 64);
+    PickArgs a{};
+    a.logits = k.logits.as<float>();
+    a.n = (int)n_rows;
+    a.V = V;
+    a.allowed = mask_b ? (const uint32_t *)(io + off_mask) : nullptr;
+    a.samplers = smp_b ? (const esp_sampler *)(io + off_smp) : nullptr;
+    uint32_t *d_ids = (uint32_t *)(io + off_out);
+    uint64_t *d_state = (uint64_t *)(io + off_out + (size_t)n_rows * 4 + 8 - ((size_t)n_rows * 4) % 8);
+    uint8_t *d_flags = (uint8_t *)(d_state + n_rows);
+    a.ids_out = d_ids;
+    a.flags_out = d_flags;
+    a.state_out = d_state;
+    a.scratch = k.pick_scratch.p;
+    a.scratch_bytes = k.pick_scratch.bytes;
+    {
+        Prof p("pick", s);
+        launch_pick(a, s);
+    }
+    std::vector<uint64_t> states(n_rows);
+    std::vector<uint8_t> flags(n_rows);
+    ESP_HIP(hipMemcpyAsync(ids_out, d_ids, (size_t)n_rows * 4, hipMemcpyDeviceToHost, s));
+    ESP_HIP(hipMemcpyAsync(states.data(), d_state, (size_t)n_rows * 8, hipMemcpyDeviceToHost, s));
+    ESP_HIP(hipMemcpyAsync(flags.data(), d_flags, n_rows, hipMemcpyDeviceToHost, s));
+    if (!con.empty()) check_cmask(*k.cmask, s);
+    ESP_HIP(hipStreamSynchronize(s));
+    bool none = false;
+    for (uint32_t i = 0; i < n_rows; ++i) {
+        if (flags_out) flags_out[i] = flags[i];
+        if (samplers && samplers[i].temperature > 0.f && !(flags[i] & ESP_PICK_NO_ELIGIBLE))
+            samplers[i].state = states[i];
+        none |= (flags[i] & ESP_PICK_NO_ELIGIBLE) != 0;
+    }
+    if (none) fail(ESP_INVALID_REQUEST, "output grammar has no finite eligible token");
+}
+
+extern "C" {
+
 esp_status esp_pick(esp_kv *kv, uint32_t n_rows, const uint32_t *allowed_bits,
                     esp_sampler *samplers, uint32_t *ids_out, uint8_t *flags_out) {
     return guard([&] {
         if (!kv) fail(ESP_INVALID_REQUEST, "null kv handle");
-        Kv &k = *(Kv *)kv;
-        if (!n_rows || (int)n_rows > k.logits_rows)
-            fail(ESP_INVALID_REQUEST, "pick: rows exceed the logits of the last forward");
-        if (!ids_out) fail(ESP_INVALID_REQUEST, "pick: null ids_out");
-        const int V = k.model->V, words = (V + 31) / 32;
-        const size_t mask_b = allowed_bits ? (size_t)n_rows * words * 4 : 0;
-        const size_t smp_b = samplers ? (size_t)n_rows * sizeof(esp_sampler) : 0;
-        const size_t out_b = (size_t)n_rows * (4 + 1 + 8) + 64;
-        size_t off_mask = 0, off_smp = (mask_b + 255) / 256 * 256,
-               off_out = off_smp + (smp_b + 255) / 256 * 256;
-        k.pick_io.ensure(off_out + out_b);
-        char *io = (char *)k.pick_io.p;
-        hipStream_t s = k.stream;
-        if (mask_b) ESP_HIP(hipMemcpyAsync(io + off_mask, allowed_bits, mask_b, hipMemcpyHostToDevice, s));
-        if (smp_b) ESP_HIP(hipMemcpyAsync(io + off_smp, samplers, smp_b, hipMemcpyHostToDevice, s));
-        bool any_sampled = false;
-        for (uint32_t i = 0; samplers && i < n_rows; ++i) any_sampled |= samplers[i].temperature > 0.f;
-        size_t scr = any_sampled ? pick_scratch_bytes((int)n_rows, V) : 0;
-        k.pick_scratch.ensure(scr ? scr : 64);
-        PickArgs a{};
-        a.logits = k.logits.as<float>();
-        a.n = (int)n_rows;
-        a.V = V;
-        a.allowed = mask_b ? (const uint32_t *)(io + off_mask) : nullptr;
-        a.samplers = smp_b ? (const esp_sampler *)(io + off_smp) : nullptr;
-        uint32_t *d_ids = (uint32_t *)(io + off_out);
-        uint64_t *d_state = (uint64_t *)(io + off_out + (size_t)n_rows * 4 + 8 - ((size_t)n_rows * 4) % 8);
-        uint8_t *d_flags = (uint8_t *)(d_state + n_rows);
-        a.ids_out = d_ids;
-        a.flags_out = d_flags;
-        a.state_out = d_state;
-        a.scratch = k.pick_scratch.p;
-        a.scratch_bytes = k.pick_scratch.bytes;
+        pick_rows(*(Kv *)kv, n_rows, allowed_bits, nullptr, samplers, ids_out, flags_out);
+    });
+}
+
+esp_status esp_pick_constrained(esp_kv *kv, uint32_t n_rows, esp_constraint *const *constraints,
+                                esp_sampler *samplers, uint32_t *ids_out, uint8_t *flags_out) {
+    return guard([&] {
+        if (!kv) fail(ESP_INVALID_REQUEST, "null kv handle");
+        if (!constraints) fail(ESP_INVALID_REQUEST, "pick: null constraints");
+        pick_rows(*(Kv *)kv, n_rows, nullptr, constraints, samplers, ids_out, flags_out);
+    });
+}
+
+// ------------------------------------------------------------ constraints
+
+struct esp_vocab {
+    std::shared_ptr<Vocab> v;
+};
+
+esp_status esp_vocab_create(const uint8_t *bytes, const uint32_t *offsets, uint32_t n_tokens,
+                            esp_vocab **out) {
+    return guard([&] {
+        if (!out) fail(ESP_INVALID_REQUEST, "vocab: null out");
+        *out = nullptr;
+        if (!offsets || !n_tokens) fail(ESP_INVALID_REQUEST, "vocab: empty token table");
+        if (offsets[0] != 0) fail(ESP_INVALID_REQUEST, "vocab: offsets must start at 0");
+        auto v = std::make_shared<Vocab>();
+        v->n = n_tokens;
+        v->off.assign(offsets, offsets + n_tokens + 1);
+        for (uint32_t i = 0; i < n_tokens; ++i) {
+            if (v->off[i + 1] < v->off[i]) fail(ESP_INVALID_REQUEST, "vocab: offsets decrease");
+            v->max_len = std::max(v->max_len, v->off[i + 1] - v->off[i]);
+        }
+        if (v->off[n_tokens] && !bytes) fail(ESP_INVALID_REQUEST, "vocab: null bytes");
+        v->bytes.assign(bytes, bytes + v->off[n_tokens]);
+        *out = new esp_vocab{std::move(v)};
+    });
+}
+
+esp_status esp_vocab_destroy(esp_vocab *vocab) {
+    return guard([&] { delete vocab; });
+}
+
+esp_status esp_constraint_create(const esp_vocab *vocab, const char *grammar_json, size_t len,
+                                 esp_constraint **out) {
+    return guard([&] {
+        if (!out) fail(ESP_INVALID_REQUEST, "constraint: null out");
+        *out = nullptr;
+        if (!vocab) fail(ESP_INVALID_REQUEST, "constraint: null vocabulary");
+        *out = (esp_constraint *)new Constraint(vocab->v, grammar_json, len);
+    });
+}
+
+esp_status esp_constraint_destroy(esp_constraint *c) {
+    return guard([&] { delete (Constraint *)c; });
+}
+
+esp_status esp_constraint_accept(esp_constraint *c, uint32_t token) {
+    return guard([&] {
+        if (!c) fail(ESP_INVALID_REQUEST, "null constraint");
+        ((Constraint *)c)->accept(token);
+    });
+}
+
+esp_status esp_constraint_complete(const esp_constraint *c, uint8_t *complete) {
+    return guard([&] {
+        if (!c || !complete) fail(ESP_INVALID_REQUEST, "null constraint");
+        *complete = ((const Constraint *)c)->complete() ? 1 : 0;
+    });
+}
+
+esp_status esp_constraint_forced_bytes(const esp_constraint *c, uint8_t *out, uint32_t cap,
+                                       uint32_t *len) {
+    return guard([&] {
+        if (!c || !len) fail(ESP_INVALID_REQUEST, "null constraint");
+        std::vector<uint8_t> b = ((const Constraint *)c)->forced_bytes();
+        *len = (uint32_t)b.size();
+        if (b.size() > cap || (!out && !b.empty()))
+            fail(ESP_INVALID_REQUEST, "forced bytes exceed the output buffer");
+        if (!b.empty()) memcpy(out, b.data(), b.size());
+    });
+}
+
+esp_status esp_constraint_mask(esp_constraint *c, void *stream, uint32_t *allowed_dev,
+                               uint32_t *allowed_host) {
+    return guard([&] {
+        if (!c) fail(ESP_INVALID_REQUEST, "null constraint");
+        Constraint &k = *(Constraint *)c;
+        hipStream_t s = (hipStream_t)stream;
+        const size_t words = ((size_t)k.vocab->n + 31) / 32;
+        uint32_t *m = allowed_dev;
+        DevMem tmp;
+        if (!m) {
+            tmp.alloc(words * 4);
+            m = tmp.as<uint32_t>();
+        }
+        Constraint *one = &k;
         {
-            Prof p("pick", s);
-            launch_pick(a, s);
+            Prof p("cmask", s);
+            run_cmask(k.ctx, &one, &m, 1, s);
         }
-        std::vector<uint64_t> states(n_rows);
-        std::vector<uint8_t> flags(n_rows);
-        ESP_HIP(hipMemcpyAsync(ids_out, d_ids, (size_t)n_rows * 4, hipMemcpyDeviceToHost, s));
-        ESP_HIP(hipMemcpyAsync(states.data(), d_state, (size_t)n_rows * 8, hipMemcpyDeviceToHost, s));
-        ESP_HIP(hipMemcpyAsync(flags.data(), d_flags, n_rows, hipMemcpyDeviceToHost, s));
-        ESP_HIP(hipStreamSynchronize(s));
-        bool none = false;
-        for (uint32_t i = 0; i < n_rows; ++i) {
-            if (flags_out) flags_out[i] = flags[i];
-            if (samplers && samplers[i].temperature > 0.f && !(flags[i] & ESP_PICK_NO_ELIGIBLE))
-                samplers[i].state = states[i];
-            none |= (flags[i] & ESP_PICK_NO_ELIGIBLE) != 0;
-        }
-        if (none) fail(ESP_INVALID_REQUEST, "output grammar has no finite eligible token");
+        if (allowed_host)
+            ESP_HIP(hipMemcpyAsync(allowed_host, m, words * 4, hipMemcpyDeviceToHost, s));
+        check_cmask(k.ctx, s);
     });
 }
 

@@ -37,6 +37,8 @@ struct DevMem {
     template <typename T> T *as() const { return (T *)p; }
 };
 
+struct MaskCtx;  // constraint.hpp
+
 struct LayerW {
     float *in_norm = nullptr, *post_norm = nullptr;
     void *qkv = nullptr;        // [qkv_rows, H]: q | k | v | LoRA-A rows (q, k, v targets)
@@ -104,6 +106,8 @@ struct Kv {
     size_t pinned_bytes = 0;
     // generation graph
     hipGraphExec_t gen_exec = nullptr;
+    // grammar mask buffers of esp_pick_constrained
+    std::shared_ptr<MaskCtx> cmask;
     ~Kv();
 };
 

@@ -8,8 +8,9 @@ no per-token callback executes as one device-resident loop
 """
 from __future__ import annotations
 
-from typing import Callable, List, Optional, Sequence
+from typing import Callable, List, Optional, Sequence, Tuple
 
+from .errors import InvalidRequest
 from .model import DecoderModel, KvCache
 from .sample import Sampler
 
@@ -73,3 +74,49 @@ def try_generate_ids_with(model: DecoderModel, prompt_ids: Sequence[int], max_ne
             break
         model.try_forward_cached_last([token], cache)
     return out
+
+
+def generate_constrained(model: DecoderModel, prompt_ids: Sequence[int], max_new: int,
+                         eos: Sequence[int], picker: TokenPicker, constraint, tokenizer,
+                         cache: Optional[KvCache] = None) -> Tuple[List[int], bool]:
+    """The token loop of provider.rs:735-883 under an output grammar.
+
+    Each turn either takes the grammar's forced span (constraint.rs:296-344;
+    a sampled picker skips one draw per forced token, provider.rs:819-824)
+    or picks one token from the logits masked on the device by the
+    constraint (provider.rs:744-817). Tokens are accepted into the
+    constraint; the loop ends when the grammar is complete or an eos id is
+    picked, and a token limit reached first is InvalidRequest
+    (provider.rs:874-878). Forced spans are evaluated as one block over the
+    warm cache. Returns (ids, complete)."""
+    if not prompt_ids:
+        raise AssertionError("prompt must not be empty")
+    need = len(prompt_ids) + max(0, max_new - 1)
+    cache = cache or model.new_cache(1, max(need, 1))
+    cache.reset(0)
+    model.try_forward_cached_last(list(prompt_ids), cache)
+    out: List[int] = []
+    sampler = picker.sampler
+    while len(out) < max_new:
+        forced = constraint.forced(tokenizer)
+        if not forced:
+            ids, _ = model.pick_constrained(cache, [constraint],
+                                            None if sampler is None else [sampler])
+            tokens = [int(ids[0])]
+        else:
+            if sampler is not None:
+                sampler.skip_draws(len(forced))
+            tokens = forced
+        evaluated: List[int] = []
+        for token in tokens[:max_new - len(out)]:
+            if token in eos:
+                return out, True
+            constraint.accept(token)
+            out.append(token)
+            evaluated.append(token)
+            if constraint.complete():
+                return out, True
+        if len(out) == max_new:
+            break
+        model.try_forward_cached_last(evaluated, cache)
+    raise InvalidRequest("token limit reached before output grammar completed")

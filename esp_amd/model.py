@@ -189,14 +189,28 @@ class DecoderModel:
              samplers: Optional[List[Optional[Sampler]]] = None) -> Tuple[np.ndarray, np.ndarray]:
         """Token choice over the device-resident logits rows of the last forward
         (generate.rs:30-44, provider.rs:807-816). Updates sampler RNG state."""
-        ids = np.zeros(n_rows, np.uint32)
-        flags = np.zeros(n_rows, np.uint8)
         bits = None
         if allowed_bits is not None:
             bits = np.ascontiguousarray(allowed_bits, dtype=np.uint32)
             words = (self.config.vocab_size + 31) // 32
             if bits.size != n_rows * words:
                 raise InvalidRequest("allowed bitmask has the wrong size")
+        return self._pick(cache, n_rows, samplers, lambda *a: _lib.load().esp_pick(
+            cache._h, n_rows, None if bits is None else bits.ctypes.data, *a))
+
+    def pick_constrained(self, cache: KvCache, constraints: Sequence[Optional["Constraint"]],
+                         samplers: Optional[List[Optional[Sampler]]] = None
+                         ) -> Tuple[np.ndarray, np.ndarray]:
+        """provider.rs:740-817: pick with each row masked on the device by its
+        constraint (None = unconstrained). Constraint states are not advanced."""
+        from .constraint import constraint_handles
+        arr, keep = constraint_handles(constraints)
+        return self._pick(cache, len(constraints), samplers, lambda *a: _lib.load()
+                          .esp_pick_constrained(cache._h, len(keep), arr, *a))
+
+    def _pick(self, cache: KvCache, n_rows: int, samplers, call) -> Tuple[np.ndarray, np.ndarray]:
+        ids = np.zeros(n_rows, np.uint32)
+        flags = np.zeros(n_rows, np.uint8)
         sarr = None
         if samplers is not None:
             sarr = (_lib.EspSampler * n_rows)()
@@ -206,9 +220,8 @@ class DecoderModel:
                 else:
                     sarr[i] = _lib.EspSampler(s.temperature,
                                               -1.0 if s.top_p is None else s.top_p, s.rng.state)
-        status = _lib.load().esp_pick(
-            cache._h, n_rows, None if bits is None else bits.ctypes.data, sarr,
-            ids.ctypes.data_as(C.POINTER(C.c_uint32)), flags.ctypes.data_as(C.POINTER(C.c_uint8)))
+        status = call(sarr, ids.ctypes.data_as(C.POINTER(C.c_uint32)),
+                      flags.ctypes.data_as(C.POINTER(C.c_uint8)))
         if samplers is not None:
             for i, s in enumerate(samplers):
                 if s is not None:

@@ -186,6 +186,63 @@ esp_status esp_generate_greedy(esp_model *model, esp_kv *kv, uint32_t seq, const
                                uint32_t n_prompt, uint32_t max_new, const int32_t *eos,
                                uint32_t n_eos, int32_t *out_ids, uint32_t *n_out);
 
+/* ---- Constrained decoding (decoder/constraint.rs) ----
+ * A vocabulary holds the byte string of every token id of a byte-level
+ * tokenizer; a constraint is one request's compiled output grammar plus its
+ * active automaton state. A constraint is owned by one caller at a time; a
+ * vocabulary may be shared by many constraints and threads. */
+typedef struct esp_vocab esp_vocab;
+typedef struct esp_constraint esp_constraint;
+
+/* The token table constraint.rs:119-154 derives from a ByteLevel
+ * tokenizer: token i is bytes[offsets[i] .. offsets[i+1]] for i <
+ * n_tokens, where n_tokens is the model's vocabulary size. An empty token
+ * (added tokens, ids the tokenizer lacks, pieces outside the byte
+ * alphabet) is never allowed. */
+esp_status esp_vocab_create(const uint8_t *bytes, const uint32_t *offsets, uint32_t n_tokens,
+                            esp_vocab **out);
+esp_status esp_vocab_destroy(esp_vocab *vocab);
+
+/* constraint.rs:56-157 Constraint::new. grammar_json is an OutputGrammar
+ * (provider.rs:55-75) in its serde form, e.g.
+ * {"kind":"sequence","items":[{"kind":"literal","value":"{\"v\":"},
+ * {"kind":"json_string","max_bytes":8},{"kind":"literal","value":"}"}]}.
+ * Bounds as the reference: nesting depth 24, 100000 states, 262144 literal
+ * bytes, JSON string bound 1..4096, 1..64 choice alternatives
+ * (ESP_INVALID_REQUEST). The constraint keeps its own reference to the
+ * vocabulary, so the vocabulary may be destroyed first. */
+esp_status esp_constraint_create(const esp_vocab *vocab, const char *grammar_json, size_t len,
+                                 esp_constraint **out);
+esp_status esp_constraint_destroy(esp_constraint *c);
+/* constraint.rs:261-273 accept: advance by one token; an empty or
+ * unknown token, or one the grammar refuses, is ESP_INVALID_REQUEST and
+ * leaves the state unchanged. */
+esp_status esp_constraint_accept(esp_constraint *c, uint32_t token);
+/* constraint.rs:256-260 complete: the grammar may end here. */
+esp_status esp_constraint_complete(const esp_constraint *c, uint8_t *complete);
+/* constraint.rs:296-318, the byte half of `forced`: the unique-byte
+ * continuation of the active state (at most 4096 bytes, cut back to valid
+ * UTF-8). The caller tokenises it and checks that the ids' bytes
+ * round-trip (constraint.rs:319-343). `len` receives the length; `out`
+ * needs `cap` >= len (4096 always suffices). */
+esp_status esp_constraint_forced_bytes(const esp_constraint *c, uint8_t *out, uint32_t cap,
+                                       uint32_t *len);
+/* constraint.rs:277-297 mask, its eligibility half, on the device: bit
+ * id%32 of word id/32 is set iff token id is non-empty and leaves the
+ * grammar alive. Runs on `stream` (hipStream_t, NULL = default); the
+ * ceil(n_tokens/32) words go to allowed_dev (device, nullable) and/or
+ * allowed_host (host, nullable). Returns after the mask is complete. */
+esp_status esp_constraint_mask(esp_constraint *c, void *stream, uint32_t *allowed_dev,
+                               uint32_t *allowed_host);
+/* provider.rs:740-817 with the mask built on the device: esp_pick where
+ * row i's mask is constraints[i]'s (NULL = unconstrained row). Disallowed
+ * or non-finite logits become -inf; a row with no eligible token sets
+ * ESP_PICK_NO_ELIGIBLE and the call returns ESP_INVALID_REQUEST
+ * (constraint.rs:292-294). Constraint states are not advanced: the caller
+ * accepts the picked ids (constraint.rs:261). */
+esp_status esp_pick_constrained(esp_kv *kv, uint32_t n_rows, esp_constraint *const *constraints,
+                                esp_sampler *samplers, uint32_t *ids_out, uint8_t *flags_out);
+
 /* Kernel timing (measurement support, no reference counterpart): while
  * enabled, every launch of the named kernel family records HIP events on
  * its stream; read returns launches and total milliseconds since enable. */
