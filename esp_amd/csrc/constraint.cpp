@@ -514,6 +514,13 @@ void Vocab::to_device() {
     if (!bytes.empty())
         ESP_HIP(hipMemcpy(d_bytes.p, bytes.data(), bytes.size(), hipMemcpyHostToDevice));
     ESP_HIP(hipMemcpy(d_off.p, off.data(), off.size() * 4, hipMemcpyHostToDevice));
+    if (max_len <= CSTR_MAX_LEN) {
+        d_scls.alloc((size_t)CSTR_STATES * n * 4);
+        launch_str_class(d_bytes.as<uint8_t>(), d_off.as<uint32_t>(), (int)n,
+                         d_scls.as<uint32_t>(), nullptr);
+        ESP_HIP(hipGetLastError());
+        ESP_HIP(hipStreamSynchronize(nullptr));
+    }
     device = dev;
 }
 
@@ -601,6 +608,9 @@ void run_cmask(MaskCtx &ctx, Constraint *const *cs, uint32_t *const *masks, int 
     }
     if (cap_max * 16 > kFrontierBudget)
         fail(ESP_UNSUPPORTED, "constrained decoding: grammar frontier exceeds the device bound");
+    // ESP_CMASK_STRCLASS=0 walks string states byte by byte (tests compare both).
+    const char *sc = getenv("ESP_CMASK_STRCLASS");
+    const bool strclass = !(sc && sc[0] == '0');
     ctx.stage.assign(bytes, 0);
     ctx.io.ensure(bytes);
     char *dev = (char *)ctx.io.p;
@@ -623,6 +633,20 @@ void run_cmask(MaskCtx &ctx, Constraint *const *cs, uint32_t *const *masks, int 
         r.V = (int)c.vocab->n;
         r.row = i;
         r.cap = caps[i];
+        if (strclass && c.active.size() == 1 && c.nodes[c.active[0].node].kind == G_STRING &&
+            c.vocab->d_scls.p) {
+            const Pos &p = c.active[0];
+            const GNode &g = c.nodes[p.node];
+            static const uint8_t st4[3] = {3, 4, 5}, st5[5] = {6, 0, 0, 7, 8};
+            uint32_t cls = range_class(p.low, p.high);
+            r.mode = 1;
+            r.s_used = p.used;
+            r.s_max = g.max;
+            r.s_next = g.next;
+            r.s_state = p.phase == 0 ? 9 : p.phase == 1 ? 0 : p.phase == 2 ? 1 : p.phase == 3 ? 2
+                      : p.phase == 4 ? st4[cls] : st5[cls];
+            r.scls = c.vocab->d_scls.as<uint32_t>() + (size_t)r.s_state * c.vocab->n;
+        }
         rows[i] = r;
     }
     int blocks = (int)std::min<uint64_t>(256, kFrontierBudget / (cap_max * 16));
@@ -641,10 +665,13 @@ void run_cmask(MaskCtx &ctx, Constraint *const *cs, uint32_t *const *masks, int 
     a.frontier = ctx.frontier.as<uint64_t>();
     a.cap_max = cap_max;
     a.blocks = blocks;
-    // ESP_CMASK_LANE_CAP (0..8, default 8) lowers the lane frontier so that
-    // tests can drive every token through the block walk.
+    // ESP_CMASK_LANE_CAP (0..8, default 8) and ESP_CMASK_WAVE_CAP (0..64,
+    // default 64) lower the lane and wave frontiers so that tests can drive
+    // tokens through the wave and block walks.
     const char *lc = getenv("ESP_CMASK_LANE_CAP");
+    const char *wc = getenv("ESP_CMASK_WAVE_CAP");
     a.lane_cap = lc ? std::max(0, std::min(8, atoi(lc))) : 8;
+    a.wave_cap = wc ? std::max(0, std::min(64, atoi(wc))) : 64;
     launch_cmask(a, s);
 }
 

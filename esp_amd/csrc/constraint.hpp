@@ -55,6 +55,7 @@ struct Vocab {
     std::mutex mu;
     int device = -1;
     DevMem d_bytes, d_off;
+    DevMem d_scls;  // [CSTR_STATES][n] string classes (launch_str_class)
     void to_device();  // idempotent; fails if already on another device
 };
 
@@ -109,6 +110,11 @@ struct Constraint {
 constexpr uint32_t CN_NODE_BITS = 17;
 constexpr uint32_t CN_NODE_MASK = (1u << CN_NODE_BITS) - 1;
 
+// Start states of the string-class table (see cstr_class_k).
+constexpr int CSTR_STATES = 10;
+// Longest token the string-class table can describe (14-bit fields).
+constexpr uint32_t CSTR_MAX_LEN = 16383;
+
 struct CRow {
     const uint32_t *nodes, *split_off, *members;
     const uint32_t *first_off;  // [257]
@@ -119,6 +125,12 @@ struct CRow {
     int V;
     int row;
     uint64_t cap;               // block-walk frontier capacity
+    // mode 1: the active set is the single JSON-string position (node with
+    // bound s_max and successor s_next, `used` s_used, start state s_state);
+    // scls = that state's row of the vocabulary's string-class table
+    int mode;
+    uint32_t s_used, s_max, s_next, s_state;
+    const uint32_t *scls;
 };
 
 struct CMaskLaunch {
@@ -131,9 +143,12 @@ struct CMaskLaunch {
     uint64_t *frontier; // [blocks][2][cap_max]
     uint64_t cap_max;
     int blocks;         // block-walk grid
-    int lane_cap;       // lane frontier capacity (0 sends every token to the block walk)
+    int lane_cap;       // lane frontier capacity (0 sends every live token to the wave walk)
+    int wave_cap;       // wave frontier capacity (0 sends those on to the block walk)
 };
 void launch_cmask(const CMaskLaunch &a, hipStream_t s);
+void launch_str_class(const uint8_t *tok, const uint32_t *off, int V, uint32_t *out,
+                      hipStream_t s);
 
 // Build the descriptors and first-byte tables of `n` constraints into ctx,
 // then launch the mask. masks[i] is the device output of row i. The error

@@ -108,13 +108,24 @@ def test_reference_mask_cases_on_device(byte_tok):
     assert np.all(row == -np.inf)
 
 
-@pytest.mark.parametrize("lane_cap", [8, 1, 0])
-@pytest.mark.parametrize("name", sorted(grammars()))
-def test_device_mask_matches_oracle(byte_tok, bpe, name, lane_cap, monkeypatch):
-    """lane_cap 0 sends every token through the block walk, 1 every token
-    whose frontier ever holds two positions."""
+# (lane capacity, wave capacity, string-class table): defaults; string
+# states walked; every live token walked by its wave; by the block kernel;
+# and small capacities that mix all three.
+WALKS = [(8, 64, 1), (8, 64, 0), (0, 64, 0), (0, 0, 0), (1, 2, 1)]
+
+
+def _walk_env(monkeypatch, lane_cap, wave_cap, strclass):
     monkeypatch.setenv("ESP_CMASK_LANE_CAP", str(lane_cap))
-    print(f"grammar {name} lane_cap {lane_cap}", flush=True)
+    monkeypatch.setenv("ESP_CMASK_WAVE_CAP", str(wave_cap))
+    monkeypatch.setenv("ESP_CMASK_STRCLASS", str(strclass))
+
+
+@pytest.mark.parametrize("lane_cap,wave_cap,strclass", WALKS)
+@pytest.mark.parametrize("name", sorted(grammars()))
+def test_device_mask_matches_oracle(byte_tok, bpe, name, lane_cap, wave_cap, strclass,
+                                    monkeypatch):
+    _walk_env(monkeypatch, lane_cap, wave_cap, strclass)
+    print(f"grammar {name} walks {lane_cap} {wave_cap} {strclass}", flush=True)
     g = grammars()[name]
     for tok, seed in ((byte_tok, 3), (bpe, 4)):
         n = tok.get_vocab_size()
@@ -122,18 +133,19 @@ def test_device_mask_matches_oracle(byte_tok, bpe, name, lane_cap, monkeypatch):
         _compare_walk(g, table, Vocabulary(table), seed, 24)
 
 
-@pytest.mark.parametrize("lane_cap", [8, 0])
+@pytest.mark.parametrize("lane_cap,wave_cap,strclass", WALKS)
 @pytest.mark.parametrize("name", ["object", "enum64", "optional", "unicode"])
-def test_device_mask_llama_sized_vocab(name, lane_cap, monkeypatch):
-    monkeypatch.setenv("ESP_CMASK_LANE_CAP", str(lane_cap))
-    print(f"grammar {name} V=128256 lane_cap {lane_cap}", flush=True)
+def test_device_mask_llama_sized_vocab(name, lane_cap, wave_cap, strclass, monkeypatch):
+    _walk_env(monkeypatch, lane_cap, wave_cap, strclass)
+    print(f"grammar {name} V=128256 walks {lane_cap} {wave_cap} {strclass}", flush=True)
     table = llama_sized_table()
     _compare_walk(grammars()[name], table, Vocabulary(table), 9, 4)
 
 
 def test_wide_frontier_tokens_take_the_block_walk(bpe):
-    """64 alternatives alive after a shared prefix: frontiers above the lane
-    capacity go through the block kernel; bits still match the oracle."""
+    """64 alternatives alive after a shared prefix (plus the continuation):
+    frontiers above the wave capacity go through the block kernel; bits
+    still match the oracle."""
     alts = [L(f"pre_fix_{i:02d}_" + "x" * (i % 5)) for i in range(64)]
     g = Q(L("<"), C(*alts), L(">"))
     table = [bytes([b]) for b in range(256)] + [b"pre_fix_", b"_fix_", b"fix_0", b"pre_fix_1",
