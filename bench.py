@@ -359,6 +359,118 @@ def c5_bench(steps: int, warmup: int = 2) -> dict:
     return res
 
 
+class _ByteIds:
+    """Tokenises text as one id per byte: ids 0..255 of the synthetic
+    128256-entry table are the single bytes, so forced spans round-trip."""
+
+    class _Enc:
+        def __init__(self, ids):
+            self.ids = ids
+
+    def encode(self, text, add_special_tokens=False):
+        return self._Enc(list(text.encode("utf-8")))
+
+
+def record_grammar():
+    """A JSON record: five fields with bounded strings, a 16-way enum and a
+    boolean (OutputGrammar serde form, provider.rs:55-75)."""
+    def lit(v):
+        return {"kind": "literal", "value": v}
+
+    def string(n):
+        return {"kind": "json_string", "max_bytes": n}
+    kinds = {"kind": "choice", "alternatives": [lit(f"\"type_{i:02d}\"") for i in range(16)]}
+    ok = {"kind": "choice", "alternatives": [lit("true"), lit("false")]}
+    return {"kind": "sequence", "items": [
+        lit("{\"id\":"), string(16), lit(",\"name\":"), string(48), lit(",\"kind\":"), kinds,
+        lit(",\"ok\":"), ok, lit(",\"note\":"), string(96), lit("}")]}
+
+
+def c5_grammar_bench(steps: int, warmup: int = 2) -> dict:
+    """C5's batch with its allowed-token masks produced by real output
+    grammars (provider.rs:735-883 run for 64 sequences at once): 1B shape
+    bf16, 64 sequences prefilled with 1024 uniform-random ids, seeded
+    temperature 0.8 / top-p 0.9. Each step, every sequence either takes its
+    grammar's forced span (constraint.rs:296-344; the sampler skips one draw
+    per forced token) or picks one token from its logits row masked on the
+    device by its constraint (esp_pick_constrained); tokens are accepted into
+    the constraints and all 64 blocks are evaluated by one forward. A
+    sequence whose record completes starts the next record. The token table
+    is a seeded synthetic 128256-entry byte-level vocabulary."""
+    import numpy as np
+    from esp_amd import DecoderModel, Sampler
+    from esp_amd.constraint import Constraint, Vocabulary
+    from esp_amd.model import profile_enable, profile_read
+    from tests.grammar_cases import llama_sized_table
+    from tests.synth import uniform_ids
+    cfg = c2_config(max_pos=4096)
+    B, ctx0, V = 64, 1024, cfg.vocab_size
+    total = warmup + steps
+    vocab = Vocabulary(llama_sized_table(n=V))
+    tok = _ByteIds()
+    grammar = json.dumps(record_grammar())
+    model = DecoderModel.synthetic(cfg, seed=1234, std=0.02, fmt="bf16")
+    kv = model.new_cache(B, ctx0 + 64 * total + 64)
+    model.forward_batch(kv, list(range(B)), [uniform_ids(5000 + i, ctx0, V) for i in range(B)],
+                        want_logits=False)
+    cons = [Constraint(grammar, vocab=vocab) for _ in range(B)]
+    samplers = [Sampler(0.8, 0.9, 0xC5C5 + i) for i in range(B)]
+    seqs = list(range(B))
+    stats = {"tokens": 0, "forced": 0, "picked": 0, "records": 0}
+    t_mask = [0.0]
+
+    def step():
+        blocks, rows_c, rows_s = [], [], []
+        for i in range(B):
+            f = cons[i].forced(tok)
+            blocks.append(f)
+            rows_c.append(None if f else cons[i])
+            rows_s.append(None if f else samplers[i])
+            if f:
+                samplers[i].skip_draws(len(f))
+        ids, _ = model.pick_constrained(kv, rows_c, rows_s)
+        for i in range(B):
+            if blocks[i]:
+                stats["forced"] += len(blocks[i])
+            else:
+                blocks[i] = [int(ids[i])]
+                stats["picked"] += 1
+            for t in blocks[i]:
+                cons[i].accept(t)
+            stats["tokens"] += len(blocks[i])
+            if cons[i].complete():
+                stats["records"] += 1
+                cons[i] = Constraint(grammar, vocab=vocab)
+        model.forward_batch(kv, seqs, blocks, want_logits=False)
+
+    # a first forward so every row holds logits before the first pick
+    model.forward_batch(kv, seqs, [[1]] * B, want_logits=False)
+    for _ in range(warmup):
+        step()
+    for k in stats:
+        stats[k] = 0
+    profile_enable("cmask", True)
+    m0 = profile_read("cmask")
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    el = time.perf_counter() - t0
+    m1 = profile_read("cmask")
+    profile_enable("cmask", False)
+    res = {"workload": "C5 with grammar masks: 1B shape bf16, 64 sequences from 1024 context, "
+                       "JSON-record output grammar per sequence, device masks + forced spans, "
+                       "seeded temperature 0.8 / top-p 0.9; synthetic 128256-entry byte-level "
+                       "token table",
+           "sequence_tokens_per_s": round(stats["tokens"] / el, 1),
+           "steps_per_s": round(steps / el, 2),
+           "ms_per_step": round(el / steps * 1e3, 3),
+           "mask_ms_per_step": round((m1[1] - m0[1]) / max(1, m1[0] - m0[0]), 4),
+           "forced_tokens": stats["forced"], "picked_tokens": stats["picked"],
+           "records_completed": stats["records"], "steps": steps}
+    model.close()
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -373,6 +485,8 @@ def main():
     ap.add_argument("--only-c4", action="store_true")
     ap.add_argument("--no-c5", action="store_true")
     ap.add_argument("--only-c5", action="store_true")
+    ap.add_argument("--no-c5g", action="store_true")
+    ap.add_argument("--only-c5g", action="store_true")
     ap.add_argument("--traffic", action="store_true",
                     help="run only the workload of the HBM-traffic counter passes")
     args = ap.parse_args()
@@ -395,6 +509,9 @@ def main():
         return
     if args.only_c5:
         print(json.dumps({"c5": c5_bench(16)}), flush=True)
+        return
+    if args.only_c5g:
+        print(json.dumps({"c5_grammar": c5_grammar_bench(32)}), flush=True)
         return
     cfg = c2_config()
     model = DecoderModel.synthetic(cfg, seed=1234, std=0.02, fmt="bf16")
@@ -497,6 +614,9 @@ def main():
     if not args.no_c5:
         result["c5"] = c5_bench(16)
         print(f"c5: {result['c5']}", file=sys.stderr, flush=True)
+    if not args.no_c5g:
+        result["c5_grammar"] = c5_grammar_bench(32)
+        print(f"c5_grammar: {result['c5_grammar']}", file=sys.stderr, flush=True)
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(cfg, int(avg_ctx))
     print(json.dumps(result), flush=True)

@@ -445,19 +445,27 @@ std::vector<uint8_t> Constraint::forced_bytes() const {
         bool end = false;
         for (const Pos &p : state) end |= nodes[p.node].kind == G_END;
         if (end) break;
+        // The live bytes are those some position steps on (a closed set's
+        // successors always close to a non-empty set); stop at the second.
         int found = -1;
-        std::vector<Pos> next;
         bool many = false;
-        for (int b = 0; b < 256 && !many; ++b) {
-            std::vector<Pos> s = step(state, (uint8_t)b);
-            if (s.empty()) continue;
-            if (found >= 0) many = true;
-            found = b;
-            next = std::move(s);
+        Pos q;
+        for (size_t i = 0; i < state.size() && !many; ++i) {
+            const Pos &p = state[i];
+            const GNode &n = nodes[p.node];
+            auto live = [&](int b) {
+                if (found >= 0 && found != b) many = true;
+                found = b;
+            };
+            if (n.kind == G_BYTE) live(n.byte);
+            else if (n.kind == G_STRING && p.phase == 0) live('"');
+            else if (n.kind == G_STRING)
+                for (int b = 0; b < 256 && !many; ++b)
+                    if (step1(p, (uint8_t)b, q)) live(b);
         }
         if (found < 0 || many) break;
         bytes.push_back((uint8_t)found);
-        state = std::move(next);
+        state = step(state, (uint8_t)found);
     }
     while (!valid_utf8(bytes.data(), bytes.size())) bytes.pop_back();
     return bytes;

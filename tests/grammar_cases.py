@@ -4,13 +4,16 @@ byte_tokenizer() is the reference's own test tokenizer (constraint.rs:
 352-371): one BPE token per byte, pieces in the GPT-2 byte alphabet, no
 merges, ByteLevel decoder. trained_bpe() trains a small ByteLevel BPE on a
 synthetic JSON-ish corpus, so tokens span several bytes, split UTF-8
-sequences and mix quotes, escapes and literal syntax.
+sequences and mix quotes, escapes and literal syntax. llama_sized_table()
+is a seeded 128256-entry token byte table of the same kinds of pieces.
 """
 from __future__ import annotations
 
 import json
 import random
 from typing import List
+
+import numpy as np
 
 _TOKENIZERS = None
 
@@ -100,3 +103,31 @@ def grammars():
         "ambiguous": Q(C(L("ab"), L("a"), L("")), C(L("b\""), S(2)), L("!")),
         "strings": Q(S(1), L(":"), S(4096)),
     }
+
+
+def llama_sized_table(seed: int = 11, n: int = 128256):
+    """Every single byte, then random multi-byte tokens: ASCII words and
+    punctuation, quotes and backslashes, whole and split UTF-8 sequences,
+    control bytes; empty entries stand for added tokens."""
+    rng = np.random.default_rng(seed)
+    pieces = [bytes([b]) for b in range(256)]
+    ascii_ = np.frombuffer(b"abcdefghijklmnopqrstuvwxyz _-:,{}[]\"\\0123456789./", np.uint8)
+    utf = ["é", "→", "日", "\U0001F600", "ü", "ß"]
+    while len(pieces) < n - 256:
+        k = int(min(1 + rng.geometric(0.22), 24))
+        out = bytearray()
+        while len(out) < k:
+            r = rng.random()
+            if r < 0.8:
+                out.append(int(rng.choice(ascii_)))
+            elif r < 0.92:
+                out += utf[int(rng.integers(len(utf)))].encode()
+            elif r < 0.97:
+                s = utf[int(rng.integers(len(utf)))].encode()
+                cut = int(rng.integers(1, len(s))) if len(s) > 1 else 1
+                out += s[:cut] if rng.random() < 0.5 else s[cut:]
+            else:
+                out.append(int(rng.integers(0, 256)))
+        pieces.append(bytes(out))
+    pieces += [b""] * (n - len(pieces))
+    return pieces

@@ -18,7 +18,8 @@ from esp_amd.constraint import Constraint, Vocabulary, token_bytes
 from oracle import constraint as ref
 from oracle import oracle, st
 from tests import synth
-from tests.grammar_cases import C, L, Q, S, byte_tokenizer, grammars, trained_bpe
+from tests.grammar_cases import (C, L, Q, S, byte_tokenizer, grammars, llama_sized_table,
+                                 trained_bpe)
 
 pytestmark = pytest.mark.gpu
 
@@ -31,34 +32,6 @@ def byte_tok():
 @pytest.fixture(scope="module")
 def bpe():
     return trained_bpe(3000)
-
-
-def llama_sized_table(seed: int = 11, n: int = 128256):
-    """Every single byte, then random multi-byte tokens: ASCII words and
-    punctuation, quotes and backslashes, whole and split UTF-8 sequences,
-    control bytes; empty entries stand for added tokens."""
-    rng = np.random.default_rng(seed)
-    pieces = [bytes([b]) for b in range(256)]
-    ascii_ = np.frombuffer(b"abcdefghijklmnopqrstuvwxyz _-:,{}[]\"\\0123456789./", np.uint8)
-    utf = ["é", "→", "日", "\U0001F600", "ü", "ß"]
-    while len(pieces) < n - 256:
-        k = int(min(1 + rng.geometric(0.22), 24))
-        out = bytearray()
-        while len(out) < k:
-            r = rng.random()
-            if r < 0.8:
-                out.append(int(rng.choice(ascii_)))
-            elif r < 0.92:
-                out += utf[int(rng.integers(len(utf)))].encode()
-            elif r < 0.97:
-                s = utf[int(rng.integers(len(utf)))].encode()
-                cut = int(rng.integers(1, len(s))) if len(s) > 1 else 1
-                out += s[:cut] if rng.random() < 0.5 else s[cut:]
-            else:
-                out.append(int(rng.integers(0, 256)))
-        pieces.append(bytes(out))
-    pieces += [b""] * (n - len(pieces))
-    return pieces
 
 
 def bits_of(words) -> np.ndarray:
