@@ -229,7 +229,9 @@ static void pick_rows(Kv &k, uint32_t n_rows, const uint32_t *allowed_bits,
     a.n = (int)n_rows;
     a.V = V;
     a.allowed = mask_b ? (const uint32_t *)(io + off_mask) : nullptr;
-    a.samplers = smp_b ? (const esp_sampler *)(io + off_smp) : nullptr;
+    // rows with temperature 0 are greedy: without a sampled row the
+    // sampler path (and its scratch) is not used at all
+    a.samplers = smp_b && any_sampled ? (const esp_sampler *)(io + off_smp) : nullptr;
     uint32_t *d_ids = (uint32_t *)(io + off_out);
     uint64_t *d_state = (uint64_t *)(io + off_out + (size_t)n_rows * 4 + 8 - ((size_t)n_rows * 4) % 8);
     uint8_t *d_flags = (uint8_t *)(d_state + n_rows);

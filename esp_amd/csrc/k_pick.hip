@@ -24,6 +24,102 @@ __device__ __forceinline__ bool before(Cand a, Cand b) {
     return a.id < b.id;
 }
 
+// Sampled rows with more candidates than the LDS sort holds are finished
+// by three more kernels. pick_k buckets the candidates by the top bits of
+// their f32 weight (bits 30..17: exponent and six mantissa bits; larger
+// bucket = larger weight) and writes them bucket by bucket in descending
+// bucket order; pick_bsort_k sorts each bucket in LDS, one wave per bucket
+// up to PB_WAVE_CAP candidates and one block per larger bucket
+// (pick_bsort_big_k sorts, one at a time, the rare buckets larger than
+// LDS); pick_chain_k then runs the sequential f32 sums and the draw over
+// the sorted list.
+constexpr int PB_BITS = 14;
+constexpr int PB_BINS = 1 << PB_BITS;
+constexpr int PB_WAVE_CAP = 1024;  // buckets up to this size are sorted by one wave
+__device__ __forceinline__ int wbucket(float w) {
+    return (int)((__float_as_uint(w) >> (31 - PB_BITS)) & (PB_BINS - 1));
+}
+
+struct PickRow {
+    int C;         // candidates (positive weights)
+    int zmax;      // largest zero-weight id, -1 if none
+    int deferred;  // 1: finished by pick_chain_k
+    int flags;
+};
+
+// Per-call scratch: [n][cap] sorted candidates | [n][cap] weights |
+// big-bucket temp [cap] | [n][PB_BINS] bucket start | [n][PB_BINS] bucket
+// count | [n] PickRow | small, medium and big bucket lists [n * PB_BINS]
+// each | counters [4] (small, big, medium).
+struct PickScratch {
+    Cand *cand, *temp;
+    float *wts;
+    int *bstart, *bcount;
+    PickRow *info;
+    uint32_t *work, *med, *big, *counts;
+    int cap;
+};
+
+__host__ __device__ inline int pick_cap(int V) {
+    int c = 1;
+    while (c < V + 1) c <<= 1;
+    return c;
+}
+
+__host__ __device__ inline PickScratch pick_layout(void *base, int n, int V) {
+    PickScratch p;
+    p.cap = pick_cap(V);
+    char *b = (char *)base;
+    p.cand = (Cand *)b;
+    b += (size_t)n * p.cap * sizeof(Cand);
+    p.wts = (float *)b;
+    b += (size_t)n * p.cap * sizeof(float);
+    p.temp = (Cand *)b;
+    b += (size_t)p.cap * sizeof(Cand);
+    p.bstart = (int *)b;
+    b += (size_t)n * PB_BINS * 4;
+    p.bcount = (int *)b;
+    b += (size_t)n * PB_BINS * 4;
+    p.info = (PickRow *)b;
+    b += (size_t)n * sizeof(PickRow);
+    p.work = (uint32_t *)b;
+    b += (size_t)n * PB_BINS * 4;
+    p.med = (uint32_t *)b;
+    b += (size_t)n * PB_BINS * 4;
+    p.big = (uint32_t *)b;
+    b += (size_t)n * PB_BINS * 4;
+    p.counts = (uint32_t *)b;
+    return p;
+}
+
+// Exclusive prefix sum over the block (blockDim.x a multiple of 64, at
+// most 32 waves); *total receives the block sum. tmp: LDS, >= 33 ints.
+__device__ int block_excl_scan(int v, int *tmp, int *total) {
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    int x = v;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const int y = __shfl_up(x, d);
+        if (lane >= d) x += y;
+    }
+    if (lane == 63) tmp[wv] = x;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        int run = 0;
+        for (int w = 0; w < nw; ++w) {
+            const int t = tmp[w];
+            tmp[w] = run;
+            run += t;
+        }
+        tmp[32] = run;
+    }
+    __syncthreads();
+    const int r = tmp[wv] + x - v;
+    *total = tmp[32];
+    __syncthreads();
+    return r;
+}
+
 __device__ __forceinline__ uint64_t splitmix_next(uint64_t &s) {
     s += 0x9E3779B97F4A7C15ull;
     uint64_t z = s;
@@ -53,11 +149,44 @@ __device__ void bitonic(Cand *buf, int n) {
     }
 }
 
+// row[i4 + q] = v[q] for ids below V (rows of ps.wts are cap-aligned).
+__device__ __forceinline__ void store4(float *row, int V, int i4, const float (&v)[4]) {
+    typedef float f4_t __attribute__((ext_vector_type(4)));
+    if (i4 + 3 < V) {
+        f4_t x;
+        x.x = v[0];
+        x.y = v[1];
+        x.z = v[2];
+        x.w = v[3];
+        *(f4_t *)(row + i4) = x;
+    } else {
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            if (i4 + q < V) row[i4 + q] = v[q];
+    }
+}
+
+// v[q] = row[i4 + q] for ids below V (row 16-byte aligned when V % 4 == 0).
+__device__ __forceinline__ void load4(const float *row, int V, int i4, float (&v)[4]) {
+    typedef float f4_t __attribute__((ext_vector_type(4)));
+    if ((V & 3) == 0 && i4 + 3 < V) {
+        const f4_t x = *(const f4_t *)(row + i4);
+        v[0] = x.x;
+        v[1] = x.y;
+        v[2] = x.z;
+        v[3] = x.w;
+    } else {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) v[q] = i4 + q < V ? row[i4 + q] : 0.f;
+    }
+}
+
 __global__ void __launch_bounds__(PICK_THREADS) pick_k(PickArgs a) {
     extern __shared__ Cand lds[];
     __shared__ float red_f[32];
     __shared__ int red_i[32];
-    __shared__ int s_count, s_zmax, s_bad, s_elig;
+    __shared__ int s_count, s_zmax, s_bad, s_elig, s_wbase, s_mbase;
+    __shared__ int s_scan[33];
     const int row = blockIdx.x;
     const int V = a.V;
     const float *L = a.logits + (size_t)row * V;
@@ -70,21 +199,36 @@ __global__ void __launch_bounds__(PICK_THREADS) pick_k(PickArgs a) {
         s_elig = 0;
     }
     __syncthreads();
-    // pass 1: mask, finiteness, greedy best and max
+    // pass 1: mask, finiteness, greedy best and max. Each thread takes four
+    // consecutive ids at a time (one 16-byte load when the row is aligned),
+    // two groups in flight.
     float best = -INFINITY;
     int best_id = 0x7fffffff;
     int bad = 0, elig = 0;
-    for (int i = tid; i < V; i += blockDim.x) {
-        float v = L[i];
-        bool fin = isfinite(v);
-        bad |= !fin;
-        bool allowed = bits ? ((bits[i >> 5] >> (i & 31)) & 1u) : true;
-        if (bits ? (!allowed || !fin) : isnan(v)) v = -INFINITY;
-        elig += (allowed && fin);
-        if (v > best || (v == best && i < best_id)) {
-            best = v;
-            best_id = i;
+    auto scan4 = [&](int i4, const float (&v4)[4]) {
+        const uint32_t bw = bits && i4 < V ? bits[i4 >> 5] : 0u;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int i = i4 + q;
+            if (i >= V) break;
+            float v = v4[q];
+            bool fin = isfinite(v);
+            bad |= !fin;
+            bool allowed = bits ? ((bw >> (i & 31)) & 1u) : true;
+            if (bits ? (!allowed || !fin) : isnan(v)) v = -INFINITY;
+            elig += (allowed && fin);
+            if (v > best || (v == best && i < best_id)) {
+                best = v;
+                best_id = i;
+            }
         }
+    };
+    for (int i4 = tid * 4; i4 < V; i4 += 8 * (int)blockDim.x) {
+        float a4[4], b4[4];
+        load4(L, V, i4, a4);
+        load4(L, V, i4 + 4 * (int)blockDim.x, b4);
+        scan4(i4, a4);
+        scan4(i4 + 4 * (int)blockDim.x, b4);
     }
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) {
@@ -123,19 +267,45 @@ __global__ void __launch_bounds__(PICK_THREADS) pick_k(PickArgs a) {
         }
         return;
     }
-    // pass 2: weights and candidate compaction
+    // pass 2: every weight once (stored per row), the candidate count, the
+    // largest zero-weight id (the fall-through of an uncut list) and the
+    // weight-bucket histogram of the candidates
     const float inv_t = 1.0f / smp->temperature;
-    Cand *gbuf = (Cand *)((char *)a.scratch + (size_t)row * (size_t)((V + 1) * sizeof(Cand)) * 2);
-    // count candidates first to choose LDS or global storage; the largest
-    // zero-weight id (the fall-through of an uncut list) is a block max
+    const PickScratch ps = pick_layout(a.scratch, a.n, V);
+    float *wrow = ps.wts + (size_t)row * ps.cap;
+    int *hist = (int *)lds, *cur = hist + PB_BINS;
+    for (int d = tid; d < PB_BINS; d += blockDim.x) hist[d] = 0;
+    __syncthreads();
     int cnt = 0, zmax = -1;
-    for (int i = tid; i < V; i += blockDim.x) {
-        float v = L[i];
-        bool allowed = bits ? ((bits[i >> 5] >> (i & 31)) & 1u) : true;
-        if (bits && (!allowed || !isfinite(v))) v = -INFINITY;
-        float w = v == -INFINITY ? 0.f : (float)exp((double)((v - mx) * inv_t));
-        if (w > 0.f) ++cnt;
-        else if (w == 0.f) zmax = i;  // ids rise along this thread's stride
+    auto weigh4 = [&](int i4, const float (&v4)[4]) {
+        if (i4 >= V) return;
+        const uint32_t bw = bits ? bits[i4 >> 5] : 0u;
+        float w4[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int i = i4 + q;
+            float v = v4[q];
+            bool allowed = bits ? ((bw >> (i & 31)) & 1u) : true;
+            if (bits && (!allowed || !isfinite(v))) v = -INFINITY;
+            const float w = v == -INFINITY ? 0.f : (float)exp((double)((v - mx) * inv_t));
+            w4[q] = w;
+            if (i < V) {
+                if (w > 0.f) {
+                    ++cnt;
+                    atomicAdd(&hist[wbucket(w)], 1);
+                } else if (w == 0.f) {
+                    zmax = i;  // ids rise along this thread's walk
+                }
+            }
+        }
+        store4(wrow, V, i4, w4);
+    };
+    for (int i4 = tid * 4; i4 < V; i4 += 8 * (int)blockDim.x) {
+        float a4[4], b4[4];
+        load4(L, V, i4, a4);
+        load4(L, V, i4 + 4 * (int)blockDim.x, b4);
+        weigh4(i4, a4);
+        weigh4(i4 + 4 * (int)blockDim.x, b4);
     }
     cnt = (int)wave_sum((float)cnt);
 #pragma unroll
@@ -154,21 +324,69 @@ __global__ void __launch_bounds__(PICK_THREADS) pick_k(PickArgs a) {
         }
         return;
     }
+    if (C > PICK_LDS_CAP) {
+        // bucketed path: descending-bucket offsets, work lists, scatter.
+        // Thread t owns the buckets at descending positions 16t .. 16t + 15.
+        constexpr int PER = PB_BINS / PICK_THREADS;
+        static_assert(PER * PICK_THREADS == PB_BINS, "buckets per thread");
+        const int dtop = PB_BINS - 1 - PER * tid;
+        int hs = 0, fs = 0, ms = 0;
+        for (int q = 0; q < PER; ++q) {
+            const int h = hist[dtop - q];
+            hs += h;
+            fs += h > 0 && h <= PB_WAVE_CAP;
+            ms += h > PB_WAVE_CAP && h <= PICK_LDS_CAP;
+        }
+        int sum, nsmall, nmed;
+        const int off = block_excl_scan(hs, s_scan, &sum);
+        const int sslot = block_excl_scan(fs, s_scan, &nsmall);
+        const int mslot = block_excl_scan(ms, s_scan, &nmed);
+        if (tid == 0) {
+            s_wbase = nsmall ? (int)atomicAdd(&ps.counts[0], (uint32_t)nsmall) : 0;
+            s_mbase = nmed ? (int)atomicAdd(&ps.counts[2], (uint32_t)nmed) : 0;
+        }
+        int *gst = ps.bstart + (size_t)row * PB_BINS, *gct = ps.bcount + (size_t)row * PB_BINS;
+        __syncthreads();
+        const uint32_t rb = (uint32_t)row << PB_BITS;
+        int o = off, si = s_wbase + sslot, mi = s_mbase + mslot;
+        for (int q = 0; q < PER; ++q) {
+            const int d = dtop - q, h = hist[d];
+            gst[d] = o;
+            gct[d] = h;
+            if (h > 0 && h <= PB_WAVE_CAP) ps.work[si++] = rb | (uint32_t)d;
+            else if (h > PB_WAVE_CAP && h <= PICK_LDS_CAP) ps.med[mi++] = rb | (uint32_t)d;
+            else if (h > PICK_LDS_CAP) ps.big[atomicAdd(&ps.counts[1], 1u)] = rb | (uint32_t)d;
+            cur[d] = o;  // each thread rewrites only its own buckets
+            o += h;
+        }
+        __syncthreads();
+        Cand *dst = ps.cand + (size_t)row * ps.cap;
+        for (int i4 = tid * 4; i4 < V; i4 += 8 * (int)blockDim.x) {
+            float a4[4], b4[4];
+            load4(wrow, V, i4, a4);
+            load4(wrow, V, i4 + 4 * (int)blockDim.x, b4);
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+                const int i = (q < 4 ? i4 : i4 + 4 * (int)blockDim.x) + (q & 3);
+                const float w = q < 4 ? a4[q & 3] : b4[q & 3];
+                if (i < V && w > 0.f) dst[atomicAdd(&cur[wbucket(w)], 1)] = Cand{w, i};
+            }
+        }
+        if (tid == 0) ps.info[row] = PickRow{C, s_zmax, 1, flags};
+        return;
+    }
+    Cand *buf = lds;
     int n2 = 1;
     while (n2 < C) n2 <<= 1;
-    Cand *buf = n2 <= PICK_LDS_CAP ? lds : gbuf;
     __syncthreads();
     if (tid == 0) s_count = 0;
     __syncthreads();
-    for (int i = tid; i < V; i += blockDim.x) {
-        float v = L[i];
-        bool allowed = bits ? ((bits[i >> 5] >> (i & 31)) & 1u) : true;
-        if (bits && (!allowed || !isfinite(v))) v = -INFINITY;
-        float w = v == -INFINITY ? 0.f : (float)exp((double)((v - mx) * inv_t));
-        if (w > 0.f) {
-            int slot = atomicAdd(&s_count, 1);
-            buf[slot] = Cand{w, i};
-        }
+    for (int i4 = tid * 4; i4 < V; i4 += 4 * (int)blockDim.x) {
+        float w4[4];
+        load4(wrow, V, i4, w4);
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            if (i4 + q < V && w4[q] > 0.f) buf[atomicAdd(&s_count, 1)] = Cand{w4[q], i4 + q};
     }
     __syncthreads();
     for (int i = C + tid; i < n2; i += blockDim.x) buf[i] = Cand{-1.f, 0x7fffffff};
@@ -177,7 +395,7 @@ __global__ void __launch_bounds__(PICK_THREADS) pick_k(PickArgs a) {
     // LDS-resident lists go to struct-of-arrays in place (weights, then ids)
     // so the serial pass below reads four weights per load; every element is
     // read into registers before any is written back
-    const bool soa = n2 <= PICK_LDS_CAP;
+    const bool soa = true;  // n2 <= PICK_LDS_CAP here
     float *sw = (float *)buf;
     int32_t *sid = (int32_t *)buf + n2;
     if (soa) {
@@ -311,8 +529,278 @@ __global__ void __launch_bounds__(PICK_THREADS) pick_k(PickArgs a) {
     if (a.state_out) a.state_out[row] = state;
 }
 
+// Clears the counters and row records of the bucketed path.
+__global__ void pick_reset_k(PickScratch ps, int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < 4) ps.counts[i] = 0;
+    if (i < n) ps.info[i] = PickRow{0, -1, 0, 0};
+}
+
+// Sorts the listed buckets in LDS by descending weight, ascending id:
+// first the small ones, one wave per bucket with wave-level barriers only,
+// then the medium ones (up to PICK_LDS_CAP), one block per bucket.
+__device__ __forceinline__ void wave_sync_lds() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+__global__ void __launch_bounds__(PICK_THREADS) pick_bsort_k(PickScratch ps) {
+    extern __shared__ Cand lds[];
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int nwaves = PICK_THREADS / 64;
+    Cand *wl = lds + wv * PB_WAVE_CAP;
+    const uint32_t nsmall = ps.counts[0];
+    for (uint32_t k = blockIdx.x * nwaves + wv; k < nsmall; k += gridDim.x * nwaves) {
+        const uint32_t item = ps.work[k];
+        const int row = (int)(item >> PB_BITS), d = (int)(item & (PB_BINS - 1));
+        const int n = ps.bcount[(size_t)row * PB_BINS + d];
+        Cand *g = ps.cand + (size_t)row * ps.cap + ps.bstart[(size_t)row * PB_BINS + d];
+        int n2 = 1;
+        while (n2 < n) n2 <<= 1;
+        for (int i = lane; i < n2; i += 64) wl[i] = i < n ? g[i] : Cand{-1.f, 0x7fffffff};
+        wave_sync_lds();
+        const int half = n2 >> 1;
+        for (int kk = 2; kk <= n2; kk <<= 1) {
+            for (int j = kk >> 1; j > 0; j >>= 1) {
+                for (int pi = lane; pi < half; pi += 64) {
+                    const int i = ((pi & ~(j - 1)) << 1) | (pi & (j - 1)), p = i + j;
+                    const Cand x = wl[i], y = wl[p];
+                    const bool up = (i & kk) == 0;
+                    const bool swap = up ? before(y, x) : before(x, y);
+                    wl[i] = swap ? y : x;
+                    wl[p] = swap ? x : y;
+                }
+                wave_sync_lds();
+            }
+        }
+        for (int i = lane; i < n; i += 64) g[i] = wl[i];
+        wave_sync_lds();
+    }
+    __syncthreads();
+    const uint32_t nmed = ps.counts[2];
+    for (uint32_t k = blockIdx.x; k < nmed; k += gridDim.x) {
+        const uint32_t item = ps.med[k];
+        const int row = (int)(item >> PB_BITS), d = (int)(item & (PB_BINS - 1));
+        const int n = ps.bcount[(size_t)row * PB_BINS + d];
+        Cand *g = ps.cand + (size_t)row * ps.cap + ps.bstart[(size_t)row * PB_BINS + d];
+        int n2 = 1;
+        while (n2 < n) n2 <<= 1;
+        for (int i = threadIdx.x; i < n2; i += blockDim.x)
+            lds[i] = i < n ? g[i] : Cand{-1.f, 0x7fffffff};
+        __syncthreads();
+        bitonic(lds, n2);
+        for (int i = threadIdx.x; i < n; i += blockDim.x) g[i] = lds[i];
+        __syncthreads();
+    }
+}
+
+// Buckets larger than LDS (many equal weights): sorted one after another
+// through the global temp area by a single block.
+__global__ void __launch_bounds__(PICK_THREADS) pick_bsort_big_k(PickScratch ps) {
+    const uint32_t total = ps.counts[1];
+    for (uint32_t k = 0; k < total; ++k) {
+        const uint32_t item = ps.big[k];
+        const int row = (int)(item >> PB_BITS), d = (int)(item & (PB_BINS - 1));
+        const int n = ps.bcount[(size_t)row * PB_BINS + d];
+        Cand *g = ps.cand + (size_t)row * ps.cap + ps.bstart[(size_t)row * PB_BINS + d];
+        int n2 = 1;
+        while (n2 < n) n2 <<= 1;
+        for (int i = threadIdx.x; i < n2; i += blockDim.x)
+            ps.temp[i] = i < n ? g[i] : Cand{-1.f, 0x7fffffff};
+        __syncthreads();
+        bitonic(ps.temp, n2);
+        for (int i = threadIdx.x; i < n; i += blockDim.x) g[i] = ps.temp[i];
+        __syncthreads();
+    }
+}
+
+// The sequential tail of sample.rs:96-120 over a sorted candidate list in
+// global memory. Lane 0 adds in the reference's order from LDS chunks that
+// the other waves stage ahead of it. The total pass records the running
+// sum at every chunk start, so the nucleus crossing is found by replaying
+// one chunk; the draw then walks the kept prefix.
+constexpr int CH_THREADS = 256;
+constexpr int CH = 4096;  // weights per LDS chunk
+
+__global__ void __launch_bounds__(CH_THREADS) pick_chain_k(PickArgs a, PickScratch ps) {
+    __shared__ float wb[2][CH];
+    __shared__ float ck[64];  // running sum at chunk starts (C <= 64 * CH)
+    __shared__ float s_val;
+    __shared__ int s_int;
+    const int row = blockIdx.x;
+    const PickRow info = ps.info[row];
+    if (!info.deferred) return;
+    const Cand *cand = ps.cand + (size_t)row * ps.cap;
+    const esp_sampler smp = a.samplers[row];
+    const int C = info.C;
+    const int tid = threadIdx.x;
+    const int nch = (C + CH - 1) / CH;
+    auto stage = [&](int c, int buf, int t0, int nt) {  // threads t0.. stage chunk c
+        const int base = c * CH, lim = min(CH, C - base);
+        for (int i = tid - t0; i < lim; i += nt) wb[buf][i] = cand[base + i].w;
+    };
+    typedef float f4_t __attribute__((ext_vector_type(4)));
+    // lane 0: x += w[0..lim) in order, 32 at a time with the next 32 loaded
+    // ahead (LDS latency hides behind the dependent adds)
+    auto add_run = [&](const float *w, int lim, float x) {
+        int j = 0;
+        if (lim >= 32) {
+            f4_t r[8];
+#pragma unroll
+            for (int q = 0; q < 8; ++q) r[q] = *(const f4_t *)(w + 4 * q);
+            for (; j + 64 <= lim; j += 32) {
+                f4_t nx[8];
+#pragma unroll
+                for (int q = 0; q < 8; ++q) nx[q] = *(const f4_t *)(w + j + 32 + 4 * q);
+#pragma unroll
+                for (int q = 0; q < 8; ++q) {
+                    x += r[q].x;
+                    x += r[q].y;
+                    x += r[q].z;
+                    x += r[q].w;
+                }
+#pragma unroll
+                for (int q = 0; q < 8; ++q) r[q] = nx[q];
+            }
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+                x += r[q].x;
+                x += r[q].y;
+                x += r[q].z;
+                x += r[q].w;
+            }
+            j += 32;
+        }
+        for (; j < lim; ++j) x += w[j];
+        return x;
+    };
+    // pass 1: the total over every candidate (Rust's f32 sum starts at -0.0)
+    float total = -0.0f;
+    stage(0, 0, 0, CH_THREADS);
+    __syncthreads();
+    for (int c = 0; c < nch; ++c) {
+        if (c + 1 < nch && tid >= 64) stage(c + 1, (c + 1) & 1, 64, CH_THREADS - 64);
+        if (tid == 0) {
+            ck[c] = total;
+            total = add_run(wb[c & 1], min(CH, C - c * CH), total);
+        }
+        __syncthreads();
+    }
+    int keep = C;
+    float kept = 0.f;
+    const float top_p = smp.top_p;
+    if (tid == 0) {
+        if (top_p >= 0.f) {
+            const float p = top_p > 1.f ? 1.f : top_p;
+            const float target = total * p;
+            // the first chunk whose end sum reaches the target
+            int c = 0;
+            while (c + 1 < nch && ck[c + 1] < target) ++c;
+            s_int = c;
+            s_val = target;
+        } else {
+            s_int = -1;
+        }
+    }
+    __syncthreads();
+    if (s_int >= 0) {
+        const int c = s_int;
+        const float target = s_val;
+        stage(c, 0, 0, CH_THREADS);
+        __syncthreads();
+        if (tid == 0) {
+            float mass = ck[c];
+            const int lim = min(CH, C - c * CH);
+            keep = c * CH + lim;
+            for (int j = 0; j < lim; ++j) {
+                mass += wb[0][j];
+                if (mass >= target) {
+                    keep = c * CH + j + 1;
+                    break;
+                }
+            }
+            if (keep < 1) keep = 1;
+            kept = -0.0f + mass;
+            s_int = keep;
+            s_val = kept;
+        }
+        __syncthreads();
+        keep = s_int;
+        kept = s_val;
+        __syncthreads();
+    } else {
+        if (tid == 0) s_val = total;
+        __syncthreads();
+        kept = s_val;
+        __syncthreads();
+    }
+    // pass 2: the draw walks the kept prefix
+    uint64_t state = smp.state;
+    const uint64_t x = splitmix_next(state);
+    float u = (float)((double)(x >> 11) / 9007199254740992.0) * kept;
+    const int kch = (keep + CH - 1) / CH;
+    int hit = -1;
+    if (tid == 0) s_int = -1;
+    stage(0, 0, 0, CH_THREADS);
+    __syncthreads();
+    for (int c = 0; c < kch; ++c) {
+        if (c + 1 < kch && tid >= 64) stage(c + 1, (c + 1) & 1, 64, CH_THREADS - 64);
+        if (tid == 0 && s_int < 0) {
+            const float *w = wb[c & 1];
+            const int lim = min(CH, keep - c * CH);
+            int j = 0;
+            // batches of 32 that keep the draw positive are taken whole (the
+            // draw only falls, so no term inside such a batch crossed zero)
+            if (lim >= 32) {
+                f4_t r[8];
+#pragma unroll
+                for (int q = 0; q < 8; ++q) r[q] = *(const f4_t *)(w + 4 * q);
+                for (; j + 32 <= lim; j += 32) {
+                    f4_t nx[8];
+                    const int jn = j + 32 + 32 <= lim ? j + 32 : j;
+#pragma unroll
+                    for (int q = 0; q < 8; ++q) nx[q] = *(const f4_t *)(w + jn + 4 * q);
+                    float u2 = u;
+#pragma unroll
+                    for (int q = 0; q < 8; ++q) {
+                        u2 -= r[q].x;
+                        u2 -= r[q].y;
+                        u2 -= r[q].z;
+                        u2 -= r[q].w;
+                    }
+                    if (!(u2 > 0.0f)) break;
+                    u = u2;
+#pragma unroll
+                    for (int q = 0; q < 8; ++q) r[q] = nx[q];
+                }
+            }
+            for (; j < lim; ++j) {
+                u -= w[j];
+                if (u <= 0.0f) {
+                    s_int = c * CH + j;
+                    break;
+                }
+            }
+        }
+        __syncthreads();
+        if (s_int >= 0) break;
+    }
+    hit = s_int;
+    if (tid == 0) {
+        int out;
+        if (hit >= 0) out = cand[hit].id;
+        else out = (top_p < 0.f && info.zmax >= 0) ? info.zmax : cand[keep - 1].id;
+        a.ids_out[row] = (uint32_t)out;
+        a.flags_out[row] = (uint8_t)info.flags;
+        if (a.state_out) a.state_out[row] = state;
+    }
+}
+
 size_t pick_scratch_bytes(int n, int V) {
-    return (size_t)n * (size_t)((V + 1) * sizeof(Cand)) * 2;
+    const size_t cap = (size_t)pick_cap(V);
+    return (size_t)n * cap * (sizeof(Cand) + sizeof(float)) + cap * sizeof(Cand) +
+           (size_t)n * PB_BINS * 4 * 5 + (size_t)n * sizeof(PickRow) + 64;
 }
 
 void launch_pick(const PickArgs &a, hipStream_t s) {
@@ -321,9 +809,25 @@ void launch_pick(const PickArgs &a, hipStream_t s) {
     if (!attr) {
         ESP_HIP(hipFuncSetAttribute((const void *)pick_k,
                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm));
+        ESP_HIP(hipFuncSetAttribute((const void *)pick_bsort_k,
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm));
         attr = true;
     }
+    const bool sampled = a.samplers != nullptr;
+    PickScratch ps{};
+    if (sampled && a.V >= 64 * CH) fail(ESP_UNSUPPORTED, "sampling: vocabulary above 262143 ids");
+    if (sampled) {
+        if (a.scratch_bytes < pick_scratch_bytes(a.n, a.V))
+            fail(ESP_BACKEND, "pick: sampling scratch too small");
+        ps = pick_layout(a.scratch, a.n, a.V);
+        pick_reset_k<<<(a.n + 2 + 255) / 256, 256, 0, s>>>(ps, a.n);
+    }
     pick_k<<<a.n, PICK_THREADS, shm, s>>>(a);
+    if (sampled) {
+        pick_bsort_k<<<256, PICK_THREADS, shm, s>>>(ps);
+        pick_bsort_big_k<<<1, PICK_THREADS, 0, s>>>(ps);
+        pick_chain_k<<<a.n, CH_THREADS, 0, s>>>(a, ps);
+    }
 }
 
 }  // namespace esp

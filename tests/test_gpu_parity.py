@@ -183,6 +183,53 @@ def test_pick_mask_and_sampling_match_oracle():
         assert ids[i] == tok
 
 
+def test_sampling_wide_candidate_sets_match_oracle():
+    """sample.rs:83-121 when most of a 40000-token vocabulary is eligible
+    (more candidates than the LDS sort holds: bucketed sort + chain
+    kernels), unmasked and masked, with and without a nucleus; and a model
+    whose logits all tie (one bucket larger than LDS). Ids and advanced
+    states bit-exact against the oracle."""
+    V = 40000
+    cfg = synth.llama_config(1, 64, 4, 2, 96, V)
+    tensors = synth.make_tensors(cfg, 77, "f32", std=0.2)
+    model = DecoderModel.from_bytes(cfg, st.dump(tensors), "f32")
+    n = 4
+    kv = model.new_cache(n, 16)
+    logits = model.forward_batch(kv, list(range(n)), [synth.uniform_ids(60 + i, 5, V)
+                                                      for i in range(n)])
+    words = (V + 31) // 32
+    rng = np.random.default_rng(9)
+    allow = rng.random((n, words * 32)) < 0.6
+    allow[:, V:] = False
+    packed = np.zeros((n, words), np.uint32)
+    for b in range(32):
+        packed |= allow[:, b::32].astype(np.uint32) << np.uint32(b)
+    cases = [(0.8, 0.9, None), (1.3, None, None), (0.7, 0.5, packed), (1.0, None, packed)]
+    for T, p, bits in cases:
+        print(f"T {T} top_p {p} masked {bits is not None}", flush=True)
+        samplers = [Sampler(T, p, 4000 + i) for i in range(n)]
+        for trial in range(2):
+            states = [s.rng.state for s in samplers]
+            ids, flags = model.pick(kv, n, bits, samplers)
+            for i in range(n):
+                row = logits[i] if bits is None else oracle.mask(logits[i], bits[i])[0]
+                tok, st2 = oracle.sample(row, T, p, states[i])
+                assert ids[i] == tok and samplers[i].rng.state == st2, (T, p, trial, i)
+    # every logit equal: all weights 1, one bucket of 40000 candidates
+    tensors["lm_head.weight"] = (np.zeros((V, 64), np.float32), tensors["lm_head.weight"][1])
+    flat = DecoderModel.from_bytes(cfg, st.dump(tensors), "f32")
+    kv = flat.new_cache(2, 16)
+    logits = flat.forward_batch(kv, [0, 1], [[1, 2], [3]])
+    assert np.all(logits == logits[0, 0])
+    for T, p in ((0.9, 0.5), (1.1, None)):
+        samplers = [Sampler(T, p, 11 + i) for i in range(2)]
+        states = [s.rng.state for s in samplers]
+        ids, _ = flat.pick(kv, 2, None, samplers)
+        for i in range(2):
+            tok, st2 = oracle.sample(logits[i], T, p, states[i])
+            assert ids[i] == tok and samplers[i].rng.state == st2, (T, p, i)
+
+
 DECODE_VARIANTS = {
     # name: (extra config, head_dim, heads, kv_heads)
     "mistral_window": ({"model_type": "mistral", "architectures": ["MistralForCausalLM"],
