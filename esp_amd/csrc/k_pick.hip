@@ -12,6 +12,9 @@ namespace esp {
 
 constexpr int PICK_THREADS = 1024;
 constexpr int PICK_LDS_CAP = 16384;  // candidates sorted in LDS (8 B each)
+// Rows with more candidates than this take the bucketed path; its parallel
+// sums beat the single-lane tail of the in-block path beyond a few thousand.
+constexpr int PICK_DIRECT_MAX = 2048;
 
 struct Cand {
     float w;
@@ -324,40 +327,71 @@ __global__ void __launch_bounds__(PICK_THREADS) pick_k(PickArgs a) {
         }
         return;
     }
-    if (C > PICK_LDS_CAP) {
+    if (C > PICK_DIRECT_MAX) {
         // bucketed path: descending-bucket offsets, work lists, scatter.
-        // Thread t owns the buckets at descending positions 16t .. 16t + 15.
-        constexpr int PER = PB_BINS / PICK_THREADS;
-        static_assert(PER * PICK_THREADS == PB_BINS, "buckets per thread");
-        const int dtop = PB_BINS - 1 - PER * tid;
+        // Wave v owns the descending positions [1024 v, 1024 v + 1024),
+        // taken 64 at a time by its lanes (consecutive LDS words).
+        constexpr int SPAN = PB_BINS / (PICK_THREADS / 64);
+        static_assert(SPAN * (PICK_THREADS / 64) == PB_BINS, "bucket spans");
         int hs = 0, fs = 0, ms = 0;
-        for (int q = 0; q < PER; ++q) {
-            const int h = hist[dtop - q];
+        for (int r = lane; r < SPAN; r += 64) {
+            const int h = hist[PB_BINS - 1 - (wv * SPAN + r)];
             hs += h;
             fs += h > 0 && h <= PB_WAVE_CAP;
             ms += h > PB_WAVE_CAP && h <= PICK_LDS_CAP;
         }
-        int sum, nsmall, nmed;
-        const int off = block_excl_scan(hs, s_scan, &sum);
-        const int sslot = block_excl_scan(fs, s_scan, &nsmall);
-        const int mslot = block_excl_scan(ms, s_scan, &nmed);
-        if (tid == 0) {
-            s_wbase = nsmall ? (int)atomicAdd(&ps.counts[0], (uint32_t)nsmall) : 0;
-            s_mbase = nmed ? (int)atomicAdd(&ps.counts[2], (uint32_t)nmed) : 0;
+        hs = (int)wave_sum((float)hs);  // < 2^24: exact in f32
+        fs = (int)wave_sum((float)fs);
+        ms = (int)wave_sum((float)ms);
+        if (lane == 0) {
+            s_scan[wv] = hs;
+            s_scan[16 + wv] = fs;
         }
-        int *gst = ps.bstart + (size_t)row * PB_BINS, *gct = ps.bcount + (size_t)row * PB_BINS;
+        if (lane == 0) red_i[wv] = ms;
         __syncthreads();
+        if (tid == 0) {
+            int ro = 0, rs = 0, rm = 0;
+            for (int v = 0; v < PICK_THREADS / 64; ++v) {
+                const int a0 = s_scan[v], a1 = s_scan[16 + v], a2 = red_i[v];
+                s_scan[v] = ro;
+                s_scan[16 + v] = rs;
+                red_i[v] = rm;
+                ro += a0;
+                rs += a1;
+                rm += a2;
+            }
+            s_wbase = rs ? (int)atomicAdd(&ps.counts[0], (uint32_t)rs) : 0;
+            s_mbase = rm ? (int)atomicAdd(&ps.counts[2], (uint32_t)rm) : 0;
+        }
+        __syncthreads();
+        int o = s_scan[wv], si = s_wbase + s_scan[16 + wv], mi = s_mbase + red_i[wv];
+        int *gst = ps.bstart + (size_t)row * PB_BINS, *gct = ps.bcount + (size_t)row * PB_BINS;
         const uint32_t rb = (uint32_t)row << PB_BITS;
-        int o = off, si = s_wbase + sslot, mi = s_mbase + mslot;
-        for (int q = 0; q < PER; ++q) {
-            const int d = dtop - q, h = hist[d];
-            gst[d] = o;
+        for (int r0 = 0; r0 < SPAN; r0 += 64) {
+            const int d = PB_BINS - 1 - (wv * SPAN + r0 + lane);
+            const int h = hist[d];
+            const int fsm = h > 0 && h <= PB_WAVE_CAP, fmd = h > PB_WAVE_CAP && h <= PICK_LDS_CAP;
+            // wave-inclusive scans of h and the two flags
+            int ph = h, pf = fsm, pm = fmd;
+#pragma unroll
+            for (int dd = 1; dd < 64; dd <<= 1) {
+                const int y0 = __shfl_up(ph, dd), y1 = __shfl_up(pf, dd), y2 = __shfl_up(pm, dd);
+                if (lane >= dd) {
+                    ph += y0;
+                    pf += y1;
+                    pm += y2;
+                }
+            }
+            const int start_d = o + ph - h;
+            gst[d] = start_d;
             gct[d] = h;
-            if (h > 0 && h <= PB_WAVE_CAP) ps.work[si++] = rb | (uint32_t)d;
-            else if (h > PB_WAVE_CAP && h <= PICK_LDS_CAP) ps.med[mi++] = rb | (uint32_t)d;
+            cur[d] = start_d;
+            if (fsm) ps.work[si + pf - 1] = rb | (uint32_t)d;
+            else if (fmd) ps.med[mi + pm - 1] = rb | (uint32_t)d;
             else if (h > PICK_LDS_CAP) ps.big[atomicAdd(&ps.counts[1], 1u)] = rb | (uint32_t)d;
-            cur[d] = o;  // each thread rewrites only its own buckets
-            o += h;
+            o += __shfl(ph, 63);
+            si += __shfl(pf, 63);
+            mi += __shfl(pm, 63);
         }
         __syncthreads();
         Cand *dst = ps.cand + (size_t)row * ps.cap;
@@ -395,7 +429,7 @@ __global__ void __launch_bounds__(PICK_THREADS) pick_k(PickArgs a) {
     // LDS-resident lists go to struct-of-arrays in place (weights, then ids)
     // so the serial pass below reads four weights per load; every element is
     // read into registers before any is written back
-    const bool soa = true;  // n2 <= PICK_LDS_CAP here
+    const bool soa = true;  // n2 <= PICK_DIRECT_MAX here
     float *sw = (float *)buf;
     int32_t *sid = (int32_t *)buf + n2;
     if (soa) {
@@ -574,7 +608,11 @@ __global__ void __launch_bounds__(PICK_THREADS) pick_bsort_k(PickScratch ps) {
                 wave_sync_lds();
             }
         }
-        for (int i = lane; i < n; i += 64) g[i] = wl[i];
+        float *gw = ps.wts + (size_t)row * ps.cap + ps.bstart[(size_t)row * PB_BINS + d];
+        for (int i = lane; i < n; i += 64) {
+            g[i] = wl[i];
+            gw[i] = wl[i].w;
+        }
         wave_sync_lds();
     }
     __syncthreads();
@@ -590,7 +628,11 @@ __global__ void __launch_bounds__(PICK_THREADS) pick_bsort_k(PickScratch ps) {
             lds[i] = i < n ? g[i] : Cand{-1.f, 0x7fffffff};
         __syncthreads();
         bitonic(lds, n2);
-        for (int i = threadIdx.x; i < n; i += blockDim.x) g[i] = lds[i];
+        float *gw = ps.wts + (size_t)row * ps.cap + ps.bstart[(size_t)row * PB_BINS + d];
+        for (int i = threadIdx.x; i < n; i += blockDim.x) {
+            g[i] = lds[i];
+            gw[i] = lds[i].w;
+        }
         __syncthreads();
     }
 }
@@ -610,183 +652,307 @@ __global__ void __launch_bounds__(PICK_THREADS) pick_bsort_big_k(PickScratch ps)
             ps.temp[i] = i < n ? g[i] : Cand{-1.f, 0x7fffffff};
         __syncthreads();
         bitonic(ps.temp, n2);
-        for (int i = threadIdx.x; i < n; i += blockDim.x) g[i] = ps.temp[i];
+        float *gw = ps.wts + (size_t)row * ps.cap + ps.bstart[(size_t)row * PB_BINS + d];
+        for (int i = threadIdx.x; i < n; i += blockDim.x) {
+            g[i] = ps.temp[i];
+            gw[i] = ps.temp[i].w;
+        }
         __syncthreads();
     }
 }
 
-// The sequential tail of sample.rs:96-120 over a sorted candidate list in
-// global memory. Lane 0 adds in the reference's order from LDS chunks that
-// the other waves stage ahead of it. The total pass records the running
-// sum at every chunk start, so the nucleus crossing is found by replaying
-// one chunk; the draw then walks the kept prefix.
-constexpr int CH_THREADS = 256;
-constexpr int CH = 4096;  // weights per LDS chunk
+// The sequential tail of sample.rs:96-120 over the sorted weights of a row,
+// computed exactly but in parallel. While a running f32 value x stays in
+// one binade [2^k, 2^(k+1)) its grid is fixed (ulp 2^(k-23)), and
+// RN(x + w) equals x plus w rounded to that grid. So a run of adds (or, for
+// the draw walk, subtracts) is an integer prefix sum on the grid; the
+// elements where the run must stop are the "events": a term whose grid
+// rounding is an exact tie (then the rounding depends on the running
+// value's parity), a result that would leave the binade (upward for sums;
+// downward, judged on the term rounded up, for the walk), and, for the
+// nucleus, reaching the cut target. Each event is one ordinary f32 add by
+// one thread; everything between events is a block scan.
+constexpr int GC_THREADS = 1024;
+constexpr int GC_IPT = 16;                    // items per thread, max window 16384
+constexpr int GC_CK = 256;                    // checkpoints kept by the total pass
+constexpr int GC_SERIAL = 256;                // stretch stepped serially near events
+constexpr uint64_t GC_HUGE = 1ull << 62;
 
-__global__ void __launch_bounds__(CH_THREADS) pick_chain_k(PickArgs a, PickScratch ps) {
-    __shared__ float wb[2][CH];
-    __shared__ float ck[64];  // running sum at chunk starts (C <= 64 * CH)
-    __shared__ float s_val;
-    __shared__ int s_int;
+// x > 0: x = K * 2^ue with K on the binade's integer grid [low, lim).
+__device__ __forceinline__ void grid_of(float x, int &ue, uint64_t &K, uint64_t &lim,
+                                        uint64_t &low) {
+    const uint32_t b = __float_as_uint(x);
+    const int ex = (int)((b >> 23) & 0xff);
+    K = ex ? (uint64_t)((b & 0x7fffff) | 0x800000) : (uint64_t)(b & 0x7fffff);
+    ue = ex ? ex - 150 : -149;
+    lim = ex ? (1ull << 24) : (1ull << 23);
+    low = ex ? (1ull << 23) : 0;
+}
+
+// The float with x's exponent field and grid value K (K within x's binade).
+__device__ __forceinline__ float from_grid(float x, uint64_t K) {
+    const uint32_t b = __float_as_uint(x);
+    const uint32_t ex = (b >> 23) & 0xff;
+    return ex ? __uint_as_float(ex << 23 | (uint32_t)(K & 0x7fffff)) : __uint_as_float((uint32_t)K);
+}
+
+// w / 2^ue rounded to nearest (q, tie = exactly half) and rounded up (qc).
+__device__ __forceinline__ uint64_t grid_units(uint32_t wb, int ue, bool &tie, uint64_t &qc) {
+    const int ew = (int)((wb >> 23) & 0xff);
+    uint64_t m = wb & 0x7fffff;
+    int e;
+    if (ew == 0) {
+        e = -149;
+    } else {
+        m |= 0x800000;
+        e = ew - 150;
+    }
+    const int sh = ue - e;
+    tie = false;
+    if (sh <= 0) {
+        qc = -sh > 37 ? GC_HUGE : m << (-sh);
+        return qc;
+    }
+    if (sh >= 64) {
+        qc = m != 0;
+        return 0;
+    }
+    uint64_t q = m >> sh;
+    const uint64_t r = m & ((1ull << sh) - 1), half = 1ull << (sh - 1);
+    qc = q + (r != 0);
+    if (r > half) ++q;
+    else if (r == half) tie = true;
+    return q;
+}
+
+// ceil(t / 2^ue) for t > 0, saturating.
+__device__ __forceinline__ uint64_t grid_ceil(float t, int ue) {
+    bool tie;
+    uint64_t qc;
+    (void)grid_units(__float_as_uint(t), ue, tie, qc);
+    return qc;
+}
+
+// Exclusive prefix sum of a u64 over the block; *total gets the sum.
+__device__ uint64_t block_scan_u64(uint64_t v, uint64_t *tmp, uint64_t *total) {
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    uint64_t x = v;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const uint64_t y = __shfl_up(x, d);
+        if (lane >= d) x += y;
+    }
+    if (lane == 63) tmp[wv] = x;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint64_t run = 0;
+        for (int w = 0; w < nw; ++w) {
+            const uint64_t t = tmp[w];
+            tmp[w] = run;
+            run += t;
+        }
+        tmp[32] = run;
+    }
+    __syncthreads();
+    const uint64_t r = tmp[wv] + x - v;
+    *total = tmp[32];
+    __syncthreads();
+    return r;
+}
+
+__global__ void __launch_bounds__(GC_THREADS) pick_chain_k(PickArgs a, PickScratch ps) {
+    __shared__ uint64_t s_tmp[33];
+    __shared__ uint64_t s_pref;
+    __shared__ float s_x;
+    __shared__ int s_i, s_ev, s_stop;
+    __shared__ float s_wev;
+    __shared__ float s_w[GC_SERIAL];
+    __shared__ int ck_i[GC_CK];
+    __shared__ float ck_x[GC_CK];
+    __shared__ int s_nck;
     const int row = blockIdx.x;
     const PickRow info = ps.info[row];
     if (!info.deferred) return;
+    const float *w = ps.wts + (size_t)row * ps.cap;  // sorted, descending
     const Cand *cand = ps.cand + (size_t)row * ps.cap;
     const esp_sampler smp = a.samplers[row];
     const int C = info.C;
     const int tid = threadIdx.x;
-    const int nch = (C + CH - 1) / CH;
-    auto stage = [&](int c, int buf, int t0, int nt) {  // threads t0.. stage chunk c
-        const int base = c * CH, lim = min(CH, C - base);
-        for (int i = tid - t0; i < lim; i += nt) wb[buf][i] = cand[base + i].w;
-    };
-    typedef float f4_t __attribute__((ext_vector_type(4)));
-    // lane 0: x += w[0..lim) in order, 32 at a time with the next 32 loaded
-    // ahead (LDS latency hides behind the dependent adds)
-    auto add_run = [&](const float *w, int lim, float x) {
-        int j = 0;
-        if (lim >= 32) {
-            f4_t r[8];
-#pragma unroll
-            for (int q = 0; q < 8; ++q) r[q] = *(const f4_t *)(w + 4 * q);
-            for (; j + 64 <= lim; j += 32) {
-                f4_t nx[8];
-#pragma unroll
-                for (int q = 0; q < 8; ++q) nx[q] = *(const f4_t *)(w + j + 32 + 4 * q);
-#pragma unroll
-                for (int q = 0; q < 8; ++q) {
-                    x += r[q].x;
-                    x += r[q].y;
-                    x += r[q].z;
-                    x += r[q].w;
-                }
-#pragma unroll
-                for (int q = 0; q < 8; ++q) r[q] = nx[q];
-            }
-#pragma unroll
-            for (int q = 0; q < 8; ++q) {
-                x += r[q].x;
-                x += r[q].y;
-                x += r[q].z;
-                x += r[q].w;
-            }
-            j += 32;
+
+    // Runs x (+= or -=) w[i] for i from i0 up to n, stopping after the
+    // element where x >= target (sum with target) or x <= 0 (walk).
+    // Leaves the final x in s_x and the stop index (or n) in s_i; s_stop = 1
+    // when it stopped early. Records checkpoints when `record`.
+    auto run = [&](bool walk, int i0, float x0, int n, bool use_target, float target,
+                   bool record) {
+        if (tid == 0) {
+            s_x = x0;
+            s_i = i0;
+            s_stop = 0;
+            if (record) s_nck = 0;
         }
-        for (; j < lim; ++j) x += w[j];
-        return x;
+        __syncthreads();
+        for (;;) {
+            const int i = s_i;
+            const float x = s_x;
+            if (s_stop || i >= n) break;
+            if (record && tid == 0 && s_nck < GC_CK) {
+                ck_i[s_nck] = i;
+                ck_x[s_nck] = x;
+                ++s_nck;
+            }
+            uint64_t K = 0, lim = 0, low = 0, T = 0;
+            int ue = 0;
+            // steps that surely stay on the current grid: the largest
+            // remaining term is w[i]
+            uint64_t D = 0;
+            if (x > 0.f) {
+                grid_of(x, ue, K, lim, low);
+                if (use_target) T = grid_ceil(target, ue);
+                bool t;
+                uint64_t qc;
+                const uint64_t qi = grid_units(__float_as_uint(w[i]), ue, t, qc);
+                if (!walk) {
+                    uint64_t room = lim - K - 1;
+                    if (use_target) room = min(room, T > K ? T - K - 1 : 0);
+                    D = room / (qi ? qi : 1);
+                } else {
+                    const uint64_t fl = low ? low : 1;
+                    D = K > fl ? (K - fl) / (qc ? qc : 1) : 0;
+                }
+            }
+            if (D < GC_SERIAL) {
+                // a short stretch of ordinary f32 steps from LDS-staged terms
+                const int len = min(GC_SERIAL, n - i);
+                for (int r = tid; r < len; r += GC_THREADS) s_w[r] = w[i + r];
+                __syncthreads();
+                if (tid == 0) {
+                    float y = x;
+                    int k = 0, stop = 0;
+                    for (; k < len; ++k) {
+                        if (!walk) {
+                            y += s_w[k];
+                            if (use_target && y >= target) {
+                                stop = 1;
+                                break;
+                            }
+                        } else {
+                            y -= s_w[k];
+                            if (y <= 0.0f) {
+                                stop = 1;
+                                break;
+                            }
+                        }
+                    }
+                    s_x = y;
+                    s_stop = stop;
+                    s_i = stop ? i + k : i + len;
+                }
+                __syncthreads();
+                continue;
+            }
+            int W = (int)min<uint64_t>(D, (uint64_t)GC_THREADS * GC_IPT);
+            W = max(W, GC_THREADS);
+            W = min(W, n - i);
+            const int ipt = (W + GC_THREADS - 1) / GC_THREADS;
+            const int base = i + tid * ipt;
+            uint64_t q[GC_IPT], qc[GC_IPT];
+            float wv[GC_IPT];
+            bool tie[GC_IPT];
+            uint64_t lsum = 0;
+#pragma unroll
+            for (int r = 0; r < GC_IPT; ++r) {
+                const int j = base + r;
+                q[r] = qc[r] = 0;
+                tie[r] = false;
+                wv[r] = 0.f;
+                if (r < ipt && j < i + W) {
+                    wv[r] = w[j];
+                    q[r] = grid_units(__float_as_uint(wv[r]), ue, tie[r], qc[r]);
+                    lsum += q[r];
+                }
+            }
+            uint64_t tot;
+            uint64_t E = block_scan_u64(lsum, s_tmp, &tot);
+            if (tid == 0) s_ev = 0x7fffffff;
+            __syncthreads();
+            int mine = 0x7fffffff;
+            uint64_t mine_pref = 0;
+            float mine_w = 0.f;
+#pragma unroll
+            for (int r = 0; r < GC_IPT; ++r) {
+                const int j = base + r;
+                if (r < ipt && j < i + W && mine == 0x7fffffff) {
+                    bool ev = tie[r];
+                    if (!walk) ev = ev || K + E + q[r] >= lim || (use_target && K + E + q[r] >= T);
+                    else ev = ev || E + qc[r] + (low ? low : 1) > K;
+                    if (ev) {
+                        mine = j - i;
+                        mine_pref = E;
+                        mine_w = wv[r];
+                    } else {
+                        E += q[r];
+                    }
+                }
+            }
+            if (mine != 0x7fffffff) atomicMin(&s_ev, mine);
+            __syncthreads();
+            const int e = s_ev;
+            if (e != 0x7fffffff && mine == e) {
+                s_pref = mine_pref;
+                s_wev = mine_w;
+            }
+            __syncthreads();
+            if (tid == 0) {
+                const uint64_t P = e == 0x7fffffff ? tot : s_pref;
+                float y = from_grid(x, walk ? K - P : K + P);
+                int k = e == 0x7fffffff ? i + W : i + e, stop = 0;
+                if (e != 0x7fffffff) {
+                    // the event term, as one ordinary f32 step
+                    if (!walk) {
+                        y += s_wev;
+                        stop = use_target && y >= target;
+                    } else {
+                        y -= s_wev;
+                        stop = y <= 0.0f;
+                    }
+                    if (!stop) ++k;
+                }
+                s_x = y;
+                s_i = k;
+                s_stop = stop;
+            }
+            __syncthreads();
+        }
     };
+
     // pass 1: the total over every candidate (Rust's f32 sum starts at -0.0)
-    float total = -0.0f;
-    stage(0, 0, 0, CH_THREADS);
-    __syncthreads();
-    for (int c = 0; c < nch; ++c) {
-        if (c + 1 < nch && tid >= 64) stage(c + 1, (c + 1) & 1, 64, CH_THREADS - 64);
-        if (tid == 0) {
-            ck[c] = total;
-            total = add_run(wb[c & 1], min(CH, C - c * CH), total);
-        }
-        __syncthreads();
-    }
+    run(false, 0, -0.0f, C, false, 0.f, true);
+    const float total = s_x;
     int keep = C;
-    float kept = 0.f;
+    float kept = total;
     const float top_p = smp.top_p;
-    if (tid == 0) {
-        if (top_p >= 0.f) {
-            const float p = top_p > 1.f ? 1.f : top_p;
-            const float target = total * p;
-            // the first chunk whose end sum reaches the target
-            int c = 0;
-            while (c + 1 < nch && ck[c + 1] < target) ++c;
-            s_int = c;
-            s_val = target;
-        } else {
-            s_int = -1;
-        }
-    }
-    __syncthreads();
-    if (s_int >= 0) {
-        const int c = s_int;
-        const float target = s_val;
-        stage(c, 0, 0, CH_THREADS);
+    if (top_p >= 0.f) {
+        const float p = top_p > 1.f ? 1.f : top_p;
+        const float target = total * p;
+        // restart from the last checkpoint still below the target
+        int c = 0;
+        const int nck = s_nck;
+        while (c + 1 < nck && ck_x[c + 1] < target) ++c;
+        const int i0 = nck ? ck_i[c] : 0;
+        const float x0 = nck ? ck_x[c] : -0.0f;
         __syncthreads();
-        if (tid == 0) {
-            float mass = ck[c];
-            const int lim = min(CH, C - c * CH);
-            keep = c * CH + lim;
-            for (int j = 0; j < lim; ++j) {
-                mass += wb[0][j];
-                if (mass >= target) {
-                    keep = c * CH + j + 1;
-                    break;
-                }
-            }
-            if (keep < 1) keep = 1;
-            kept = -0.0f + mass;
-            s_int = keep;
-            s_val = kept;
-        }
-        __syncthreads();
-        keep = s_int;
-        kept = s_val;
-        __syncthreads();
-    } else {
-        if (tid == 0) s_val = total;
-        __syncthreads();
-        kept = s_val;
-        __syncthreads();
+        run(false, i0, x0, C, true, target, false);
+        keep = s_stop ? s_i + 1 : C;
+        kept = -0.0f + s_x;
     }
     // pass 2: the draw walks the kept prefix
     uint64_t state = smp.state;
     const uint64_t x = splitmix_next(state);
-    float u = (float)((double)(x >> 11) / 9007199254740992.0) * kept;
-    const int kch = (keep + CH - 1) / CH;
-    int hit = -1;
-    if (tid == 0) s_int = -1;
-    stage(0, 0, 0, CH_THREADS);
+    const float u = (float)((double)(x >> 11) / 9007199254740992.0) * kept;
     __syncthreads();
-    for (int c = 0; c < kch; ++c) {
-        if (c + 1 < kch && tid >= 64) stage(c + 1, (c + 1) & 1, 64, CH_THREADS - 64);
-        if (tid == 0 && s_int < 0) {
-            const float *w = wb[c & 1];
-            const int lim = min(CH, keep - c * CH);
-            int j = 0;
-            // batches of 32 that keep the draw positive are taken whole (the
-            // draw only falls, so no term inside such a batch crossed zero)
-            if (lim >= 32) {
-                f4_t r[8];
-#pragma unroll
-                for (int q = 0; q < 8; ++q) r[q] = *(const f4_t *)(w + 4 * q);
-                for (; j + 32 <= lim; j += 32) {
-                    f4_t nx[8];
-                    const int jn = j + 32 + 32 <= lim ? j + 32 : j;
-#pragma unroll
-                    for (int q = 0; q < 8; ++q) nx[q] = *(const f4_t *)(w + jn + 4 * q);
-                    float u2 = u;
-#pragma unroll
-                    for (int q = 0; q < 8; ++q) {
-                        u2 -= r[q].x;
-                        u2 -= r[q].y;
-                        u2 -= r[q].z;
-                        u2 -= r[q].w;
-                    }
-                    if (!(u2 > 0.0f)) break;
-                    u = u2;
-#pragma unroll
-                    for (int q = 0; q < 8; ++q) r[q] = nx[q];
-                }
-            }
-            for (; j < lim; ++j) {
-                u -= w[j];
-                if (u <= 0.0f) {
-                    s_int = c * CH + j;
-                    break;
-                }
-            }
-        }
-        __syncthreads();
-        if (s_int >= 0) break;
-    }
-    hit = s_int;
+    run(true, 0, u, keep, false, 0.f, false);
+    const int hit = s_stop ? s_i : -1;
     if (tid == 0) {
         int out;
         if (hit >= 0) out = cand[hit].id;
@@ -815,7 +981,6 @@ void launch_pick(const PickArgs &a, hipStream_t s) {
     }
     const bool sampled = a.samplers != nullptr;
     PickScratch ps{};
-    if (sampled && a.V >= 64 * CH) fail(ESP_UNSUPPORTED, "sampling: vocabulary above 262143 ids");
     if (sampled) {
         if (a.scratch_bytes < pick_scratch_bytes(a.n, a.V))
             fail(ESP_BACKEND, "pick: sampling scratch too small");
@@ -826,7 +991,7 @@ void launch_pick(const PickArgs &a, hipStream_t s) {
     if (sampled) {
         pick_bsort_k<<<256, PICK_THREADS, shm, s>>>(ps);
         pick_bsort_big_k<<<1, PICK_THREADS, 0, s>>>(ps);
-        pick_chain_k<<<a.n, CH_THREADS, 0, s>>>(a, ps);
+        pick_chain_k<<<a.n, GC_THREADS, 0, s>>>(a, ps);
     }
 }
 
