@@ -770,8 +770,13 @@ static void run_layer_decode(Model &m, Kv &kv, const Rows &rows, LayerW &w, int 
 
 // One pass of `Mc` rows (already on the device at `rows`) through all layers.
 // `x_is_gemv` selects the single-row decode kernels.
+// A run of chunk rows that are consecutive positions of one sequence.
+struct Seg {
+    int seq, row0, len, p0;
+};
+
 static void run_layers(Model &m, Kv &kv, const Rows &rows, int Mc, int max_t, int one_seq = -1,
-                       int p0 = 0) {
+                       int p0 = 0, const std::vector<Seg> *segs = nullptr) {
     hipStream_t s = kv.stream;
     const bool single = Mc == 1;
     // activations keep f32 precision; bf16 models hand them to the matrix
@@ -852,7 +857,33 @@ static void run_layers(Model &m, Kv &kv, const Rows &rows, int Mc, int max_t, in
             Prof p("rope_kv", s);
             launch_rope_kv(m.wt, kv.dt, r, s);
         }
-        if (one_seq >= 0 && Mc >= 16 && m.wt == DT_BF16 && flash_ok(m.hd)) {
+        bool seg_flash = segs && !segs->empty() && m.wt == DT_BF16 && flash_ok(m.hd);
+        for (size_t i = 0; seg_flash && i < segs->size(); ++i) seg_flash = (*segs)[i].len >= 16;
+        if (seg_flash) {
+            // several sequences' prompt blocks: the tiled MFMA attention per block
+            uint16_t *lo = (uint16_t *)lo_plane(act, kv.attn, Mc, m.qw);
+            Prof p("attention", s);
+            for (const Seg &g : *segs) {
+                FlashArgs f{};
+                f.q = kv.q.as<float>() + (size_t)g.row0 * m.qw;
+                f.kv = kv.cache.as<float>() + (size_t)l * kv.layer_stride;
+                f.seq_stride = kv.seq_stride;
+                f.kv_half_stride = kv.half_stride;
+                f.head_stride = kv.head_stride;
+                f.seq = g.seq;
+                f.p0 = g.p0;
+                f.M = g.len;
+                f.nq = m.nq;
+                f.nkv = m.nkv;
+                f.hd = m.hd;
+                f.window = w.window;
+                // f32 rows, or the hi plane's bf16 rows when split
+                f.out = lo ? (float *)(kv.attn.as<uint16_t>() + (size_t)g.row0 * m.qw)
+                           : kv.attn.as<float>() + (size_t)g.row0 * m.qw;
+                f.out_lo = lo ? lo + (size_t)g.row0 * m.qw : nullptr;
+                launch_flash(f, s);
+            }
+        } else if (one_seq >= 0 && Mc >= 16 && m.wt == DT_BF16 && flash_ok(m.hd)) {
             // rows are consecutive positions of one sequence: tiled MFMA attention
             FlashArgs f{};
             f.q = kv.q.as<float>();
@@ -1121,8 +1152,19 @@ void forward(Model &m, Kv &kv, int n_seqs, const uint32_t *seqs, const uint32_t 
             Prof p("embed", s);
             launch_embed(m.wt, m.embed, rows.ids, Mc, m.H, kv.h.as<float>(), s);
         }
-        if (n_seqs == 1) run_layers(m, kv, rows, Mc, max_t, (int)seqs[0], rpos[c0]);
-        else run_layers(m, kv, rows, Mc, max_t);
+        if (n_seqs == 1) {
+            run_layers(m, kv, rows, Mc, max_t, (int)seqs[0], rpos[c0]);
+        } else {
+            std::vector<Seg> segs;
+            for (int r = 0; r < Mc; ++r) {
+                const long long g = c0 + r;
+                if (segs.empty() || rseq[g] != segs.back().seq ||
+                    rpos[g] != segs.back().p0 + segs.back().len)
+                    segs.push_back(Seg{rseq[g], r, 0, rpos[g]});
+                segs.back().len++;
+            }
+            run_layers(m, kv, rows, Mc, max_t, -1, 0, &segs);
+        }
         if (one_chunk) break;
         // keep the hidden state of every sequence's last row in this chunk
         for (int i = 0; i < n_seqs; ++i)

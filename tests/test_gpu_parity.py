@@ -120,6 +120,39 @@ def test_batch_equals_independent_sequences():
         assert kvb.position(i) == len(prompts[i]) + len(blocks[i])
 
 
+def test_bf16_batched_prefill_segments_match_oracle():
+    """Several sequences' prompt blocks in one forward (each >= 16 rows: the
+    MFMA attention per sequence), including blocks over a warm cache and a
+    sequence whose rows straddle two 4096-row chunks; last logits vs the
+    oracle within the bf16 tolerance, and close to each sequence alone."""
+    cfg = synth.llama_config(2, 128, 4, 2, 256, 300, head_dim=64, max_pos=4096)
+    tensors = synth.make_tensors(cfg, 71, "bf16")
+    model = DecoderModel.from_bytes(cfg, st.dump(tensors), "bf16")
+    ref = oracle.OracleModel(cfg, tensors)
+    lens = [40, 100, 17, 64]
+    prompts = [synth.uniform_ids(700 + i, n, cfg.vocab_size) for i, n in enumerate(lens)]
+    kvb = model.new_cache(4, 256)
+    got = model.forward_batch(kvb, [0, 1, 2, 3], prompts)
+    more = [synth.uniform_ids(800 + i, 20 + i, cfg.vocab_size) for i in range(4)]
+    got2 = model.forward_batch(kvb, [3, 2, 1, 0], more)
+    for i in range(4):
+        rkv = ref.new_cache()
+        want = ref.forward_last(rkv, prompts[i])
+        assert _close_bf16(got[i], want), f"seq {i}: {np.abs(got[i] - want).max()}"
+        want2 = ref.forward_last(rkv, more[3 - i])
+        assert _close_bf16(got2[3 - i], want2), f"seq {i} warm: {np.abs(got2[3 - i] - want2).max()}"
+        kv = model.new_cache(1, 256)
+        alone = model.try_forward_cached_last(prompts[i], kv)
+        assert np.abs(alone - got[i]).max() < 1e-3
+    # two 2100-token prompts: the second one's rows span the chunk boundary
+    long = [synth.uniform_ids(900 + i, 2100, cfg.vocab_size) for i in range(2)]
+    kvl = model.new_cache(2, 2200)
+    got = model.forward_batch(kvl, [0, 1], long)
+    for i in range(2):
+        want = ref.forward_last(ref.new_cache(), long[i])
+        assert _close_bf16(got[i], want), f"long seq {i}: {np.abs(got[i] - want).max()}"
+
+
 def test_cached_blocks_match_full_recompute():
     """model.rs:725-763: blocks of 1, 2, 3 over a warm cache == full prefill."""
     cfg, tensors, blob, _ = synth.tiny_llama_case(4, 2, 64, 4, 2, 96, 50, 6)
