@@ -13,7 +13,7 @@ from .errors import raise_for_status
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libesp_hip.so")
 
-ESP_FORMAT_F32, ESP_FORMAT_BF16 = 0, 1
+ESP_FORMAT_F32, ESP_FORMAT_BF16, ESP_FORMAT_Q8, ESP_FORMAT_Q4 = 0, 1, 2, 3
 ESP_ROPE_NONE, ESP_ROPE_LINEAR, ESP_ROPE_LLAMA3 = 0, 1, 2
 ESP_PICK_NONFINITE, ESP_PICK_NO_ELIGIBLE = 1, 2
 

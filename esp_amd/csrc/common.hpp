@@ -29,9 +29,14 @@ typedef uint16_t bf16_t;  // raw bf16 bits in host code
 // Element kinds. DT_SPLIT is an f32 activation matrix stored as two bf16
 // planes of the same shape, hi = bf16(x) then lo = bf16(x - hi), so matrix
 // cores can consume it exactly (R x C matrix: hi[r*C+c], lo[R*C + r*C+c]).
-enum Dt { DT_F32 = 0, DT_BF16 = 1, DT_SPLIT = 2 };
+// DT_Q8 / DT_Q4: packed projection weights, signed 8- or 4-bit integers
+// along K with one f32 scale per 32 inputs (values, then the scales).
+enum Dt { DT_F32 = 0, DT_BF16 = 1, DT_SPLIT = 2, DT_Q8 = 3, DT_Q4 = 4 };
 
 inline size_t dt_size(Dt d) { return d == DT_BF16 ? 2 : 4; }
+inline bool dt_packed(Dt d) { return d == DT_Q8 || d == DT_Q4; }
+// bytes of the packed values of n weights (n a multiple of 32)
+inline size_t packed_value_bytes(Dt d, size_t n) { return d == DT_Q8 ? n : n / 2; }
 
 // ---------------------------------------------------------------------------
 // Kernel launch interfaces (implemented in the .hip files). Every launcher
@@ -137,6 +142,14 @@ struct PickArgs {
 };
 void launch_pick(const PickArgs &a, hipStream_t s);
 size_t pick_scratch_bytes(int n, int V);
+
+// Packed weights: out[i] = q_i * scale[i / 32] in f32 (n a multiple of 32).
+void launch_dequant(Dt wt, const void *values, const float *scales, size_t n, float *out,
+                    hipStream_t s);
+// decoder/weight_format.rs:150-183 on the device: rows x cols f32 (cols a
+// multiple of 32) to packed values + block scales.
+void launch_quantize(Dt wt, const float *src, size_t rows, size_t cols, void *values,
+                     float *scales, hipStream_t s);
 
 // Device-side generation hand-off (see k_basic.hip).
 void launch_gen_step(const uint32_t *picked, int32_t *gen, hipStream_t s);

@@ -10,6 +10,7 @@ constexpr int DG_MAX_PART = 2048;  // argmax partials (blocks) of the head GEMV
 
 struct DecodeGemvArgs {
     const void *w, *w2;   // [N, K] weight rows (SWIGLU: gate, up)
+    const float *ws, *ws2;  // packed formats: [N, K/32] block scales of w, w2
     const float *x;       // [K] input row
     const float *gamma;   // nullable: fused RMSNorm of x
     float eps;

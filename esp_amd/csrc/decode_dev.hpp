@@ -32,11 +32,33 @@ __device__ __forceinline__ int32_t ld_agent(const int32_t *p) {
 }
 __device__ __forceinline__ void wait_stores() { __builtin_amdgcn_s_waitcnt(0x0F70); }  // vmcnt(0)
 
+// Packed projection weights (decoder/weight_format.rs:138-223): signed
+// integers along K in each [out, in] row, one f32 scale per 32 inputs;
+// weight = q * scale. q8: one byte per weight. q4: two per byte, the even
+// input in the low nibble.
+struct q8_t {
+    int8_t v;
+};
+struct q4_t {
+    uint8_t v;
+};
+template <typename WT> struct WPacked { static constexpr bool v = false; };
+template <> struct WPacked<q8_t> { static constexpr bool v = true; };
+template <> struct WPacked<q4_t> { static constexpr bool v = true; };
+
+typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
+
+// Chunk<WT>: 8 consecutive weights of one row and their dot product with 8
+// f32 inputs. load_at(base, e, scales) reads weights e .. e+7 of a
+// row-major matrix (e a multiple of 8; scales used by packed formats).
 template <typename WT> struct Chunk;
 template <> struct Chunk<uint16_t> {  // 8 bf16 = 16 bytes
     u32x4_t v;
     __device__ __forceinline__ void load(const uint16_t *p) {
         v = __builtin_nontemporal_load((const u32x4_t *)p);
+    }
+    __device__ __forceinline__ void load_at(const void *base, size_t e, const float *) {
+        load((const uint16_t *)base + e);
     }
     __device__ __forceinline__ float dot(const float *x) const {
         float s = 0.f;
@@ -57,6 +79,9 @@ template <> struct Chunk<float> {  // 8 f32 = 2 x 16 bytes
         a = __builtin_nontemporal_load((const f32x4_t *)p);
         b = __builtin_nontemporal_load((const f32x4_t *)p + 1);
     }
+    __device__ __forceinline__ void load_at(const void *base, size_t e, const float *) {
+        load((const float *)base + e);
+    }
     __device__ __forceinline__ float dot(const float *x) const {
         float s = 0.f;
         s += a.x * x[0];
@@ -68,6 +93,37 @@ template <> struct Chunk<float> {  // 8 f32 = 2 x 16 bytes
         s += b.z * x[6];
         s += b.w * x[7];
         return s;
+    }
+};
+
+template <> struct Chunk<q8_t> {  // 8 x int8 = 8 bytes + the block scale
+    u32x2_t v;
+    float sc;
+    __device__ __forceinline__ void load_at(const void *base, size_t e, const float *scales) {
+        v = __builtin_nontemporal_load((const u32x2_t *)((const int8_t *)base + e));
+        sc = scales[e >> 5];
+    }
+    __device__ __forceinline__ float dot(const float *x) const {
+        float s = 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) s += (float)((int)(v.x << (24 - 8 * i)) >> 24) * x[i];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) s += (float)((int)(v.y << (24 - 8 * i)) >> 24) * x[4 + i];
+        return s * sc;
+    }
+};
+template <> struct Chunk<q4_t> {  // 8 x int4 = 4 bytes + the block scale
+    unsigned int v;
+    float sc;
+    __device__ __forceinline__ void load_at(const void *base, size_t e, const float *scales) {
+        v = __builtin_nontemporal_load((const unsigned int *)((const uint8_t *)base + (e >> 1)));
+        sc = scales[e >> 5];
+    }
+    __device__ __forceinline__ float dot(const float *x) const {
+        float s = 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) s += (float)((int)(v << (28 - 4 * i)) >> 28) * x[i];
+        return s * sc;
     }
 };
 

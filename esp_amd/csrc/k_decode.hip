@@ -44,15 +44,18 @@ __global__ void __launch_bounds__(DG_THREADS) decode_gemv_k(DecodeGemvArgs a) {
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int K = a.K, kq = K / DG_WAVES, nch = kq / 8;  // chunks in this wave's quarter
     const int k0 = wave * kq;
-    const WT *W = (const WT *)a.w;
-    const WT *W2 = (const WT *)a.w2;
+    const void *W = a.w;
+    const void *W2 = a.w2;
+    size_t ex0 = 0;  // element offset of the routed expert (RESID)
     if (EPI == DG_RESID && a.ex_sel)  // one routed expert's rows
-        W += (size_t)min(max(a.ex_sel[a.ex_slot], 0), a.ex_count - 1) * a.ex_stride;
+        ex0 = (size_t)min(max(a.ex_sel[a.ex_slot], 0), a.ex_count - 1) * a.ex_stride;
     const int units = EPI == DG_QKVROPE ? a.N / 2 : a.N;
 
     Chunk<WT> wc[R][NCH];
     auto load_rows = [&](int u0) {
-        const WT *rp[R];
+        const void *rb[R];    // matrix of each row (gate or up for SWIGLU)
+        const float *rs[R];   // its block scales (packed formats)
+        size_t ro[R];         // element offset of the row's first weight
 #pragma unroll
         for (int r = 0; r < RB; ++r) {
             int u = min(u0 + r, units - 1);
@@ -62,15 +65,22 @@ __global__ void __launch_bounds__(DG_THREADS) decode_gemv_k(DecodeGemvArgs a) {
                     const int j = u / a.ex_rows, e = min(max(a.ex_sel[j], 0), a.ex_count - 1);
                     off = (size_t)e * a.ex_stride + (size_t)(u - j * a.ex_rows) * K;
                 }
-                rp[r * 2] = W + off;
-                rp[r * 2 + 1] = W2 + off;
+                rb[r * 2] = W;
+                rb[r * 2 + 1] = W2;
+                rs[r * 2] = a.ws;
+                rs[r * 2 + 1] = a.ws2;
+                ro[r * 2] = ro[r * 2 + 1] = off;
             } else if (EPI == DG_QKVROPE) {
                 int half = a.hd / 2, head = u / half, d = u % half;
                 int row = head * a.hd + d;
-                rp[r * 2] = W + (size_t)row * K;
-                rp[r * 2 + 1] = W + (size_t)(row + half) * K;
+                rb[r * 2] = rb[r * 2 + 1] = W;
+                rs[r * 2] = rs[r * 2 + 1] = a.ws;
+                ro[r * 2] = (size_t)row * K;
+                ro[r * 2 + 1] = (size_t)(row + half) * K;
             } else {
-                rp[r] = W + (size_t)u * K;
+                rb[r] = W;
+                rs[r] = a.ws;
+                ro[r] = ex0 + (size_t)u * K;
             }
         }
 #pragma unroll
@@ -78,7 +88,7 @@ __global__ void __launch_bounds__(DG_THREADS) decode_gemv_k(DecodeGemvArgs a) {
             const int ch = lane + 64 * c;
             if (ch < nch) {
 #pragma unroll
-                for (int r = 0; r < R; ++r) wc[r][c].load(rp[r] + k0 + ch * 8);
+                for (int r = 0; r < R; ++r) wc[r][c].load_at(rb[r], ro[r] + k0 + ch * 8, rs[r]);
             }
         }
     };
@@ -179,7 +189,7 @@ __global__ void __launch_bounds__(DG_THREADS) decode_gemv_k(DecodeGemvArgs a) {
             }
             if (a.lora_t) {  // unmerged LoRA, before RoPE (lora.rs:93-97)
                 const int j = head < a.nq ? 0 : (head < a.nq + a.nkv ? 1 : 2);
-                if (a.lora_b[j]) {
+                if constexpr (!WPacked<WT>::v) if (a.lora_b[j]) {
                     const WT *B = (const WT *)a.lora_b[j];
                     const int rank = a.lora_rank[j];
                     const int off = j == 0 ? 0 : (j == 1 ? a.nq * hd : (a.nq + a.nkv) * hd);
@@ -354,8 +364,12 @@ void launch_decode_gemv(Dt wt, int epi, const DecodeGemvArgs &a, hipStream_t s) 
 #define DG_CASE(E)                                                   \
     case E:                                                          \
         if (wt == DT_BF16) dg_launch<uint16_t, E>(a, cus, s);        \
+        else if (wt == DT_Q8) dg_launch<q8_t, E>(a, cus, s);         \
+        else if (wt == DT_Q4) dg_launch<q4_t, E>(a, cus, s);         \
         else dg_launch<float, E>(a, cus, s);                         \
         break;
+    if ((wt == DT_Q8 || wt == DT_Q4) && (!a.ws || (epi == DG_SWIGLU && !a.ws2) || a.ex_sel))
+        fail(ESP_BACKEND, "decode_gemv: packed weights need their block scales (no routed experts)");
     switch (epi) {
         DG_CASE(DG_STORE)
         DG_CASE(DG_RESID)

@@ -240,4 +240,71 @@ void launch_fill_bits(uint16_t *dst, size_t n, uint16_t bits, hipStream_t s) {
     fill_bits_k<<<blocks, 256, 0, s>>>(dst, n, bits);
 }
 
+// ------------------------------------------------- packed weight formats
+
+// out[i] = q_i * scale[i / 32]: the weight value the packed formats define
+// (weight_format.rs:390-397).
+template <bool Q4>
+__global__ void __launch_bounds__(256) dequant_k(const void *values, const float *scales,
+                                                 size_t n, float *out) {
+    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n;
+         i += (size_t)gridDim.x * blockDim.x) {
+        int q;
+        if (Q4) {
+            const uint8_t b = ((const uint8_t *)values)[i >> 1];
+            q = ((int)((unsigned)b << (28 - 4 * (int)(i & 1)))) >> 28;
+        } else {
+            q = ((const int8_t *)values)[i];
+        }
+        out[i] = (float)q * scales[i >> 5];
+    }
+}
+
+void launch_dequant(Dt wt, const void *values, const float *scales, size_t n, float *out,
+                    hipStream_t s) {
+    if (!n) return;
+    int blocks = (int)std::min<size_t>((n + 255) / 256, 65536);
+    if (wt == DT_Q4) dequant_k<true><<<blocks, 256, 0, s>>>(values, scales, n, out);
+    else dequant_k<false><<<blocks, 256, 0, s>>>(values, scales, n, out);
+}
+
+// weight_format.rs:150-183, one thread per 32-input block: scale = peak /
+// max (1 for an all-zero block, at least the smallest normal f32), q =
+// round-half-away(v / scale) clamped to [-max, max]; q4 packs two per byte,
+// the even input in the low nibble.
+template <bool Q4>
+__global__ void __launch_bounds__(256) quantize_k(const float *src, size_t blocks, void *values,
+                                                  float *scales) {
+    const float qmax = Q4 ? 7.f : 127.f;
+    for (size_t b = blockIdx.x * (size_t)blockDim.x + threadIdx.x; b < blocks;
+         b += (size_t)gridDim.x * blockDim.x) {
+        const float *v = src + b * 32;
+        float peak = 0.f;
+        for (int i = 0; i < 32; ++i) peak = fmaxf(peak, fabsf(v[i]));
+        const float scale = peak == 0.f ? 1.f : fmaxf(peak / qmax, 1.17549435e-38f);
+        scales[b] = scale;
+        if (Q4) {
+            uint8_t *o = (uint8_t *)values + b * 16;
+            for (int i = 0; i < 32; i += 2) {
+                const int q0 = (int)fminf(fmaxf(roundf(v[i] / scale), -qmax), qmax);
+                const int q1 = (int)fminf(fmaxf(roundf(v[i + 1] / scale), -qmax), qmax);
+                o[i / 2] = (uint8_t)((q0 & 15) | ((q1 & 15) << 4));
+            }
+        } else {
+            int8_t *o = (int8_t *)values + b * 32;
+            for (int i = 0; i < 32; ++i)
+                o[i] = (int8_t)(int)fminf(fmaxf(roundf(v[i] / scale), -qmax), qmax);
+        }
+    }
+}
+
+void launch_quantize(Dt wt, const float *src, size_t rows, size_t cols, void *values,
+                     float *scales, hipStream_t s) {
+    const size_t blocks = rows * cols / 32;
+    if (!blocks) return;
+    int grid = (int)std::min<size_t>((blocks + 255) / 256, 65536);
+    if (wt == DT_Q4) quantize_k<true><<<grid, 256, 0, s>>>(src, blocks, values, scales);
+    else quantize_k<false><<<grid, 256, 0, s>>>(src, blocks, values, scales);
+}
+
 }  // namespace esp

@@ -82,8 +82,8 @@ static void validate_config(const esp_config &c) {
     if (!(c.rms_norm_eps > 0.f) || !isfinite(c.rms_norm_eps) || !(c.rope_theta > 0.f) ||
         !isfinite(c.rope_theta))
         fail(ESP_INVALID_CONFIG, "zero, non-finite or overflowing decoder dimensions/settings");
-    if (c.format != ESP_FORMAT_F32 && c.format != ESP_FORMAT_BF16)
-        fail(ESP_UNSUPPORTED, "weight format: only f32 and bf16 are implemented");
+    if (c.format > ESP_FORMAT_Q4_BLOCK32)
+        fail(ESP_INVALID_CONFIG, "unknown weight format " + std::to_string(c.format));
     if (c.head_dim > 256) fail(ESP_UNSUPPORTED, "head_dim: values above 256 are not implemented");
     if (c.num_attention_heads / c.num_key_value_heads * c.head_dim > 2048)
         fail(ESP_UNSUPPORTED, "attention: query group x head_dim above 2048 is not implemented");
@@ -102,7 +102,11 @@ static void init_model_shape(Model &m, const esp_config &c) {
     m.cfg = c;
     m.cfg.layer_window = nullptr;
     m.cfg.layer_is_moe = nullptr;
-    m.wt = c.format == ESP_FORMAT_BF16 ? DT_BF16 : DT_F32;
+    m.wt = c.format == ESP_FORMAT_BF16 ? DT_BF16
+         : c.format == ESP_FORMAT_Q8_BLOCK32 ? DT_Q8
+         : c.format == ESP_FORMAT_Q4_BLOCK32 ? DT_Q4 : DT_F32;
+    m.et = dt_packed(m.wt) ? DT_F32 : m.wt;
+    m.ht = m.wt;
     m.H = c.hidden_size;
     m.L = c.num_hidden_layers;
     m.nq = c.num_attention_heads;
@@ -123,6 +127,20 @@ static void init_model_shape(Model &m, const esp_config &c) {
         m.layers[l].moe = m.E && c.layer_is_moe && c.layer_is_moe[l];
     }
     ESP_HIP(hipGetDevice(&m.device));
+}
+
+// Packed formats (weight_format.rs:138-223) run dense llama-family layers:
+// every projection input width a multiple of 32 within the decode GEMV.
+static void check_packed(const Model &m, uint32_t n_adapters) {
+    if (!dt_packed(m.wt)) return;
+    const char *id = m.wt == DT_Q8 ? "weight format q8-k32-f32-scale-f16-shared-v1"
+                                   : "weight format q4-k32-f32-scale-f16-shared-v1";
+    if (m.E) fail(ESP_UNSUPPORTED, std::string(id) + ": routed experts are not implemented");
+    if (n_adapters) fail(ESP_UNSUPPORTED, std::string(id) + ": unmerged LoRA is not implemented");
+    for (int k : {m.H, m.qw, m.F})
+        if (k % 32 || !decode_gemv_ok(k))
+            fail(ESP_INVALID_WEIGHTS, "weight format: packed projection input width " +
+                                          std::to_string(k) + " must be divisible by 32");
 }
 
 static void upload(void *dst, const void *src, size_t bytes) {
@@ -192,8 +210,9 @@ struct Stager {
         const StTensor &s = get(name, shape);
         size_t n = 1;
         for (auto d : shape) n *= d;
-        Dt dst = force_f32 ? DT_F32 : m.wt;
-        if (m.wt == DT_BF16 && !force_f32 && s.dtype != "BF16")
+        Dt dst = force_f32 || dt_packed(m.wt) ? DT_F32 : m.wt;
+        if ((m.wt == DT_BF16 && !force_f32 && s.dtype != "BF16") ||
+            (dt_packed(m.wt) && s.dtype != "F16"))
             fail(ESP_INVALID_WEIGHTS, "weight format: artifact dtype disagrees with declared format (" +
                                           name + ")");
         size_t base = out.size();
@@ -217,6 +236,56 @@ struct Stager {
                 memcpy(o + 2 * i, &b, 2);
             }
         }
+    }
+    // A packed projection [rows, cols] (weight_format.rs:225-273): a U8
+    // tensor whose shape is its byte count, the packed values then the
+    // f32 block scales, every scale finite and positive. Appends to vals
+    // and scales.
+    void read_packed(const std::string &name, uint64_t rows, uint64_t cols,
+                     std::vector<uint8_t> &vals, std::vector<uint8_t> &scales) {
+        auto it = t.find(name);
+        if (it == t.end()) fail(ESP_INVALID_WEIGHTS, "missing tensor: " + name);
+        const StTensor &s = it->second;
+        if (s.dtype != "U8")
+            fail(ESP_INVALID_WEIGHTS, "weight format: unpacked projection in a quantized row (" +
+                                          name + ")");
+        if (cols % 32)
+            fail(ESP_INVALID_WEIGHTS, "weight format: packed projection input width must be "
+                                      "divisible by 32");
+        const size_t n = rows * cols, vb = packed_value_bytes(m.wt, n), sb = n / 32 * 4;
+        if (s.shape.size() != 1 || s.shape[0] != s.bytes)
+            fail(ESP_INVALID_WEIGHTS, "weight format: packed buffer must have its encoded "
+                                      "byte-count shape");
+        bool ok = s.bytes == vb + sb;
+        for (size_t i = 0; ok && i < n / 32; ++i) {
+            float sc;
+            memcpy(&sc, s.data + vb + 4 * i, 4);
+            ok = isfinite(sc) && sc > 0.f;
+        }
+        if (!ok)
+            fail(ESP_INVALID_WEIGHTS, "weight format: packed projection byte count or block scales "
+                                      "are invalid (" + name + ")");
+        consumed.insert(name);
+        vals.insert(vals.end(), s.data, s.data + vb);
+        scales.insert(scales.end(), s.data + vb, s.data + vb + sb);
+    }
+    // values then scales in one allocation; *scales_out points at the scales
+    void *packed(const std::vector<uint8_t> &vals, const std::vector<uint8_t> &scales,
+                 const float **scales_out) {
+        std::vector<uint8_t> all(vals);
+        size_t pad = (256 - all.size() % 256) % 256;  // 256-byte aligned scales
+        all.resize(all.size() + pad, 0);
+        const size_t off = all.size();
+        all.insert(all.end(), scales.begin(), scales.end());
+        char *d = (char *)to_device(all);
+        *scales_out = (const float *)(d + off);
+        return d;
+    }
+    void *proj(const std::string &name, uint64_t rows, uint64_t cols, const float **scales_out) {
+        if (!dt_packed(m.wt)) return tensor(name, {rows, cols});
+        std::vector<uint8_t> v, sc;
+        read_packed(name, rows, cols, v, sc);
+        return packed(v, sc, scales_out);
     }
     void *to_device(const std::vector<uint8_t> &host) {
         void *d = m.alloc(host.size());
@@ -269,6 +338,7 @@ Model *load_model(const esp_config *cfg, const uint8_t *bytes, size_t len,
     std::unique_ptr<Model> mp(new Model());
     Model &m = *mp;
     init_model_shape(m, *cfg);
+    check_packed(m, n_adapters);
     auto tensors = parse_safetensors(bytes, len);
     Stager s{m, tensors, {}};
     const uint64_t H = m.H, qw = m.qw, kvw = m.kvw, hd = m.hd;
@@ -310,10 +380,16 @@ Model *load_model(const esp_config *cfg, const uint8_t *bytes, size_t len,
         w.in_norm = (float *)s.tensor(p + "input_layernorm.weight", {H}, true);
         w.post_norm = (float *)s.tensor(p + "post_attention_layernorm.weight", {H}, true);
         // fused q | k | v | LoRA-A rows (loader.rs:508-535 read order)
-        std::vector<uint8_t> qkv;
-        s.read(p + "self_attn.q_proj.weight", {qw, H}, qkv);
-        s.read(p + "self_attn.k_proj.weight", {kvw, H}, qkv);
-        s.read(p + "self_attn.v_proj.weight", {kvw, H}, qkv);
+        std::vector<uint8_t> qkv, qkv_sc;
+        if (dt_packed(m.wt)) {
+            s.read_packed(p + "self_attn.q_proj.weight", qw, H, qkv, qkv_sc);
+            s.read_packed(p + "self_attn.k_proj.weight", kvw, H, qkv, qkv_sc);
+            s.read_packed(p + "self_attn.v_proj.weight", kvw, H, qkv, qkv_sc);
+        } else {
+            s.read(p + "self_attn.q_proj.weight", {qw, H}, qkv);
+            s.read(p + "self_attn.k_proj.weight", {kvw, H}, qkv);
+            s.read(p + "self_attn.v_proj.weight", {kvw, H}, qkv);
+        }
         w.qkv_rows = (int)(qw + 2 * kvw) + lora_total;
         int tcol = (int)(qw + 2 * kvw);
         for (int j = 0; j < 3; ++j) {
@@ -342,7 +418,7 @@ Model *load_model(const esp_config *cfg, const uint8_t *bytes, size_t len,
             w.lora_scale[j] = tscale[j];
             tcol += rank_sum[j];
         }
-        w.qkv = s.to_device(qkv);
+        w.qkv = dt_packed(m.wt) ? s.packed(qkv, qkv_sc, &w.qkv_s) : s.to_device(qkv);
         if (cfg->qkv_bias) {
             std::vector<uint8_t> b;
             s.read(p + "self_attn.q_proj.bias", {qw}, b, true);
@@ -351,7 +427,7 @@ Model *load_model(const esp_config *cfg, const uint8_t *bytes, size_t len,
             b.resize((size_t)w.qkv_rows * 4, 0);
             w.qkv_bias = (float *)s.to_device(b);
         }
-        w.o = s.tensor(p + "self_attn.o_proj.weight", {H, qw});
+        w.o = s.proj(p + "self_attn.o_proj.weight", H, qw, &w.o_s);
         if (cfg->output_bias) w.o_bias = (float *)s.tensor(p + "self_attn.o_proj.bias", {H}, true);
         if (cfg->qk_norm) {
             w.q_norm = (float *)s.tensor(p + "self_attn.q_norm.weight", {hd}, true);
@@ -359,9 +435,9 @@ Model *load_model(const esp_config *cfg, const uint8_t *bytes, size_t len,
         }
         if (!w.moe) {
             uint64_t F = m.F;
-            w.gate = s.tensor(p + "mlp.gate_proj.weight", {F, H});
-            w.up = s.tensor(p + "mlp.up_proj.weight", {F, H});
-            w.down = s.tensor(p + "mlp.down_proj.weight", {H, F});
+            w.gate = s.proj(p + "mlp.gate_proj.weight", F, H, &w.gate_s);
+            w.up = s.proj(p + "mlp.up_proj.weight", F, H, &w.up_s);
+            w.down = s.proj(p + "mlp.down_proj.weight", H, F, &w.down_s);
         } else {
             uint64_t E = m.E, Fe = m.Fe, Fs = m.Fs;
             w.router = s.tensor(p + "mlp.gate.weight", {E, H});
@@ -386,9 +462,10 @@ Model *load_model(const esp_config *cfg, const uint8_t *bytes, size_t len,
     m.embed = s.tensor("model.embed_tokens.weight", {(uint64_t)m.V, H});
     m.final_norm = (float *)s.tensor("model.norm.weight", {H}, true);
     if (s.has("lm_head.weight")) {
-        m.head = s.tensor("lm_head.weight", {(uint64_t)m.V, H});
+        m.head = s.proj("lm_head.weight", (uint64_t)m.V, H, &m.head_s);
     } else if (cfg->tie_word_embeddings) {
         m.head = m.embed;  // model.rs:167-169 tied head
+        m.ht = m.et;
     } else {
         fail(ESP_INVALID_WEIGHTS, "lm_head.weight missing but tie_word_embeddings is false");
     }
@@ -408,10 +485,27 @@ Model *synthetic_model(const esp_config *cfg, uint64_t seed, float std, uint32_t
     std::unique_ptr<Model> mp(new Model());
     Model &m = *mp;
     init_model_shape(m, *cfg);
+    check_packed(m, lora_rank && lora_mask ? 1 : 0);
     uint64_t tensor_id = 0;
-    auto rnd = [&](size_t n, float sd) {
-        void *p = m.alloc(n * dt_size(m.wt));
-        launch_fill_normal(m.wt, p, n, seed * 0x100000001B3ull + (++tensor_id), sd, nullptr);
+    auto rnd_dt = [&](size_t n, float sd, Dt dt) {
+        void *p = m.alloc(n * dt_size(dt));
+        launch_fill_normal(dt, p, n, seed * 0x100000001B3ull + (++tensor_id), sd, nullptr);
+        return p;
+    };
+    auto rnd = [&](size_t n, float sd) { return rnd_dt(n, sd, m.wt); };
+    // a projection: N(0, std) weights, quantized on the device for the
+    // packed formats (values, 256-byte aligned block scales)
+    DevMem tmp;
+    auto prj = [&](size_t rows, size_t cols, float sd, const float **sc) -> void * {
+        if (!dt_packed(m.wt)) return rnd(rows * cols, sd);
+        tmp.ensure(rows * cols * 4);
+        launch_fill_normal(DT_F32, tmp.p, rows * cols, seed * 0x100000001B3ull + (++tensor_id), sd,
+                           nullptr);
+        const size_t vb = (packed_value_bytes(m.wt, rows * cols) + 255) / 256 * 256;
+        char *p = (char *)m.alloc(vb + rows * cols / 32 * 4);
+        launch_quantize(m.wt, tmp.as<float>(), rows, cols, p, (float *)(p + vb), nullptr);
+        ESP_HIP(hipStreamSynchronize(nullptr));  // tmp is reused
+        *sc = (const float *)(p + vb);
         return p;
     };
     auto cst = [&](size_t n, float v) {
@@ -432,10 +526,14 @@ Model *synthetic_model(const esp_config *cfg, uint64_t seed, float std, uint32_t
         w.in_norm = cst(H, 1.f);
         w.post_norm = cst(H, 1.f);
         w.qkv_rows = m.qw + 2 * m.kvw + lora_total;
-        w.qkv = m.alloc((size_t)w.qkv_rows * H * dt_size(m.wt));
         size_t base_rows = m.qw + 2 * m.kvw;
-        launch_fill_normal(m.wt, w.qkv, base_rows * H, seed * 0x100000001B3ull + (++tensor_id), std,
-                           nullptr);
+        if (dt_packed(m.wt)) {
+            w.qkv = prj(base_rows, H, std, &w.qkv_s);
+        } else {
+            w.qkv = m.alloc((size_t)w.qkv_rows * H * dt_size(m.wt));
+            launch_fill_normal(m.wt, w.qkv, base_rows * H, seed * 0x100000001B3ull + (++tensor_id),
+                               std, nullptr);
+        }
         int tcol = (int)base_rows;
         for (int j = 0; j < 3; ++j) {
             if (!rank_t[j]) continue;
@@ -450,16 +548,16 @@ Model *synthetic_model(const esp_config *cfg, uint64_t seed, float std, uint32_t
             tcol += rank_t[j];
         }
         if (cfg->qkv_bias) w.qkv_bias = cst(w.qkv_rows, 0.f);
-        w.o = rnd((size_t)H * m.qw, std);
+        w.o = prj(H, m.qw, std, &w.o_s);
         if (cfg->output_bias) w.o_bias = cst(H, 0.f);
         if (cfg->qk_norm) {
             w.q_norm = cst(m.hd, 1.f);
             w.k_norm = cst(m.hd, 1.f);
         }
         if (!w.moe) {
-            w.gate = rnd((size_t)m.F * H, std);
-            w.up = rnd((size_t)m.F * H, std);
-            w.down = rnd((size_t)H * m.F, std);
+            w.gate = prj(m.F, H, std, &w.gate_s);
+            w.up = prj(m.F, H, std, &w.up_s);
+            w.down = prj(H, m.F, std, &w.down_s);
         } else {
             w.router = rnd((size_t)m.E * H, std);
             if (m.Fs) {
@@ -473,8 +571,13 @@ Model *synthetic_model(const esp_config *cfg, uint64_t seed, float std, uint32_t
             w.ex_down = rnd((size_t)m.E * H * m.Fe, std);
         }
     }
-    m.embed = rnd((size_t)m.V * H, std);
-    m.head = cfg->tie_word_embeddings ? m.embed : rnd((size_t)m.V * H, std);
+    m.embed = rnd_dt((size_t)m.V * H, std, m.et);
+    if (cfg->tie_word_embeddings) {
+        m.head = m.embed;
+        m.ht = m.et;
+    } else {
+        m.head = prj(m.V, H, std, &m.head_s);
+    }
     m.final_norm = cst(H, 1.f);
     stage_rope(m);
     ESP_HIP(hipDeviceSynchronize());
@@ -545,6 +648,21 @@ static void *lo_plane(Dt act, const DevMem &b, int rows, int cols) {
     return act == DT_SPLIT ? (void *)((uint16_t *)b.p + (size_t)rows * cols) : nullptr;
 }
 
+// GEMM weight operand: packed projections are dequantized to f32 first
+// (into slot 0 or 1 of kv.deq, in stream order before the GEMM reading it)
+// and multiplied by the f32 GEMM.
+static const void *gemm_w(Kv &kv, int slot, Dt wt, const void *w, const float *ws, size_t N,
+                          size_t K) {
+    if (!dt_packed(wt)) return w;
+    DevMem &d = kv.deq[slot];
+    d.ensure(N * K * 4);
+    launch_dequant(wt, w, ws, N * K, d.as<float>(), kv.stream);
+    return d.p;
+}
+static Dt gemm_dt(Dt wt) { return dt_packed(wt) ? DT_F32 : wt; }
+// element type of LoRA B rows (packed formats carry no LoRA)
+static Dt lora_dt(Dt wt) { return dt_packed(wt) ? DT_F32 : wt; }
+
 // Split-K decode attention of Mc rows (each row its own query position)
 // into kv.attn (f32), with the plan from attn_decode_splits.
 static void attn_decode_rows(Model &m, Kv &kv, const Rows &rows, int Mc, int l, const LayerW &w,
@@ -605,6 +723,7 @@ static void run_layer_decode(Model &m, Kv &kv, const Rows &rows, LayerW &w, int 
         }
         DecodeGemvArgs g{};
         g.w = w.qkv;
+        g.ws = w.qkv_s;
         g.x = kv.h.as<float>();
         g.gamma = w.in_norm;
         g.eps = m.cfg.rms_norm_eps;
@@ -638,6 +757,7 @@ static void run_layer_decode(Model &m, Kv &kv, const Rows &rows, LayerW &w, int 
         if (decode_gemv_ok(H)) {
             DecodeGemvArgs g{};
             g.w = w.qkv;
+            g.ws = w.qkv_s;
             g.x = kv.h.as<float>();
             g.gamma = w.in_norm;
             g.eps = m.cfg.rms_norm_eps;
@@ -685,7 +805,7 @@ static void run_layer_decode(Model &m, Kv &kv, const Rows &rows, LayerW &w, int 
         r.nkv = m.nkv;
         r.hd = m.hd;
         Prof p("rope_kv", s);
-        launch_rope_kv(m.wt, kv.dt, r, s);
+        launch_rope_kv(lora_dt(m.wt), kv.dt, r, s);
     }
     if (attn_decode_ok(m.hd, m.nq / m.nkv)) {
         Prof p("attention", s);
@@ -711,10 +831,12 @@ static void run_layer_decode(Model &m, Kv &kv, const Rows &rows, LayerW &w, int 
         Prof p("attention", s);
         launch_attention(kv.dt, a, s);
     }
-    auto resid = [&](const char *fam, const void *wt, const float *x, const float *bias, int N, int K) {
+    auto resid = [&](const char *fam, const void *wt, const float *ws, const float *x,
+                     const float *bias, int N, int K) {
         if (decode_gemv_ok(K)) {
             DecodeGemvArgs g{};
             g.w = wt;
+            g.ws = ws;
             g.x = x;
             g.bias = bias;
             g.y = kv.h.as<float>();
@@ -734,7 +856,7 @@ static void run_layer_decode(Model &m, Kv &kv, const Rows &rows, LayerW &w, int 
             launch_gemv(m.wt, GEMV_RESIDUAL, g, s);
         }
     };
-    resid("gemv_o", w.o, kv.attn.as<float>(), w.o_bias, H, m.qw);
+    resid("gemv_o", w.o, w.o_s, kv.attn.as<float>(), w.o_bias, H, m.qw);
     if (w.moe) {
         if (moe_decode_ok(m)) moe_decode(m, kv, w, s);
         else moe_block(m, kv, w, 1, s);
@@ -744,6 +866,8 @@ static void run_layer_decode(Model &m, Kv &kv, const Rows &rows, LayerW &w, int 
         DecodeGemvArgs g{};
         g.w = w.gate;
         g.w2 = w.up;
+        g.ws = w.gate_s;
+        g.ws2 = w.up_s;
         g.x = kv.h.as<float>();
         g.gamma = w.post_norm;
         g.eps = m.cfg.rms_norm_eps;
@@ -765,7 +889,7 @@ static void run_layer_decode(Model &m, Kv &kv, const Rows &rows, LayerW &w, int 
         Prof p("gemv_mlp", s);
         launch_gemv(m.wt, GEMV_SWIGLU, g, s);
     }
-    resid("gemv_down", w.down, kv.act.as<float>(), nullptr, H, m.F);
+    resid("gemv_down", w.down, w.down_s, kv.act.as<float>(), nullptr, H, m.F);
 }
 
 // One pass of `Mc` rows (already on the device at `rows`) through all layers.
@@ -819,7 +943,7 @@ static void run_layers(Model &m, Kv &kv, const Rows &rows, int Mc, int max_t, in
             g.ws_bytes = kv.gemm_ws.bytes;
             g.a = kv.xn.p;
             g.a_lo = lo_plane(act, kv.xn, Mc, H);
-            g.w = w.qkv;
+            g.w = gemm_w(kv, 0, m.wt, w.qkv, w.qkv_s, w.qkv_rows, H);
             g.bias = w.qkv_bias;
             g.c = kv.qkv.p;
             g.M = Mc;
@@ -827,7 +951,7 @@ static void run_layers(Model &m, Kv &kv, const Rows &rows, int Mc, int max_t, in
             g.K = H;
             g.ldc = w.qkv_rows;
             Prof p("gemm_qkv", s);
-            launch_gemm(m.wt, GEMM_STORE, g, s);
+            launch_gemm(gemm_dt(m.wt), GEMM_STORE, g, s);
         }
         {
             RopeKvArgs r{};
@@ -855,7 +979,7 @@ static void run_layers(Model &m, Kv &kv, const Rows &rows, int Mc, int max_t, in
             r.nkv = m.nkv;
             r.hd = m.hd;
             Prof p("rope_kv", s);
-            launch_rope_kv(m.wt, kv.dt, r, s);
+            launch_rope_kv(lora_dt(m.wt), kv.dt, r, s);
         }
         bool seg_flash = segs && !segs->empty() && m.wt == DT_BF16 && flash_ok(m.hd);
         for (size_t i = 0; seg_flash && i < segs->size(); ++i) seg_flash = (*segs)[i].len >= 16;
@@ -942,7 +1066,7 @@ static void run_layers(Model &m, Kv &kv, const Rows &rows, int Mc, int max_t, in
             g.ws_bytes = kv.gemm_ws.bytes;
             g.a = kv.attn.p;
             g.a_lo = lo_plane(act, kv.attn, Mc, m.qw);
-            g.w = w.o;
+            g.w = gemm_w(kv, 0, m.wt, w.o, w.o_s, H, m.qw);
             g.bias = w.o_bias;
             g.c = kv.h.p;
             g.M = Mc;
@@ -950,7 +1074,7 @@ static void run_layers(Model &m, Kv &kv, const Rows &rows, int Mc, int max_t, in
             g.K = m.qw;
             g.ldc = H;
             Prof p("gemm_o", s);
-            launch_gemm(m.wt, GEMM_RESIDUAL, g, s);
+            launch_gemm(gemm_dt(m.wt), GEMM_RESIDUAL, g, s);
         }
         // ---- MLP block (layer.rs:147-151)
         if (w.moe) {
@@ -988,8 +1112,8 @@ static void run_layers(Model &m, Kv &kv, const Rows &rows, int Mc, int max_t, in
             g.ws_bytes = kv.gemm_ws.bytes;
             g.a = kv.xn.p;
             g.a_lo = lo_plane(act, kv.xn, Mc, H);
-            g.w = w.gate;
-            g.w2 = w.up;
+            g.w = gemm_w(kv, 0, m.wt, w.gate, w.gate_s, m.F, H);
+            g.w2 = gemm_w(kv, 1, m.wt, w.up, w.up_s, m.F, H);
             g.c = kv.act.p;
             g.c_lo = lo_plane(act, kv.act, Mc, m.F);
             g.M = Mc;
@@ -998,21 +1122,21 @@ static void run_layers(Model &m, Kv &kv, const Rows &rows, int Mc, int max_t, in
             g.ldc = m.F;
             {
                 Prof p("gemm_mlp", s);
-                launch_gemm(m.wt, GEMM_SWIGLU, g, s);
+                launch_gemm(gemm_dt(m.wt), GEMM_SWIGLU, g, s);
             }
             GemmArgs d{};
             d.ws = kv.gemm_ws.as<float>();
             d.ws_bytes = kv.gemm_ws.bytes;
             d.a = kv.act.p;
             d.a_lo = lo_plane(act, kv.act, Mc, m.F);
-            d.w = w.down;
+            d.w = gemm_w(kv, 0, m.wt, w.down, w.down_s, H, m.F);
             d.c = kv.h.p;
             d.M = Mc;
             d.N = H;
             d.K = m.F;
             d.ldc = H;
             Prof p("gemm_down", s);
-            launch_gemm(m.wt, GEMM_RESIDUAL, d, s);
+            launch_gemm(gemm_dt(m.wt), GEMM_RESIDUAL, d, s);
         }
     }
 }
@@ -1044,6 +1168,7 @@ static void run_head(Model &m, Kv &kv, int n_seqs, const float *h_src, const int
         int32_t *t = kv.tickets.as<int32_t>();
         DecodeGemvArgs g{};
         g.w = m.head;
+        g.ws = m.head_s;
         g.x = h_src;
         g.gamma = m.final_norm;
         g.eps = m.cfg.rms_norm_eps;
@@ -1056,7 +1181,7 @@ static void run_head(Model &m, Kv &kv, int n_seqs, const float *h_src, const int
         g.picked = (uint32_t *)(t + 4096 + 8 + 2 * DG_MAX_PART);
         g.gen = gen;
         Prof p("gemv_head", s);
-        launch_decode_gemv(m.wt, DG_HEAD, g, s);
+        launch_decode_gemv(m.ht, DG_HEAD, g, s);
         return;
     }
     if (n_seqs == 1) {
@@ -1069,27 +1194,27 @@ static void run_head(Model &m, Kv &kv, int n_seqs, const float *h_src, const int
         g.N = m.V;
         g.K = m.H;
         Prof p("gemv", s);
-        launch_gemv(m.wt, GEMV_STORE, g, s);
+        launch_gemv(m.ht, GEMV_STORE, g, s);
         return;
     }
     {
         Prof p("rmsnorm", s);
         launch_rmsnorm(h_src, m.final_norm, m.cfg.rms_norm_eps, n_seqs, m.H,
-                       m.wt == DT_BF16 ? DT_SPLIT : DT_F32, kv.xn.p, row_index, s);
+                       m.ht == DT_BF16 ? DT_SPLIT : DT_F32, kv.xn.p, row_index, s);
     }
     GemmArgs g{};
     g.ws = kv.gemm_ws.as<float>();
     g.ws_bytes = kv.gemm_ws.bytes;
     g.a = kv.xn.p;
-    g.a_lo = lo_plane(m.wt == DT_BF16 ? DT_SPLIT : DT_F32, kv.xn, n_seqs, m.H);
-    g.w = m.head;
+    g.a_lo = lo_plane(m.ht == DT_BF16 ? DT_SPLIT : DT_F32, kv.xn, n_seqs, m.H);
+    g.w = gemm_w(kv, 0, m.ht, m.head, m.head_s, m.V, m.H);
     g.c = kv.logits.p;
     g.M = n_seqs;
     g.N = m.V;
     g.K = m.H;
     g.ldc = m.V;
     Prof p("gemm", s);
-    launch_gemm(m.wt, GEMM_STORE, g, s);
+    launch_gemm(gemm_dt(m.ht), GEMM_STORE, g, s);
 }
 
 void forward(Model &m, Kv &kv, int n_seqs, const uint32_t *seqs, const uint32_t *lens,
@@ -1150,7 +1275,7 @@ void forward(Model &m, Kv &kv, int n_seqs, const uint32_t *seqs, const uint32_t 
         }
         {
             Prof p("embed", s);
-            launch_embed(m.wt, m.embed, rows.ids, Mc, m.H, kv.h.as<float>(), s);
+            launch_embed(m.et, m.embed, rows.ids, Mc, m.H, kv.h.as<float>(), s);
         }
         if (n_seqs == 1) {
             run_layers(m, kv, rows, Mc, max_t, (int)seqs[0], rpos[c0]);
@@ -1308,7 +1433,7 @@ void decode_step_dev(Model &m, Kv &kv, int seq, int max_t, int32_t *gen) {
     }
     {
         Prof p("embed", s);
-        launch_embed(m.wt, m.embed, rows.ids, 1, m.H, kv.h.as<float>(), s);
+        launch_embed(m.et, m.embed, rows.ids, 1, m.H, kv.h.as<float>(), s);
     }
     run_layers(m, kv, rows, 1, max_t);
     if (decode_gemv_ok(m.H)) {

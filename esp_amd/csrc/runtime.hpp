@@ -44,6 +44,9 @@ struct LayerW {
     void *qkv = nullptr;        // [qkv_rows, H]: q | k | v | LoRA-A rows (q, k, v targets)
     float *qkv_bias = nullptr;  // [qkv_rows] or null
     int qkv_rows = 0;
+    // packed formats: block scales [rows, K/32] of qkv, o, gate, up, down
+    const float *qkv_s = nullptr, *o_s = nullptr, *gate_s = nullptr, *up_s = nullptr,
+                *down_s = nullptr;
     void *o = nullptr;          // [H, qw]
     float *o_bias = nullptr;
     float *q_norm = nullptr, *k_norm = nullptr;
@@ -63,7 +66,10 @@ struct LayerW {
 
 struct Model {
     esp_config cfg{};
-    Dt wt = DT_F32;  // weight (and KV) element type
+    Dt wt = DT_F32;  // projection weight element type
+    Dt et = DT_F32;  // embedding element type (and the head's when tied)
+    Dt ht = DT_F32;  // head element type
+    const float *head_s = nullptr;  // packed head: block scales
     int H = 0, L = 0, nq = 0, nkv = 0, hd = 0, F = 0, V = 0, qw = 0, kvw = 0;
     int E = 0, topk = 0, Fe = 0, Fs = 0;
     bool norm_topk = false;
@@ -98,6 +104,7 @@ struct Kv {
     DevMem rows_dev;   // ids | row_seq | row_pos | last_row  (int32)
     DevMem h, xn, qkv, q, attn, act, part, last_h, logits, pick_scratch, pick_io;
     DevMem gemm_ws;  // split-K partial sums of the prefill GEMMs
+    DevMem deq[2];   // packed formats: f32 weights of the GEMMs in flight
     DevMem tickets;  // zeroed counters for last-block merges (attention, head argmax)
     DevMem moe_logits, moe_sel, moe_w, moe_slot, moe_offs, moe_perm, moe_x, moe_y, moe_ys, moe_sg,
         moe_act;

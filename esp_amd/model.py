@@ -17,7 +17,10 @@ from .config import DecoderConfig
 from .errors import InvalidRequest
 from .sample import Sampler
 
-FORMATS = {"f32": _lib.ESP_FORMAT_F32, "bf16": _lib.ESP_FORMAT_BF16}
+# weight_format.rs:34-49 names (short and versioned)
+FORMATS = {"f32": _lib.ESP_FORMAT_F32, "bf16": _lib.ESP_FORMAT_BF16,
+           "q8-block32": _lib.ESP_FORMAT_Q8, "q8-k32-f32-scale-f16-shared-v1": _lib.ESP_FORMAT_Q8,
+           "q4-block32": _lib.ESP_FORMAT_Q4, "q4-k32-f32-scale-f16-shared-v1": _lib.ESP_FORMAT_Q4}
 TARGET_BITS = {"q_proj": 1, "k_proj": 2, "v_proj": 4, "o_proj": 8}
 
 

@@ -42,8 +42,19 @@ typedef enum esp_status {
  * F32 widens every checkpoint tensor to f32 (the reference's default
  * corridor); BF16 keeps bf16 weights in HBM, bf16 MFMA inputs, f32
  * accumulation and an f32 residual stream; its artifacts must be BF16
- * (weight_format.rs:283-291). */
-typedef enum esp_format { ESP_FORMAT_F32 = 0, ESP_FORMAT_BF16 = 1 } esp_format;
+ * (weight_format.rs:283-291). Q8_BLOCK32 / Q4_BLOCK32
+ * ("q8-k32-f32-scale-f16-shared-v1" / "q4-..."): every projection is a U8
+ * tensor of packed signed 8- or 4-bit values along K plus one f32 scale per
+ * 32 inputs (weight_format.rs:138-223, 225-273), every other tensor F16;
+ * decode GEMVs read the packed bytes and dequantize in registers,
+ * activations stay f32. Dense llama-family layers only (no routed experts,
+ * no unmerged LoRA: ESP_UNSUPPORTED). */
+typedef enum esp_format {
+    ESP_FORMAT_F32 = 0,
+    ESP_FORMAT_BF16 = 1,
+    ESP_FORMAT_Q8_BLOCK32 = 2,
+    ESP_FORMAT_Q4_BLOCK32 = 3
+} esp_format;
 
 typedef enum esp_rope_scaling {
     ESP_ROPE_NONE = 0,
