@@ -208,6 +208,54 @@ def c3_bench(steps: int) -> dict:
     return res
 
 
+def packed_decode_bytes(cfg, ctx: int, bits: int) -> dict:
+    """Algorithmic HBM bytes of one batch-1 decode step with packed
+    projections (weight_format.rs:138-223): bits/8 bytes per weight plus one
+    f32 scale per 32, the head packed too (untied), the K/V cache (f32)."""
+    H, L, F, V = cfg.hidden_size, cfg.num_hidden_layers, cfg.intermediate_size, cfg.vocab_size
+    qw, kvw = cfg.query_width(), cfg.kv_heads() * cfg.head_dim()
+    per = bits / 8 + 4 / 32
+    layer_w = (H * (qw + 2 * kvw) + H * qw + 3 * H * F) * per
+    head_w = V * H * per
+    kv = 2 * L * kvw * ctx * 4
+    return {"gemv_weights": int(L * layer_w + head_w), "kv": kv,
+            "total": int(L * layer_w + head_w + kv)}
+
+
+def c3_packed_bench(bits: int) -> dict:
+    """The C3 shape (Llama-3-8B, no LoRA) with packed q8 / q4 block-32
+    projections: batch-1 greedy decode at ~4.1k context. Decode time per
+    token is the difference of two device loops (16 and 80 new tokens) over
+    the same 4064-token prompt, so the prompt's prefill cancels."""
+    from esp_amd import DecoderModel
+    from tests.synth import uniform_ids
+    cfg = c3_config()
+    fmt = "q8-block32" if bits == 8 else "q4-block32"
+    model = DecoderModel.synthetic(cfg, seed=4321, std=0.02, fmt=fmt)
+    prompt = uniform_ids(7, 4064, cfg.vocab_size)
+    kv = model.new_cache(1, 4064 + 80)
+
+    def gen(n):
+        t0 = time.perf_counter()
+        out = model.generate_greedy_device(kv, prompt, n, eos=[])
+        assert len(out) == n
+        return time.perf_counter() - t0
+
+    gen(16)
+    t16, t80 = gen(16), gen(80)
+    t_dec = (t80 - t16) / 64
+    db = packed_decode_bytes(cfg, 4064 + 48, bits)
+    res = {"workload": f"C3 shape (Llama-3-8B, no LoRA) with {fmt} projections; batch-1 greedy "
+                       "decode at 4080-4144 context",
+           "decode_tokens_per_s": round(1.0 / t_dec, 2),
+           "decode_ms_per_token": round(t_dec * 1e3, 4),
+           "decode_hbm_frac": round(db["total"] / t_dec / 1e9 / HBM_PEAK_GBS, 4),
+           "decode_bytes_per_token": db["total"],
+           "weight_bytes": model.weight_bytes()}
+    model.close()
+    return res
+
+
 def c4_config(max_pos=4096):
     from esp_amd.config import DecoderConfig
     return DecoderConfig.mixtral_style(vocab_size=32000, hidden_size=4096, intermediate_size=14336,
@@ -486,6 +534,8 @@ def main():
     ap.add_argument("--no-c5", action="store_true")
     ap.add_argument("--only-c5", action="store_true")
     ap.add_argument("--no-c5g", action="store_true")
+    ap.add_argument("--no-packed", action="store_true")
+    ap.add_argument("--only-packed", action="store_true")
     ap.add_argument("--only-c5g", action="store_true")
     ap.add_argument("--traffic", action="store_true",
                     help="run only the workload of the HBM-traffic counter passes")
@@ -509,6 +559,9 @@ def main():
         return
     if args.only_c5:
         print(json.dumps({"c5": c5_bench(16)}), flush=True)
+        return
+    if args.only_packed:
+        print(json.dumps({"c3_q8": c3_packed_bench(8), "c3_q4": c3_packed_bench(4)}), flush=True)
         return
     if args.only_c5g:
         print(json.dumps({"c5_grammar": c5_grammar_bench(32)}), flush=True)
@@ -617,6 +670,10 @@ def main():
     if not args.no_c5g:
         result["c5_grammar"] = c5_grammar_bench(32)
         print(f"c5_grammar: {result['c5_grammar']}", file=sys.stderr, flush=True)
+    if not args.no_packed:
+        for bits in (8, 4):
+            result[f"c3_q{bits}"] = c3_packed_bench(bits)
+            print(f"c3_q{bits}: {result[f'c3_q{bits}']}", file=sys.stderr, flush=True)
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(cfg, int(avg_ctx))
     print(json.dumps(result), flush=True)

@@ -48,6 +48,7 @@ struct DecodeGemvArgs {
 };
 
 bool decode_gemv_ok(int K);
+bool decode_gemv_packed_ok(Dt wt, int K);
 void launch_decode_gemv(Dt wt, int epi, const DecodeGemvArgs &a, hipStream_t s);
 
 struct AttnDecodeArgs {

@@ -13,6 +13,7 @@ constexpr int DG_MAXC = 8;  // max 8-element chunks per lane per row (K <= 4*64*
 
 typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
 
 // Cross-block hand-off without flushing L2: partials are written with
 // agent-scope (write-through) stores, the writer waits for its stores to
@@ -46,13 +47,12 @@ template <typename WT> struct WPacked { static constexpr bool v = false; };
 template <> struct WPacked<q8_t> { static constexpr bool v = true; };
 template <> struct WPacked<q4_t> { static constexpr bool v = true; };
 
-typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
-
-// Chunk<WT>: 8 consecutive weights of one row and their dot product with 8
-// f32 inputs. load_at(base, e, scales) reads weights e .. e+7 of a
-// row-major matrix (e a multiple of 8; scales used by packed formats).
+// Chunk<WT>: W consecutive weights of one row and their dot product with W
+// f32 inputs. load_at(base, e, scales) reads weights e .. e+W-1 of a
+// row-major matrix (e a multiple of W; scales used by packed formats).
 template <typename WT> struct Chunk;
 template <> struct Chunk<uint16_t> {  // 8 bf16 = 16 bytes
+    static constexpr int W = 8;  // weights per chunk
     u32x4_t v;
     __device__ __forceinline__ void load(const uint16_t *p) {
         v = __builtin_nontemporal_load((const u32x4_t *)p);
@@ -72,8 +72,10 @@ template <> struct Chunk<uint16_t> {  // 8 bf16 = 16 bytes
         s += __uint_as_float(v.w & 0xffff0000u) * x[7];
         return s;
     }
+    __device__ __forceinline__ float dot(const float *x, float) const { return dot(x); }
 };
 template <> struct Chunk<float> {  // 8 f32 = 2 x 16 bytes
+    static constexpr int W = 8;
     f32x4_t a, b;
     __device__ __forceinline__ void load(const float *p) {
         a = __builtin_nontemporal_load((const f32x4_t *)p);
@@ -94,36 +96,61 @@ template <> struct Chunk<float> {  // 8 f32 = 2 x 16 bytes
         s += b.w * x[7];
         return s;
     }
+    __device__ __forceinline__ float dot(const float *x, float) const { return dot(x); }
 };
 
-template <> struct Chunk<q8_t> {  // 8 x int8 = 8 bytes + the block scale
+// Packed chunks hold 16 weights (16 bytes of q8, 8 of q4) inside one
+// 32-input scale block. The signed values are biased to unsigned bytes / nibbles
+// (xor 0x80 / 0x8) so each converts to f32 in one instruction; the bias
+// comes back once per chunk through xsum, the sum of the chunk's inputs:
+// sum q x = sum (q + b) x - b * xsum.
+template <> struct Chunk<q8_t> {
+    static constexpr int W = 16;
+    u32x4_t v;
+    float sc;
+    __device__ __forceinline__ void load_at(const void *base, size_t e, const float *scales) {
+        v = __builtin_nontemporal_load((const u32x4_t *)((const int8_t *)base + e));
+        sc = scales[e >> 5];
+    }
+    __device__ __forceinline__ float dot(const float *x, float xsum) const {
+        float s = 0.f;
+        const unsigned d[4] = {v.x ^ 0x80808080u, v.y ^ 0x80808080u, v.z ^ 0x80808080u,
+                               v.w ^ 0x80808080u};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            s += (float)(d[j] & 0xff) * x[4 * j];
+            s += (float)((d[j] >> 8) & 0xff) * x[4 * j + 1];
+            s += (float)((d[j] >> 16) & 0xff) * x[4 * j + 2];
+            s += (float)(d[j] >> 24) * x[4 * j + 3];
+        }
+        return (s - 128.f * xsum) * sc;
+    }
+};
+template <> struct Chunk<q4_t> {  // 16 q4 weights = 8 bytes (all 64 lanes busy at K 4096)
+    static constexpr int W = 16;
     u32x2_t v;
     float sc;
     __device__ __forceinline__ void load_at(const void *base, size_t e, const float *scales) {
-        v = __builtin_nontemporal_load((const u32x2_t *)((const int8_t *)base + e));
+        v = __builtin_nontemporal_load((const u32x2_t *)((const uint8_t *)base + (e >> 1)));
         sc = scales[e >> 5];
     }
-    __device__ __forceinline__ float dot(const float *x) const {
+    __device__ __forceinline__ float dot(const float *x, float xsum) const {
         float s = 0.f;
+        const unsigned d[2] = {v.x ^ 0x88888888u, v.y ^ 0x88888888u};
 #pragma unroll
-        for (int i = 0; i < 4; ++i) s += (float)((int)(v.x << (24 - 8 * i)) >> 24) * x[i];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) s += (float)((int)(v.y << (24 - 8 * i)) >> 24) * x[4 + i];
-        return s * sc;
-    }
-};
-template <> struct Chunk<q4_t> {  // 8 x int4 = 4 bytes + the block scale
-    unsigned int v;
-    float sc;
-    __device__ __forceinline__ void load_at(const void *base, size_t e, const float *scales) {
-        v = __builtin_nontemporal_load((const unsigned int *)((const uint8_t *)base + (e >> 1)));
-        sc = scales[e >> 5];
-    }
-    __device__ __forceinline__ float dot(const float *x) const {
-        float s = 0.f;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) s += (float)((int)(v << (28 - 4 * i)) >> 28) * x[i];
-        return s * sc;
+        for (int j = 0; j < 2; ++j) {
+            const unsigned lo = d[j] & 0x0f0f0f0fu, hi = (d[j] >> 4) & 0x0f0f0f0fu;
+            // byte b of dword j holds weights 8j + 2b (low) and 8j + 2b + 1 (high)
+            s += (float)(lo & 0xff) * x[8 * j];
+            s += (float)(hi & 0xff) * x[8 * j + 1];
+            s += (float)((lo >> 8) & 0xff) * x[8 * j + 2];
+            s += (float)((hi >> 8) & 0xff) * x[8 * j + 3];
+            s += (float)((lo >> 16) & 0xff) * x[8 * j + 4];
+            s += (float)((hi >> 16) & 0xff) * x[8 * j + 5];
+            s += (float)(lo >> 24) * x[8 * j + 6];
+            s += (float)(hi >> 24) * x[8 * j + 7];
+        }
+        return (s - 8.f * xsum) * sc;
     }
 };
 

@@ -42,7 +42,8 @@ __global__ void __launch_bounds__(DG_THREADS) decode_gemv_k(DecodeGemvArgs a) {
     __shared__ int best_i[DG_WAVES];
     __shared__ int last;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int K = a.K, kq = K / DG_WAVES, nch = kq / 8;  // chunks in this wave's quarter
+    constexpr int CW = Chunk<WT>::W;  // weights per chunk
+    const int K = a.K, kq = K / DG_WAVES, nch = kq / CW;  // chunks in this wave's quarter
     const int k0 = wave * kq;
     const void *W = a.w;
     const void *W2 = a.w2;
@@ -88,25 +89,30 @@ __global__ void __launch_bounds__(DG_THREADS) decode_gemv_k(DecodeGemvArgs a) {
             const int ch = lane + 64 * c;
             if (ch < nch) {
 #pragma unroll
-                for (int r = 0; r < R; ++r) wc[r][c].load_at(rb[r], ro[r] + k0 + ch * 8, rs[r]);
+                for (int r = 0; r < R; ++r) wc[r][c].load_at(rb[r], ro[r] + k0 + ch * CW, rs[r]);
             }
         }
     };
     if ((int)blockIdx.x * RB < units) load_rows(blockIdx.x * RB);
 
     // ---- x slice in registers (+ fused RMSNorm)
-    float xr[NCH][8];
+    float xr[NCH][CW];
     float ss = 0.f;
 #pragma unroll
     for (int c = 0; c < NCH; ++c) {
         int ch = lane + 64 * c;
         if (ch < nch) {
-            const float *xp = a.x + k0 + ch * 8;
-            f32x4_t p0 = *(const f32x4_t *)xp, p1 = *(const f32x4_t *)(xp + 4);
-            xr[c][0] = p0.x; xr[c][1] = p0.y; xr[c][2] = p0.z; xr[c][3] = p0.w;
-            xr[c][4] = p1.x; xr[c][5] = p1.y; xr[c][6] = p1.z; xr[c][7] = p1.w;
+            const float *xp = a.x + k0 + ch * CW;
 #pragma unroll
-            for (int i = 0; i < 8; ++i) ss += xr[c][i] * xr[c][i];
+            for (int q = 0; q < CW / 4; ++q) {
+                const f32x4_t p = *(const f32x4_t *)(xp + 4 * q);
+                xr[c][4 * q] = p.x;
+                xr[c][4 * q + 1] = p.y;
+                xr[c][4 * q + 2] = p.z;
+                xr[c][4 * q + 3] = p.w;
+            }
+#pragma unroll
+            for (int i = 0; i < CW; ++i) ss += xr[c][i] * xr[c][i];
         }
     }
     if (a.gamma) {
@@ -121,10 +127,20 @@ __global__ void __launch_bounds__(DG_THREADS) decode_gemv_k(DecodeGemvArgs a) {
         for (int c = 0; c < NCH; ++c) {
             int ch = lane + 64 * c;
             if (ch < nch) {
-                const float *g = a.gamma + k0 + ch * 8;
+                const float *g = a.gamma + k0 + ch * CW;
 #pragma unroll
-                for (int i = 0; i < 8; ++i) xr[c][i] = (xr[c][i] / rms) * g[i];
+                for (int i = 0; i < CW; ++i) xr[c][i] = (xr[c][i] / rms) * g[i];
             }
+        }
+    }
+    // per-chunk input sums (the packed formats' bias term; unused otherwise)
+    float xs[NCH];
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+        xs[c] = 0.f;
+        if (WPacked<WT>::v) {
+#pragma unroll
+            for (int i = 0; i < CW; ++i) xs[c] += xr[c][i];
         }
     }
     // ---- stream rows; each wave parks its sums in LDS (no barrier)
@@ -138,7 +154,7 @@ __global__ void __launch_bounds__(DG_THREADS) decode_gemv_k(DecodeGemvArgs a) {
             int ch = lane + 64 * c;
             if (ch < nch) {
 #pragma unroll
-                for (int r = 0; r < R; ++r) acc[r] += wc[r][c].dot(xr[c]);
+                for (int r = 0; r < R; ++r) acc[r] += wc[r][c].dot(xr[c], xs[c]);
             }
         }
         if (u0 + gridDim.x * RB < units) load_rows(u0 + gridDim.x * RB);
@@ -337,7 +353,7 @@ template <typename WT, int EPI>
 static void dg_launch(const DecodeGemvArgs &a, int cus, hipStream_t s) {
     // Measured on MI355X: two rows per block (more blocks in flight) beats
     // one or four rows per block at the projection shapes.
-    const int nch = (a.K / DG_WAVES / 8 + 63) / 64;  // chunks per lane and row
+    const int nch = (a.K / DG_WAVES / Chunk<WT>::W + 63) / 64;  // chunks per lane and row
     // the head over a short K (one chunk per lane) streams best with four
     // rows per block (measured at H 2048: 90.6 vs 97.4 us for 128256 rows)
     if (EPI == DG_HEAD && nch <= 1) {
@@ -352,8 +368,15 @@ static void dg_launch(const DecodeGemvArgs &a, int cus, hipStream_t s) {
 
 bool decode_gemv_ok(int K) { return K % 32 == 0 && K / 32 <= 64 * DG_MAXC; }
 
+// Packed formats read chunks of 16 weights: each wave's quarter of K must
+// hold whole chunks.
+bool decode_gemv_packed_ok(Dt wt, int K) {
+    return decode_gemv_ok(K) && (!dt_packed(wt) || K % (DG_WAVES * 16) == 0);
+}
+
 void launch_decode_gemv(Dt wt, int epi, const DecodeGemvArgs &a, hipStream_t s) {
-    if (!decode_gemv_ok(a.K)) fail(ESP_BACKEND, "decode_gemv: unsupported width");
+    if (!decode_gemv_ok(a.K) || (dt_packed(wt) && !decode_gemv_packed_ok(wt, a.K)))
+        fail(ESP_BACKEND, "decode_gemv: unsupported width");
     static int cus = 0;
     if (!cus) {
         int dev = 0;

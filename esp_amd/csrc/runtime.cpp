@@ -137,10 +137,15 @@ static void check_packed(const Model &m, uint32_t n_adapters) {
                                    : "weight format q4-k32-f32-scale-f16-shared-v1";
     if (m.E) fail(ESP_UNSUPPORTED, std::string(id) + ": routed experts are not implemented");
     if (n_adapters) fail(ESP_UNSUPPORTED, std::string(id) + ": unmerged LoRA is not implemented");
-    for (int k : {m.H, m.qw, m.F})
-        if (k % 32 || !decode_gemv_ok(k))
+    for (int k : {m.H, m.qw, m.F}) {
+        if (k % 32)
             fail(ESP_INVALID_WEIGHTS, "weight format: packed projection input width " +
                                           std::to_string(k) + " must be divisible by 32");
+        if (!decode_gemv_packed_ok(m.wt, k))
+            fail(ESP_UNSUPPORTED, std::string(id) + ": projection input width " +
+                                      std::to_string(k) + " (the decode kernels need a multiple of 64, "
+                                      "at most 16384)");
+    }
 }
 
 static void upload(void *dst, const void *src, size_t bytes) {
