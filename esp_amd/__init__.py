@@ -13,3 +13,5 @@ from .generate import (TokenPicker, generate_constrained, generate_ids,  # noqa:
                        generate_ids_with)
 from .sample import Sampler  # noqa: F401
 from .constraint import Constraint, Vocabulary  # noqa: F401
+from .streaming import (ArtifactSource, FnSource, LayerSource, StreamingOptions,  # noqa: F401
+                        cache_verified_layers, split_checkpoint, with_expert_reader)

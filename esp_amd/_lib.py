@@ -47,6 +47,28 @@ class EspSampler(C.Structure):
     _fields_ = [("temperature", C.c_float), ("top_p", C.c_float), ("state", C.c_uint64)]
 
 
+class EspStreamingOptions(C.Structure):
+    _fields_ = [("query_chunk", C.c_uint64), ("max_layer_bytes", C.c_uint64),
+                ("max_shared_bytes", C.c_uint64)]
+
+
+# esp_layer_read_fn(user, index, limit, dst, cap, *len) -> esp_status
+LAYER_READ_FN = C.CFUNCTYPE(C.c_int, C.c_void_p, C.c_uint32, C.c_uint64, C.c_void_p,
+                            C.c_uint64, C.POINTER(C.c_uint64))
+
+
+class EspLayerSource(C.Structure):
+    _fields_ = [("read_layer", LAYER_READ_FN), ("user", C.c_void_p)]
+
+
+class EspStreamingStats(C.Structure):
+    _fields_ = [("streamed", C.c_uint32), ("device_cache", C.c_uint32),
+                ("layer_reads", C.c_uint64), ("encoded_bytes_read", C.c_uint64),
+                ("largest_encoded_layer", C.c_uint64), ("cache_hits", C.c_uint64),
+                ("cache_misses", C.c_uint64), ("retained_payload_bytes", C.c_uint64),
+                ("payload_budget_bytes", C.c_uint64), ("cached_layers", C.c_uint64)]
+
+
 _lib = None
 
 
@@ -87,6 +109,11 @@ def load():
         "esp_constraint_complete": (C.c_int, [vp, P(C.c_uint8)]),
         "esp_constraint_forced_bytes": (C.c_int, [vp, P(C.c_uint8), u32, P(u32)]),
         "esp_constraint_mask": (C.c_int, [vp, vp, P(u32), P(u32)]),
+        "esp_model_load_streamed": (C.c_int, [P(EspConfig), vp, C.c_size_t, P(EspLayerSource),
+                                              P(EspStreamingOptions), P(vp)]),
+        "esp_model_layer_cache": (C.c_int, [vp, C.c_uint64]),
+        "esp_model_resident_layers": (C.c_int, [vp]),
+        "esp_model_streaming_stats": (C.c_int, [vp, P(EspStreamingStats)]),
         "esp_profile_enable": (C.c_int, [C.c_char_p, C.c_int]),
         "esp_profile_read": (C.c_int, [C.c_char_p, P(C.c_uint64), P(C.c_double)]),
     }
@@ -104,8 +131,9 @@ EXPORTED = ["esp_last_error", "esp_version", "esp_model_load", "esp_model_create
             "esp_forward_batch", "esp_pick", "esp_pick_constrained", "esp_generate_greedy",
             "esp_vocab_create", "esp_vocab_destroy", "esp_constraint_create",
             "esp_constraint_destroy", "esp_constraint_accept", "esp_constraint_complete",
-            "esp_constraint_forced_bytes", "esp_constraint_mask", "esp_profile_enable",
-            "esp_profile_read"]
+            "esp_constraint_forced_bytes", "esp_constraint_mask", "esp_model_load_streamed",
+            "esp_model_layer_cache", "esp_model_resident_layers", "esp_model_streaming_stats",
+            "esp_profile_enable", "esp_profile_read"]
 
 
 def check(status: int) -> None:

@@ -11,6 +11,7 @@
 #include "profile.hpp"
 #include "constraint.hpp"
 #include "runtime.hpp"
+#include "streaming.hpp"
 
 namespace esp {
 Model *load_model(const esp_config *cfg, const uint8_t *bytes, size_t len,
@@ -78,6 +79,55 @@ esp_status esp_model_create_synthetic(const esp_config *config, uint64_t seed, f
         *out = nullptr;
         *out = (esp_model *)synthetic_model(config, seed, std, lora_rank, lora_mask, lora_a_std,
                                             lora_b_std, lora_scale);
+    });
+}
+
+esp_status esp_model_load_streamed(const esp_config *config, const uint8_t *shared,
+                                   size_t shared_len, const esp_layer_source *source,
+                                   const esp_streaming_options *options, esp_model **out) {
+    return guard([&] {
+        if (!out) fail(ESP_INVALID_REQUEST, "null output handle");
+        *out = nullptr;
+        *out = (esp_model *)load_streamed_model(config, shared, shared_len, source, options);
+    });
+}
+
+esp_status esp_model_layer_cache(esp_model *model, uint64_t budget) {
+    return guard([&] {
+        if (!model) fail(ESP_MODEL_NOT_LOADED, "model not loaded");
+        Model &m = *(Model *)model;
+        if (!m.st) {
+            if (budget == 0) return;  // model.rs:337-340
+            fail(ESP_INVALID_CONFIG, "device layer caching requires a dense f32 indexed model");
+        }
+        std::lock_guard<std::recursive_mutex> lk(m.st->mu);
+        stream_set_cache(m, budget);
+    });
+}
+
+esp_status esp_model_resident_layers(esp_model *model) {
+    return guard([&] {
+        if (!model) fail(ESP_MODEL_NOT_LOADED, "model not loaded");
+        Model &m = *(Model *)model;
+        if (!m.st) return;
+        std::shared_ptr<Streamer> keep = m.st;  // outlives the switch to resident layers
+        std::lock_guard<std::recursive_mutex> lk(keep->mu);
+        stream_make_resident(m);
+    });
+}
+
+esp_status esp_model_streaming_stats(const esp_model *model, esp_streaming_stats *out) {
+    return guard([&] {
+        if (!model) fail(ESP_MODEL_NOT_LOADED, "model not loaded");
+        if (!out) fail(ESP_INVALID_REQUEST, "null output");
+        const Model &m = *(const Model *)model;
+        std::shared_ptr<Streamer> keep = m.st;
+        if (!keep) {
+            stream_stats(m, out);
+            return;
+        }
+        std::lock_guard<std::recursive_mutex> lk(keep->mu);
+        stream_stats(m, out);
     });
 }
 
@@ -409,6 +459,32 @@ esp_status esp_generate_greedy(esp_model *model, esp_kv *kv, uint32_t seq, const
         launch_pick(a, s);
         launch_gen_step(a.ids_out, g, s);
         const int max_t = (int)last_pos;
+        if (m.st) {
+            // Streamed layers are read between kernels: one host-driven step
+            // per token, stopping at eos (generate.rs:154-168) so no layer
+            // is read for a step the reference does not take.
+            std::shared_ptr<Streamer> keep = m.st;
+            std::lock_guard<std::recursive_mutex> lk(keep->mu);
+            uint32_t n = 0, fed = 0;
+            for (uint32_t i = 0; i < max_new; ++i) {
+                int32_t id = 0;
+                ESP_HIP(hipMemcpyAsync(&id, g + 8 + i, 4, hipMemcpyDeviceToHost, s));
+                ESP_HIP(hipStreamSynchronize(s));
+                stream_check(m);
+                bool stop = false;
+                for (uint32_t e = 0; e < n_eos; ++e) stop |= id == eos[e];
+                if (stop) break;
+                if (out_ids) out_ids[n] = id;
+                ++n;
+                if (i + 1 < max_new) {
+                    decode_step_dev(m, k, (int)seq, max_t, g);
+                    ++fed;
+                }
+            }
+            k.pos[seq] = (int)(n_prompt + fed);
+            if (n_out) *n_out = n;
+            return;
+        }
         // Multi-row MoE layers read their expert row counts back to the
         // host, which a captured graph cannot do; single-row decode routes on
         // the device when the expert shapes fit the decode GEMV. ESP_GRAPHS=0

@@ -17,6 +17,7 @@
 #include "profile.hpp"
 #include "safetensors.hpp"
 #include "step.hpp"
+#include "streaming.hpp"
 
 namespace esp {
 
@@ -184,6 +185,55 @@ static inline float half_to_f32(uint16_t h) {
     return r;
 }
 
+// The named tensor with exactly `shape` (tensors.rs:22-66 messages).
+const StTensor &expect_tensor(const std::map<std::string, StTensor> &t, const std::string &name,
+                              const std::vector<uint64_t> &shape) {
+    auto it = t.find(name);
+    if (it == t.end()) fail(ESP_INVALID_WEIGHTS, "missing tensor: " + name);
+    if (it->second.shape != shape) {
+        std::string e = "weight format: expected [";
+        for (size_t i = 0; i < shape.size(); ++i) e += (i ? ", " : "") + std::to_string(shape[i]);
+        e += "], got [";
+        for (size_t i = 0; i < it->second.shape.size(); ++i)
+            e += (i ? ", " : "") + std::to_string(it->second.shape[i]);
+        fail(ESP_INVALID_WEIGHTS, e + "] for " + name);
+    }
+    return it->second;
+}
+
+// Dtype admission of one non-packed tensor (weight_format.rs:110-133,
+// 283-291): bf16 models take BF16 projections, the packed formats F16 for
+// every tensor that is not a packed projection; force_f32 tensors (norms,
+// biases) of unpacked models may be F32, BF16 or F16.
+void check_tensor_dtype(const Model &m, const std::string &name, const StTensor &s,
+                        bool force_f32) {
+    if ((m.wt == DT_BF16 && !force_f32 && s.dtype != "BF16") ||
+        (dt_packed(m.wt) && s.dtype != "F16"))
+        fail(ESP_INVALID_WEIGHTS, "weight format: artifact dtype disagrees with declared format (" +
+                                      name + ")");
+    if (s.dtype != "F32" && s.dtype != "BF16" && s.dtype != "F16")
+        fail(ESP_INVALID_WEIGHTS, "weight format: cannot import " + s.dtype + " (" + name + ")");
+}
+
+// The header side of a packed projection [rows, cols]
+// (weight_format.rs:225-273): a U8 tensor whose shape is its byte count.
+// Returns whether the byte count is the packed values plus the f32 block
+// scales; the scales themselves are checked by the caller.
+bool check_packed_header(const Model &m, const std::string &name, const StTensor &s,
+                         uint64_t rows, uint64_t cols) {
+    if (s.dtype != "U8")
+        fail(ESP_INVALID_WEIGHTS, "weight format: unpacked projection in a quantized row (" +
+                                      name + ")");
+    if (cols % 32)
+        fail(ESP_INVALID_WEIGHTS, "weight format: packed projection input width must be "
+                                  "divisible by 32");
+    const size_t n = rows * cols, vb = packed_value_bytes(m.wt, n), sb = n / 32 * 4;
+    if (s.shape.size() != 1 || s.shape[0] != s.bytes)
+        fail(ESP_INVALID_WEIGHTS, "weight format: packed buffer must have its encoded "
+                                  "byte-count shape");
+    return s.bytes == vb + sb;
+}
+
 // Reads checkpoint tensors into a host staging vector in the model's
 // format, checking shape, dtype admission and finiteness
 // (decoder/weight_format.rs:110-133, 225-315; tensors.rs:22-66).
@@ -193,18 +243,9 @@ struct Stager {
     std::set<std::string> consumed;
 
     const StTensor &get(const std::string &name, std::vector<uint64_t> shape) {
-        auto it = t.find(name);
-        if (it == t.end()) fail(ESP_INVALID_WEIGHTS, "missing tensor: " + name);
-        if (it->second.shape != shape) {
-            std::string e = "weight format: expected [";
-            for (size_t i = 0; i < shape.size(); ++i) e += (i ? ", " : "") + std::to_string(shape[i]);
-            e += "], got [";
-            for (size_t i = 0; i < it->second.shape.size(); ++i)
-                e += (i ? ", " : "") + std::to_string(it->second.shape[i]);
-            fail(ESP_INVALID_WEIGHTS, e + "] for " + name);
-        }
+        const StTensor &s = expect_tensor(t, name, shape);
         consumed.insert(name);
-        return it->second;
+        return s;
     }
     bool has(const std::string &name) const { return t.count(name) != 0; }
 
@@ -216,10 +257,7 @@ struct Stager {
         size_t n = 1;
         for (auto d : shape) n *= d;
         Dt dst = force_f32 || dt_packed(m.wt) ? DT_F32 : m.wt;
-        if ((m.wt == DT_BF16 && !force_f32 && s.dtype != "BF16") ||
-            (dt_packed(m.wt) && s.dtype != "F16"))
-            fail(ESP_INVALID_WEIGHTS, "weight format: artifact dtype disagrees with declared format (" +
-                                          name + ")");
+        check_tensor_dtype(m, name, s, force_f32);
         size_t base = out.size();
         out.resize(base + n * dt_size(dst));
         uint8_t *o = out.data() + base;
@@ -251,17 +289,8 @@ struct Stager {
         auto it = t.find(name);
         if (it == t.end()) fail(ESP_INVALID_WEIGHTS, "missing tensor: " + name);
         const StTensor &s = it->second;
-        if (s.dtype != "U8")
-            fail(ESP_INVALID_WEIGHTS, "weight format: unpacked projection in a quantized row (" +
-                                          name + ")");
-        if (cols % 32)
-            fail(ESP_INVALID_WEIGHTS, "weight format: packed projection input width must be "
-                                      "divisible by 32");
         const size_t n = rows * cols, vb = packed_value_bytes(m.wt, n), sb = n / 32 * 4;
-        if (s.shape.size() != 1 || s.shape[0] != s.bytes)
-            fail(ESP_INVALID_WEIGHTS, "weight format: packed buffer must have its encoded "
-                                      "byte-count shape");
-        bool ok = s.bytes == vb + sb;
+        bool ok = check_packed_header(m, name, s, rows, cols);
         for (size_t i = 0; ok && i < n / 32; ++i) {
             float sc;
             memcpy(&sc, s.data + vb + 4 * i, 4);
@@ -476,6 +505,52 @@ Model *load_model(const esp_config *cfg, const uint8_t *bytes, size_t len,
     }
     refuse_unconsumed(s);
     stage_rope(m);
+    return mp.release();
+}
+
+Model *load_streamed_model(const esp_config *cfg, const uint8_t *shared, size_t len,
+                           const esp_layer_source *source, const esp_streaming_options *opt) {
+    if (!cfg) fail(ESP_INVALID_CONFIG, "null config");
+    if (!source || !source->read_layer) fail(ESP_INVALID_REQUEST, "null layer source");
+    // provider.rs:381-387 (StreamingOptions::validate, streaming.rs:195-201)
+    if (!opt || !opt->query_chunk || !opt->max_layer_bytes || !opt->max_shared_bytes)
+        fail(ESP_INVALID_CONFIG, "streaming limits must be positive");
+    if (len > opt->max_shared_bytes)
+        fail(ESP_INVALID_WEIGHTS, "shared artifact exceeds its byte limit");
+    validate_config(*cfg);
+    std::unique_ptr<Model> mp(new Model());
+    Model &m = *mp;
+    init_model_shape(m, *cfg);
+    std::map<std::string, StTensor> tensors;
+    try {
+        tensors = parse_safetensors(shared, len);
+    } catch (const Error &e) {
+        fail(ESP_INVALID_WEIGHTS, "shared tensors: " + e.msg);
+    }
+    for (auto &kv : tensors)  // provider.rs:394-405
+        if (kv.first != "model.embed_tokens.weight" && kv.first != "model.norm.weight" &&
+            kv.first != "lm_head.weight")
+            fail(ESP_INVALID_WEIGHTS, "unexpected tensor in shared artifact");
+    if (m.E)
+        fail(ESP_UNSUPPORTED, "native expert streaming: routed-expert layers are not streamed by "
+                              "this library");
+    check_packed(m, 0);
+    // the geometry every staged block binds (scratch buffers are sized from it)
+    for (auto &w : m.layers) w.qkv_rows = m.qw + 2 * m.kvw;
+    Stager s{m, tensors, {}};
+    const uint64_t H = m.H;
+    m.embed = s.tensor("model.embed_tokens.weight", {(uint64_t)m.V, H});
+    m.final_norm = (float *)s.tensor("model.norm.weight", {H}, true);
+    if (s.has("lm_head.weight")) {
+        m.head = s.proj("lm_head.weight", (uint64_t)m.V, H, &m.head_s);
+    } else if (cfg->tie_word_embeddings) {
+        m.head = m.embed;
+        m.ht = m.et;
+    } else {
+        fail(ESP_INVALID_WEIGHTS, "lm_head.weight missing but tie_word_embeddings is false");
+    }
+    stage_rope(m);
+    streamer_init(m, *source, *opt);
     return mp.release();
 }
 
@@ -918,8 +993,19 @@ static void run_layers(Model &m, Kv &kv, const Rows &rows, int Mc, int max_t, in
         plan.n_split = attn_decode_splits(m.hd, m.nkv, m.nq / m.nkv, Mc, max_t, &plan.split_len);
     plan.max_t = max_t;
     kv.part.ensure((size_t)Mc * m.nq * plan.n_split * (m.hd + ATT_PART_PAD) * 4);
+    // a streamed layer's block stays reserved until its kernels are queued
+    struct Release {
+        Model &m;
+        Kv &kv;
+        ~Release() {
+            if (m.st) stream_release(m, kv);
+        }
+    };
     for (int l = 0; l < m.L; ++l) {
-        LayerW &w = m.layers[l];
+        LayerW staged;
+        if (m.st) staged = stream_acquire(m, kv, l);
+        Release rel{m, kv};
+        LayerW &w = m.st ? staged : m.layers[l];
         if (single) {
             run_layer_decode(m, kv, rows, w, l, plan);
             continue;
@@ -1150,6 +1236,7 @@ static void ensure_scratch(Model &m, Kv &kv, int Mc, int n_seqs) {
     const size_t H = m.H;
     int qkv_rows = 0;
     for (auto &w : m.layers) qkv_rows = std::max(qkv_rows, w.qkv_rows);
+    if (qkv_rows <= 0) fail(ESP_BACKEND, "layer geometry missing: no fused q/k/v rows");
     int fmax = std::max(m.F, std::max(m.Fe, m.Fs));
     kv.h.ensure((size_t)Mc * H * 4);
     kv.xn.ensure((size_t)Mc * H * 4);
@@ -1225,6 +1312,8 @@ static void run_head(Model &m, Kv &kv, int n_seqs, const float *h_src, const int
 void forward(Model &m, Kv &kv, int n_seqs, const uint32_t *seqs, const uint32_t *lens,
              const int32_t *ids) {
     if (n_seqs <= 0) fail(ESP_INVALID_REQUEST, "cached input is empty or exceeds the context window");
+    std::unique_lock<std::recursive_mutex> streaming;
+    if (m.st) streaming = std::unique_lock<std::recursive_mutex>(m.st->mu);
     // validate (model.rs:548-556) before touching any state
     std::vector<int> seen(kv.batch, 0);
     long long M = 0;
@@ -1309,6 +1398,7 @@ void forward(Model &m, Kv &kv, int n_seqs, const uint32_t *seqs, const uint32_t 
         run_head(m, kv, n_seqs, hl, nullptr);
     }
     ESP_HIP(hipStreamSynchronize(s));
+    if (m.st) stream_check(m);  // a streamed layer that failed its device checks
     for (int i = 0; i < n_seqs; ++i) kv.pos[seqs[i]] += (int)lens[i];
     kv.logits_rows = n_seqs;
 }
@@ -1325,6 +1415,7 @@ namespace esp {
 // grid barriers (~3-4 us each, six or seven per layer) cost more than the
 // launch gaps of the per-kernel decode path they replace.
 static bool step_usable(Model &m) {
+    if (m.st) return false;  // streamed layers are staged between kernels
     if (m.step_mode < 0) {
         bool qk = false, moe = false;
         for (auto &w : m.layers) {

@@ -37,7 +37,9 @@ struct DevMem {
     template <typename T> T *as() const { return (T *)p; }
 };
 
-struct MaskCtx;  // constraint.hpp
+struct MaskCtx;   // constraint.hpp
+struct Streamer;  // streaming.hpp
+struct StTensor;  // safetensors.hpp
 
 struct LayerW {
     float *in_norm = nullptr, *post_norm = nullptr;
@@ -84,6 +86,9 @@ struct Model {
     // persistent decode-step kernel: -1 not decided, 0 not usable, 1 usable
     int step_mode = -1;
     std::unique_ptr<DevMem> step_layers;  // StepLayer[L]
+    // layer streaming: layers come from a host source per forward
+    // (`layers` then holds only their geometry and windows)
+    std::shared_ptr<Streamer> st;
 
     void *alloc(size_t bytes) {
         mem.emplace_back(new DevMem(bytes));
@@ -121,5 +126,18 @@ struct Kv {
 // The forward over prepared rows; defined in runtime.cpp.
 void forward(Model &m, Kv &kv, int n_seqs, const uint32_t *seqs, const uint32_t *lens,
              const int32_t *ids);
+
+// Checkpoint admission rules shared by the resident loader and the layer
+// streamer (runtime.cpp).
+const StTensor &expect_tensor(const std::map<std::string, StTensor> &t, const std::string &name,
+                              const std::vector<uint64_t> &shape);
+void check_tensor_dtype(const Model &m, const std::string &name, const StTensor &s,
+                        bool force_f32);
+bool check_packed_header(const Model &m, const std::string &name, const StTensor &s,
+                         uint64_t rows, uint64_t cols);
+// A model whose layers stream from `source` (model.rs:196-312): only the
+// shared artifact's embedding, final norm and head are staged here.
+Model *load_streamed_model(const esp_config *cfg, const uint8_t *shared, size_t len,
+                           const esp_layer_source *source, const esp_streaming_options *opt);
 
 }  // namespace esp

@@ -156,6 +156,66 @@ class DecoderModel:
         del keep
         return DecoderModel(h, config, fmt)
 
+    @staticmethod
+    def from_layer_source(config: DecoderConfig, shared: bytes, source: "LayerSource",
+                          options: Optional["StreamingOptions"] = None,
+                          fmt: str = "f32") -> "DecoderModel":
+        """provider.rs:370-426 + model.rs:268-312: resident embedding, final
+        norm and head from the shared artifact; every forward reads each
+        layer through ``source`` and stages it into HBM."""
+        from .streaming import SourceBridge, StreamingOptions
+        options = options or StreamingOptions()
+        options.validate()
+        L = _lib.load()
+        c, keep = esp_config(config, fmt)
+        bridge = SourceBridge(source)
+        src = _lib.EspLayerSource(bridge.fn, None)
+        opt = _lib.EspStreamingOptions(options.query_chunk, options.max_layer_bytes,
+                                       options.max_shared_bytes)
+        buf = (C.c_uint8 * len(shared)).from_buffer_copy(shared) if shared else None
+        h = C.c_void_p()
+        _lib.check(L.esp_model_load_streamed(C.byref(c), buf, len(shared), C.byref(src),
+                                             C.byref(opt), C.byref(h)))
+        del keep
+        m = DecoderModel(h, config, fmt)
+        m._bridge = bridge  # the callback must outlive the handle
+        return m
+
+    def with_layer_cache(self, budget: int) -> "DecoderModel":
+        """model.rs:336-362: keep a first-fit subset of streamed layers in HBM."""
+        _lib.check(_lib.load().esp_model_layer_cache(self._h, budget))
+        return self
+
+    def with_resident_layers(self) -> "DecoderModel":
+        """model.rs:384-415: read every layer once and keep all of them."""
+        self._check(_lib.load().esp_model_resident_layers(self._h))
+        return self
+
+    def streaming_stats(self) -> Optional["StreamingReadStats"]:
+        """model.rs:314-333: None unless layers stream."""
+        from .streaming import DeviceLayerCacheStats, StreamingReadStats
+        s = _lib.EspStreamingStats()
+        _lib.check(_lib.load().esp_model_streaming_stats(self._h, C.byref(s)))
+        if not s.streamed:
+            return None
+        bridge = getattr(self, "_bridge", None)
+        out = StreamingReadStats(layer_reads=s.layer_reads, encoded_bytes_read=s.encoded_bytes_read,
+                                 largest_encoded_layer=s.largest_encoded_layer,
+                                 verified_cache=bridge.source.cache_stats() if bridge else None)
+        if s.device_cache:
+            out.device_cache = DeviceLayerCacheStats(s.cache_hits, s.cache_misses,
+                                                     s.retained_payload_bytes,
+                                                     s.payload_budget_bytes, s.cached_layers)
+        return out
+
+    def _check(self, status: int) -> None:
+        """_lib.check, re-raising unchanged what a layer source raised."""
+        bridge = getattr(self, "_bridge", None)
+        err = bridge.take() if bridge is not None else None
+        if status and err is not None:
+            raise err
+        _lib.check(status)
+
     def weight_bytes(self) -> int:
         n = C.c_uint64()
         _lib.check(_lib.load().esp_model_weight_bytes(self._h, C.byref(n)))
@@ -170,7 +230,7 @@ class DecoderModel:
         """model.rs:502-539: logits [vocab] (f32) of the block's last position."""
         ids = np.ascontiguousarray(ids, dtype=np.int32)
         out = np.empty(self.config.vocab_size, np.float32)
-        _lib.check(_lib.load().esp_forward_last(
+        self._check(_lib.load().esp_forward_last(
             self._h, cache._h, seq, ids.ctypes.data_as(C.POINTER(C.c_int32)), len(ids),
             out.ctypes.data))
         return out
@@ -182,7 +242,7 @@ class DecoderModel:
         lens = np.ascontiguousarray([len(b) for b in blocks], dtype=np.uint32)
         ids = np.ascontiguousarray([t for b in blocks for t in b], dtype=np.int32)
         out = np.empty((len(seqs_a), self.config.vocab_size), np.float32) if want_logits else None
-        _lib.check(_lib.load().esp_forward_batch(
+        self._check(_lib.load().esp_forward_batch(
             self._h, cache._h, len(seqs_a), seqs_a.ctypes.data_as(C.POINTER(C.c_uint32)),
             lens.ctypes.data_as(C.POINTER(C.c_uint32)), ids.ctypes.data_as(C.POINTER(C.c_int32)),
             None if out is None else out.ctypes.data))
@@ -240,7 +300,7 @@ class DecoderModel:
         out = np.zeros(max(1, max_new), np.int32)
         n = C.c_uint32()
         P = C.POINTER(C.c_int32)
-        _lib.check(_lib.load().esp_generate_greedy(
+        self._check(_lib.load().esp_generate_greedy(
             self._h, cache._h, seq, p.ctypes.data_as(P), len(p), max_new, e.ctypes.data_as(P),
             len(eos), out.ctypes.data_as(P), C.byref(n)))
         return [int(x) for x in out[:n.value]]

@@ -1,0 +1,365 @@
+"""Layer sources and artifacts for streamed decoding, mirroring esp's host side.
+
+crates/esp/src/infer/decoder/streaming.rs (``LayerSource``,
+``with_expert_reader``, ``cache_verified_layers``, ``StreamingOptions``,
+the read statistics) and decoder/checkpoint.rs (splitting a checkpoint into
+one shared artifact and one safetensors artifact per layer). The device side
+(staging each artifact into HBM, checking it, running the layer) lives in
+libesp_hip.so behind ``DecoderModel.from_layer_source``; this module only
+moves bytes and enforces the byte limits.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import json
+import struct
+import threading
+from concurrent.futures import ThreadPoolExecutor
+from dataclasses import asdict, dataclass
+from typing import Callable, Dict, List, Optional, Sequence, Tuple
+
+import numpy as np
+
+from .config import DecoderConfig
+from .errors import Backend, InferError, InvalidConfig, InvalidWeights
+
+
+@dataclass
+class StreamingOptions:
+    """streaming.rs:172-202: per-provider limits, all positive."""
+
+    query_chunk: int = 32
+    max_layer_bytes: int = 256 * 1024 * 1024
+    max_shared_bytes: int = 1024 * 1024 * 1024
+
+    def validate(self) -> None:
+        if self.query_chunk <= 0 or self.max_layer_bytes <= 0 or self.max_shared_bytes <= 0:
+            raise InvalidConfig("streaming limits must be positive")
+
+    def to_json(self) -> str:
+        return json.dumps(asdict(self))
+
+    @staticmethod
+    def from_json(text: str) -> "StreamingOptions":
+        """serde(deny_unknown_fields): every field present, nothing else."""
+        raw = json.loads(text)
+        names = {"query_chunk", "max_layer_bytes", "max_shared_bytes"}
+        if not isinstance(raw, dict) or set(raw) != names or not all(
+                isinstance(raw[k], int) and not isinstance(raw[k], bool) and raw[k] >= 0
+                for k in names):
+            raise InvalidConfig("streaming options: expected exactly query_chunk, "
+                                "max_layer_bytes and max_shared_bytes as unsigned integers")
+        return StreamingOptions(**raw)
+
+
+@dataclass
+class LayerCacheStats:
+    """streaming.rs:83-91 host allocation accounting of the verified cache."""
+
+    hits: int = 0
+    misses: int = 0
+    retained_capacity_bytes: int = 0
+    entries: int = 0
+    capacity_budget_bytes: int = 0
+
+
+@dataclass
+class DeviceLayerCacheStats:
+    """streaming.rs:204-220 logical tensor payload kept in HBM."""
+
+    hits: int = 0
+    misses: int = 0
+    retained_payload_bytes: int = 0
+    payload_budget_bytes: int = 0
+    layers: int = 0
+
+
+@dataclass
+class StreamingReadStats:
+    """streaming.rs:222-238 logical verified artifact reads."""
+
+    layer_reads: int = 0
+    encoded_bytes_read: int = 0
+    largest_encoded_layer: int = 0
+    expert_reads: int = 0
+    expert_encoded_bytes_read: int = 0
+    largest_encoded_expert: int = 0
+    verified_cache: Optional[LayerCacheStats] = None
+    device_cache: Optional[DeviceLayerCacheStats] = None
+
+
+class Artifact(bytes):
+    """Artifact bytes that may sit in a larger allocation: ``capacity`` is
+    what a verified cache charges against its budget (streaming.rs:129-138
+    counts Vec capacity, not length)."""
+
+    capacity: int
+
+    def __new__(cls, data: bytes, capacity: Optional[int] = None):
+        obj = super().__new__(cls, data)
+        obj.capacity = len(data) if capacity is None else max(capacity, len(data))
+        return obj
+
+
+def _capacity(b) -> int:
+    return getattr(b, "capacity", len(b))
+
+
+class LayerSource:
+    """streaming.rs:17-37: a host-owned source of verified standalone layer
+    artifacts. ``read_layer`` must check the declared size against ``limit``
+    before reading and verify content identity before returning bytes."""
+
+    def read_layer(self, index: int, limit: int) -> bytes:
+        raise NotImplementedError
+
+    def read_layer_shared(self, index: int, limit: int) -> bytes:
+        return self.read_layer(index, limit)
+
+    def cache_stats(self) -> Optional[LayerCacheStats]:
+        return None
+
+    def read_expert(self, layer: int, expert: int, limit: int) -> bytes:
+        raise InvalidWeights("layer source has no expert reader")
+
+
+class FnSource(LayerSource):
+    """streaming.rs:177-184: any ``f(index, limit) -> bytes`` is a source."""
+
+    def __init__(self, read: Callable[[int, int], bytes]):
+        self._read = read
+
+    def read_layer(self, index: int, limit: int) -> bytes:
+        return self._read(index, limit)
+
+
+def with_expert_reader(layers: Callable[[int, int], bytes],
+                       experts: Callable[[int, int, int], bytes]) -> LayerSource:
+    """streaming.rs:41-66: compose a layer reader and an expert reader."""
+
+    class _Readers(LayerSource):
+        def read_layer(self, index, limit):
+            return layers(index, limit)
+
+        def read_expert(self, layer, expert, limit):
+            return experts(layer, expert, limit)
+
+    return _Readers()
+
+
+def cache_verified_layers(source: LayerSource, budget: int) -> LayerSource:
+    """streaming.rs:93-170: cache verified immutable artifacts by index.
+
+    First-fit admission, at most 128 entries and ``budget`` bytes of
+    allocation capacity; hits return the same object and re-check the
+    caller's limit; errors and oversized reads are never cached; experts
+    keep the uncached path. ``budget`` 0 returns ``source`` itself."""
+    if budget == 0:
+        return source
+
+    class _Cached(LayerSource):
+        def __init__(self):
+            self._lock = threading.Lock()
+            self._entries: List[Tuple[int, bytes]] = []
+            self._stats = LayerCacheStats(capacity_budget_bytes=budget)
+
+        def read_layer(self, index, limit):
+            return bytes(self.read_layer_shared(index, limit))
+
+        def read_layer_shared(self, index, limit):
+            with self._lock:
+                for key, data in self._entries:
+                    if key == index:
+                        if len(data) > limit:
+                            raise InvalidWeights("cached layer exceeds its byte limit")
+                        self._stats.hits += 1
+                        return data
+                self._stats.misses += 1
+                data = source.read_layer_shared(index, limit)
+                if len(data) > limit:
+                    raise InvalidWeights("layer source exceeded its byte limit")
+                cap = _capacity(data)
+                st = self._stats
+                if len(self._entries) < 128 and cap <= st.capacity_budget_bytes - st.retained_capacity_bytes:
+                    st.retained_capacity_bytes += cap
+                    self._entries.append((index, data))
+                    st.entries = len(self._entries)
+                return data
+
+        def read_expert(self, layer, expert, limit):
+            return source.read_expert(layer, expert, limit)
+
+        def cache_stats(self):
+            with self._lock:
+                return LayerCacheStats(**asdict(self._stats))
+
+    return _Cached()
+
+
+class ArtifactSource(LayerSource):
+    """Verified in-memory artifacts (one per layer), the shape of a host
+    reader over an artifact index (layer_library.rs:107-140): the declared
+    byte size is checked against ``limit`` before the bytes are handed out,
+    and against the bytes themselves."""
+
+    def __init__(self, artifacts: Sequence[bytes]):
+        self._artifacts = list(artifacts)
+
+    def read_layer(self, index: int, limit: int) -> bytes:
+        if index >= len(self._artifacts):
+            raise InvalidWeights(f"layer library: missing layer artifact {index}")
+        data = self._artifacts[index]
+        if len(data) > limit:
+            raise InvalidWeights("layer library: layer artifact identity, schema or byte limit "
+                                 "mismatch")
+        return data
+
+
+# ---- safetensors artifacts (checkpoint.rs:246-292 pack) ----
+
+_ALIGN = {"F64": 8, "I64": 8, "U64": 8, "F32": 4, "I32": 4, "U32": 4, "F16": 2, "BF16": 2,
+          "I16": 2, "U16": 2, "I8": 1, "U8": 1, "BOOL": 1}
+
+
+def read_header(buf) -> Tuple[Dict[str, dict], int]:
+    """The safetensors header of ``buf``: tensor entries and the data start."""
+    if len(buf) < 8:
+        raise InvalidWeights("checkpoint: invalid safetensors header length")
+    (n,) = struct.unpack_from("<Q", buf, 0)
+    if n > len(buf) - 8 or n > 100_000_000:
+        raise InvalidWeights("checkpoint: invalid safetensors header length")
+    header = json.loads(bytes(buf[8:8 + n]))
+    header.pop("__metadata__", None)
+    return header, 8 + n
+
+
+def pack(entries: Sequence[Tuple[str, str, Sequence[int], bytes]]) -> bytes:
+    """Serialize (name, dtype, shape, raw bytes) tensors: data ordered by
+    dtype alignment (largest first) then name, header padded with spaces to
+    8 bytes, as the safetensors crate writes them."""
+    order = sorted(entries, key=lambda e: (-_ALIGN.get(e[1], 1), e[0]))
+    header, off, blobs = {}, 0, []
+    for name, dt, shape, data in order:
+        header[name] = {"dtype": dt, "shape": list(shape), "data_offsets": [off, off + len(data)]}
+        off += len(data)
+        blobs.append(bytes(data))
+    text = json.dumps(header, separators=(",", ":")).encode()
+    text += b" " * ((8 - len(text) % 8) % 8)
+    return struct.pack("<Q", len(text)) + text + b"".join(blobs)
+
+
+def layer_tensor_names(config: DecoderConfig) -> List[str]:
+    """loader.rs:48-64 per-layer tensors of a dense Llama block."""
+    names = ["input_layernorm.weight", "post_attention_layernorm.weight",
+             "self_attn.q_proj.weight", "self_attn.k_proj.weight", "self_attn.v_proj.weight",
+             "self_attn.o_proj.weight", "mlp.gate_proj.weight", "mlp.up_proj.weight",
+             "mlp.down_proj.weight"]
+    if config.qkv_bias():
+        names += ["self_attn.q_proj.bias", "self_attn.k_proj.bias", "self_attn.v_proj.bias"]
+    if config.output_bias():
+        names.append("self_attn.o_proj.bias")
+    if config.qk_norm():
+        names += ["self_attn.q_norm.weight", "self_attn.k_norm.weight"]
+    return names
+
+
+class CheckpointReader:
+    """checkpoint.rs:47-293 over one safetensors checkpoint held in memory:
+    the declared names are checked once, then the shared artifact and each
+    layer's artifact are packed on request within a byte limit."""
+
+    def __init__(self, checkpoint: bytes, config: DecoderConfig):
+        if config.moe is not None:
+            raise InvalidConfig("checkpoint: routed-expert layers are split by the expert "
+                                "reader, which this library does not stream")
+        self._buf = memoryview(checkpoint)
+        self._header, self._start = read_header(self._buf)
+        self._config = config
+        want = {"model.embed_tokens.weight", "model.norm.weight"}
+        for i in range(config.num_hidden_layers):
+            want |= {f"model.layers.{i}.{s}" for s in layer_tensor_names(config)}
+        if not config.tie_word_embeddings or "lm_head.weight" in self._header:
+            want.add("lm_head.weight")
+        have = {n for n in self._header if not n.endswith(".rotary_emb.inv_freq")}
+        if want != have:
+            raise InvalidWeights("checkpoint: tensor names do not match the declared Llama block")
+
+    def _pack(self, names: List[str], limit: int) -> bytes:
+        total = 0
+        for n in names:
+            b, e = self._header[n]["data_offsets"]
+            total += e - b
+        if total > limit:
+            raise InvalidWeights("checkpoint: artifact tensor data exceeds configured byte limit")
+        entries = []
+        for n in names:
+            h = self._header[n]
+            b, e = h["data_offsets"]
+            entries.append((n, h["dtype"], h["shape"], self._buf[self._start + b:self._start + e]))
+        out = pack(entries)
+        if len(out) > limit:
+            raise InvalidWeights("checkpoint: encoded artifact exceeds configured byte limit")
+        return out
+
+    def shared_bytes(self, limit: int) -> bytes:
+        names = [n for n in ("model.embed_tokens.weight", "model.norm.weight", "lm_head.weight")
+                 if n in self._header]
+        return self._pack(names, limit)
+
+    def layer_bytes(self, index: int, limit: int) -> bytes:
+        return self._pack([f"model.layers.{index}.{s}" for s in layer_tensor_names(self._config)],
+                          limit)
+
+
+def split_checkpoint(checkpoint: bytes, config: DecoderConfig,
+                     options: Optional[StreamingOptions] = None) -> Tuple[bytes, List[bytes]]:
+    """layer_library.rs:211-266 import without the store: the shared
+    artifact and one artifact per layer, each within the options' limits."""
+    options = options or StreamingOptions()
+    options.validate()
+    r = CheckpointReader(checkpoint, config)
+    return (r.shared_bytes(options.max_shared_bytes),
+            [r.layer_bytes(i, options.max_layer_bytes) for i in range(config.num_hidden_layers)])
+
+
+# ---- the C callback behind esp_model_load_streamed ----
+
+class SourceBridge:
+    """Adapts a LayerSource to esp_layer_read_fn: copies each artifact into
+    the library's pinned staging buffer (large ones in parallel slices) and
+    keeps the exception a source raised so the caller sees it unchanged."""
+
+    _SLICE = 64 << 20
+
+    def __init__(self, source: LayerSource):
+        from . import _lib
+        self.source = source
+        self.error: Optional[BaseException] = None
+        self._pool = ThreadPoolExecutor(8)
+        self.fn = _lib.LAYER_READ_FN(self._read)
+
+    def _read(self, user, index, limit, dst, cap, plen):
+        try:
+            data = self.source.read_layer_shared(int(index), int(limit))
+            n = len(data)
+            plen[0] = n
+            if n <= cap:
+                src = np.frombuffer(data, np.uint8).ctypes.data if n else 0
+                if n <= self._SLICE:
+                    C.memmove(dst, src, n)
+                else:
+                    jobs = [self._pool.submit(C.memmove, dst + o, src + o, min(self._SLICE, n - o))
+                            for o in range(0, n, self._SLICE)]
+                    for j in jobs:
+                        j.result()
+            return 0
+        except InferError as e:
+            self.error = e
+            return e.code
+        except BaseException as e:  # noqa: BLE001 - reported through the status
+            self.error = e
+            return Backend.code
+
+    def take(self) -> Optional[BaseException]:
+        e, self.error = self.error, None
+        return e

@@ -197,6 +197,75 @@ esp_status esp_generate_greedy(esp_model *model, esp_kv *kv, uint32_t seq, const
                                uint32_t n_prompt, uint32_t max_new, const int32_t *eos,
                                uint32_t n_eos, int32_t *out_ids, uint32_t *n_out);
 
+/* ---- Layer streaming (decoder/streaming.rs, model.rs:196-415) ---- */
+
+/* streaming.rs:172-201 StreamingOptions; every field must be positive
+ * (validate, :195-201). query_chunk bounds the reference's per-chunk
+ * attention; this library's attention is row-independent, so it is
+ * checked and kept but does not change results. */
+typedef struct esp_streaming_options {
+    uint64_t query_chunk;      /* reference default 32 */
+    uint64_t max_layer_bytes;  /* reference default 256 MiB */
+    uint64_t max_shared_bytes; /* reference default 1 GiB */
+} esp_streaming_options;
+
+/* streaming.rs:17-37 LayerSource::read_layer in fill form. Copy layer
+ * `index`'s verified safetensors artifact into `dst` (pinned host memory
+ * owned by the library, `cap` bytes, cap <= limit) and set *len to its
+ * size. An artifact larger than `limit` is refused before it is read
+ * (return ESP_INVALID_WEIGHTS); one larger than `cap` but within `limit`
+ * is reported by setting *len without copying (the library refuses it: it
+ * cannot be the declared block). Any other non-zero return fails the
+ * forward with that status and no position advances. The library calls it
+ * on the thread running the forward, one call at a time. */
+typedef esp_status (*esp_layer_read_fn)(void *user, uint32_t index, uint64_t limit, uint8_t *dst,
+                                        uint64_t cap, uint64_t *len);
+typedef struct esp_layer_source {
+    esp_layer_read_fn read_layer;
+    void *user;
+} esp_layer_source;
+
+/* provider.rs:370-426 from_layer_source_with_format + model.rs:268-312
+ * DecoderModel::from_layer_source_with_format. `shared` holds only
+ * model.embed_tokens.weight, model.norm.weight and (unless tied)
+ * lm_head.weight; it is borrowed for the call. shared_len above
+ * max_shared_bytes -> ESP_INVALID_WEIGHTS "shared artifact exceeds its byte
+ * limit"; any other tensor name -> "unexpected tensor in shared artifact".
+ * Each forward then reads every layer through `source` (model.rs:556-646):
+ * the artifact must hold exactly model.layers.{i}.* of the declared block
+ * (loader.rs:830-848), is staged into HBM on a copy stream while the
+ * previous layer computes, and is checked on the device (dtype admission,
+ * finiteness, packed block scales) before its results are used. `source`
+ * is copied; its `user` must outlive the model. MoE configurations ->
+ * ESP_UNSUPPORTED. */
+esp_status esp_model_load_streamed(const esp_config *config, const uint8_t *shared,
+                                   size_t shared_len, const esp_layer_source *source,
+                                   const esp_streaming_options *options, esp_model **out);
+
+/* model.rs:336-362 with_layer_cache: keep a first-fit subset (at most 128
+ * layers) of streamed layers resident in HBM within `budget` bytes of
+ * payload (counted as the reference does: 4 bytes per element of every
+ * tensor in the artifact). budget 0 turns the cache off. A model that does
+ * not stream -> ESP_INVALID_CONFIG. */
+esp_status esp_model_layer_cache(esp_model *model, uint64_t budget);
+
+/* model.rs:384-415 with_resident_layers: read every layer once through
+ * the source and keep all of them in HBM; the model then no longer
+ * streams. A model that does not stream is left unchanged. */
+esp_status esp_model_resident_layers(esp_model *model);
+
+/* streaming.rs:228-252 StreamingReadStats (logical verified reads) and
+ * :210-220 DeviceLayerCacheStats. `streamed` is 0 (and every other field
+ * 0) for a model that does not stream (model.rs:314-333 returns None). */
+typedef struct esp_streaming_stats {
+    uint32_t streamed;
+    uint32_t device_cache; /* 1 when a device layer cache is set */
+    uint64_t layer_reads, encoded_bytes_read, largest_encoded_layer;
+    uint64_t cache_hits, cache_misses, retained_payload_bytes, payload_budget_bytes;
+    uint64_t cached_layers;
+} esp_streaming_stats;
+esp_status esp_model_streaming_stats(const esp_model *model, esp_streaming_stats *out);
+
 /* ---- Constrained decoding (decoder/constraint.rs) ----
  * A vocabulary holds the byte string of every token id of a byte-level
  * tokenizer; a constraint is one request's compiled output grammar plus its

@@ -12,6 +12,7 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 def declared():
     text = open(os.path.join(ROOT, "include", "esp_hip.h")).read()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    text = re.sub(r"typedef[^;]*\(\s*\*[^;]*;", "", text)  # function-pointer types
     return sorted(set(re.findall(r"\b(esp_[a-z_0-9]+)\s*\(", text)))
 
 
