@@ -19,6 +19,8 @@ import os
 import sys
 import time
 
+import numpy as np
+
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
@@ -252,6 +254,115 @@ def c3_packed_bench(bits: int) -> dict:
            "decode_hbm_frac": round(db["total"] / t_dec / 1e9 / HBM_PEAK_GBS, 4),
            "decode_bytes_per_token": db["total"],
            "weight_bytes": model.weight_bytes()}
+    model.close()
+    return res
+
+
+def synthetic_layer_artifacts(cfg, seed: int = 9):
+    """bf16 artifacts of cfg's dense block in esp's streamed layout: the
+    shared artifact (embedding, final norm, head) and one safetensors
+    artifact per layer. Values are uniform bf16 in [2^-7, 2^-6); every layer
+    carries the same bytes under its own names."""
+    from esp_amd.streaming import layer_tensor_names, pack
+    rng = np.random.default_rng(seed)
+    H, F, V = cfg.hidden_size, cfg.intermediate_size, cfg.vocab_size
+    qw, kvw = cfg.query_width(), cfg.kv_heads() * cfg.head_dim()
+    shapes = {"input_layernorm.weight": (H,), "post_attention_layernorm.weight": (H,),
+              "self_attn.q_proj.weight": (qw, H), "self_attn.k_proj.weight": (kvw, H),
+              "self_attn.v_proj.weight": (kvw, H), "self_attn.o_proj.weight": (H, qw),
+              "mlp.gate_proj.weight": (F, H), "mlp.up_proj.weight": (F, H),
+              "mlp.down_proj.weight": (H, F)}
+    assert set(shapes) == set(layer_tensor_names(cfg))
+
+    def vals(shape):
+        return rng.integers(0x3c00, 0x3c80, size=int(np.prod(shape)), dtype=np.uint16).tobytes()
+
+    data = {k: vals(v) for k, v in shapes.items()}
+    layers = [pack([(f"model.layers.{l}.{k}", "BF16", v, data[k]) for k, v in shapes.items()])
+              for l in range(cfg.num_hidden_layers)]
+    shared = pack([("model.embed_tokens.weight", "BF16", (V, H), vals((V, H))),
+                   ("model.norm.weight", "BF16", (H,), vals((H,))),
+                   ("lm_head.weight", "BF16", (V, H), vals((V, H)))])
+    return shared, layers
+
+
+def h2d_gbs(nbytes: int = 512 << 20, reps: int = 8) -> float:
+    """Pinned host-to-device copy rate of this box: hipMemcpyAsync from
+    hipHostMalloc memory on one stream, through the HIP runtime the library
+    itself links."""
+    import ctypes as C
+    hip = C.CDLL("libamdhip64.so.7")  # the runtime libesp_hip.so is linked to
+    h, d = C.c_void_p(), C.c_void_p()
+    assert hip.hipHostMalloc(C.byref(h), C.c_size_t(nbytes), 0) == 0
+    assert hip.hipMalloc(C.byref(d), C.c_size_t(nbytes)) == 0
+    try:
+        def copy():
+            assert hip.hipMemcpyAsync(d, h, C.c_size_t(nbytes), 1, None) == 0  # host to device
+
+        for _ in range(2):
+            copy()
+        assert hip.hipDeviceSynchronize() == 0
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            copy()
+        assert hip.hipDeviceSynchronize() == 0
+        return nbytes * reps / (time.perf_counter() - t0) / 1e9
+    finally:
+        hip.hipFree(d)
+        hip.hipHostFree(h)
+
+
+def c3_stream_bench() -> dict:
+    """The C3 shape (Llama-3-8B, bf16, no LoRA) with every layer streamed
+    from host artifacts through a LayerSource (esp.layer-weights layout):
+    each forward reads all 32 layers (~14 GB) and stages them into HBM on a
+    copy stream while the previous layer computes. Bound: the host link.
+    Then the same model with a device layer cache holding every layer."""
+    from esp_amd import DecoderModel
+    from esp_amd.streaming import ArtifactSource, StreamingOptions
+    from tests.synth import uniform_ids
+    cfg = c3_config()
+    shared, layers = synthetic_layer_artifacts(cfg)
+    per_forward = sum(len(x) for x in layers)
+    opts = StreamingOptions(max_layer_bytes=max(len(x) for x in layers),
+                            max_shared_bytes=len(shared))
+    model = DecoderModel.from_layer_source(cfg, shared, ArtifactSource(layers), opts, "bf16")
+    prompt = uniform_ids(7, 2048, cfg.vocab_size)
+    kv = model.new_cache(1, 2048 + 32)
+    model.try_forward_cached_last(prompt[:8], kv)  # staging buffers, scratch
+    kv.reset(0)
+    t0 = time.perf_counter()
+    model.try_forward_cached_last(prompt, kv)
+    t_pre = time.perf_counter() - t0
+    n_dec = 4
+    t0 = time.perf_counter()
+    for i in range(n_dec):
+        model.try_forward_cached_last([i + 1], kv)
+    t_dec = (time.perf_counter() - t0) / n_dec
+    reads = model.streaming_stats().layer_reads
+    link = h2d_gbs()
+    # every layer kept in HBM after one pass
+    model.with_layer_cache(1 << 40)
+    kv.reset(0)
+    model.try_forward_cached_last(prompt, kv)
+    n_c = 16
+    t0 = time.perf_counter()
+    for i in range(n_c):
+        model.try_forward_cached_last([i + 1], kv)
+    t_cached = (time.perf_counter() - t0) / n_c
+    dc = model.streaming_stats().device_cache
+    res = {"workload": "C3 shape (Llama-3-8B, bf16, no LoRA), every layer streamed from host "
+                       "safetensors artifacts per forward; 2048-token prefill, batch-1 decode at "
+                       "2048+ context; then a device layer cache holding all 32 layers",
+           "streamed_bytes_per_forward": per_forward,
+           "streamed_prefill_2048_ms": round(t_pre * 1e3, 2),
+           "streamed_decode_ms_per_token": round(t_dec * 1e3, 2),
+           "streamed_gbs": round(per_forward / t_dec / 1e9, 2),
+           "h2d_pinned_gbs": round(link, 2),
+           "streamed_link_frac": round(per_forward / t_dec / 1e9 / link, 4),
+           "layer_reads": reads,
+           "cached_decode_ms_per_token": round(t_cached * 1e3, 3),
+           "cached_layers": dc.layers, "cache_hits": dc.hits}
     model.close()
     return res
 
@@ -537,6 +648,8 @@ def main():
     ap.add_argument("--no-packed", action="store_true")
     ap.add_argument("--only-packed", action="store_true")
     ap.add_argument("--only-c5g", action="store_true")
+    ap.add_argument("--no-stream", action="store_true")
+    ap.add_argument("--only-stream", action="store_true")
     ap.add_argument("--traffic", action="store_true",
                     help="run only the workload of the HBM-traffic counter passes")
     args = ap.parse_args()
@@ -562,6 +675,9 @@ def main():
         return
     if args.only_packed:
         print(json.dumps({"c3_q8": c3_packed_bench(8), "c3_q4": c3_packed_bench(4)}), flush=True)
+        return
+    if args.only_stream:
+        print(json.dumps({"c3_stream": c3_stream_bench()}), flush=True)
         return
     if args.only_c5g:
         print(json.dumps({"c5_grammar": c5_grammar_bench(32)}), flush=True)
@@ -674,6 +790,9 @@ def main():
         for bits in (8, 4):
             result[f"c3_q{bits}"] = c3_packed_bench(bits)
             print(f"c3_q{bits}: {result[f'c3_q{bits}']}", file=sys.stderr, flush=True)
+    if not args.no_stream:
+        result["c3_stream"] = c3_stream_bench()
+        print(f"c3_stream: {result['c3_stream']}", file=sys.stderr, flush=True)
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(cfg, int(avg_ctx))
     print(json.dumps(result), flush=True)
