@@ -114,6 +114,10 @@ def load():
         "esp_model_layer_cache": (C.c_int, [vp, C.c_uint64]),
         "esp_model_resident_layers": (C.c_int, [vp]),
         "esp_model_streaming_stats": (C.c_int, [vp, P(EspStreamingStats)]),
+        "esp_stage_create": (C.c_int, [P(EspConfig), u32, u32, P(EspLayerSource),
+                                       P(EspStreamingOptions), vp, C.c_size_t, u32, P(vp)]),
+        "esp_stage_destroy": (C.c_int, [vp]),
+        "esp_stage_forward": (C.c_int, [vp, vp, u32, u32, vp]),
         "esp_profile_enable": (C.c_int, [C.c_char_p, C.c_int]),
         "esp_profile_read": (C.c_int, [C.c_char_p, P(C.c_uint64), P(C.c_double)]),
     }
@@ -133,6 +137,7 @@ EXPORTED = ["esp_last_error", "esp_version", "esp_model_load", "esp_model_create
             "esp_constraint_destroy", "esp_constraint_accept", "esp_constraint_complete",
             "esp_constraint_forced_bytes", "esp_constraint_mask", "esp_model_load_streamed",
             "esp_model_layer_cache", "esp_model_resident_layers", "esp_model_streaming_stats",
+            "esp_stage_create", "esp_stage_destroy", "esp_stage_forward",
             "esp_profile_enable", "esp_profile_read"]
 
 

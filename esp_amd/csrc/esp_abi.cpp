@@ -4,6 +4,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -128,6 +129,68 @@ esp_status esp_model_streaming_stats(const esp_model *model, esp_streaming_stats
         }
         std::lock_guard<std::recursive_mutex> lk(keep->mu);
         stream_stats(m, out);
+    });
+}
+
+}  // extern "C"
+
+// One stage of a layer-range chain: its resident layers, its own
+// one-sequence KV cache and the position rules of stage.rs:471-527.
+struct esp_stage {
+    std::unique_ptr<Model> model;
+    std::unique_ptr<Kv> kv;
+    bool head = false;
+    int position = 0;
+    bool failed = false;
+    std::mutex mu;
+    ~esp_stage() {
+        (void)hipDeviceSynchronize();
+        kv.reset();  // before the model it refers to
+    }
+};
+
+extern "C" {
+
+esp_status esp_stage_create(const esp_config *config, uint32_t first, uint32_t end,
+                            const esp_layer_source *source, const esp_streaming_options *options,
+                            const uint8_t *shared, size_t shared_len, uint32_t max_ctx,
+                            esp_stage **out) {
+    return guard([&] {
+        if (!out) fail(ESP_INVALID_REQUEST, "null output handle");
+        *out = nullptr;
+        std::unique_ptr<esp_stage> st(new esp_stage());
+        st->model.reset(load_stage_model(config, first, end, source, options, shared, shared_len));
+        st->head = shared != nullptr;
+        const uint32_t ctx = max_ctx ? max_ctx : config->max_position_embeddings;
+        st->kv.reset(create_kv(st->model.get(), 1, ctx));
+        *out = st.release();
+    });
+}
+
+esp_status esp_stage_destroy(esp_stage *stage) {
+    return guard([&] { delete stage; });
+}
+
+esp_status esp_stage_forward(esp_stage *stage, const float *hidden, uint32_t seq, uint32_t start,
+                             float *out) {
+    return guard([&] {
+        if (!stage) fail(ESP_MODEL_NOT_LOADED, "stage not loaded");
+        esp_stage &st = *stage;
+        Model &m = *st.model;
+        if (!hidden || !out || seq == 0 || (uint64_t)start + seq > m.cfg.max_position_embeddings ||
+            (uint64_t)start + seq > (uint64_t)st.kv->max_ctx)
+            fail(ESP_INVALID_REQUEST, "stage hidden shape, dtype or context");
+        std::lock_guard<std::mutex> lk(st.mu);
+        if (start == 0) {  // a fresh generation rebuilds the stage's cache
+            st.position = 0;
+            st.failed = false;
+        }
+        if (st.failed || st.position != (int)start || (start != 0 && seq != 1))
+            fail(ESP_INVALID_REQUEST, "stage KV position mismatch; restart from checkpoint");
+        st.failed = true;  // a partial failure invalidates the cache until a prefill
+        forward_hidden(m, *st.kv, hidden, (int)seq, (int)start, out, st.head);
+        st.position += (int)seq;
+        st.failed = false;
     });
 }
 

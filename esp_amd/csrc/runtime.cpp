@@ -554,6 +554,66 @@ Model *load_streamed_model(const esp_config *cfg, const uint8_t *shared, size_t 
     return mp.release();
 }
 
+Model *load_stage_model(const esp_config *cfg, uint32_t first, uint32_t end,
+                        const esp_layer_source *source, const esp_streaming_options *opt,
+                        const uint8_t *shared, size_t shared_len) {
+    if (!cfg) fail(ESP_INVALID_CONFIG, "null config");
+    if (!source || !source->read_layer) fail(ESP_INVALID_REQUEST, "null layer source");
+    if (first >= end || end > cfg->num_hidden_layers)  // stage.rs:28-35
+        fail(ESP_INVALID_CONFIG, "empty or out-of-model stage range");
+    if (!opt || !opt->query_chunk || !opt->max_layer_bytes || !opt->max_shared_bytes)
+        fail(ESP_INVALID_CONFIG, "streaming limits must be positive");
+    validate_config(*cfg);
+    esp_config c = *cfg;  // the range as a model of its own
+    c.num_hidden_layers = end - first;
+    if (cfg->layer_window) c.layer_window = cfg->layer_window + first;
+    if (cfg->layer_is_moe) c.layer_is_moe = cfg->layer_is_moe + first;
+    std::unique_ptr<Model> mp(new Model());
+    Model &m = *mp;
+    init_model_shape(m, c);
+    if (m.E)
+        fail(ESP_UNSUPPORTED, "native expert streaming: routed-expert layers are not streamed by "
+                              "this library");
+    check_packed(m, 0);
+    for (auto &w : m.layers) w.qkv_rows = m.qw + 2 * m.kvw;
+    if (shared) {  // stage.rs:384-413 with_output: the final range owns norm and head
+        if (end != cfg->num_hidden_layers)
+            fail(ESP_INVALID_WEIGHTS, "only the final stage may own the output head");
+        if (shared_len > opt->max_shared_bytes)
+            fail(ESP_INVALID_WEIGHTS, "shared artifact exceeds its byte limit");
+        std::map<std::string, StTensor> tensors;
+        try {
+            tensors = parse_safetensors(shared, shared_len);
+        } catch (const Error &e) {
+            fail(ESP_INVALID_WEIGHTS, "shared tensors: " + e.msg);
+        }
+        for (auto &kv : tensors)
+            if (kv.first != "model.embed_tokens.weight" && kv.first != "model.norm.weight" &&
+                kv.first != "lm_head.weight")
+                fail(ESP_INVALID_WEIGHTS, "unexpected tensor in shared artifact");
+        Stager s{m, tensors, {}};
+        const uint64_t H = m.H;
+        m.final_norm = (float *)s.tensor("model.norm.weight", {H}, true);
+        if (s.has("lm_head.weight")) {  // an untied embedding is not kept
+            m.head = s.proj("lm_head.weight", (uint64_t)m.V, H, &m.head_s);
+        } else if (cfg->tie_word_embeddings) {
+            m.embed = s.tensor("model.embed_tokens.weight", {(uint64_t)m.V, H});
+            m.head = m.embed;
+            m.ht = m.et;
+        } else {
+            fail(ESP_INVALID_WEIGHTS, "lm_head.weight missing but tie_word_embeddings is false");
+        }
+    }
+    stage_rope(m);
+    streamer_init(m, *source, *opt, (int)first);
+    {
+        std::shared_ptr<Streamer> keep = m.st;
+        std::lock_guard<std::recursive_mutex> lk(keep->mu);
+        stream_make_resident(m);
+    }
+    return mp.release();
+}
+
 // Synthetic model: every projection / embedding N(0, std) from a seeded
 // device generator, norms 1, biases 0 (bench and large-shape tests).
 Model *synthetic_model(const esp_config *cfg, uint64_t seed, float std, uint32_t lora_rank,
@@ -1401,6 +1461,47 @@ void forward(Model &m, Kv &kv, int n_seqs, const uint32_t *seqs, const uint32_t 
     if (m.st) stream_check(m);  // a streamed layer that failed its device checks
     for (int i = 0; i < n_seqs; ++i) kv.pos[seqs[i]] += (int)lens[i];
     kv.logits_rows = n_seqs;
+}
+
+// A stage's forward (stage.rs:471-527): `hidden` [S, H] f32 enters the
+// range's first layer at absolute positions start..start+S of sequence 0;
+// `out` receives the last layer's hidden rows [S, H], or with `logits` the
+// final norm + head on the last row ([V] f32).
+void forward_hidden(Model &m, Kv &kv, const float *hidden, int S, int start, float *out,
+                    bool logits) {
+    hipStream_t s = kv.stream;
+    const int H = m.H;
+    ensure_scratch(m, kv, std::min(S, kMaxRows), 1);
+    const int lastoff = 3 * kMaxRows;
+    ensure_pinned(kv, (size_t)(3 * kMaxRows + kv.batch + 64) * 4);
+    int32_t *pin = (int32_t *)kv.pinned;
+    int32_t *dev = kv.rows_dev.as<int32_t>();
+    const int max_t = start + S;
+    for (int c0 = 0; c0 < S; c0 += kMaxRows) {
+        const int Mc = std::min(kMaxRows, S - c0);
+        ESP_HIP(hipStreamSynchronize(s));  // pinned staging buffer reuse
+        for (int r = 0; r < Mc; ++r) {
+            pin[r] = 0;
+            pin[kMaxRows + r] = 0;
+            pin[2 * kMaxRows + r] = start + c0 + r;
+        }
+        pin[lastoff] = Mc - 1;
+        ESP_HIP(hipMemcpyAsync(dev, pin, (size_t)(lastoff + 1) * 4, hipMemcpyHostToDevice, s));
+        ESP_HIP(hipMemcpyAsync(kv.h.p, hidden + (size_t)c0 * H, (size_t)Mc * H * 4,
+                               hipMemcpyHostToDevice, s));
+        Rows rows{dev, dev + kMaxRows, dev + 2 * kMaxRows, Mc, 0};
+        run_layers(m, kv, rows, Mc, max_t, 0, start + c0);
+        if (!logits) {
+            ESP_HIP(hipMemcpyAsync(out + (size_t)c0 * H, kv.h.p, (size_t)Mc * H * 4,
+                                   hipMemcpyDeviceToHost, s));
+        } else if (c0 + Mc == S) {
+            run_head(m, kv, 1, kv.h.as<float>() + (size_t)(Mc - 1) * H, nullptr);
+            ESP_HIP(hipMemcpyAsync(out, kv.logits.p, (size_t)m.V * 4, hipMemcpyDeviceToHost, s));
+        }
+    }
+    ESP_HIP(hipStreamSynchronize(s));
+    kv.pos[0] = start + S;
+    kv.logits_rows = logits ? 1 : 0;
 }
 
 }  // namespace esp

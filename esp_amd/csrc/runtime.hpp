@@ -139,5 +139,13 @@ bool check_packed_header(const Model &m, const std::string &name, const StTensor
 // shared artifact's embedding, final norm and head are staged here.
 Model *load_streamed_model(const esp_config *cfg, const uint8_t *shared, size_t len,
                            const esp_layer_source *source, const esp_streaming_options *opt);
+// One stage of a layer-range chain (stage.rs:280-527): layers first..end-1
+// read once from `source` and kept resident; with `shared`, the final
+// norm and output head.
+Model *load_stage_model(const esp_config *cfg, uint32_t first, uint32_t end,
+                        const esp_layer_source *source, const esp_streaming_options *opt,
+                        const uint8_t *shared, size_t shared_len);
+void forward_hidden(Model &m, Kv &kv, const float *hidden, int S, int start, float *out,
+                    bool logits);
 
 }  // namespace esp

@@ -257,8 +257,10 @@ static Plan plan_layer(const Model &m, const Streamer &st,
     return pl;
 }
 
-void streamer_init(Model &m, const esp_layer_source &src, const esp_streaming_options &opt) {
+void streamer_init(Model &m, const esp_layer_source &src, const esp_streaming_options &opt,
+                   int first) {
     auto st = std::make_shared<Streamer>();
+    st->first = first;
     st->src = src;
     st->opt = opt;
     st->lay = block_layout(m);
@@ -288,15 +290,16 @@ static LayerW stage_layer(Model &m, hipStream_t compute, int l, DevMem *perm, ui
     ESP_HIP(hipEventSynchronize(st.copied[sl]));  // this staging buffer's last transfer is done
     if (!st.stage[sl]) ESP_HIP(hipHostMalloc((void **)&st.stage[sl], st.stage_cap, hipHostMallocDefault));
     uint64_t len = 0;
-    const int rc = (int)st.src.read_layer(st.src.user, (uint32_t)l, st.opt.max_layer_bytes,
+    const int gl = l + st.first;  // the layer's index in the whole model
+    const int rc = (int)st.src.read_layer(st.src.user, (uint32_t)gl, st.opt.max_layer_bytes,
                                           st.stage[sl], st.stage_cap, &len);
     if (rc != ESP_OK)
         fail(rc > 0 && rc <= ESP_UNSUPPORTED ? (esp_status)rc : ESP_BACKEND,
-             "layer " + std::to_string(l) + ": layer source read failed");
+             "layer " + std::to_string(gl) + ": layer source read failed");
     if (len > st.opt.max_layer_bytes)
         fail(ESP_INVALID_WEIGHTS, "layer source exceeded its byte limit");
     if (len > st.stage_cap)
-        fail(ESP_INVALID_WEIGHTS, "layer " + std::to_string(l) + ": artifact of " +
+        fail(ESP_INVALID_WEIGHTS, "layer " + std::to_string(gl) + ": artifact of " +
                                       std::to_string(len) +
                                       " bytes exceeds the declared block's encoded size");
     ++st.reads;
@@ -306,9 +309,9 @@ static LayerW stage_layer(Model &m, hipStream_t compute, int l, DevMem *perm, ui
     try {
         t = parse_safetensors(st.stage[sl], (size_t)len);
     } catch (const Error &e) {
-        fail(ESP_INVALID_WEIGHTS, "layer " + std::to_string(l) + ": " + e.msg);
+        fail(ESP_INVALID_WEIGHTS, "layer " + std::to_string(gl) + ": " + e.msg);
     }
-    Plan pl = plan_layer(m, st, t, l);
+    Plan pl = plan_layer(m, st, t, gl);
     if (st.tag_names.empty()) {
         st.tag_names = pl.tags;
         st.tag_scales = pl.tag_scales;
@@ -398,7 +401,7 @@ void stream_check(Model &m) {
         std::vector<int> clean(m.L, INT_MAX);
         ESP_HIP(hipMemcpy(st.bad.p, clean.data(), (size_t)m.L * 4, hipMemcpyHostToDevice));
         const int tag = bad[l];
-        const std::string name = "model.layers." + std::to_string(l) + "." +
+        const std::string name = "model.layers." + std::to_string(l + st.first) + "." +
                                  (tag < (int)st.tag_names.size() ? st.tag_names[tag] : "?");
         if (tag < (int)st.tag_scales.size() && st.tag_scales[tag])
             fail(ESP_INVALID_WEIGHTS, "weight format: packed projection byte count or block scales "

@@ -58,6 +58,7 @@ struct StreamEntry {
 
 struct Streamer {
     esp_layer_source src{};
+    int first = 0;  // global index of local layer 0 (a stage's range start)
     esp_streaming_options opt{};
     BlockLayout lay;
     // logical verified reads (streaming.rs:228-252)
@@ -83,7 +84,8 @@ struct Streamer {
     ~Streamer();
 };
 
-void streamer_init(Model &m, const esp_layer_source &src, const esp_streaming_options &opt);
+void streamer_init(Model &m, const esp_layer_source &src, const esp_streaming_options &opt,
+                   int first = 0);
 // The weights of layer l for a forward on kv's stream: a cached block, or
 // the layer read through the source and staged into the next transient
 // block. stream_release marks the end of the layer's kernels.

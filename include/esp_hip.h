@@ -150,7 +150,8 @@ esp_status esp_model_weight_bytes(const esp_model *model, uint64_t *bytes);
 
 /* model.rs:476-483 DecoderModel::new_cache, for `batch` independent
  * sequences of up to `max_ctx` positions each (max_ctx <=
- * max_position_embeddings). Contiguous per-sequence bf16 (or f32) KV. */
+ * max_position_embeddings). Contiguous per-sequence f32 keys and values
+ * (every weight format). */
 esp_status esp_kv_create(esp_model *model, uint32_t batch, uint32_t max_ctx, esp_kv **out);
 esp_status esp_kv_destroy(esp_kv *kv);
 /* Forget sequence `seq` (or every sequence when seq == UINT32_MAX). */
@@ -265,6 +266,35 @@ typedef struct esp_streaming_stats {
     uint64_t cached_layers;
 } esp_streaming_stats;
 esp_status esp_model_streaming_stats(const esp_model *model, esp_streaming_stats *out);
+
+/* ---- Stage chain (decoder/stage.rs) ---- */
+
+typedef struct esp_stage esp_stage;
+
+/* stage.rs:301-372 DecoderStage::from_source (+ :384-413 with_output when
+ * `shared` is non-NULL): layers first..end-1 read once through `source`
+ * (artifacts named model.layers.{i}.*, checked as esp_model_load_streamed
+ * checks them) and kept in HBM, with a one-sequence KV cache of max_ctx
+ * positions (0 = max_position_embeddings). Only the final range
+ * (end == num_hidden_layers) may take `shared`, whose final norm and head
+ * it then owns. first >= end or end beyond the model -> ESP_INVALID_CONFIG
+ * "empty or out-of-model stage range". */
+esp_status esp_stage_create(const esp_config *config, uint32_t first, uint32_t end,
+                            const esp_layer_source *source, const esp_streaming_options *options,
+                            const uint8_t *shared, size_t shared_len, uint32_t max_ctx,
+                            esp_stage **out);
+esp_status esp_stage_destroy(esp_stage *stage);
+
+/* stage.rs:471-527 StageExecutor::forward: hidden [seq, hidden_size] f32
+ * (host memory, the f32 hidden wire's values) at absolute positions
+ * start..start+seq. start 0 restarts the stage's cache; otherwise start
+ * must equal the stage's position and seq must be 1, and a stage whose
+ * last forward failed refuses until a restart (ESP_INVALID_REQUEST "stage
+ * KV position mismatch; restart from checkpoint"). `out` receives the
+ * hidden rows [seq, hidden_size], or for a stage with the output head the
+ * last position's logits [vocab_size] (f32). */
+esp_status esp_stage_forward(esp_stage *stage, const float *hidden, uint32_t seq, uint32_t start,
+                             float *out);
 
 /* ---- Constrained decoding (decoder/constraint.rs) ----
  * A vocabulary holds the byte string of every token id of a byte-level

@@ -1,0 +1,77 @@
+"""Stage chain (stage.rs) on the MI355X: disjoint layer-range stages chained
+through the f32 hidden wire give the resident model's logits bit for bit
+(the same kernels over the same weights; the resident model is pinned to
+the oracle by the parity tests), and enforce the reference's positions."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from esp_amd import DecoderModel, InvalidConfig, InvalidRequest, InvalidWeights
+from esp_amd.stage import (DecoderStage, LayerRange, StageChain, StagedModel, decode_hidden,
+                           encode_hidden)
+from esp_amd.streaming import ArtifactSource, split_checkpoint
+from oracle import st
+from tests import synth
+
+pytestmark = pytest.mark.gpu
+
+
+def _case(art, layers=3):
+    cfg = synth.llama_config(layers, 128, 4, 2, 256, 300, head_dim=32)
+    blob = st.dump(synth.make_tensors(cfg, 21, art, std=0.05))
+    return cfg, blob
+
+
+@pytest.mark.parametrize("fmt", ["f32", "bf16"])
+def test_disjoint_stages_match_the_resident_model(fmt):
+    print(f"stages {fmt}", flush=True)
+    cfg, blob = _case(fmt)
+    shared, layers = split_checkpoint(blob, cfg)
+    src = ArtifactSource(layers)
+    first = DecoderStage.from_source(cfg, LayerRange(0, 1), src, fmt=fmt, max_ctx=64)
+    last = DecoderStage.from_source(cfg, LayerRange(1, 3), src, fmt=fmt, shared=shared, max_ctx=64)
+    staged = StagedModel(cfg, shared, StageChain([first, last]))
+    resident = DecoderModel.from_bytes(cfg, blob, fmt)
+    kv = resident.new_cache(1, 64)
+    prompt = synth.uniform_ids(3, 9, cfg.vocab_size)
+    want = resident.try_forward_cached_last(prompt, kv)
+    got = staged.try_forward_cached_last(prompt)
+    assert np.array_equal(got, want)
+    for _ in range(3):
+        t = int(np.argmax(want))
+        want = resident.try_forward_cached_last([t], kv)
+        got = staged.try_forward_cached_last([t])
+        assert np.array_equal(got, want)
+    # a restart at 0 rebuilds every stage's cache
+    staged.reset()
+    assert np.array_equal(staged.try_forward_cached_last(prompt),
+                          resident.try_forward_cached_last(prompt, resident.new_cache(1, 64)))
+
+
+def test_stage_positions_wire_and_ownership():
+    cfg, blob = _case("f32")
+    shared, layers = split_checkpoint(blob, cfg)
+    src = ArtifactSource(layers)
+    first = DecoderStage.from_source(cfg, LayerRange(0, 2), src, max_ctx=32)
+    x = np.random.default_rng(0).standard_normal((3, cfg.hidden_size)).astype(np.float32) * 0.1
+    h0 = first.forward(x, 0)
+    assert h0.shape == (3, cfg.hidden_size)
+    with pytest.raises(InvalidRequest, match="position mismatch"):
+        first.forward(x[:1], 4)
+    with pytest.raises(InvalidRequest, match="position mismatch"):
+        first.forward(x[:2], 3)  # only single tokens after the prefill
+    first.forward(x[:1], 3)
+    assert np.array_equal(first.forward(x, 0), h0)  # restart: same rows
+    # the wire form of the same call
+    wire = first.forward_bytes(encode_hidden(x, 1 << 20), 0, 1 << 20)
+    assert np.array_equal(decode_hidden(wire, cfg.hidden_size, 64), h0)
+    with pytest.raises(InvalidRequest, match="hidden wire budget"):
+        first.forward_bytes(encode_hidden(x, 1 << 20), 0, 64)
+    with pytest.raises(InvalidWeights, match="only the final stage may own the output head"):
+        DecoderStage.from_source(cfg, LayerRange(0, 2), src, shared=shared)
+    with pytest.raises(InvalidConfig, match="empty or out-of-model stage range"):
+        DecoderStage.from_source(cfg, LayerRange(1, 4), src)
+    with pytest.raises(InvalidConfig, match="contiguous"):
+        last = DecoderStage.from_source(cfg, LayerRange(2, 3), src, shared=shared)
+        StageChain([DecoderStage.from_source(cfg, LayerRange(0, 1), src), last])
