@@ -144,6 +144,13 @@ void launch_pick(const PickArgs &a, hipStream_t s);
 size_t pick_scratch_bytes(int n, int V);
 
 // Packed weights: out[i] = q_i * scale[i / 32] in f32 (n a multiple of 32).
+// Packed [N, K] -> bf16 [N, 2K] rows [hi(q*scale) | lo(q*scale)], and split
+// activation planes [M, K] -> [M, 2K] ([hi | hi], [lo | 0]): the doubled-K
+// form of a packed projection for the bf16 matrix-core GEMM.
+void launch_dequant_split(Dt wt, const void *values, const float *scales, size_t N, size_t K,
+                          uint16_t *out, hipStream_t s);
+void launch_widen_split(const uint16_t *hi, const uint16_t *lo, size_t M, size_t K, uint16_t *hi2,
+                        uint16_t *lo2, hipStream_t s);
 void launch_dequant(Dt wt, const void *values, const float *scales, size_t n, float *out,
                     hipStream_t s);
 // decoder/weight_format.rs:150-183 on the device: rows x cols f32 (cols a

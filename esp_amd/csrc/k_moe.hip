@@ -268,6 +268,67 @@ void launch_dequant(Dt wt, const void *values, const float *scales, size_t n, fl
     else dequant_k<false><<<blocks, 256, 0, s>>>(values, scales, n, out);
 }
 
+// A packed projection [N, K] as the two bf16 planes of a doubled-K matrix
+// for the matrix cores: row n = [hi(w) | lo(w)] with w = q * scale (f32,
+// the format's definition), hi = bf16(w), lo = bf16(w - hi), so hi + lo
+// holds w to ~2^-17 relative. Multiplied against activation rows
+// [a_hi | a_hi] (hi plane) and [a_lo | 0] (lo plane), the bf16 GEMM sums
+// a_hi w_hi + a_lo w_hi + a_hi w_lo over the original K.
+template <bool Q4>
+__global__ void __launch_bounds__(256) dequant_split_k(const void *values, const float *scales,
+                                                       size_t N, size_t K, uint16_t *out) {
+    const size_t n_all = N * K;
+    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n_all;
+         i += (size_t)gridDim.x * blockDim.x) {
+        int q;
+        if (Q4) {
+            const uint8_t b = ((const uint8_t *)values)[i >> 1];
+            q = ((int)((unsigned)b << (28 - 4 * (int)(i & 1)))) >> 28;
+        } else {
+            q = ((const int8_t *)values)[i];
+        }
+        const float w = (float)q * scales[i >> 5];
+        const uint16_t h = f2bf(w);
+        const size_t n = i / K, k = i - n * K;
+        out[n * 2 * K + k] = h;
+        out[n * 2 * K + K + k] = f2bf(w - bf2f(h));
+    }
+}
+
+void launch_dequant_split(Dt wt, const void *values, const float *scales, size_t N, size_t K,
+                          uint16_t *out, hipStream_t s) {
+    if (!N || !K) return;
+    int blocks = (int)std::min<size_t>((N * K + 255) / 256, 65536);
+    if (wt == DT_Q4) dequant_split_k<true><<<blocks, 256, 0, s>>>(values, scales, N, K, out);
+    else dequant_split_k<false><<<blocks, 256, 0, s>>>(values, scales, N, K, out);
+}
+
+// Split activation planes [M, K] widened for the doubled-K product above:
+// hi2 = [hi | hi], lo2 = [lo | 0], both [M, 2K]; four bf16 per lane.
+__global__ void __launch_bounds__(256) widen_split_k(const uint16_t *hi, const uint16_t *lo,
+                                                     size_t M, size_t K, uint16_t *hi2,
+                                                     uint16_t *lo2) {
+    const size_t q = K / 4, n_all = M * q;
+    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n_all;
+         i += (size_t)gridDim.x * blockDim.x) {
+        const size_t m = i / q, c = (i - m * q) * 4;
+        const uint2 h = *(const uint2 *)(hi + m * K + c);
+        const uint2 l = *(const uint2 *)(lo + m * K + c);
+        *(uint2 *)(hi2 + m * 2 * K + c) = h;
+        *(uint2 *)(hi2 + m * 2 * K + K + c) = h;
+        *(uint2 *)(lo2 + m * 2 * K + c) = l;
+        *(uint2 *)(lo2 + m * 2 * K + K + c) = make_uint2(0u, 0u);
+    }
+}
+
+void launch_widen_split(const uint16_t *hi, const uint16_t *lo, size_t M, size_t K, uint16_t *hi2,
+                        uint16_t *lo2, hipStream_t s) {
+    if (!M || !K) return;
+    if (K % 4) fail(ESP_BACKEND, "widen_split: K must be a multiple of 4");
+    int blocks = (int)std::min<size_t>((M * K / 4 + 255) / 256, 65536);
+    widen_split_k<<<blocks, 256, 0, s>>>(hi, lo, M, K, hi2, lo2);
+}
+
 // weight_format.rs:150-183, one thread per 32-input block: scale = peak /
 // max (1 for an all-zero block, at least the smallest normal f32), q =
 // round-half-away(v / scale) clamped to [-max, max]; q4 packs two per byte,

@@ -800,6 +800,28 @@ static const void *gemm_w(Kv &kv, int slot, Dt wt, const void *w, const float *w
     return d.p;
 }
 static Dt gemm_dt(Dt wt) { return dt_packed(wt) ? DT_F32 : wt; }
+// Layer GEMMs of packed models run on the matrix cores in doubled-K form:
+// weights dequantized to [N, 2K] bf16 rows [hi | lo] (kernel comment in
+// k_moe.hip), activations (split planes) widened to [hi | hi], [lo | 0].
+static const void *gemm_w_split(Kv &kv, int slot, Dt wt, const void *w, const float *ws, size_t N,
+                                size_t K) {
+    if (!dt_packed(wt)) return w;
+    DevMem &d = kv.deq[slot];
+    d.ensure(N * K * 4);
+    launch_dequant_split(wt, w, ws, N, K, d.as<uint16_t>(), kv.stream);
+    return d.p;
+}
+static Dt layer_gemm_dt(Dt wt) { return dt_packed(wt) ? DT_BF16 : wt; }
+static void widen_k(const Model &m, Kv &kv, GemmArgs &g) {
+    if (!dt_packed(m.wt)) return;
+    const size_t M = g.M, K = g.K;
+    kv.wide.ensure(M * K * 8);
+    uint16_t *hi2 = kv.wide.as<uint16_t>(), *lo2 = hi2 + M * 2 * K;
+    launch_widen_split((const uint16_t *)g.a, (const uint16_t *)g.a_lo, M, K, hi2, lo2, kv.stream);
+    g.a = hi2;
+    g.a_lo = lo2;
+    g.K = (int)(2 * K);
+}
 // element type of LoRA B rows (packed formats carry no LoRA)
 static Dt lora_dt(Dt wt) { return dt_packed(wt) ? DT_F32 : wt; }
 
@@ -1045,7 +1067,7 @@ static void run_layers(Model &m, Kv &kv, const Rows &rows, int Mc, int max_t, in
     const bool single = Mc == 1;
     // activations keep f32 precision; bf16 models hand them to the matrix
     // cores as split hi/lo bf16 planes, f32 models as plain f32
-    const Dt act = m.wt == DT_BF16 ? DT_SPLIT : DT_F32;
+    const Dt act = m.wt == DT_BF16 || dt_packed(m.wt) ? DT_SPLIT : DT_F32;
     const int H = m.H;
     const bool dec_attn = use_attn_decode(m, kv, Mc);
     Plan plan = attn_plan(m, Mc, max_t);
@@ -1094,7 +1116,7 @@ static void run_layers(Model &m, Kv &kv, const Rows &rows, int Mc, int max_t, in
             g.ws_bytes = kv.gemm_ws.bytes;
             g.a = kv.xn.p;
             g.a_lo = lo_plane(act, kv.xn, Mc, H);
-            g.w = gemm_w(kv, 0, m.wt, w.qkv, w.qkv_s, w.qkv_rows, H);
+            g.w = gemm_w_split(kv, 0, m.wt, w.qkv, w.qkv_s, w.qkv_rows, H);
             g.bias = w.qkv_bias;
             g.c = kv.qkv.p;
             g.M = Mc;
@@ -1102,7 +1124,8 @@ static void run_layers(Model &m, Kv &kv, const Rows &rows, int Mc, int max_t, in
             g.K = H;
             g.ldc = w.qkv_rows;
             Prof p("gemm_qkv", s);
-            launch_gemm(gemm_dt(m.wt), GEMM_STORE, g, s);
+            widen_k(m, kv, g);
+            launch_gemm(layer_gemm_dt(m.wt), GEMM_STORE, g, s);
         }
         {
             RopeKvArgs r{};
@@ -1132,7 +1155,7 @@ static void run_layers(Model &m, Kv &kv, const Rows &rows, int Mc, int max_t, in
             Prof p("rope_kv", s);
             launch_rope_kv(lora_dt(m.wt), kv.dt, r, s);
         }
-        bool seg_flash = segs && !segs->empty() && m.wt == DT_BF16 && flash_ok(m.hd);
+        bool seg_flash = segs && !segs->empty() && act == DT_SPLIT && flash_ok(m.hd);
         for (size_t i = 0; seg_flash && i < segs->size(); ++i) seg_flash = (*segs)[i].len >= 16;
         if (seg_flash) {
             // several sequences' prompt blocks: the tiled MFMA attention per block
@@ -1158,7 +1181,7 @@ static void run_layers(Model &m, Kv &kv, const Rows &rows, int Mc, int max_t, in
                 f.out_lo = lo ? lo + (size_t)g.row0 * m.qw : nullptr;
                 launch_flash(f, s);
             }
-        } else if (one_seq >= 0 && Mc >= 16 && m.wt == DT_BF16 && flash_ok(m.hd)) {
+        } else if (one_seq >= 0 && Mc >= 16 && act == DT_SPLIT && flash_ok(m.hd)) {
             // rows are consecutive positions of one sequence: tiled MFMA attention
             FlashArgs f{};
             f.q = kv.q.as<float>();
@@ -1217,7 +1240,7 @@ static void run_layers(Model &m, Kv &kv, const Rows &rows, int Mc, int max_t, in
             g.ws_bytes = kv.gemm_ws.bytes;
             g.a = kv.attn.p;
             g.a_lo = lo_plane(act, kv.attn, Mc, m.qw);
-            g.w = gemm_w(kv, 0, m.wt, w.o, w.o_s, H, m.qw);
+            g.w = gemm_w_split(kv, 0, m.wt, w.o, w.o_s, H, m.qw);
             g.bias = w.o_bias;
             g.c = kv.h.p;
             g.M = Mc;
@@ -1225,7 +1248,8 @@ static void run_layers(Model &m, Kv &kv, const Rows &rows, int Mc, int max_t, in
             g.K = m.qw;
             g.ldc = H;
             Prof p("gemm_o", s);
-            launch_gemm(gemm_dt(m.wt), GEMM_RESIDUAL, g, s);
+            widen_k(m, kv, g);
+            launch_gemm(layer_gemm_dt(m.wt), GEMM_RESIDUAL, g, s);
         }
         // ---- MLP block (layer.rs:147-151)
         if (w.moe) {
@@ -1263,8 +1287,8 @@ static void run_layers(Model &m, Kv &kv, const Rows &rows, int Mc, int max_t, in
             g.ws_bytes = kv.gemm_ws.bytes;
             g.a = kv.xn.p;
             g.a_lo = lo_plane(act, kv.xn, Mc, H);
-            g.w = gemm_w(kv, 0, m.wt, w.gate, w.gate_s, m.F, H);
-            g.w2 = gemm_w(kv, 1, m.wt, w.up, w.up_s, m.F, H);
+            g.w = gemm_w_split(kv, 0, m.wt, w.gate, w.gate_s, m.F, H);
+            g.w2 = gemm_w_split(kv, 1, m.wt, w.up, w.up_s, m.F, H);
             g.c = kv.act.p;
             g.c_lo = lo_plane(act, kv.act, Mc, m.F);
             g.M = Mc;
@@ -1273,21 +1297,23 @@ static void run_layers(Model &m, Kv &kv, const Rows &rows, int Mc, int max_t, in
             g.ldc = m.F;
             {
                 Prof p("gemm_mlp", s);
-                launch_gemm(gemm_dt(m.wt), GEMM_SWIGLU, g, s);
+                widen_k(m, kv, g);
+                launch_gemm(layer_gemm_dt(m.wt), GEMM_SWIGLU, g, s);
             }
             GemmArgs d{};
             d.ws = kv.gemm_ws.as<float>();
             d.ws_bytes = kv.gemm_ws.bytes;
             d.a = kv.act.p;
             d.a_lo = lo_plane(act, kv.act, Mc, m.F);
-            d.w = gemm_w(kv, 0, m.wt, w.down, w.down_s, H, m.F);
+            d.w = gemm_w_split(kv, 0, m.wt, w.down, w.down_s, H, m.F);
             d.c = kv.h.p;
             d.M = Mc;
             d.N = H;
             d.K = m.F;
             d.ldc = H;
             Prof p("gemm_down", s);
-            launch_gemm(gemm_dt(m.wt), GEMM_RESIDUAL, d, s);
+            widen_k(m, kv, d);
+            launch_gemm(layer_gemm_dt(m.wt), GEMM_RESIDUAL, d, s);
         }
     }
 }
@@ -1307,7 +1333,8 @@ static void ensure_scratch(Model &m, Kv &kv, int Mc, int n_seqs) {
     kv.last_h.ensure((size_t)n_seqs * H * 4);
     kv.logits.ensure((size_t)std::max(n_seqs, kv.batch) * m.V * 4);
     kv.rows_dev.ensure((size_t)(3 * kMaxRows + 2 * kv.batch + 64) * 4);
-    if (Mc > 1 && m.wt == DT_BF16) kv.gemm_ws.ensure((size_t)256 << 20);  // split-K partials
+    if (Mc > 1 && (m.wt == DT_BF16 || dt_packed(m.wt)))
+        kv.gemm_ws.ensure((size_t)256 << 20);  // split-K partials
 }
 
 // Head on the last row of each sequence (model.rs:531-538): final RMSNorm

@@ -109,7 +109,8 @@ struct Kv {
     DevMem rows_dev;   // ids | row_seq | row_pos | last_row  (int32)
     DevMem h, xn, qkv, q, attn, act, part, last_h, logits, pick_scratch, pick_io;
     DevMem gemm_ws;  // split-K partial sums of the prefill GEMMs
-    DevMem deq[2];   // packed formats: f32 weights of the GEMMs in flight
+    DevMem deq[2];   // packed formats: dequantized weights of the GEMMs in flight
+    DevMem wide;     // packed formats: activation planes widened to the doubled K
     DevMem tickets;  // zeroed counters for last-block merges (attention, head argmax)
     DevMem moe_logits, moe_sel, moe_w, moe_slot, moe_offs, moe_perm, moe_x, moe_y, moe_ys, moe_sg,
         moe_act;
