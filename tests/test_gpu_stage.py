@@ -75,3 +75,29 @@ def test_stage_positions_wire_and_ownership():
     with pytest.raises(InvalidConfig, match="contiguous"):
         last = DecoderStage.from_source(cfg, LayerRange(2, 3), src, shared=shared)
         StageChain([DecoderStage.from_source(cfg, LayerRange(0, 1), src), last])
+
+
+def test_stage_windows_follow_the_global_layer_index():
+    """A qwen2 config whose layers from index 1 on use a 4-token sliding
+    window (config.rs:467-485): a stage over layers 1..3 must apply the
+    windows of global layers 1 and 2, so the chain stays bit-identical to
+    the resident model past the window."""
+    cfg = synth.llama_config(3, 128, 4, 2, 256, 300, head_dim=32, extra={
+        "model_type": "qwen2", "architectures": ["Qwen2ForCausalLM"], "use_sliding_window": True,
+        "sliding_window": 4, "max_window_layers": 1})
+    assert cfg.layer_window(0) is None and cfg.layer_window(1) == 4
+    blob = st.dump(synth.make_tensors(cfg, 23, "bf16", std=0.05, bias_std=0.05))
+    shared, layers = split_checkpoint(blob, cfg)
+    src = ArtifactSource(layers)
+    chain = StageChain([DecoderStage.from_source(cfg, LayerRange(0, 1), src, fmt="bf16", max_ctx=64),
+                        DecoderStage.from_source(cfg, LayerRange(1, 3), src, fmt="bf16",
+                                                 shared=shared, max_ctx=64)])
+    staged = StagedModel(cfg, shared, chain)
+    resident = DecoderModel.from_bytes(cfg, blob, "bf16")
+    kv = resident.new_cache(1, 64)
+    prompt = synth.uniform_ids(5, 20, cfg.vocab_size)
+    want = resident.try_forward_cached_last(prompt, kv)
+    assert np.array_equal(staged.try_forward_cached_last(prompt), want)
+    for t in (7, 8, 9):
+        assert np.array_equal(staged.try_forward_cached_last([t]),
+                              resident.try_forward_cached_last([t], kv))

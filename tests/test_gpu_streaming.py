@@ -42,6 +42,9 @@ CASES = [
     ("f32", "bf16", None, 0.0),  # f32 model from bf16 artifacts: widened on the device
     ("bf16", "bf16", {"model_type": "qwen2", "architectures": ["Qwen2ForCausalLM"]}, 0.05),
     ("f32", "f32", {"model_type": "qwen3", "architectures": ["Qwen3ForCausalLM"]}, 0.0),
+    # sliding window of 4 on layers 1.. (config.rs:467-485), past the window
+    ("bf16", "bf16", {"model_type": "qwen2", "architectures": ["Qwen2ForCausalLM"],
+                      "use_sliding_window": True, "sliding_window": 4, "max_window_layers": 1}, 0.0),
 ]
 
 
