@@ -363,3 +363,159 @@ class SourceBridge:
     def take(self) -> Optional[BaseException]:
         e, self.error = self.error, None
         return e
+
+
+# ---- esp.layer-weights index objects (layer_library.rs:16-152) ----
+# Blob ids come from the reference's content-addressed store (eidetic
+# ManifestId, not in this build): they are kept as opaque strings and the
+# reader given to IndexedSource verifies content identity.
+
+WEIGHT_FORMATS = ("f32", "f16", "bf16", "q8-k32-f32-scale-f16-shared-v1",
+                  "q4-k32-f32-scale-f16-shared-v1")  # weight_format.rs:20-32 serde names
+
+
+def _strict(raw, names: Sequence[str], what: str) -> dict:
+    """serde(deny_unknown_fields) with every field required."""
+    if not isinstance(raw, dict) or set(raw) != set(names):
+        raise InvalidWeights(f"layer library: {what} fields must be exactly {sorted(names)}")
+    return raw
+
+
+def _uint(v, what: str) -> int:
+    if not isinstance(v, int) or isinstance(v, bool) or v < 0:
+        raise InvalidWeights(f"layer library: {what} must be an unsigned integer")
+    return v
+
+
+@dataclass(frozen=True)
+class LayerArtifact:
+    """layer_library.rs:105-140: one verified artifact by blob id and size."""
+
+    blob: str
+    byte_size: int
+
+    def to_json(self) -> dict:
+        return {"blob": self.blob, "byte_size": self.byte_size}
+
+    @staticmethod
+    def from_json(raw) -> "LayerArtifact":
+        r = _strict(raw, ("blob", "byte_size"), "artifact")
+        if not isinstance(r["blob"], str) or not r["blob"]:
+            raise InvalidWeights("layer library: artifact blob must be a non-empty id")
+        return LayerArtifact(r["blob"], _uint(r["byte_size"], "byte_size"))
+
+
+@dataclass(frozen=True)
+class LayerWeightIndex:
+    """layer_library.rs:140-152 (schema esp.layer-weights/v1): the shared
+    artifact, one artifact per layer in order, and the streaming limits."""
+
+    shared: LayerArtifact
+    layers: Tuple[LayerArtifact, ...]
+    options: StreamingOptions
+
+    def to_json(self) -> dict:
+        return {"shared": self.shared.to_json(), "layers": [a.to_json() for a in self.layers],
+                "options": asdict(self.options)}
+
+    @staticmethod
+    def from_json(raw) -> "LayerWeightIndex":
+        r = _strict(raw, ("shared", "layers", "options"), "layer index")
+        if not isinstance(r["layers"], list):
+            raise InvalidWeights("layer library: layers must be a list")
+        opts = StreamingOptions.from_json(json.dumps(r["options"]))
+        return LayerWeightIndex(LayerArtifact.from_json(r["shared"]),
+                                tuple(LayerArtifact.from_json(a) for a in r["layers"]), opts)
+
+
+@dataclass(frozen=True)
+class PromptDeviation:
+    """layer_library.rs:34-45"""
+
+    rendered_prompt: str
+    baseline_tokens: Tuple[int, ...]
+    format_tokens: Tuple[int, ...]
+    logit_rmse: float
+    logit_max_abs: float
+
+
+@dataclass(frozen=True)
+class FormatQualification:
+    """layer_library.rs:46-88: the measurement a formatted candidate needs
+    before a resident may select it."""
+
+    baseline_model: str
+    baseline_loader: str
+    measured_loader: str
+    prompts: Tuple[PromptDeviation, ...]
+    encoded_weight_bytes: int
+    weight_payload_bytes: int
+    streaming_resident_payload_bytes: int
+    largest_layer_bytes: int
+    logical_stream_bytes: int
+    elapsed_seconds: float
+
+    def validate(self) -> None:
+        fin = lambda x: isinstance(x, (int, float)) and np.isfinite(x)  # noqa: E731
+        bad = (not self.baseline_loader or not self.measured_loader or not self.prompts
+               or self.encoded_weight_bytes == 0 or self.weight_payload_bytes == 0
+               or self.streaming_resident_payload_bytes == 0 or self.largest_layer_bytes == 0
+               or self.logical_stream_bytes == 0 or not fin(self.elapsed_seconds)
+               or self.elapsed_seconds <= 0.0)
+        for p in self.prompts:
+            bad = bad or (not p.rendered_prompt or not p.baseline_tokens or not p.format_tokens
+                          or not fin(p.logit_rmse) or p.logit_rmse < 0.0
+                          or not fin(p.logit_max_abs) or p.logit_max_abs < p.logit_rmse)
+        if bad:
+            raise InvalidWeights("layer library: incomplete or non-finite format qualification")
+
+
+@dataclass(frozen=True)
+class FormattedLayerWeightIndex:
+    """layer_library.rs:89-103 (schema esp.layer-weights/v2): an explicit
+    execution format over exact layer artifacts, with the source artifacts
+    and an optional measured qualification."""
+
+    weights: LayerWeightIndex
+    format: str
+    source_artifacts: Tuple[str, ...]
+    qualification: Optional[FormatQualification] = None
+
+    def __post_init__(self):
+        if self.format not in WEIGHT_FORMATS:
+            raise InvalidWeights(f"layer library: unknown weight format {self.format!r}")
+
+    def selectable(self) -> bool:
+        """A candidate cannot be selected by the resident until measured."""
+        if self.qualification is None:
+            return False
+        self.qualification.validate()
+        return True
+
+
+class IndexedSource(LayerSource):
+    """Reads a LayerWeightIndex's artifacts through ``read(blob, size)``
+    (the host's verified store reader), checking each declared size against
+    the caller's limit before reading and the bytes against the declared
+    size after (layer_library.rs:115-139)."""
+
+    def __init__(self, index: LayerWeightIndex, read: Callable[[str, int], bytes]):
+        self.index = index
+        self._read = read
+
+    def _fetch(self, art: LayerArtifact, limit: int) -> bytes:
+        if art.byte_size > limit:
+            raise InvalidWeights("layer library: layer artifact identity, schema or byte limit "
+                                 "mismatch")
+        data = self._read(art.blob, art.byte_size)
+        if len(data) != art.byte_size:
+            raise InvalidWeights("layer library: layer artifact bytes do not match their reference")
+        return data
+
+    def shared(self) -> bytes:
+        return self._fetch(self.index.shared, self.index.options.max_shared_bytes)
+
+    def read_layer(self, index: int, limit: int) -> bytes:
+        if index >= len(self.index.layers):
+            raise InvalidWeights(f"layer library: missing layer artifact {index}")
+        return self._fetch(self.index.layers[index], limit)

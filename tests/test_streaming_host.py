@@ -112,3 +112,49 @@ def test_split_checkpoint_keeps_exact_tensors_per_artifact():
     t["model.layers.0.extra.weight"] = (np.zeros(4, np.float32), "F32")
     with pytest.raises(InvalidWeights, match="tensor names do not match"):
         split_checkpoint(st.dump(t), cfg)
+
+
+def test_layer_index_round_trip_and_strict_fields():
+    from esp_amd.streaming import IndexedSource, LayerArtifact, LayerWeightIndex
+    idx = LayerWeightIndex(LayerArtifact("blob-s", 4), (LayerArtifact("b0", 3), LayerArtifact("b1", 5)),
+                           StreamingOptions(8, 16, 32))
+    raw = idx.to_json()
+    assert LayerWeightIndex.from_json(raw) == idx
+    bad = dict(raw, extra=1)
+    with pytest.raises(InvalidWeights):
+        LayerWeightIndex.from_json(bad)
+    bad = dict(raw, shared={"blob": "x"})
+    with pytest.raises(InvalidWeights):
+        LayerWeightIndex.from_json(bad)
+    store = {"blob-s": b"ssss", "b0": b"abc", "b1": b"wrong"}
+    src = IndexedSource(idx, lambda blob, size: store[blob])
+    assert src.shared() == b"ssss" and src.read_layer(0, 16) == b"abc"
+    with pytest.raises(InvalidWeights, match="byte limit mismatch"):
+        src.read_layer(1, 4)  # declared 5 > limit 4: refused before reading
+    store["b1"] = b"1234"
+    with pytest.raises(InvalidWeights, match="do not match their reference"):
+        src.read_layer(1, 16)
+    with pytest.raises(InvalidWeights, match="missing layer artifact 2"):
+        src.read_layer(2, 16)
+
+
+def test_format_qualification_rules():
+    """layer_library.rs:61-87: every measure present, finite and consistent;
+    unmeasured candidates are not selectable."""
+    from esp_amd.streaming import (FormatQualification, FormattedLayerWeightIndex, LayerArtifact,
+                                   LayerWeightIndex, PromptDeviation)
+    idx = LayerWeightIndex(LayerArtifact("s", 1), (), StreamingOptions())
+    p = PromptDeviation("hi", (1, 2), (1, 3), 0.1, 0.5)
+    q = FormatQualification("base", "bf16", "q8", (p,), 1, 2, 3, 4, 5, 1.5)
+    q.validate()
+    f = FormattedLayerWeightIndex(idx, "q8-k32-f32-scale-f16-shared-v1", ("src",), None)
+    assert not f.selectable()
+    assert FormattedLayerWeightIndex(idx, "bf16", (), q).selectable()
+    for bad in (q.__class__(**{**q.__dict__, "prompts": ()}),
+                q.__class__(**{**q.__dict__, "elapsed_seconds": float("nan")}),
+                q.__class__(**{**q.__dict__, "largest_layer_bytes": 0}),
+                q.__class__(**{**q.__dict__, "prompts": (PromptDeviation("hi", (1,), (1,), 0.6, 0.5),)})):
+        with pytest.raises(InvalidWeights, match="incomplete or non-finite"):
+            bad.validate()
+    with pytest.raises(InvalidWeights, match="unknown weight format"):
+        FormattedLayerWeightIndex(idx, "int3", (), None)
