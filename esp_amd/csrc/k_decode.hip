@@ -498,7 +498,12 @@ __global__ void __launch_bounds__(NW * 64) attn_decode_k(AttnDecodeArgs a) {
     constexpr int LPK = HD / DPL;        // lanes per key
     constexpr int KPW = 64 / LPK;        // keys per wave per step
     constexpr int STEP = NW * KPW;       // keys per block step
-    constexpr int NS = AttSteps<GM>::v;  // steps per chunk
+    // the narrow (4-wave, many-row) form double-buffers its chunks: the
+    // next chunk's loads are in flight while the current one is consumed
+    // (two steps per buffer measured best on MI355X at the C5 batch: 65.0 us
+    // per launch vs 66.4 with three, 69.9 with five, 70.7 single-buffered)
+    constexpr bool PIPE = NW == 4;
+    constexpr int NS = PIPE ? 2 : AttSteps<GM>::v;  // steps per chunk
     constexpr int CH = NS * STEP;        // keys per chunk
     constexpr int HALF = HD / 2;
     constexpr int STRIDE = HD + ATT_PART_PAD;
@@ -529,20 +534,21 @@ __global__ void __launch_bounds__(NW * 64) attn_decode_k(AttnDecodeArgs a) {
     const float *kb = a.kv + (size_t)seq * a.seq_stride + (size_t)g * a.head_stride + sub * 4;
     const float *vb = kb + a.kv_half_stride;
     f32x4_t kk[NS][2], vv[NS][2];
+    f32x4_t kk2[PIPE ? NS : 1][2], vv2[PIPE ? NS : 1][2];  // second buffer (PIPE)
     // lanes past the chunk end re-read its last key (masked later)
-    auto issue = [&](int c0, int c1) {
+    auto issue = [&](f32x4_t (&K)[NS][2], f32x4_t (&V)[NS][2], int c0, int c1) {
 #pragma unroll
         for (int st = 0; st < NS; ++st) {
             if (c0 + st * STEP < c1) {  // block-uniform
                 const int t = min(c0 + st * STEP + wave * KPW + grp, c1 - 1);
-                kk[st][0] = __builtin_nontemporal_load((const f32x4_t *)(kb + (size_t)t * HD));
-                kk[st][1] = __builtin_nontemporal_load((const f32x4_t *)(kb + (size_t)t * HD + HALF));
-                vv[st][0] = __builtin_nontemporal_load((const f32x4_t *)(vb + (size_t)t * HD));
-                vv[st][1] = __builtin_nontemporal_load((const f32x4_t *)(vb + (size_t)t * HD + HALF));
+                K[st][0] = __builtin_nontemporal_load((const f32x4_t *)(kb + (size_t)t * HD));
+                K[st][1] = __builtin_nontemporal_load((const f32x4_t *)(kb + (size_t)t * HD + HALF));
+                V[st][0] = __builtin_nontemporal_load((const f32x4_t *)(vb + (size_t)t * HD));
+                V[st][1] = __builtin_nontemporal_load((const f32x4_t *)(vb + (size_t)t * HD + HALF));
             }
         }
     };
-    issue(s0, min(s0 + CH, s1));
+    issue(kk, vv, s0, min(s0 + CH, s1));
     // q for the group's heads: this lane's 8 dims
     float q[GM][DPL];
     const float *qrow = a.q + (size_t)row * a.nq * HD + (size_t)g * G * HD + sub * 4;
@@ -568,9 +574,8 @@ __global__ void __launch_bounds__(NW * 64) attn_decode_k(AttnDecodeArgs a) {
 #pragma unroll
         for (int e = 0; e < DPL; ++e) acc[j][e] = 0.f;
     }
-    for (int c0 = s0; c0 < hi; c0 += CH) {
-        const int c1 = min(c0 + CH, hi);
-        if (c0 > s0) issue(c0, c1);
+    // one chunk's keys [c0, c1) from a register buffer
+    auto consume = [&](const f32x4_t (&kk)[NS][2], f32x4_t (&vv)[NS][2], int c0, int c1) {
         bool ok[NS];
 #pragma unroll
         for (int st = 0; st < NS; ++st) {
@@ -613,6 +618,25 @@ __global__ void __launch_bounds__(NW * 64) attn_decode_k(AttnDecodeArgs a) {
                 }
             }
             m[j] = mx;
+        }
+    };
+    if constexpr (PIPE) {
+        int c0 = s0;
+        while (c0 < hi) {
+            const int c1 = min(c0 + CH, hi);
+            if (c1 < hi) issue(kk2, vv2, c1, min(c1 + CH, hi));
+            consume(kk, vv, c0, c1);
+            if (c1 >= hi) break;
+            const int c2 = min(c1 + CH, hi);
+            if (c2 < hi) issue(kk, vv, c2, min(c2 + CH, hi));
+            consume(kk2, vv2, c1, c2);
+            c0 = c2;
+        }
+    } else {
+        for (int c0 = s0; c0 < hi; c0 += CH) {
+            const int c1 = min(c0 + CH, hi);
+            if (c0 > s0) issue(kk, vv, c0, c1);
+            consume(kk, vv, c0, c1);
         }
     }
     // merge the KPW key groups of the wave: lane pairs at distance LPK .. 32
