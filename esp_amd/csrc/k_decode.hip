@@ -412,7 +412,6 @@ constexpr int ATT_MB = 32;        // splits whose partials one merge batch loads
 
 // Steps (of ATT_WAVES * 64 * 8 / HD keys) whose K/V loads a block keeps in
 // flight together: 16 VGPRs per step and lane.
-template <int GM> struct AttSteps { static constexpr int v = GM <= 4 ? 5 : 3; };
 
 // Both values of the lane pair (lane, lane ^ X), lower lane first, in every
 // lane of the pair: X = 32 and 16 with the gfx950 permlane swaps, X = 8 with
@@ -474,7 +473,7 @@ __device__ __forceinline__ void att_store(const AttnDecodeArgs &a, size_t i, flo
 // [4 sub, 4 sub + 4) and [hd/2 + 4 sub, hd/2 + 4 sub + 4), so each 16-byte
 // load of the group covers a contiguous hd/2 * 4 bytes of the key row, and
 // a dot product is finished with DPP swaps inside the group. The loads of
-// the first chunk of the split (up to AttSteps steps) are issued before the
+// the first chunk of the split (one buffer's steps) are issued before the
 // row's position is known: they cover the split's planned range (clamped to
 // max_t, the plan's key bound; lanes past the range load nothing) and keys
 // past the position are masked afterwards, so the position read and the K/V
@@ -498,12 +497,13 @@ __global__ void __launch_bounds__(NW * 64) attn_decode_k(AttnDecodeArgs a) {
     constexpr int LPK = HD / DPL;        // lanes per key
     constexpr int KPW = 64 / LPK;        // keys per wave per step
     constexpr int STEP = NW * KPW;       // keys per block step
-    // the narrow (4-wave, many-row) form double-buffers its chunks: the
-    // next chunk's loads are in flight while the current one is consumed
-    // (two steps per buffer measured best on MI355X at the C5 batch: 65.0 us
-    // per launch vs 66.4 with three, 69.9 with five, 70.7 single-buffered)
-    constexpr bool PIPE = NW == 4;
-    constexpr int NS = PIPE ? 2 : AttSteps<GM>::v;  // steps per chunk
+    // Key chunks are double-buffered: the next chunk's loads are in flight
+    // while the current one is consumed. Steps per buffer, measured on
+    // MI355X: the narrow (4-wave, many-row) form at the C5 batch 65.0 us per
+    // launch with two (66.4 with three, 69.9 with five, 70.7 single-
+    // buffered with five); the 8-wave form three (C2 decode 1327 vs
+    // 1287-1312 tok/s single-buffered with five).
+    constexpr int NS = NW == 4 ? 2 : 3;  // steps per chunk
     constexpr int CH = NS * STEP;        // keys per chunk
     constexpr int HALF = HD / 2;
     constexpr int STRIDE = HD + ATT_PART_PAD;
@@ -534,7 +534,7 @@ __global__ void __launch_bounds__(NW * 64) attn_decode_k(AttnDecodeArgs a) {
     const float *kb = a.kv + (size_t)seq * a.seq_stride + (size_t)g * a.head_stride + sub * 4;
     const float *vb = kb + a.kv_half_stride;
     f32x4_t kk[NS][2], vv[NS][2];
-    f32x4_t kk2[PIPE ? NS : 1][2], vv2[PIPE ? NS : 1][2];  // second buffer (PIPE)
+    f32x4_t kk2[NS][2], vv2[NS][2];  // the second buffer
     // lanes past the chunk end re-read its last key (masked later)
     auto issue = [&](f32x4_t (&K)[NS][2], f32x4_t (&V)[NS][2], int c0, int c1) {
 #pragma unroll
@@ -620,24 +620,17 @@ __global__ void __launch_bounds__(NW * 64) attn_decode_k(AttnDecodeArgs a) {
             m[j] = mx;
         }
     };
-    if constexpr (PIPE) {
-        int c0 = s0;
-        while (c0 < hi) {
-            const int c1 = min(c0 + CH, hi);
-            if (c1 < hi) issue(kk2, vv2, c1, min(c1 + CH, hi));
-            consume(kk, vv, c0, c1);
-            if (c1 >= hi) break;
-            const int c2 = min(c1 + CH, hi);
-            if (c2 < hi) issue(kk, vv, c2, min(c2 + CH, hi));
-            consume(kk2, vv2, c1, c2);
-            c0 = c2;
-        }
-    } else {
-        for (int c0 = s0; c0 < hi; c0 += CH) {
-            const int c1 = min(c0 + CH, hi);
-            if (c0 > s0) issue(kk, vv, c0, c1);
-            consume(kk, vv, c0, c1);
-        }
+    // chunks alternate between the buffers; each buffer is refilled only
+    // after it has been consumed, with exactly the range consumed from it
+    for (int c0 = s0; c0 < hi;) {
+        const int c1 = min(c0 + CH, hi);
+        if (c1 < hi) issue(kk2, vv2, c1, min(c1 + CH, hi));
+        consume(kk, vv, c0, c1);
+        if (c1 >= hi) break;
+        const int c2 = min(c1 + CH, hi);
+        if (c2 < hi) issue(kk, vv, c2, min(c2 + CH, hi));
+        consume(kk2, vv2, c1, c2);
+        c0 = c2;
     }
     // merge the KPW key groups of the wave: lane pairs at distance LPK .. 32
     if constexpr (LPK <= 8) att_pair_merge<8, GM>(G, m, l, acc);
