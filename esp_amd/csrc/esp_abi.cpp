@@ -522,7 +522,20 @@ esp_status esp_generate_greedy(esp_model *model, esp_kv *kv, uint32_t seq, const
         launch_pick(a, s);
         launch_gen_step(a.ids_out, g, s);
         const int max_t = (int)last_pos;
-        if (m.st) {
+        // Streamed layers that all sit in the device layer cache read
+        // nothing more: such a model replays the captured decode step like
+        // a resident one, and its hit counter is set afterwards to the
+        // forwards the reference takes (one per emitted token before the
+        // last, generate.rs:154-168).
+        std::shared_ptr<Streamer> cached_st =
+            m.st && (int)m.st->cache.size() == m.L ? m.st : nullptr;
+        std::unique_lock<std::recursive_mutex> cached_lk;
+        uint64_t hits0 = 0;
+        if (cached_st) {
+            cached_lk = std::unique_lock<std::recursive_mutex>(cached_st->mu);
+            hits0 = cached_st->hits;
+        }
+        if (m.st && !cached_st) {
             // Streamed layers are read between kernels: one host-driven step
             // per token, stopping at eos (generate.rs:154-168) so no layer
             // is read for a step the reference does not take.
@@ -603,6 +616,11 @@ esp_status esp_generate_greedy(esp_model *model, esp_kv *kv, uint32_t seq, const
             if (out_ids) out_ids[n] = list[n];
         }
         if (n_out) *n_out = n;
+        if (cached_st) {
+            stream_check(m);
+            const uint64_t fwd = std::min<uint64_t>(n, max_new - 1);
+            cached_st->hits = hits0 + fwd * (uint64_t)m.L;
+        }
     });
 }
 

@@ -242,3 +242,28 @@ def test_shared_artifact_refusals():
         "shared_expert_intermediate_size": 64, "decoder_sparse_step": 1})
     with pytest.raises(Unsupported, match="expert streaming"):
         DecoderModel.from_layer_source(moe, shared, ArtifactSource(layers))
+
+
+def test_fully_cached_stream_replays_the_decode_graph():
+    """Once every layer is in the device cache, greedy generation replays
+    the captured step; ids equal the resident model's and the cache counts
+    one hit per layer for each forward the reference takes (prefill, then
+    one per emitted token before the last; generate.rs:154-168)."""
+    cfg, _, blob = _case("bf16")
+    L = cfg.num_hidden_layers
+    shared, layers = split_checkpoint(blob, cfg)
+    resident = DecoderModel.from_bytes(cfg, blob, "bf16")
+    m = DecoderModel.from_layer_source(cfg, shared, ArtifactSource(layers), fmt="bf16")
+    m.with_layer_cache(1 << 32)
+    prompt = synth.uniform_ids(12, 9, cfg.vocab_size)
+    want = resident.generate_greedy_device(resident.new_cache(1, 64), prompt, 6, eos=[])
+    got = m.generate_greedy_device(m.new_cache(1, 64), prompt, 6, eos=[])
+    assert got == want
+    s = m.streaming_stats()
+    assert s.layer_reads == L and s.device_cache.misses == L and s.device_cache.hits == 5 * L
+    # eos = the first id not seen earlier: generation stops before it
+    k = next(i for i in range(1, len(want)) if want[i] not in want[:i])
+    got = m.generate_greedy_device(m.new_cache(1, 64), prompt, 6, eos=[want[k]])
+    assert got == want[:k]
+    s = m.streaming_stats()
+    assert s.layer_reads == L and s.device_cache.hits == 5 * L + L + k * L
