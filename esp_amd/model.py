@@ -63,6 +63,16 @@ def esp_config(cfg: DecoderConfig, fmt: str = "f32"):
     return c, (win, moe)
 
 
+def _borrow(data) -> Optional[C.c_void_p]:
+    """A pointer to `data`'s bytes for the duration of one call, without a
+    copy (bytes, bytearray or a writable buffer; the library only reads)."""
+    if not data:
+        return None
+    if isinstance(data, bytes):
+        return C.cast(C.c_char_p(data), C.c_void_p)
+    return C.c_void_p(C.addressof((C.c_uint8 * len(data)).from_buffer(data)))
+
+
 class LoraAdapter:
     """One PEFT LoRA adapter (lora.rs:99-217): rank, alpha, selection scale,
     target modules and the adapter safetensors bytes. Applied unmerged."""
@@ -130,7 +140,7 @@ class DecoderModel:
         """loader.rs:573-580 load_decoder_from_bytes (+ lora.rs adapters)."""
         L = _lib.load()
         c, keep = esp_config(config, fmt)
-        buf = (C.c_uint8 * len(weights)).from_buffer_copy(weights) if weights else None
+        buf = _borrow(weights)
         ads = adapters or []
         arr = (_lib.EspLora * max(1, len(ads)))()
         bufs = []

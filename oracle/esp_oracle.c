@@ -63,6 +63,29 @@ static float dot_row(const float *x, orc_tensor w, size_t row, int n) {
     return fold16(acc);
 }
 
+/* dot_row of one input row against four consecutive weight rows: the input
+ * chunk is loaded once for all four; each dot keeps dot_row's own
+ * accumulation order, so out[i] == dot_row(x, w, row + i, n) bit for bit. */
+static void dot_row_w4(const float *x, orc_tensor w, size_t row, int n, float *out) {
+    float acc[4][LANES] = {{0}};
+    int j = 0;
+    if (w.dtype == ORC_BF16) {
+        const uint16_t *r = (const uint16_t *)w.data + row * (size_t)n;
+        for (; j + LANES <= n; j += LANES)
+            for (int i = 0; i < 4; ++i)
+                for (int l = 0; l < LANES; ++l)
+                    acc[i][l] += x[j + l] * bf16_to_f32(r[(size_t)i * n + j + l]);
+    } else {
+        const float *r = (const float *)w.data + row * (size_t)n;
+        for (; j + LANES <= n; j += LANES)
+            for (int i = 0; i < 4; ++i)
+                for (int l = 0; l < LANES; ++l) acc[i][l] += x[j + l] * r[(size_t)i * n + j + l];
+    }
+    for (; j < n; ++j)
+        for (int i = 0; i < 4; ++i) acc[i][j % LANES] += x[j] * tget(w, (row + i) * (size_t)n + j);
+    for (int i = 0; i < 4; ++i) out[i] = fold16(acc[i]);
+}
+
 static float dot_f32(const float *a, const float *b, int n) {
     float acc[LANES] = {0};
     int j = 0;
@@ -78,12 +101,34 @@ static float sumsq(const float *x, int n) { return dot_f32(x, x, n); }
  * here, so y[o] = dot(x, W[o]) + b[o]).  x [rows, in] -> y [rows, out]. */
 static void linear(const float *x, int rows, int in_f, orc_tensor w, orc_tensor bias,
                    int out_f, float *y) {
+    /* Rows go in blocks whose inputs fit a core's L2, outputs in fours
+     * whose weight rows stay in L1 while the block's rows stream past; every
+     * output is the same dot_row sum, so blocking does not change a bit. */
+    int rb = (int)((512u * 1024u) / ((unsigned)in_f * sizeof(float)));
+    if (rb < 1) rb = 1;
+    for (int s0 = 0; s0 < rows; s0 += rb) {
+        int s1 = s0 + rb < rows ? s0 + rb : rows;
 #pragma omp parallel for schedule(static)
-    for (int o = 0; o < out_f; ++o) {
-        float b = bias.data ? tget(bias, (size_t)o) : 0.0f;
-        for (int s = 0; s < rows; ++s) {
-            float v = dot_row(x + (size_t)s * in_f, w, (size_t)o, in_f);
-            y[(size_t)s * out_f + o] = bias.data ? v + b : v;
+        for (int o4 = 0; o4 < (out_f + 3) / 4; ++o4) {
+            int o = 4 * o4;
+            if (o + 4 <= out_f) {
+                for (int s = s0; s < s1; ++s) {
+                    float v[4];
+                    dot_row_w4(x + (size_t)s * in_f, w, (size_t)o, in_f, v);
+                    for (int i = 0; i < 4; ++i) {
+                        float b = bias.data ? tget(bias, (size_t)(o + i)) : 0.0f;
+                        y[(size_t)s * out_f + o + i] = bias.data ? v[i] + b : v[i];
+                    }
+                }
+                continue;
+            }
+            for (; o < out_f; ++o) {
+                float b = bias.data ? tget(bias, (size_t)o) : 0.0f;
+                for (int s = s0; s < s1; ++s) {
+                    float v = dot_row(x + (size_t)s * in_f, w, (size_t)o, in_f);
+                    y[(size_t)s * out_f + o] = bias.data ? v + b : v;
+                }
+            }
         }
     }
 }
@@ -186,51 +231,63 @@ static inline float *kv_row(const orc_kv *kv, float *base, int l, int h, int t) 
 
 /* ---------------------------------------------------------------- MLP */
 
-/* moe.rs:87-89 Expert::forward = down(silu(x·gate) * (x·up)) for one row. */
-static void expert_row(const float *x, int h, orc_tensor gate, orc_tensor up, orc_tensor down,
-                       int f, float *act, float *y) {
-    for (int j = 0; j < f; ++j) {
-        float g = dot_row(x, gate, (size_t)j, h);
-        float u = dot_row(x, up, (size_t)j, h);
-        act[j] = silu(g) * u;
-    }
-    for (int o = 0; o < h; ++o) y[o] = dot_row(act, down, (size_t)o, f);
-}
-
-/* Dense SwiGLU MLP over rows, parallel over output features. */
+/* moe.rs:76-90 SwiGLU MLP (Expert::forward = down(silu(x·gate) * (x·up)))
+ * over rows, parallel over output features. */
 static void dense_mlp(const float *x, int rows, int h, int f, orc_tensor gate, orc_tensor up,
                       orc_tensor down, float *act, float *y) {
+    /* row blocks as in linear() */
+    int rb = (int)((512u * 1024u) / ((unsigned)h * sizeof(float)));
+    if (rb < 1) rb = 1;
+    for (int s0 = 0; s0 < rows; s0 += rb) {
+        int s1 = s0 + rb < rows ? s0 + rb : rows;
 #pragma omp parallel for schedule(static)
-    for (int j = 0; j < f; ++j) {
-        for (int s = 0; s < rows; ++s) {
-            const float *xr = x + (size_t)s * h;
-            float g = dot_row(xr, gate, (size_t)j, h);
-            float u = dot_row(xr, up, (size_t)j, h);
-            act[(size_t)s * f + j] = silu(g) * u;
+        for (int j4 = 0; j4 < (f + 3) / 4; ++j4) {
+            int j = 4 * j4;
+            if (j + 4 <= f) {
+                for (int s = s0; s < s1; ++s) {
+                    float g[4], u[4];
+                    dot_row_w4(x + (size_t)s * h, gate, (size_t)j, h, g);
+                    dot_row_w4(x + (size_t)s * h, up, (size_t)j, h, u);
+                    for (int i = 0; i < 4; ++i) act[(size_t)s * f + j + i] = silu(g[i]) * u[i];
+                }
+                continue;
+            }
+            for (; j < f; ++j) {
+                for (int s = s0; s < s1; ++s) {
+                    const float *xr = x + (size_t)s * h;
+                    float g = dot_row(xr, gate, (size_t)j, h);
+                    float u = dot_row(xr, up, (size_t)j, h);
+                    act[(size_t)s * f + j] = silu(g) * u;
+                }
+            }
         }
     }
     orc_tensor none = {0};
     linear(act, rows, f, down, none, h, y);
 }
 
-/* moe.rs:135-256 DecoderMlp::forward (Moe arm). Returns 0 or -2/-3. */
+/* moe.rs:135-256 DecoderMlp::forward (Moe arm). Returns 0 or -2/-3.
+ * Routing per row first; then, as the reference does, expert by expert in
+ * ascending id over the rows that chose it (moe.rs:183-251), each row
+ * adding delta * weight in that order; then the shared expert. */
 static int moe_mlp(const orc_model *m, int l, const float *x, int rows, float *y) {
     const orc_tensor *lt = m->layer + (size_t)l * ORC_LAYER_SLOTS;
     int h = m->hidden, e_n = m->n_experts, k = m->top_k;
     int f = m->moe_ffn, fs = m->shared_ffn;
     int status = 0;
     float *probs = (float *)malloc(sizeof(float) * (size_t)rows * e_n);
+    float *wsel = (float *)calloc((size_t)rows * e_n, sizeof(float));
+    unsigned char *chosen = (unsigned char *)calloc((size_t)rows * e_n, 1);
     orc_tensor none = {0};
     linear(x, rows, h, lt[ORC_ROUTER], none, e_n, probs);
 #pragma omp parallel
     {
-        int fmax = f > fs ? f : fs;
-        float *act = (float *)malloc(sizeof(float) * (size_t)(fmax > 0 ? fmax : 1));
-        float *delta = (float *)malloc(sizeof(float) * (size_t)h);
         int *order = (int *)malloc(sizeof(int) * (size_t)e_n);
-#pragma omp for schedule(dynamic, 1)
+#pragma omp for schedule(static)
         for (int s = 0; s < rows; ++s) {
             float *p = probs + (size_t)s * e_n;
+            float *yr = y + (size_t)s * h;
+            for (int j = 0; j < h; ++j) yr[j] = 0.0f;
             /* fp32 softmax over all experts (moe.rs:156-159) */
             float mx = -INFINITY;
             for (int e = 0; e < e_n; ++e) mx = fmaxf(mx, p[e]);
@@ -244,8 +301,6 @@ static int moe_mlp(const orc_model *m, int l, const float *x, int rows, float *y
                 p[e] = p[e] / sum;
                 if (!isfinite(p[e])) bad = 1;
             }
-            float *yr = y + (size_t)s * h;
-            for (int j = 0; j < h; ++j) yr[j] = 0.0f;
             if (bad) {
 #pragma omp atomic write
                 status = -2;
@@ -271,29 +326,54 @@ static int moe_mlp(const orc_model *m, int l, const float *x, int rows, float *y
                 status = -3;
                 continue;
             }
-            /* experts in ascending id, each adding delta*w (moe.rs:183-245) */
-            for (int e = 0; e < e_n; ++e) {
-                int chosen = 0;
-                for (int i = 0; i < k; ++i) chosen |= order[i] == e;
-                if (!chosen) continue;
-                float w = p[e] / mass;
-                const orc_tensor *ex = m->experts + ((size_t)l * e_n + e) * 3;
-                expert_row(x + (size_t)s * h, h, ex[0], ex[1], ex[2], f, act, delta);
-                for (int j = 0; j < h; ++j) yr[j] = yr[j] + delta[j] * w;
-            }
-            /* + sigmoid(shared_gate·x) * shared(x) (moe.rs:253) */
-            if (fs > 0 && lt[ORC_SH_GATE].data) {
-                float g = sigmoidf_(dot_row(x + (size_t)s * h, lt[ORC_SHARED_GATE], 0, h));
-                expert_row(x + (size_t)s * h, h, lt[ORC_SH_GATE], lt[ORC_SH_UP], lt[ORC_SH_DOWN],
-                           fs, act, delta);
-                for (int j = 0; j < h; ++j) yr[j] = yr[j] + g * delta[j];
+            for (int i = 0; i < k; ++i) {
+                chosen[(size_t)s * e_n + order[i]] = 1;
+                wsel[(size_t)s * e_n + order[i]] = p[order[i]] / mass;
             }
         }
-        free(act);
-        free(delta);
         free(order);
     }
+    int fmax = f > fs ? f : fs;
+    int *idx = (int *)malloc(sizeof(int) * (size_t)(rows > 0 ? rows : 1));
+    float *xs = (float *)malloc(sizeof(float) * (size_t)rows * h);
+    float *ys = (float *)malloc(sizeof(float) * (size_t)rows * h);
+    float *act = (float *)malloc(sizeof(float) * (size_t)rows * (size_t)(fmax > 0 ? fmax : 1));
+    /* experts in ascending id, each row adding delta*w (moe.rs:183-245) */
+    for (int e = 0; e < e_n && status == 0; ++e) {
+        int ne = 0;
+        for (int s = 0; s < rows; ++s)
+            if (chosen[(size_t)s * e_n + e]) idx[ne++] = s;
+        if (ne == 0) continue;
+        for (int i = 0; i < ne; ++i)
+            memcpy(xs + (size_t)i * h, x + (size_t)idx[i] * h, sizeof(float) * h);
+        const orc_tensor *ex = m->experts + ((size_t)l * e_n + e) * 3;
+        dense_mlp(xs, ne, h, f, ex[0], ex[1], ex[2], act, ys);
+#pragma omp parallel for schedule(static)
+        for (int i = 0; i < ne; ++i) {
+            float w = wsel[(size_t)idx[i] * e_n + e];
+            float *yr = y + (size_t)idx[i] * h;
+            const float *d = ys + (size_t)i * h;
+            for (int j = 0; j < h; ++j) yr[j] = yr[j] + d[j] * w;
+        }
+    }
+    /* + sigmoid(shared_gate·x) * shared(x) (moe.rs:253) */
+    if (status == 0 && fs > 0 && lt[ORC_SH_GATE].data) {
+        dense_mlp(x, rows, h, fs, lt[ORC_SH_GATE], lt[ORC_SH_UP], lt[ORC_SH_DOWN], act, ys);
+#pragma omp parallel for schedule(static)
+        for (int s = 0; s < rows; ++s) {
+            float g = sigmoidf_(dot_row(x + (size_t)s * h, lt[ORC_SHARED_GATE], 0, h));
+            float *yr = y + (size_t)s * h;
+            const float *d = ys + (size_t)s * h;
+            for (int j = 0; j < h; ++j) yr[j] = yr[j] + g * d[j];
+        }
+    }
+    free(idx);
+    free(xs);
+    free(ys);
+    free(act);
     free(probs);
+    free(wsel);
+    free(chosen);
     return status;
 }
 

@@ -49,6 +49,32 @@ def dump(tensors: Dict[str, Tuple[np.ndarray, str]]) -> bytes:
     return struct.pack("<Q", len(hb)) + hb + b"".join(blobs)
 
 
+def dump_buffer(tensors: Dict[str, Tuple[np.ndarray, str]]) -> bytearray:
+    """dump() into one preallocated bytearray (same bytes): each tensor is
+    copied once, for multi-GB checkpoints."""
+    header = {}
+    offset = 0
+    for name in sorted(tensors):
+        arr, dt = tensors[name]
+        nbytes = int(np.prod(arr.shape)) * np.dtype(_NP[dt]).itemsize
+        header[name] = {"dtype": dt, "shape": list(arr.shape),
+                        "data_offsets": [offset, offset + nbytes]}
+        offset += nbytes
+    hb = json.dumps(header, separators=(",", ":")).encode()
+    hb += b" " * ((8 - len(hb) % 8) % 8)
+    base = 8 + len(hb)
+    out = bytearray(base + offset)
+    out[:8] = struct.pack("<Q", len(hb))
+    out[8:base] = hb
+    view = np.frombuffer(out, dtype=np.uint8)
+    for name in sorted(tensors):
+        arr, dt = tensors[name]
+        a, b = header[name]["data_offsets"]
+        src = np.ascontiguousarray(arr, dtype=_NP[dt]).reshape(-1).view(np.uint8)
+        view[base + a:base + b] = src
+    return out
+
+
 def bf16_round(x: np.ndarray) -> np.ndarray:
     """f32 -> bf16 bits, round-to-nearest-even (half::bf16::from_f32)."""
     u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)

@@ -56,8 +56,13 @@ def uniform_ids(seed: int, n: int, vocab: int) -> List[int]:
 
 
 def make_tensors(cfg: DecoderConfig, seed: int, fmt: str = "f32", std: float = 0.02,
-                 bias_std: float = 0.0) -> Dict[str, Tuple[np.ndarray, str]]:
-    """HF-named tensors for `cfg` (dense, or qwen2_moe / Mixtral-style experts)."""
+                 bias_std: float = 0.0, fast: bool = False) -> Dict[str, Tuple[np.ndarray, str]]:
+    """HF-named tensors for `cfg` (dense, or qwen2_moe / Mixtral-style experts).
+
+    fast=True draws the same splitmix64 / Box-Muller stream with the CPU
+    oracle's OpenMP generator (glibc log/cos/sin instead of numpy's; the f32
+    values can differ by an ulp, bf16 roundings almost never): for the
+    full-width shapes, whose weights numpy would take minutes to draw."""
     H, F, V = cfg.hidden_size, cfg.intermediate_size, cfg.vocab_size
     qw, kvw, hd = cfg.query_width(), cfg.kv_heads() * cfg.head_dim(), cfg.head_dim()
     out: Dict[str, Tuple[np.ndarray, str]] = {}
@@ -68,6 +73,11 @@ def make_tensors(cfg: DecoderConfig, seed: int, fmt: str = "f32", std: float = 0
             arr = np.ones(n, np.float32)
         elif kind == "bias":
             arr = normal(tensor_seed(seed, name), n, bias_std) if bias_std else np.zeros(n, np.float32)
+        elif fast:
+            from oracle import oracle
+            raw = oracle.fill_normal(tensor_seed(seed, name), n, std, fmt == "bf16")
+            out[name] = (raw.reshape(shape), "BF16" if fmt == "bf16" else "F32")
+            return
         else:
             arr = normal(tensor_seed(seed, name), n, std)
         arr = arr.reshape(shape)
