@@ -101,6 +101,7 @@ def load():
         "esp_generate_greedy": (C.c_int, [vp, vp, u32, P(i32), u32, u32, P(i32), u32, P(i32),
                                           P(u32)]),
         "esp_pick_constrained": (C.c_int, [vp, u32, P(vp), P(EspSampler), P(u32), P(C.c_uint8)]),
+        "esp_pick_noalloc": (C.c_int, [vp, u32, vp, vp, vp, vp]),
         "esp_vocab_create": (C.c_int, [vp, P(u32), u32, P(vp)]),
         "esp_vocab_destroy": (C.c_int, [vp]),
         "esp_constraint_create": (C.c_int, [vp, C.c_char_p, C.c_size_t, P(vp)]),
@@ -132,7 +133,8 @@ def load():
 EXPORTED = ["esp_last_error", "esp_version", "esp_model_load", "esp_model_create_synthetic",
             "esp_model_destroy", "esp_model_weight_bytes", "esp_kv_create", "esp_kv_destroy",
             "esp_kv_reset", "esp_kv_position", "esp_kv_stream", "esp_forward_last",
-            "esp_forward_batch", "esp_pick", "esp_pick_constrained", "esp_generate_greedy",
+            "esp_forward_batch", "esp_pick", "esp_pick_constrained", "esp_pick_noalloc",
+            "esp_generate_greedy",
             "esp_vocab_create", "esp_vocab_destroy", "esp_constraint_create",
             "esp_constraint_destroy", "esp_constraint_accept", "esp_constraint_complete",
             "esp_constraint_forced_bytes", "esp_constraint_mask", "esp_model_load_streamed",

@@ -142,6 +142,11 @@ struct PickArgs {
 };
 void launch_pick(const PickArgs &a, hipStream_t s);
 size_t pick_scratch_bytes(int n, int V);
+// esp_pick_noalloc: the pick over device inputs and outputs with all scratch
+// in the library's fixed device array (k_pick_fixed.hip).
+void launch_pick_fixed(int device, const float *logits, int n, int V, const uint32_t *allowed_dev,
+                       esp_sampler *samplers_dev, uint32_t *ids_dev, uint8_t *flags_dev,
+                       hipStream_t s);
 
 // Packed weights: out[i] = q_i * scale[i / 32] in f32 (n a multiple of 32).
 // Packed [N, K] -> bf16 [N, 2K] rows [hi(q*scale) | lo(q*scale)], and split

@@ -384,6 +384,19 @@ esp_status esp_pick(esp_kv *kv, uint32_t n_rows, const uint32_t *allowed_bits,
     });
 }
 
+esp_status esp_pick_noalloc(esp_kv *kv, uint32_t n_rows, const uint32_t *allowed_bits_dev,
+                            esp_sampler *samplers_dev, uint32_t *ids_dev, uint8_t *flags_dev) {
+    return guard([&] {
+        if (!kv) fail(ESP_INVALID_REQUEST, "null kv handle");
+        Kv &k = *(Kv *)kv;
+        if (!n_rows || (int)n_rows > k.logits_rows)
+            fail(ESP_INVALID_REQUEST, "pick: rows exceed the logits of the last forward");
+        if (!ids_dev) fail(ESP_INVALID_REQUEST, "pick: null ids_out");
+        launch_pick_fixed(k.model->device, k.logits.as<float>(), (int)n_rows, k.model->V,
+                          allowed_bits_dev, samplers_dev, ids_dev, flags_dev, k.stream);
+    });
+}
+
 esp_status esp_pick_constrained(esp_kv *kv, uint32_t n_rows, esp_constraint *const *constraints,
                                 esp_sampler *samplers, uint32_t *ids_out, uint8_t *flags_out) {
     return guard([&] {

@@ -189,6 +189,24 @@ esp_status esp_forward_batch(esp_model *model, esp_kv *kv, uint32_t n_seqs, cons
 esp_status esp_pick(esp_kv *kv, uint32_t n_rows, const uint32_t *allowed_bits,
                     esp_sampler *samplers, uint32_t *ids_out, uint8_t *flags_out);
 
+/* No counterpart in the reference. For callers that cannot allocate device
+ * memory: code under HIP stream capture, serving loops and harnesses that
+ * forbid hipMalloc. esp_pick with every input and output in device memory
+ * and no device allocation, synchronisation or host copy: allowed_bits_dev
+ * (nullable) as esp_pick's allowed_bits; samplers_dev (nullable) whose
+ * sampled rows' states advance in place, exactly as esp_pick advances
+ * them (not for a row with no eligible token); ids_dev[n_rows];
+ * flags_dev[n_rows] (nullable) gets the ESP_PICK_* bits. It is enqueued on
+ * the KV handle's stream and returns without waiting, so a row with no
+ * eligible token is reported only in flags_dev. All scratch lives in one
+ * fixed device array of ESP_PICK_NOALLOC_SCRATCH_BYTES per GPU (held from
+ * library load until the process ends); rows x vocabulary needing more
+ * (about 30 MiB for 16 sampled rows of a 128256-token vocabulary) ->
+ * ESP_INVALID_REQUEST. Calls that overlap on one GPU race on that array. */
+#define ESP_PICK_NOALLOC_SCRATCH_BYTES (32u << 20)
+esp_status esp_pick_noalloc(esp_kv *kv, uint32_t n_rows, const uint32_t *allowed_bits_dev,
+                            esp_sampler *samplers_dev, uint32_t *ids_dev, uint8_t *flags_dev);
+
 /* generate.rs:134-170 try_generate_ids_with + TokenPicker::Greedy, run on
  * the device: prefill `prompt`, then up to max_new greedy steps, stopping
  * at (and excluding) any id in `eos`. Writes generated ids to out_ids
