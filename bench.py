@@ -1,15 +1,22 @@
 """Benchmark: llama-family decode & prefill tokens/s on one MI355X.
 
-Workload ("C2"): Llama-3.2-1B-shape decoder, bf16
-weights (random init N(0, 0.02), synthetic), batch 1, a 512-token
-uniform-random prompt prefill followed by 256 greedy decode steps. One
-"step" is that whole generation; `value` is decode tokens/s.
+Headline workload ("C3"): Llama-3-8B-shape
+decoder, bf16 weights (random init N(0, 0.02), synthetic) with rank-16 LoRA
+(alpha 32) on q_proj and v_proj, batch 1: a 4064-token uniform-random prompt
+then 64 greedy decode steps, i.e. decode at 4064-4128 (mean 4096) context.
+One "step" is that whole request; `value` is decode tokens/s (the prompt's
+prefill, timed separately, is subtracted). A separate 2048-token prefill is
+reported as prefill tokens/s and a fraction of bf16 MFMA peak.
 
-Extra fields report the prefill rate, the decode HBM roofline fraction
-for the whole step, and the dominant kernel's roofline from HIP events
-recorded on the KV handle's stream around every launch of that kernel
-family in a profiled pass. `cpu_baseline` times the CPU restatement of
-esp's burn-ndarray path (oracle/) on a bounded sample of the same decode.
+`decode_hbm_frac` counts BASELINE.md's algorithmic bytes per token (every
+weight once in bf16 + the K/V cache once at 2 bytes per element); the
+`roofline` object describes the dominant decode kernel (the SwiGLU gate/up
+GEMV) from HIP events recorded on the KV handle's stream around every launch
+of that kernel in an eager pass; `traffic` is its measured HBM bytes per
+launch from the committed FETCH_SIZE / WRITE_SIZE counter summary.
+`cpu_baseline` times the CPU restatement of esp's burn-ndarray path
+(oracle/) on the same C3 decode at 4096 context on all host cores. The
+other BASELINE configs (C2, C4, C5) and the widened rows are extra objects.
 """
 from __future__ import annotations
 
@@ -26,23 +33,59 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, AMD spec
 BF16_PEAK_TFLOPS = 2516.6      # MI355X dense bf16 MFMA, AMD spec
+GOLDEN = 0x9E3779B97F4A7C15
+
+
+def uniform_ids(seed: int, n: int, vocab: int):
+    """n token ids uniform in [0, vocab): splitmix64 outputs seed + k*gamma
+    (k = 1..n) reduced mod vocab."""
+    with np.errstate(over="ignore"):
+        z = np.uint64(seed) + np.uint64(GOLDEN) * np.arange(1, n + 1, dtype=np.uint64)
+        z = (z ^ (z >> np.uint64(30))) * np.uint64(0xBF58476D1CE4E5B9)
+        z = (z ^ (z >> np.uint64(27))) * np.uint64(0x94D049BB133111EB)
+        z = z ^ (z >> np.uint64(31))
+    return [int(v % vocab) for v in z]
+
+
+def llama_config(layers, hidden, heads, kv_heads, ffn, vocab, theta=10000.0, max_pos=2048,
+                 extra=None):
+    from esp_amd.config import DecoderConfig
+    raw = {"architectures": ["LlamaForCausalLM"], "model_type": "llama",
+           "hidden_size": hidden, "intermediate_size": ffn, "num_hidden_layers": layers,
+           "num_attention_heads": heads, "num_key_value_heads": kv_heads,
+           "max_position_embeddings": max_pos, "rms_norm_eps": 1e-5, "rope_theta": theta,
+           "vocab_size": vocab, "tie_word_embeddings": False, "hidden_act": "silu"}
+    raw.update(extra or {})
+    return DecoderConfig.from_json_bytes(json.dumps(raw).encode())
 
 
 def c2_config(max_pos=2048):
-    from tests.synth import llama_config
     return llama_config(16, 2048, 32, 8, 8192, 128256, theta=500000.0, max_pos=max_pos,
                         extra={"tie_word_embeddings": True})
 
 
 def c3_config(max_pos=8192):
-    from tests.synth import llama_config
     return llama_config(32, 4096, 32, 8, 14336, 128256, theta=500000.0, max_pos=max_pos)
 
 
-def decode_bytes(cfg, ctx: int, kv_bytes_per_elem: int = 4, lora_rank: int = 0,
+C3_LORA = dict(lora_rank=16, lora_targets=["q_proj", "v_proj"], lora_a_std=0.02,
+               lora_b_std=0.01, lora_scale=2.0)
+
+
+def device_sync() -> None:
+    """hipDeviceSynchronize through the HIP runtime the library links."""
+    import ctypes as C
+    global _HIP
+    if "_HIP" not in globals():
+        _HIP = C.CDLL("libamdhip64.so.7")
+    assert _HIP.hipDeviceSynchronize() == 0
+
+
+def decode_bytes(cfg, ctx: int, kv_bytes_per_elem: int = 2, lora_rank: int = 0,
                  lora_targets=()) -> dict:
     """Algorithmic HBM bytes of one batch-1 decode step at context `ctx`:
-    every weight once (bf16) + the K/V cache once (f32) + LoRA A/B (bf16)."""
+    every weight once (bf16) + the K/V cache once (kv_bytes_per_elem bytes
+    per element; BASELINE.md counts 2) + LoRA A/B (bf16)."""
     H, L, F, V = cfg.hidden_size, cfg.num_hidden_layers, cfg.intermediate_size, cfg.vocab_size
     qw, kvw = cfg.query_width(), cfg.kv_heads() * cfg.head_dim()
     lora = 0
@@ -63,7 +106,7 @@ def mlp_gemv_bytes(cfg) -> int:
     return 2 * F * H * 2 + 2 * H * 4 + F * 4
 
 
-def measured_traffic(name: str = "decode_gemv_mlp_c2_traffic.md"):
+def measured_traffic(name: str = "decode_gemv_mlp_c3_traffic.md"):
     """HBM bytes per launch of the roofline kernel from the committed
     FETCH_SIZE / WRITE_SIZE counter summary (profiles/), or None."""
     path = os.path.join(ROOT, "profiles", name)
@@ -79,17 +122,16 @@ def measured_traffic(name: str = "decode_gemv_mlp_c2_traffic.md"):
 def traffic_run(steps: int = 8) -> None:
     """Workload for the FETCH_SIZE / WRITE_SIZE counter passes: one plain
     device-to-device copy of known size (the calibration dispatch), then a
-    C2 prefill and `steps` eager decode steps (the SwiGLU GEMV dispatches)."""
+    C3 prompt and `steps` eager decode steps (the SwiGLU GEMV dispatches)."""
     import torch
     from esp_amd import DecoderModel
-    from tests.synth import uniform_ids
     n = 64 << 20
     src = torch.ones(n, dtype=torch.float32, device="cuda")
     dst = torch.empty_like(src)
     dst.copy_(src)
     torch.cuda.synchronize()
-    cfg = c2_config()
-    model = DecoderModel.synthetic(cfg, seed=1234, std=0.02, fmt="bf16")
+    cfg = c3_config()
+    model = DecoderModel.synthetic(cfg, seed=4321, std=0.02, fmt="bf16", **C3_LORA)
     kv = model.new_cache(1, 600)
     model.try_forward_cached_last(uniform_ids(42, 512, cfg.vocab_size), kv)
     for i in range(steps):
@@ -108,14 +150,28 @@ def prefill_flops(cfg, S: int) -> float:
     return gemm + attn + head
 
 
-def cpu_baseline(cfg, ctx: int, budget_s: float = 15.0) -> dict:
-    """Oracle (CPU restatement of esp's f32 corridor) decode on the host
-    cores: same shape, bf16 weights widened to f32 on the fly, KV cache
-    filled synthetically to `ctx` positions."""
-    import numpy as np
+def cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(cfg, ctx: int = 4096, decode_runs: int = 7, prefill_len: int = 32,
+                 prefill_runs: int = 5) -> dict:
+    """The oracle (CPU restatement of esp's f32 corridor: bf16 weights widened
+    to f32 on the fly, head on the last position) on every host core: the
+    whole C3 model (32 layers, untied head) decoding one token at `ctx`
+    context over a K/V cache filled from the seed, median of `decode_runs`
+    single-token steps after one warm-up; and a `prefill_len`-token prompt
+    on an empty cache, median of `prefill_runs`. LoRA is left out: the
+    reference merges adapters into the weights at load (lora.rs:93-97), so
+    its decode cost is the base model's."""
     from oracle import oracle
     threads = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
-    threads = max(1, min(threads, 16))
     oracle.set_threads(threads)
     H, F, V = cfg.hidden_size, cfg.intermediate_size, cfg.vocab_size
     qw, kvw = cfg.query_width(), cfg.kv_heads() * cfg.head_dim()
@@ -124,15 +180,17 @@ def cpu_baseline(cfg, ctx: int, budget_s: float = 15.0) -> dict:
 
     def put(name, shape, one=False):
         nonlocal seed
-        n = int(np.prod(shape))
         if one:
             tensors[name] = (np.ones(shape, np.float32), "F32")
         else:
             seed += 1
-            tensors[name] = (oracle.fill_normal(seed, n, 0.02, True).reshape(shape), "BF16")
+            tensors[name] = (oracle.fill_normal(seed, int(np.prod(shape)), 0.02, True)
+                             .reshape(shape), "BF16")
 
+    t0 = time.perf_counter()
     put("model.embed_tokens.weight", (V, H))
     put("model.norm.weight", (H,), True)
+    put("lm_head.weight", (V, H))
     for l in range(cfg.num_hidden_layers):
         p = f"model.layers.{l}."
         put(p + "input_layernorm.weight", (H,), True)
@@ -144,34 +202,52 @@ def cpu_baseline(cfg, ctx: int, budget_s: float = 15.0) -> dict:
         put(p + "mlp.gate_proj.weight", (F, H))
         put(p + "mlp.up_proj.weight", (F, H))
         put(p + "mlp.down_proj.weight", (H, F))
-    m = oracle.OracleModel(cfg, tensors)
-    kv = m.new_cache(ctx + 80)
+    m = oracle.OracleModel(cfg, tensors, rope_max_pos=ctx + decode_runs + 8)
+    print(f"cpu_baseline: weights ready in {time.perf_counter() - t0:.1f} s on {threads} threads",
+          file=sys.stderr, flush=True)
+    kv = m.new_cache(ctx + decode_runs + 8)
     kv.fill_synthetic(ctx, 5)
-    m.forward_last(kv, [1])  # warm-up
-    steps, t0 = 0, time.perf_counter()
-    while True:
-        m.forward_last(kv, [steps % V])
-        steps += 1
-        el = time.perf_counter() - t0
-        if el > budget_s or steps >= 64:
-            break
-    return {"value": round(steps / el, 4), "unit": "tokens/s", "cores": threads,
-            "kind": "port",
-            "sample": f"{steps} batch-1 decode steps at context {ctx}+ of the C2 shape "
-                      f"(16 layers, bf16 weights widened to f32), CPU restatement of esp's "
-                      f"burn-ndarray path, OpenMP over {threads} threads"}
+    m.forward_last(kv, [1])  # warm-up (position ctx)
+    dec = []
+    for i in range(decode_runs):
+        t1 = time.perf_counter()
+        m.forward_last(kv, [(i * 7919) % V])
+        dec.append(time.perf_counter() - t1)
+    t_dec = sorted(dec)[len(dec) // 2]
+    pre = []
+    prompt = uniform_ids(77, prefill_len, V)
+    for _ in range(prefill_runs):
+        kvp = m.new_cache(prefill_len + 8)
+        t1 = time.perf_counter()
+        m.forward_last(kvp, prompt)
+        pre.append(time.perf_counter() - t1)
+        del kvp
+    t_pre = sorted(pre)[len(pre) // 2]
+    return {"value": round(1.0 / t_dec, 4), "unit": "tokens/s (decode, batch 1)",
+            "cores": threads, "kind": "port",
+            "sample": f"whole C3 model ({cfg.num_hidden_layers} layers, hidden {H}, ffn {F}, "
+                      f"vocab {V}, bf16 weights widened to f32), one decode token at context {ctx + 1}-"
+                      f"{ctx + decode_runs} over a seeded synthetic K/V cache, median of "
+                      f"{decode_runs} steps; CPU restatement of esp's burn-ndarray path, "
+                      f"OpenMP over {threads} threads",
+            "cpu_model": cpu_model(), "nproc": os.cpu_count(),
+            "decode_ms_per_token": round(t_dec * 1e3, 2),
+            "prefill_tokens_per_s": round(prefill_len / t_pre, 3),
+            "prefill_sample": f"{prefill_len}-token prompt on an empty cache, median of "
+                              f"{prefill_runs} runs"}
 
 
-def c3_bench(steps: int) -> dict:
+def c3_headline(steps: int, warmup: int) -> dict:
     """Llama-3-8B shape bf16 with rank-16 LoRA (alpha 32)
-    on q_proj and v_proj; batch-1 greedy decode at ~4096 context and a
-    separate 2048-token prefill."""
+    on q_proj and v_proj. One step = one request: a 4064-token prompt and 64
+    greedy decode tokens through the device loop (one captured decode step
+    replayed per token); decode time = step time minus the prompt's prefill
+    (the same 4064 tokens timed alone). Plus a separate 2048-token prefill
+    and the roofline pass over the dominant decode kernel."""
     from esp_amd import DecoderModel
-    from tests.synth import uniform_ids
+    from esp_amd.model import profile_enable, profile_read
     cfg = c3_config()
-    model = DecoderModel.synthetic(cfg, seed=4321, std=0.02, fmt="bf16", lora_rank=16,
-                                   lora_targets=["q_proj", "v_proj"], lora_a_std=0.02,
-                                   lora_b_std=0.01, lora_scale=2.0)
+    model = DecoderModel.synthetic(cfg, seed=4321, std=0.02, fmt="bf16", **C3_LORA)
     prompt = uniform_ids(7, 4064, cfg.vocab_size)
     n_dec = 64
     kv = model.new_cache(1, 4064 + n_dec)
@@ -189,25 +265,97 @@ def c3_bench(steps: int) -> dict:
         assert len(out) == n_dec
         return time.perf_counter() - t0
 
-    gen()
-    prefill(pre)
-    t_gen = sorted(gen() for _ in range(steps))[steps // 2]
+    for _ in range(max(1, warmup)):
+        gen()
+        prefill(pre)
+    device_sync()
+    t0 = time.perf_counter()
+    t_gen = [gen() for _ in range(steps)]
+    device_sync()
+    el = time.perf_counter() - t0
     t_p4 = sorted(prefill(prompt) for _ in range(steps))[steps // 2]
     t_p2 = sorted(prefill(pre) for _ in range(steps))[steps // 2]
-    t_dec = (t_gen - t_p4) / (n_dec - 1)
-    db = decode_bytes(cfg, 4064 + n_dec // 2, lora_rank=16, lora_targets=["q_proj", "v_proj"])
+    tg = sorted(t_gen)[steps // 2]
+    t_dec = (tg - t_p4) / (n_dec - 1)
+    ctx = 4064 + n_dec // 2
+    db = decode_bytes(cfg, ctx, 2, **{k: C3_LORA[k] for k in ("lora_rank", "lora_targets")})
+    own = decode_bytes(cfg, ctx, 4, **{k: C3_LORA[k] for k in ("lora_rank", "lora_targets")})
     fl = prefill_flops(cfg, 2048) + 2.0 * 2048 * 32 * 16 * (4096 + 4096 + 4096 + 1024)  # + LoRA
-    res = {"workload": "C3: Llama-3-8B shape bf16, LoRA r16 on q/v; decode at 4064-4128 "
-                       "context, separate 2048-token prefill (BASELINE configs[2])",
-           "decode_tokens_per_s": round(1.0 / t_dec, 2),
-           "decode_ms_per_token": round(t_dec * 1e3, 4),
-           "decode_hbm_frac": round(db["total"] / t_dec / 1e9 / HBM_PEAK_GBS, 4),
-           "decode_bytes_per_token": db["total"],
-           "prefill_2048_tokens_per_s": round(2048 / t_p2, 1),
-           "prefill_2048_ms": round(t_p2 * 1e3, 3),
-           "prefill_mfma_frac": round(fl / t_p2 / 1e12 / BF16_PEAK_TFLOPS, 4)}
+    # roofline pass: HIP events around every launch of the SwiGLU GEMV
+    # family over 16 eager decode steps at the same context
+    kv.reset(0)
+    model.try_forward_cached_last(prompt, kv)
+    profile_enable("gemv_mlp", True)
+    before = profile_read("gemv_mlp")
+    for i in range(16):
+        model.try_forward_cached_last([i + 1], kv)
+    after = profile_read("gemv_mlp")
+    profile_enable("gemv_mlp", False)
+    launches = after[0] - before[0]
+    ms = after[1] - before[1]
+    gbs = mlp_gemv_bytes(cfg) * launches / (ms / 1e3) / 1e9
     model.close()
-    return res
+    return {
+        "value": round(1.0 / t_dec, 2), "ms_per_step": round(tg * 1e3, 3),
+        "timed_region_s": round(el, 3),
+        "decode_ms_per_token": round(t_dec * 1e3, 4),
+        "decode_hbm_frac": round(db["total"] / t_dec / 1e9 / HBM_PEAK_GBS, 4),
+        "decode_bytes_per_token": db["total"],
+        "decode_hbm_frac_own_bytes": round(own["total"] / t_dec / 1e9 / HBM_PEAK_GBS, 4),
+        "decode_own_bytes_per_token": own["total"],
+        "prefill_tokens_per_s": round(2048 / t_p2, 1),
+        "prefill_2048_ms": round(t_p2 * 1e3, 3),
+        "prefill_mfma_frac": round(fl / t_p2 / 1e12 / BF16_PEAK_TFLOPS, 4),
+        "prompt_4064_prefill_ms": round(t_p4 * 1e3, 3),
+        "roofline": {"bound": "hbm",
+                     "kernel": "decode_gemv_k<bf16, SWIGLU> (C3 gate+up projections, fused "
+                               "RMSNorm: 2 x 14336 x 4096 bf16 weights per launch)",
+                     "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
+                     "algorithmic_bytes": mlp_gemv_bytes(cfg), "launches": launches,
+                     "avg_launch_us": round(ms / max(1, launches) * 1e3, 3)},
+    }
+
+
+def c2_bench(steps: int, warmup: int, prompt_len: int = 512, n_decode: int = 256) -> dict:
+    """Llama-3.2-1B shape bf16, batch 1: a 512-token
+    prompt then 256 greedy decode steps (device loop); decode tokens/s with
+    the prefill subtracted, and the prefill rate."""
+    from esp_amd import DecoderModel
+    cfg = c2_config()
+    model = DecoderModel.synthetic(cfg, seed=1234, std=0.02, fmt="bf16")
+    prompt = uniform_ids(42, prompt_len, cfg.vocab_size)
+    kv = model.new_cache(1, prompt_len + n_decode)
+
+    def gen():
+        t0 = time.perf_counter()
+        out = model.generate_greedy_device(kv, prompt, n_decode, eos=[])
+        assert len(out) == n_decode
+        return time.perf_counter() - t0
+
+    def prefill():
+        kv.reset(0)
+        t0 = time.perf_counter()
+        model.try_forward_cached_last(prompt, kv)
+        return time.perf_counter() - t0
+
+    for _ in range(max(1, warmup)):
+        gen()
+        prefill()
+    tg = sorted(gen() for _ in range(steps))[steps // 2]
+    tp = sorted(prefill() for _ in range(steps))[steps // 2]
+    t_dec = (tg - tp) / (n_decode - 1)
+    db = decode_bytes(cfg, prompt_len + n_decode // 2)
+    model.close()
+    return {"workload": "C2: Llama-3.2-1B shape bf16, 512-token prefill + 256 greedy decode "
+                        "steps, batch 1 (BASELINE configs[1])",
+            "decode_tokens_per_s": round(1.0 / t_dec, 2),
+            "decode_ms_per_token": round(t_dec * 1e3, 4),
+            "decode_hbm_frac": round(db["total"] / t_dec / 1e9 / HBM_PEAK_GBS, 4),
+            "decode_bytes_per_token": db["total"],
+            "prefill_tokens_per_s": round(prompt_len / tp, 1),
+            "prefill_ms": round(tp * 1e3, 3),
+            "prefill_mfma_frac": round(prefill_flops(cfg, prompt_len) / tp / 1e12 / BF16_PEAK_TFLOPS, 4)}
 
 
 def packed_decode_bytes(cfg, ctx: int, bits: int) -> dict:
@@ -230,7 +378,6 @@ def c3_packed_bench(bits: int) -> dict:
     token is the difference of two device loops (16 and 80 new tokens) over
     the same 4064-token prompt, so the prompt's prefill cancels."""
     from esp_amd import DecoderModel
-    from tests.synth import uniform_ids
     cfg = c3_config()
     fmt = "q8-block32" if bits == 8 else "q4-block32"
     model = DecoderModel.synthetic(cfg, seed=4321, std=0.02, fmt=fmt)
@@ -331,7 +478,6 @@ def c3_stream_bench() -> dict:
     Then the same model with a device layer cache holding every layer."""
     from esp_amd import DecoderModel
     from esp_amd.streaming import ArtifactSource, StreamingOptions
-    from tests.synth import uniform_ids
     cfg = c3_config()
     shared, layers = synthetic_layer_artifacts(cfg)
     per_forward = sum(len(x) for x in layers)
@@ -397,13 +543,14 @@ def c4_config(max_pos=4096):
 def moe_decode_bytes(cfg, ctx: int) -> int:
     """Algorithmic HBM bytes of one batch-1 MoE decode step: attention
     weights, router and the top-k experts' gate/up/down rows of every layer
-    (bf16), the head (bf16) and the K/V cache (f32) once."""
+    (bf16), the head (bf16) and the K/V cache once (2 bytes per element, as
+    BASELINE.md counts it)."""
     H, L, V = cfg.hidden_size, cfg.num_hidden_layers, cfg.vocab_size
     qw, kvw = cfg.query_width(), cfg.kv_heads() * cfg.head_dim()
     m = cfg.moe
     layer = (H * (qw + 2 * kvw) + H * qw + m.num_experts * H
              + m.num_experts_per_tok * 3 * H * m.moe_intermediate_size) * 2
-    return L * layer + V * H * 2 + 2 * L * kvw * ctx * 4
+    return L * layer + V * H * 2 + 2 * L * kvw * ctx * 2
 
 
 def moe_prefill_flops(cfg, S: int) -> float:
@@ -424,7 +571,6 @@ def c4_bench(steps: int) -> dict:
     synthetic N(0, 0.02) weights: a 2048-token uniform-random prefill, then
     batch-1 greedy decode at ~2048 context (device loop, captured step)."""
     from esp_amd import DecoderModel
-    from tests.synth import uniform_ids
     cfg = c4_config()
     model = DecoderModel.synthetic(cfg, seed=777, std=0.02, fmt="bf16")
     prompt = uniform_ids(17, 2048, cfg.vocab_size)
@@ -476,7 +622,6 @@ def c5_bench(steps: int, warmup: int = 2) -> dict:
     uniform-random ids before timing."""
     import numpy as np
     from esp_amd import DecoderModel, Sampler
-    from tests.synth import uniform_ids
     cfg = c2_config(max_pos=2048)
     B, ctx0, V = 64, 1024, cfg.vocab_size
     total = warmup + steps
@@ -521,7 +666,7 @@ def c5_bench(steps: int, warmup: int = 2) -> dict:
         step(st)
     el = time.perf_counter() - t0
     ctx_mid = ctx0 + 8 * total // 2
-    qkv_kv = 2 * cfg.num_hidden_layers * cfg.kv_heads() * cfg.head_dim() * 4
+    qkv_kv = 2 * cfg.num_hidden_layers * cfg.kv_heads() * cfg.head_dim() * 2
     step_bytes = decode_bytes(cfg, 0)["gemv_weights"] + B * ctx_mid * qkv_kv + 2 * B * V * 4 + B * words * 4
     res = {"workload": "C5: 1B shape bf16, 64 sequences at 1024-1200 context; per step 56 decode "
                        "rows + 8 forced 8-token blocks, allowed-token bitmask (5%) + seeded "
@@ -579,7 +724,6 @@ def c5_grammar_bench(steps: int, warmup: int = 2) -> dict:
     from esp_amd.constraint import Constraint, Vocabulary
     from esp_amd.model import profile_enable, profile_read
     from tests.grammar_cases import llama_sized_table
-    from tests.synth import uniform_ids
     cfg = c2_config(max_pos=4096)
     B, ctx0, V = 64, 1024, cfg.vocab_size
     total = warmup + steps
@@ -653,21 +797,11 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=3)
     ap.add_argument("--warmup", type=int, default=1)
-    ap.add_argument("--prompt", type=int, default=512)
-    ap.add_argument("--decode", type=int, default=256)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--no-c3", action="store_true")
-    ap.add_argument("--only-c3", action="store_true")
-    ap.add_argument("--no-c4", action="store_true")
-    ap.add_argument("--only-c4", action="store_true")
-    ap.add_argument("--no-c5", action="store_true")
-    ap.add_argument("--only-c5", action="store_true")
-    ap.add_argument("--no-c5g", action="store_true")
-    ap.add_argument("--no-packed", action="store_true")
-    ap.add_argument("--only-packed", action="store_true")
-    ap.add_argument("--only-c5g", action="store_true")
-    ap.add_argument("--no-stream", action="store_true")
-    ap.add_argument("--only-stream", action="store_true")
+    for leg in ("c2", "c4", "c5", "c5g", "packed", "stream"):
+        ap.add_argument(f"--no-{leg}", action="store_true")
+        ap.add_argument(f"--only-{leg}", action="store_true")
+    ap.add_argument("--only-c3", action="store_true", help="the headline leg alone (no CPU baseline)")
     ap.add_argument("--traffic", action="store_true",
                     help="run only the workload of the HBM-traffic counter passes")
     args = ap.parse_args()
@@ -675,135 +809,50 @@ def main():
         print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 "
                                    "(multi-GPU sharding is design-only)"}))
         sys.exit(2)
-    from esp_amd import DecoderModel
-    from esp_amd.model import profile_enable, profile_read
-    from tests.synth import uniform_ids
-
+    steps = max(1, args.steps)
     if args.traffic:
         traffic_run()
         return
-    if args.only_c3:
-        print(json.dumps({"c3": c3_bench(max(1, args.steps))}), flush=True)
-        return
-    if args.only_c4:
-        print(json.dumps({"c4": c4_bench(max(1, args.steps))}), flush=True)
-        return
-    if args.only_c5:
-        print(json.dumps({"c5": c5_bench(16)}), flush=True)
-        return
+    only = {"c2": lambda: c2_bench(steps, args.warmup), "c4": lambda: c4_bench(steps),
+            "c5": lambda: c5_bench(16), "c5g": lambda: c5_grammar_bench(32),
+            "stream": lambda: c3_stream_bench()}
+    for leg, fn in only.items():
+        if getattr(args, f"only_{leg}"):
+            print(json.dumps({leg: fn()}), flush=True)
+            return
     if args.only_packed:
         print(json.dumps({"c3_q8": c3_packed_bench(8), "c3_q4": c3_packed_bench(4)}), flush=True)
         return
-    if args.only_stream:
-        print(json.dumps({"c3_stream": c3_stream_bench()}), flush=True)
-        return
-    if args.only_c5g:
-        print(json.dumps({"c5_grammar": c5_grammar_bench(32)}), flush=True)
-        return
-    cfg = c2_config()
-    model = DecoderModel.synthetic(cfg, seed=1234, std=0.02, fmt="bf16")
-    prompt = uniform_ids(42, args.prompt, cfg.vocab_size)
-    ctx = args.prompt + args.decode
-    kv = model.new_cache(1, ctx)
-
-    def gen():
-        return model.generate_greedy_device(kv, prompt, args.decode, eos=[])
-
-    def prefill():
-        kv.reset(0)
-        model.try_forward_cached_last(prompt, kv)
-
-    for _ in range(args.warmup):
-        gen()
-        prefill()
-    t_gen, t_pre = [], []
-    for _ in range(args.steps):
-        t0 = time.perf_counter()
-        out = gen()
-        t_gen.append(time.perf_counter() - t0)
-        assert len(out) == args.decode
-    for _ in range(args.steps):
-        t0 = time.perf_counter()
-        prefill()
-        t_pre.append(time.perf_counter() - t0)
-    tg = sorted(t_gen)[len(t_gen) // 2]
-    tp = sorted(t_pre)[len(t_pre) // 2]
-    n_dec = args.decode - 1
-    t_dec = tg - tp
-    dec_tps = n_dec / t_dec
-    pre_tps = args.prompt / tp
-    avg_ctx = args.prompt + args.decode / 2
-    db = decode_bytes(cfg, int(avg_ctx))
-    # profiled pass: per-launch HIP events on the KV stream. The dominant
-    # decode kernel is the SwiGLU GEMV (decode_gemv_k, gate+up: the largest
-    # per-layer weight stream); with ESP_STEP=1 it is the persistent step
-    # kernel (one launch = all layers + head: every weight + the K/V once).
-    fams = ("step", "gemv_mlp")
-    for fam in fams:
-        profile_enable(fam, True)
-    gen_eager_steps = 16
-    kv2 = model.new_cache(1, ctx)
-    kv2.reset(0)
-    model.try_forward_cached_last(prompt, kv2)
-    before = {fam: profile_read(fam) for fam in fams}
-    for i in range(gen_eager_steps):
-        model.try_forward_cached_last([i + 1], kv2)
-    after = {fam: profile_read(fam) for fam in fams}
-    for fam in fams:
-        profile_enable(fam, False)
-    if after["step"][0] > before["step"][0]:
-        fam, kname = "step", "step_k (persistent decode step: all layers + head)"
-        fam_bytes = sum(decode_bytes(cfg, args.prompt + i + 1)["total"] for i in range(gen_eager_steps))
-    else:
-        fam, kname = "gemv_mlp", "decode_gemv_k<bf16, SWIGLU> (gate+up projections, fused RMSNorm)"
-        fam_bytes = mlp_gemv_bytes(cfg) * (after[fam][0] - before[fam][0])
-    gemv_launches = after[fam][0] - before[fam][0]
-    gemv_ms = after[fam][1] - before[fam][1]
-    gemv_gbs = fam_bytes / (gemv_ms / 1e3) / 1e9
+    cfg = c3_config()
+    h = c3_headline(steps, args.warmup)
     result = {
         "metric": "decode & prefill tokens/s on 1 MI355X; % of HBM / bf16-MFMA roofline",
-        "value": round(dec_tps, 2),
+        "value": h["value"],
         "unit": "tokens/s (decode, batch 1)",
         "n_gpus": 1,
-        "steps": args.steps,
+        "steps": steps,
         "warmup": args.warmup,
-        "ms_per_step": round(tg * 1e3, 3),
+        "ms_per_step": h["ms_per_step"],
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16 weights, f32 activations/accumulation",
-        "data": "synthetic (random-init N(0,0.02) weights, uniform-random prompt ids)",
-        "config": {"workload": "C2: Llama-3.2-1B shape, 512-token prefill + 256 greedy decode "
-                               "steps, batch 1 (BASELINE configs[1])",
-                   "global_batch": 1, "seq_len": ctx, "parallelism": "none (1 GPU)"},
-        "prefill_tokens_per_s": round(pre_tps, 1),
-        "prefill_ms": round(tp * 1e3, 3),
-        "prefill_mfma_frac": round(prefill_flops(cfg, args.prompt) / tp / 1e12 / BF16_PEAK_TFLOPS, 4),
-        "decode_ms_per_token": round(t_dec / n_dec * 1e3, 4),
-        "decode_hbm_frac": round(db["total"] / (t_dec / n_dec) / 1e9 / HBM_PEAK_GBS, 4),
-        "roofline": {"bound": "hbm", "kernel": kname,
-                     "achieved": round(gemv_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gemv_gbs / HBM_PEAK_GBS, 4),
-                     "traffic": measured_traffic() if fam == "gemv_mlp" else None,
-                     "launches": gemv_launches,
-                     "avg_launch_us": round(gemv_ms / max(1, gemv_launches) * 1e3, 3)},
+        "data": "synthetic (random-init N(0,0.02) weights, LoRA A~N(0,0.02) B~N(0,0.01), "
+                "uniform-random prompt ids)",
+        "config": {"workload": "C3: Llama-3-8B shape bf16 + LoRA r16 alpha 32 on q/v; 4064-token "
+                               "prompt then 64 greedy decode steps (decode at 4064-4128 context), "
+                               "batch 1; separate 2048-token prefill (BASELINE configs[2])",
+                   "global_batch": 1, "seq_len": 4128, "parallelism": "none (1 GPU)"},
     }
-    print(f"gpu: decode {dec_tps:.1f} tok/s, prefill {pre_tps:.1f} tok/s, {fam} {gemv_gbs:.0f} GB/s",
-          file=sys.stderr, flush=True)
-    if not args.no_c3:
-        del kv, kv2
-        model.close()
-        result["c3"] = c3_bench(max(1, args.steps))
-        print(f"c3: {result['c3']}", file=sys.stderr, flush=True)
-    if not args.no_c4:
-        result["c4"] = c4_bench(max(1, args.steps))
-        print(f"c4: {result['c4']}", file=sys.stderr, flush=True)
-    if not args.no_c5:
-        result["c5"] = c5_bench(16)
-        print(f"c5: {result['c5']}", file=sys.stderr, flush=True)
-    if not args.no_c5g:
-        result["c5_grammar"] = c5_grammar_bench(32)
-        print(f"c5_grammar: {result['c5_grammar']}", file=sys.stderr, flush=True)
+    result.update({k: v for k, v in h.items() if k not in ("value", "ms_per_step")})
+    print(f"c3: decode {h['value']} tok/s ({h['decode_hbm_frac']} of HBM on BASELINE bytes), "
+          f"prefill {h['prefill_tokens_per_s']} tok/s", file=sys.stderr, flush=True)
+    legs = [("c2", lambda: c2_bench(steps, args.warmup)), ("c4", lambda: c4_bench(steps)),
+            ("c5", lambda: c5_bench(16)), ("c5_grammar", lambda: c5_grammar_bench(32))]
+    for name, fn in legs:
+        if not getattr(args, "no_" + ("c5g" if name == "c5_grammar" else name)):
+            result[name] = fn()
+            print(f"{name}: {result[name]}", file=sys.stderr, flush=True)
     if not args.no_packed:
         for bits in (8, 4):
             result[f"c3_q{bits}"] = c3_packed_bench(bits)
@@ -812,7 +861,8 @@ def main():
         result["c3_stream"] = c3_stream_bench()
         print(f"c3_stream: {result['c3_stream']}", file=sys.stderr, flush=True)
     if not args.no_cpu:
-        result["cpu_baseline"] = cpu_baseline(cfg, int(avg_ctx))
+        result["cpu_baseline"] = cpu_baseline(cfg)
+        print(f"cpu_baseline: {result['cpu_baseline']}", file=sys.stderr, flush=True)
     print(json.dumps(result), flush=True)
 
 

@@ -21,7 +21,6 @@ Model *synthetic_model(const esp_config *cfg, uint64_t seed, float std, uint32_t
                        uint32_t lora_mask, float lora_a_std, float lora_b_std, float lora_scale);
 Kv *create_kv(Model *m, uint32_t batch, uint32_t max_ctx);
 void decode_step_dev(Model &m, Kv &kv, int seq, int max_t, int32_t *gen);
-void check_step_barrier(Kv &kv);
 void launch_gen_step(const uint32_t *picked, int32_t *gen, hipStream_t s);
 }  // namespace esp
 
@@ -619,7 +618,6 @@ esp_status esp_generate_greedy(esp_model *model, esp_kv *kv, uint32_t seq, const
         std::vector<int32_t> list(max_new);
         ESP_HIP(hipMemcpyAsync(list.data(), g + 8, (size_t)max_new * 4, hipMemcpyDeviceToHost, s));
         ESP_HIP(hipStreamSynchronize(s));
-        check_step_barrier(k);
         k.pos[seq] = (int)last_pos;
         uint32_t n = 0;
         for (; n < max_new; ++n) {

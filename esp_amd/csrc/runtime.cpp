@@ -16,18 +16,14 @@
 #include "kernels_extra.hpp"
 #include "profile.hpp"
 #include "safetensors.hpp"
-#include "step.hpp"
 #include "streaming.hpp"
 
 namespace esp {
 
-// word offset of the step kernel's barrier state in Kv::tickets (128-byte aligned)
-static const int kStepBarOff = (4096 + 8 + 2 * DG_MAX_PART + 8 + 31) / 32 * 32;
+// words of Kv::tickets (128-byte multiple)
+static const int kTicketWords = (4096 + 8 + 2 * DG_MAX_PART + 8 + 31) / 32 * 32;
 
 struct Rows;
-static bool step_usable(Model &m);
-static void run_step(Model &m, Kv &kv, const Rows &rows, int max_t, int32_t *gen);
-void check_step_barrier(Kv &kv);
 
 Kv::~Kv() {
     if (gen_exec) (void)hipGraphExecDestroy(gen_exec);
@@ -744,9 +740,8 @@ Kv *create_kv(Model *m, uint32_t batch, uint32_t max_ctx) {
     kv->pos.assign(batch, 0);
     ESP_HIP(hipStreamCreateWithFlags(&kv->stream, hipStreamNonBlocking));
     // [0, 4096): attention merge tickets; [4096]: head ticket; then argmax
-    // partials (values, ids) and the picked id; then the step kernel's
-    // barrier words
-    kv->tickets.alloc((size_t)(kStepBarOff + STEP_BAR_WORDS) * 4);
+    // partials (values, ids) and the picked id
+    kv->tickets.alloc((size_t)kTicketWords * 4);
     ESP_HIP(hipMemset(kv->tickets.p, 0, kv->tickets.bytes));
     (void)attn_xcd_mode();  // one-time dispatch probe, outside any graph capture
     return kv.release();
@@ -1446,14 +1441,6 @@ void forward(Model &m, Kv &kv, int n_seqs, const uint32_t *seqs, const uint32_t 
         memcpy(pin + lastoff, last.data(), n_seqs * 4);
         ESP_HIP(hipMemcpyAsync(dev, pin, (size_t)(lastoff + n_seqs) * 4, hipMemcpyHostToDevice, s));
         Rows rows{dev, dev + kMaxRows, dev + 2 * kMaxRows, Mc, n_seqs == 1 ? (int)seqs[0] : -1};
-        if (M == 1 && step_usable(m)) {  // one decode row: the persistent step kernel
-            run_step(m, kv, rows, max_t, nullptr);
-            ESP_HIP(hipStreamSynchronize(s));
-            check_step_barrier(kv);
-            kv.pos[seqs[0]] += 1;
-            kv.logits_rows = 1;
-            return;
-        }
         {
             Prof p("embed", s);
             launch_embed(m.et, m.embed, rows.ids, Mc, m.H, kv.h.as<float>(), s);
@@ -1538,123 +1525,10 @@ namespace esp {
 // One greedy decode step whose input token, position and output slot live
 // in device memory (gen layout in k_basic.hip), so the step can be captured
 // once and replayed: generate.rs:154-168 without the host round trip.
-// Whether single-row forwards run as one persistent step kernel. Opt-in
-// (environment ESP_STEP=1, read once per model): measured on MI355X, its
-// grid barriers (~3-4 us each, six or seven per layer) cost more than the
-// launch gaps of the per-kernel decode path they replace.
-static bool step_usable(Model &m) {
-    if (m.st) return false;  // streamed layers are staged between kernels
-    if (m.step_mode < 0) {
-        bool qk = false, moe = false;
-        for (auto &w : m.layers) {
-            qk = qk || w.q_norm || w.k_norm;
-            moe = moe || w.moe;
-        }
-        const char *env = getenv("ESP_STEP");
-        const bool on = env && env[0] == '1';
-        m.step_mode = on && step_ok(m.hd, m.nq / m.nkv, m.H, m.qw, m.F, qk, moe, m.wt) ? 1 : 0;
-        if (m.step_mode) {
-            const int qkv_n = m.qw + 2 * m.kvw;
-            std::vector<StepLayer> v(m.L);
-            for (int l = 0; l < m.L; ++l) {
-                const LayerW &w = m.layers[l];
-                StepLayer &o = v[l];
-                o.qkv = w.qkv;
-                o.qkv_bias = w.qkv_bias;
-                o.in_norm = w.in_norm;
-                o.post_norm = w.post_norm;
-                o.o = w.o;
-                o.o_bias = w.o_bias;
-                o.gate = w.gate;
-                o.up = w.up;
-                o.down = w.down;
-                o.lora_rows = w.qkv_rows - qkv_n;
-                for (int j = 0; j < 3; ++j) {
-                    o.lora_b[j] = w.lora_rank[j] ? w.lora_b[j] : nullptr;
-                    o.lora_rank[j] = w.lora_rank[j];
-                    o.lora_t_col[j] = w.lora_rank[j] ? w.lora_t_col[j] - qkv_n : 0;
-                    o.lora_scale[j] = w.lora_scale[j];
-                }
-                o.window = w.window;
-            }
-            m.step_layers.reset(new DevMem(sizeof(StepLayer) * v.size()));
-            ESP_HIP(hipMemcpy(m.step_layers->p, v.data(), sizeof(StepLayer) * v.size(),
-                              hipMemcpyHostToDevice));
-        }
-    }
-    return m.step_mode == 1;
-}
-
-// One decode step for one row (embedding, layers, head) as a single
-// persistent kernel; `gen` (device-loop state) receives the greedy id.
-static void run_step(Model &m, Kv &kv, const Rows &rows, int max_t, int32_t *gen) {
-    hipStream_t s = kv.stream;
-    StepArgs a{};
-    a.layers = m.step_layers->as<StepLayer>();
-    a.L = m.L;
-    a.H = m.H;
-    a.F = m.F;
-    a.V = m.V;
-    a.nq = m.nq;
-    a.nkv = m.nkv;
-    a.hd = m.hd;
-    a.eps = m.cfg.rms_norm_eps;
-    a.embed = m.embed;
-    a.head = m.head;
-    a.final_norm = m.final_norm;
-    a.rope_cos = m.rope_cos;
-    a.rope_sin = m.rope_sin;
-    a.ids = rows.ids;
-    a.row_seq = rows.row_seq;
-    a.row_pos = rows.row_pos;
-    a.kv = kv.cache.as<float>();
-    a.seq_stride = kv.seq_stride;
-    a.layer_stride = kv.layer_stride;
-    a.kv_half_stride = kv.half_stride;
-    a.head_stride = kv.head_stride;
-    a.n_split = step_attn_splits(m.hd, m.nq / m.nkv, m.nkv, max_t, &a.split_len);
-    kv.part.ensure((size_t)m.nq * a.n_split * (m.hd + ATT_PART_PAD) * 4);
-    a.h = kv.h.as<float>();
-    a.t = kv.qkv.as<float>();
-    a.q = kv.q.as<float>();
-    a.attn = kv.attn.as<float>();
-    a.act = kv.act.as<float>();
-    a.part = kv.part.as<float>();
-    a.logits = kv.logits.as<float>();
-    a.nch_h = step_nch(m.H);
-    a.nch_q = step_nch(m.qw);
-    a.nch_f = step_nch(m.F);
-    int32_t *t = kv.tickets.as<int32_t>();
-    a.part_v = (float *)(t + 4096 + 8);
-    a.part_i = t + 4096 + 8 + DG_MAX_PART;
-    a.picked = gen ? (uint32_t *)(t + 4096 + 8 + 2 * DG_MAX_PART) : nullptr;
-    a.gen = gen;
-    a.bar = (unsigned *)(t + kStepBarOff);
-    Prof p("step", s);
-    launch_step(a, m.nq / m.nkv, s);
-}
-
-// Reports (and clears) a grid-barrier time-out of the step kernel; call
-// after the stream has drained.
-void check_step_barrier(Kv &kv) {
-    unsigned *bar = (unsigned *)(kv.tickets.as<int32_t>() + kStepBarOff);
-    unsigned err = 0;
-    ESP_HIP(hipMemcpy(&err, bar + 2, 4, hipMemcpyDeviceToHost));
-    if (err) {
-        ESP_HIP(hipMemset(bar, 0, STEP_BAR_WORDS * 4));
-        fail(ESP_BACKEND, "decode step: a grid barrier timed out");
-    }
-}
-
 void decode_step_dev(Model &m, Kv &kv, int seq, int max_t, int32_t *gen) {
     hipStream_t s = kv.stream;
     ensure_scratch(m, kv, 1, 1);
     Rows rows{gen, gen + 2, gen + 3, 1, seq};
-    if (step_usable(m)) {
-        run_step(m, kv, rows, max_t, gen);
-        kv.logits_rows = 1;
-        return;
-    }
     {
         Prof p("embed", s);
         launch_embed(m.et, m.embed, rows.ids, 1, m.H, kv.h.as<float>(), s);

@@ -83,9 +83,6 @@ struct Model {
     std::vector<std::unique_ptr<DevMem>> mem;
     uint64_t weight_bytes = 0;
     int device = 0;
-    // persistent decode-step kernel: -1 not decided, 0 not usable, 1 usable
-    int step_mode = -1;
-    std::unique_ptr<DevMem> step_layers;  // StepLayer[L]
     // layer streaming: layers come from a host source per forward
     // (`layers` then holds only their geometry and windows)
     std::shared_ptr<Streamer> st;

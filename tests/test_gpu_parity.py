@@ -455,53 +455,6 @@ def test_lora_unmerged_matches_merged_oracle(fmt):
     assert model.generate_greedy_device(model.new_cache(1, 64), prompt, 6, eos=[]) == ids
 
 
-STEP_VARIANTS = {
-    "llama_hd128_lora": ({}, 128, 8, 2, True),
-    "mistral_window_hd64_g8": ({"model_type": "mistral", "architectures": ["MistralForCausalLM"],
-                                "sliding_window": 20}, 64, 8, 1, False),
-    "qwen2_bias_hd64": ({"model_type": "qwen2", "architectures": ["Qwen2ForCausalLM"]}, 64, 4, 2, False),
-}
-
-
-@pytest.mark.parametrize("variant", sorted(STEP_VARIANTS))
-def test_step_kernel_opt_in_matches_oracle(variant, monkeypatch):
-    """The persistent decode-step kernel (ESP_STEP=1): embedding, every layer
-    and the head of a single-token step in one launch with grid barriers;
-    bf16 weights, logits within the bf16 tolerance of the oracle over a
-    prefill and 5 teacher-forced steps, and the device greedy loop (one
-    step-kernel launch per token) equal to the host loop."""
-    from esp_amd.model import LoraAdapter
-    monkeypatch.setenv("ESP_STEP", "1")
-    extra, hd, nq, nkv, lora = STEP_VARIANTS[variant]
-    cfg = synth.llama_config(2, 256, nq, nkv, 320, 777, head_dim=hd, max_pos=96, extra=extra)
-    tensors = synth.make_tensors(cfg, 41, "bf16", bias_std=0.05)
-    adapters, ref_tensors = [], tensors
-    if lora:
-        ad = _adapter(cfg, 16, ["q_proj", "v_proj"], 3, "bf16")
-        adapters = [LoraAdapter(16, 32.0, ["q_proj", "v_proj"], st.dump(ad))]
-        ref_tensors = oracle.apply_lora(cfg, tensors, {"rank": 16, "alpha": 32.0,
-                                                       "targets": ["q_proj", "v_proj"], "tensors": ad})
-    model = DecoderModel.from_bytes(cfg, st.dump(tensors), "bf16", adapters=adapters)
-    ref = oracle.OracleModel(cfg, ref_tensors)
-    prompt = synth.uniform_ids(23, 40, cfg.vocab_size)
-    kv, rkv = model.new_cache(1, 64), ref.new_cache(64)
-    got = model.try_forward_cached_last(prompt, kv)
-    want = ref.forward_last(rkv, prompt)
-    for step in range(5):
-        assert _close_bf16(got, want), (variant, step, float(np.abs(got - want).max()))
-        t = oracle.argmax(want)
-        got = model.try_forward_cached_last([t], kv)
-        want = ref.forward_last(rkv, [t])
-    assert _close_bf16(got, want), (variant, "last", float(np.abs(got - want).max()))
-    kv2 = model.new_cache(1, 64)
-    logits = model.try_forward_cached_last(prompt, kv2)
-    ids = []
-    for _ in range(6):
-        ids.append(int(np.argmax(logits)))
-        logits = model.try_forward_cached_last([ids[-1]], kv2)
-    assert model.generate_greedy_device(model.new_cache(1, 64), prompt, 6, eos=[]) == ids
-
-
 @pytest.mark.parametrize("protocol", ["xcd", "agent"])
 def test_decode_attention_merge_protocols(protocol, monkeypatch):
     """Split-K decode attention with either cross-block merge: partials
