@@ -820,6 +820,9 @@ def main():
         if getattr(args, f"only_{leg}"):
             print(json.dumps({leg: fn()}), flush=True)
             return
+    if args.only_c3:
+        print(json.dumps({"c3": c3_headline(steps, args.warmup)}), flush=True)
+        return
     if args.only_packed:
         print(json.dumps({"c3_q8": c3_packed_bench(8), "c3_q4": c3_packed_bench(4)}), flush=True)
         return

@@ -24,12 +24,12 @@ struct DecodeGemvArgs {
     float *kv;            // layer base of the f32 cache
     long long seq_stride, kv_half_stride, head_stride;
     int nq, nkv, hd;
-    // QKVROPE unmerged LoRA (targets 0 q, 1 k, 2 v): row o of target j gets
-    // + lora_scale[j] * B_j[o, :] . t_j with t_j at lora_t + lora_t_col[j]
-    const float *lora_t;  // nullable = no LoRA
-    const void *lora_b[3];
-    int lora_rank[3], lora_t_col[3];
-    float lora_scale[3];
+    // QKVROPE unmerged LoRA: the lora_rows rows after the q/k/v rows (the
+    // adapters' A rows) are projected in the same launch and stored, not
+    // rotated, to lora_t_out (t = A . norm(x)); the decode attention then adds
+    // scale * B t (lora.rs:93-97) to q, k and v.
+    int lora_rows;
+    float *lora_t_out;
     // routed experts (moe.rs:135-256, one row): with ex_sel set, SWIGLU
     // units are (slot, row) pairs, slot = unit / ex_rows, reading expert
     // ex_sel[slot] (clamped to [0, ex_count)) of the [E][rows][K] tensors;
@@ -65,6 +65,19 @@ struct AttnDecodeArgs {
     float *out;           // [M, nq*hd] f32, or the bf16 hi plane when out_lo is set
     uint16_t *out_lo;     // nullable: bf16 lo plane (split activation output)
     int xcd_nx;           // set by the launcher: merge protocol (0 = agent scope)
+    // Unmerged LoRA of a single decode row (M == 1), targets 0 q, 1 k, 2 v:
+    // with lora_on, q gets + RoPE_pos(scale_q * B_q t_q) when loaded, and the
+    // key row at the row's position gets + RoPE_pos(scale_k * B_k t_k) and its
+    // value row + scale_v * B_v t_v, written back to the cache by the block
+    // whose split holds that position (lora.rs:93-97; RoPE is linear, so
+    // RoPE(y + d) = RoPE(y) + RoPE(d)). lora_b[j] null = target j untouched.
+    int lora_on, lora_b_f32;
+    int lora_vec;           // bf16 B, every rank a multiple of 8, every t 16-byte aligned
+    const void *lora_b[3];  // [rows, rank] bf16 (or f32 when lora_b_f32)
+    const float *lora_t[3];
+    int lora_rank[3];
+    float lora_scale[3];
+    const float *rope_cos, *rope_sin;  // [max_pos, hd]
 };
 
 bool attn_decode_ok(int hd, int G);

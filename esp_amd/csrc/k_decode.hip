@@ -50,7 +50,8 @@ __global__ void __launch_bounds__(DG_THREADS) decode_gemv_k(DecodeGemvArgs a) {
     size_t ex0 = 0;  // element offset of the routed expert (RESID)
     if (EPI == DG_RESID && a.ex_sel)  // one routed expert's rows
         ex0 = (size_t)min(max(a.ex_sel[a.ex_slot], 0), a.ex_count - 1) * a.ex_stride;
-    const int units = EPI == DG_QKVROPE ? a.N / 2 : a.N;
+    // QKVROPE: N/2 rotary pairs, then the LoRA A rows in pairs
+    const int units = EPI == DG_QKVROPE ? a.N / 2 + (a.lora_rows + 1) / 2 : a.N;
 
     Chunk<WT> wc[R][NCH];
     auto load_rows = [&](int u0) {
@@ -72,12 +73,18 @@ __global__ void __launch_bounds__(DG_THREADS) decode_gemv_k(DecodeGemvArgs a) {
                 rs[r * 2 + 1] = a.ws2;
                 ro[r * 2] = ro[r * 2 + 1] = off;
             } else if (EPI == DG_QKVROPE) {
-                int half = a.hd / 2, head = u / half, d = u % half;
-                int row = head * a.hd + d;
                 rb[r * 2] = rb[r * 2 + 1] = W;
                 rs[r * 2] = rs[r * 2 + 1] = a.ws;
-                ro[r * 2] = (size_t)row * K;
-                ro[r * 2 + 1] = (size_t)(row + half) * K;
+                if (u < a.N / 2) {
+                    int half = a.hd / 2, head = u / half, d = u % half;
+                    int row = head * a.hd + d;
+                    ro[r * 2] = (size_t)row * K;
+                    ro[r * 2 + 1] = (size_t)(row + half) * K;
+                } else {  // LoRA A rows 2i, 2i + 1 (the last one clamped)
+                    const int i = 2 * (u - a.N / 2);
+                    ro[r * 2] = (size_t)(a.N + i) * K;
+                    ro[r * 2 + 1] = (size_t)(a.N + min(i + 1, a.lora_rows - 1)) * K;
+                }
             } else {
                 rb[r] = W;
                 rs[r] = a.ws;
@@ -196,28 +203,18 @@ __global__ void __launch_bounds__(DG_THREADS) decode_gemv_k(DecodeGemvArgs a) {
         } else if (EPI == DG_SWIGLU) {
             a.y[u] = silu(y[0]) * y[1];
         } else {  // DG_QKVROPE
+            if (u >= a.N / 2) {  // LoRA t = A . norm(x), stored as is
+                const int i = 2 * (u - a.N / 2);
+                a.lora_t_out[i] = y[0];
+                if (i + 1 < a.lora_rows) a.lora_t_out[i + 1] = y[1];
+                continue;
+            }
             const int hd = a.hd, half = hd / 2, head = u / half, d = u % half;
             const int r0 = head * hd + d, r1 = r0 + half;
             float v0 = y[0], v1 = y[1];
             if (a.bias) {
                 v0 = v0 + a.bias[r0];
                 v1 = v1 + a.bias[r1];
-            }
-            if (a.lora_t) {  // unmerged LoRA, before RoPE (lora.rs:93-97)
-                const int j = head < a.nq ? 0 : (head < a.nq + a.nkv ? 1 : 2);
-                if constexpr (!WPacked<WT>::v) if (a.lora_b[j]) {
-                    const WT *B = (const WT *)a.lora_b[j];
-                    const int rank = a.lora_rank[j];
-                    const int off = j == 0 ? 0 : (j == 1 ? a.nq * hd : (a.nq + a.nkv) * hd);
-                    const float *t = a.lora_t + a.lora_t_col[j];
-                    float c0 = 0.f, c1 = 0.f;
-                    for (int i = 0; i < rank; ++i) {
-                        c0 += ld(B, (size_t)(r0 - off) * rank + i) * t[i];
-                        c1 += ld(B, (size_t)(r1 - off) * rank + i) * t[i];
-                    }
-                    v0 = v0 + c0 * a.lora_scale[j];
-                    v1 = v1 + c1 * a.lora_scale[j];
-                }
             }
             const int pos = a.row_pos[0], seq = a.row_seq[0];
             const float *cs = a.rope_cos + (size_t)pos * hd;
@@ -335,7 +332,7 @@ static void dg_launch_nch(const DecodeGemvArgs &a, int cus, hipStream_t s) {
             &per_cu, reinterpret_cast<const void *>(decode_gemv_k<WT, EPI, RB, NCH>), DG_THREADS, 0));
         if (per_cu <= 0) per_cu = 1;
     }
-    const int units = EPI == DG_QKVROPE ? a.N / 2 : a.N;
+    const int units = EPI == DG_QKVROPE ? a.N / 2 + (a.lora_rows + 1) / 2 : a.N;
     const int groups = (units + RB - 1) / RB;
     // one round of resident blocks, every block doing the same number of
     // iterations
@@ -561,6 +558,80 @@ __global__ void __launch_bounds__(NW * 64) attn_decode_k(AttnDecodeArgs a) {
             q[j][4] = v1.x; q[j][5] = v1.y; q[j][6] = v1.z; q[j][7] = v1.w;
         }
     const int pos = a.row_pos[row];
+    // Unmerged LoRA of a single decode row: c = scale * B t for the group's
+    // query heads (and, in the block whose split holds the new key, for this
+    // kv head's key and value rows), one (head, dim) per thread into LDS;
+    // each lane then adds its dims' rotated deltas to q, and keeps the new
+    // key / value row's deltas for the patch in consume().
+    __shared__ float lc[GM + 2][HD];
+    float kd[DPL], vd[DPL];
+    bool kv_patch = false;
+    if (a.lora_on) {  // block-uniform
+        const bool own = pos >= s0 && pos < s1;
+        for (int o = tid; o < (G + 2) * HD; o += NT) {
+            const int j = o / HD, d = o % HD;
+            if (j >= G && !own) continue;
+            const int tg = j < G ? 0 : j - G + 1;
+            const size_t brow = j < G ? (size_t)(g * G + j) * HD + d : (size_t)g * HD + d;
+            float c = 0.f;
+            if (a.lora_b[tg]) {
+                const int rank = a.lora_rank[tg];
+                const float *t = a.lora_t[tg];
+                if (a.lora_vec) {  // bf16 rows of 8k values, 16-byte aligned rows and t
+                    const uint4 *B = (const uint4 *)((const uint16_t *)a.lora_b[tg] + brow * rank);
+                    const f32x4_t *t4 = (const f32x4_t *)t;
+#pragma unroll 4
+                    for (int i = 0; i < rank / 8; ++i) {
+                        const uint4 b = B[i];
+                        const f32x4_t ta = t4[2 * i], tb = t4[2 * i + 1];
+                        c += __uint_as_float(b.x << 16) * ta.x + __uint_as_float(b.x & 0xffff0000u) * ta.y +
+                             __uint_as_float(b.y << 16) * ta.z + __uint_as_float(b.y & 0xffff0000u) * ta.w +
+                             __uint_as_float(b.z << 16) * tb.x + __uint_as_float(b.z & 0xffff0000u) * tb.y +
+                             __uint_as_float(b.w << 16) * tb.z + __uint_as_float(b.w & 0xffff0000u) * tb.w;
+                    }
+                } else if (a.lora_b_f32) {
+                    const float *B = (const float *)a.lora_b[tg] + brow * rank;
+                    for (int i = 0; i < rank; ++i) c += B[i] * t[i];
+                } else {
+                    const uint16_t *B = (const uint16_t *)a.lora_b[tg] + brow * rank;
+                    for (int i = 0; i < rank; ++i) c += bf2f(B[i]) * t[i];
+                }
+                c = c * a.lora_scale[tg];
+            }
+            lc[j][d] = c;
+        }
+        const float *cs = a.rope_cos + (size_t)pos * HD + sub * 4;
+        const float *sn = a.rope_sin + (size_t)pos * HD + sub * 4;
+        const f32x4_t c_lo = *(const f32x4_t *)cs, c_hi = *(const f32x4_t *)(cs + HALF);
+        const f32x4_t s_lo = *(const f32x4_t *)sn, s_hi = *(const f32x4_t *)(sn + HALF);
+        __syncthreads();
+        // RoPE of the delta pair (d, d + HD/2), as the QKV epilogue rotates y
+        auto rot = [&](const float *c, float *out) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float x0 = c[sub * 4 + e], x1 = c[HALF + sub * 4 + e];
+                out[e] = x0 * c_lo[e] + (-x1) * s_lo[e];
+                out[4 + e] = x1 * c_hi[e] + x0 * s_hi[e];
+            }
+        };
+#pragma unroll
+        for (int j = 0; j < GM; ++j) {
+            if (j >= G) break;
+            float dq[DPL];
+            rot(lc[j], dq);
+#pragma unroll
+            for (int e = 0; e < DPL; ++e) q[j][e] += dq[e];
+        }
+        if (own && (a.lora_b[1] || a.lora_b[2])) {
+            kv_patch = true;
+            rot(lc[G], kd);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                vd[e] = lc[G + 1][sub * 4 + e];
+                vd[4 + e] = lc[G + 1][HALF + sub * 4 + e];
+            }
+        }
+    }
     int lo = a.window > 0 ? max(0, pos - a.window + 1) : 0;
     int hi = min(pos + 1, a.max_t);
     lo = max(lo, s0);
@@ -575,13 +646,28 @@ __global__ void __launch_bounds__(NW * 64) attn_decode_k(AttnDecodeArgs a) {
         for (int e = 0; e < DPL; ++e) acc[j][e] = 0.f;
     }
     // one chunk's keys [c0, c1) from a register buffer
-    auto consume = [&](const f32x4_t (&kk)[NS][2], f32x4_t (&vv)[NS][2], int c0, int c1) {
+    auto consume = [&](f32x4_t (&kk)[NS][2], f32x4_t (&vv)[NS][2], int c0, int c1) {
         bool ok[NS];
 #pragma unroll
         for (int st = 0; st < NS; ++st) {
             const int t = c0 + st * STEP + wave * KPW + grp;
             ok[st] = t >= lo && t < c1;
             if (!ok[st]) vv[st][0] = vv[st][1] = f32x4_t{0.f, 0.f, 0.f, 0.f};  // unread or unwritten rows
+            if (kv_patch && t == pos && c0 + st * STEP < c1) {
+                // the new key's LoRA deltas, kept in the cache for later steps
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    kk[st][0][e] += kd[e];
+                    kk[st][1][e] += kd[4 + e];
+                    vv[st][0][e] += vd[e];
+                    vv[st][1][e] += vd[4 + e];
+                }
+                float *kr = (float *)kb + (size_t)pos * HD, *vr = (float *)vb + (size_t)pos * HD;
+                *(f32x4_t *)kr = kk[st][0];
+                *(f32x4_t *)(kr + HALF) = kk[st][1];
+                *(f32x4_t *)vr = vv[st][0];
+                *(f32x4_t *)(vr + HALF) = vv[st][1];
+            }
         }
 #pragma unroll
         for (int j = 0; j < GM; ++j) {

@@ -822,9 +822,27 @@ static Dt lora_dt(Dt wt) { return dt_packed(wt) ? DT_F32 : wt; }
 
 // Split-K decode attention of Mc rows (each row its own query position)
 // into kv.attn (f32), with the plan from attn_decode_splits.
+// With `lora` (a single decode row whose QKV launch stored the LoRA t rows),
+// the attention adds the adapters' deltas to q and to the new key/value row.
 static void attn_decode_rows(Model &m, Kv &kv, const Rows &rows, int Mc, int l, const LayerW &w,
-                             const Plan &plan, Dt out_dt = DT_F32) {
+                             const Plan &plan, Dt out_dt = DT_F32, bool lora = false) {
     AttnDecodeArgs a{};
+    if (lora) {
+        a.lora_on = 1;
+        a.lora_b_f32 = lora_dt(m.wt) == DT_F32;
+        for (int j = 0; j < 3; ++j) {
+            if (!w.lora_rank[j]) continue;
+            a.lora_b[j] = w.lora_b[j];
+            a.lora_t[j] = kv.qkv.as<float>() + w.lora_t_col[j];
+            a.lora_rank[j] = w.lora_rank[j];
+            a.lora_scale[j] = w.lora_scale[j];
+        }
+        a.rope_cos = m.rope_cos;
+        a.rope_sin = m.rope_sin;
+        a.lora_vec = !a.lora_b_f32;
+        for (int j = 0; j < 3; ++j)
+            if (w.lora_rank[j] && (w.lora_rank[j] % 8 || w.lora_t_col[j] % 4)) a.lora_vec = 0;
+    }
     a.q = kv.q.as<float>();
     a.kv = kv.cache.as<float>() + (size_t)l * kv.layer_stride;
     a.seq_stride = kv.seq_stride;
@@ -864,20 +882,11 @@ static void run_layer_decode(Model &m, Kv &kv, const Rows &rows, LayerW &w, int 
     const int H = m.H;
     float *kvl = kv.cache.as<float>() + (size_t)l * kv.layer_stride;
     const bool lora = w.lora_rank[0] || w.lora_rank[1] || w.lora_rank[2];
-    if (!w.q_norm && decode_gemv_ok(H)) {
+    const bool attn_fast = attn_decode_ok(m.hd, m.nq / m.nkv);
+    // LoRA deltas ride the decode attention, so a LoRA layer takes the fused
+    // QKV launch only when that attention runs
+    if (!w.q_norm && decode_gemv_ok(H) && (!lora || attn_fast)) {
         const int qkv_n = m.qw + 2 * m.kvw;
-        if (lora) {  // t rows (LoRA A . norm(x)) into their qkv-buffer columns
-            DecodeGemvArgs t{};
-            t.w = (const char *)w.qkv + (size_t)qkv_n * H * dt_size(m.wt);
-            t.x = kv.h.as<float>();
-            t.gamma = w.in_norm;
-            t.eps = m.cfg.rms_norm_eps;
-            t.y = kv.qkv.as<float>() + qkv_n;
-            t.N = w.qkv_rows - qkv_n;
-            t.K = H;
-            Prof p("gemv_lora", s);
-            launch_decode_gemv(m.wt, DG_STORE, t, s);
-        }
         DecodeGemvArgs g{};
         g.w = w.qkv;
         g.ws = w.qkv_s;
@@ -899,14 +908,9 @@ static void run_layer_decode(Model &m, Kv &kv, const Rows &rows, LayerW &w, int 
         g.nq = m.nq;
         g.nkv = m.nkv;
         g.hd = m.hd;
-        if (lora) {
-            g.lora_t = kv.qkv.as<float>();
-            for (int j = 0; j < 3; ++j) {
-                g.lora_b[j] = w.lora_b[j];
-                g.lora_rank[j] = w.lora_rank[j];
-                g.lora_t_col[j] = w.lora_t_col[j];
-                g.lora_scale[j] = w.lora_scale[j];
-            }
+        if (lora) {  // t = A . norm(x) rows, in their qkv-buffer columns
+            g.lora_rows = w.qkv_rows - qkv_n;
+            g.lora_t_out = kv.qkv.as<float>() + qkv_n;
         }
         Prof p("gemv_qkv", s);
         launch_decode_gemv(m.wt, DG_QKVROPE, g, s);
@@ -964,9 +968,10 @@ static void run_layer_decode(Model &m, Kv &kv, const Rows &rows, LayerW &w, int 
         Prof p("rope_kv", s);
         launch_rope_kv(lora_dt(m.wt), kv.dt, r, s);
     }
-    if (attn_decode_ok(m.hd, m.nq / m.nkv)) {
+    if (attn_fast) {
         Prof p("attention", s);
-        attn_decode_rows(m, kv, rows, 1, l, w, plan);
+        attn_decode_rows(m, kv, rows, 1, l, w, plan, DT_F32,
+                         lora && !w.q_norm && decode_gemv_ok(H));
     } else {
         AttnArgs a{};
         a.q = kv.q.as<float>();

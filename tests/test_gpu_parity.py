@@ -411,30 +411,36 @@ def _adapter(cfg, rank, targets, seed, fmt):
 
 
 @pytest.mark.parametrize("fmt", ["f32", "bf16"])
-def test_lora_unmerged_matches_merged_oracle(fmt):
+@pytest.mark.parametrize("prompt_len", [40, 300])
+def test_lora_unmerged_matches_merged_oracle(fmt, prompt_len):
     """lora.rs:99-217: rank-16 alpha-32 adapters on q_proj and v_proj, applied
     unmerged on the GPU (y += s B (A x)) vs the oracle's merged W + s B A;
-    plus a second adapter stacked on q_proj."""
+    plus a second adapter stacked on q_proj and k_proj. Prefill adds the
+    deltas in the rotary/KV kernel; single-row decode stores t = A.norm(x)
+    from the QKV launch and adds the deltas in the split-K attention (q, and
+    the new key/value row in the split holding it: one split after a
+    40-token prompt, several after 300)."""
     from esp_amd.model import LoraAdapter
-    cfg = synth.llama_config(2, 256, 4, 2, 320, 500, head_dim=64, max_pos=128)
+    cfg = synth.llama_config(2, 256, 4, 2, 320, 500, head_dim=64, max_pos=384)
     tensors = synth.make_tensors(cfg, 61, fmt, std=0.05)
     ad1 = _adapter(cfg, 16, ["q_proj", "v_proj"], 1, fmt)
-    ad2 = _adapter(cfg, 8, ["q_proj"], 2, fmt)
+    ad2 = _adapter(cfg, 8, ["q_proj", "k_proj"], 2, fmt)
     model = DecoderModel.from_bytes(
         cfg, st.dump(tensors), fmt,
         adapters=[LoraAdapter(16, 32.0, ["q_proj", "v_proj"], st.dump(ad1)),
-                  LoraAdapter(8, 16.0, ["q_proj"], st.dump(ad2))])
+                  LoraAdapter(8, 16.0, ["q_proj", "k_proj"], st.dump(ad2))])
     merged = oracle.apply_lora(cfg, tensors, {"rank": 16, "alpha": 32.0, "targets": ["q_proj", "v_proj"],
                                               "tensors": ad1})
-    merged = oracle.apply_lora(cfg, merged, {"rank": 8, "alpha": 16.0, "targets": ["q_proj"],
+    merged = oracle.apply_lora(cfg, merged, {"rank": 8, "alpha": 16.0, "targets": ["q_proj", "k_proj"],
                                              "tensors": ad2})
     ref = oracle.OracleModel(cfg, merged)
     plain = oracle.OracleModel(cfg, tensors)
-    prompt = synth.uniform_ids(8, 40, cfg.vocab_size)
-    kv, rkv = model.new_cache(1, 64), ref.new_cache(64)
+    prompt = synth.uniform_ids(8, prompt_len, cfg.vocab_size)
+    ctx = prompt_len + 24
+    kv, rkv = model.new_cache(1, ctx), ref.new_cache(ctx)
     got = model.try_forward_cached_last(prompt, kv)
     want = ref.forward_last(rkv, prompt)
-    base = plain.forward_last(plain.new_cache(64), prompt)
+    base = plain.forward_last(plain.new_cache(ctx), prompt)
     assert np.abs(want - base).max() > 1e-3  # the adapters matter
     for step in range(4):
         if fmt == "f32":
@@ -446,13 +452,13 @@ def test_lora_unmerged_matches_merged_oracle(fmt):
         want = ref.forward_last(rkv, [t])
     # the device-resident greedy loop (graph replay) runs the same LoRA
     # decode kernels as the host loop: same ids
-    kv2 = model.new_cache(1, 64)
+    kv2 = model.new_cache(1, ctx)
     logits = model.try_forward_cached_last(prompt, kv2)
     ids = []
     for _ in range(6):
         ids.append(int(np.argmax(logits)))
         logits = model.try_forward_cached_last([ids[-1]], kv2)
-    assert model.generate_greedy_device(model.new_cache(1, 64), prompt, 6, eos=[]) == ids
+    assert model.generate_greedy_device(model.new_cache(1, ctx), prompt, 6, eos=[]) == ids
 
 
 @pytest.mark.parametrize("protocol", ["xcd", "agent"])
