@@ -31,9 +31,10 @@ typedef uint16_t bf16_t;  // raw bf16 bits in host code
 // cores can consume it exactly (R x C matrix: hi[r*C+c], lo[R*C + r*C+c]).
 // DT_Q8 / DT_Q4: packed projection weights, signed 8- or 4-bit integers
 // along K with one f32 scale per 32 inputs (values, then the scales).
-enum Dt { DT_F32 = 0, DT_BF16 = 1, DT_SPLIT = 2, DT_Q8 = 3, DT_Q4 = 4 };
+// DT_F16: IEEE binary16 (the K/V cache of the bf16 and packed formats).
+enum Dt { DT_F32 = 0, DT_BF16 = 1, DT_SPLIT = 2, DT_Q8 = 3, DT_Q4 = 4, DT_F16 = 5 };
 
-inline size_t dt_size(Dt d) { return d == DT_BF16 ? 2 : 4; }
+inline size_t dt_size(Dt d) { return d == DT_BF16 || d == DT_F16 ? 2 : 4; }
 inline bool dt_packed(Dt d) { return d == DT_Q8 || d == DT_Q4; }
 // bytes of the packed values of n weights (n a multiple of 32)
 inline size_t packed_value_bytes(Dt d, size_t n) { return d == DT_Q8 ? n : n / 2; }

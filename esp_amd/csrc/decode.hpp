@@ -21,7 +21,8 @@ struct DecodeGemvArgs {
     const float *rope_cos, *rope_sin;
     const int32_t *row_pos, *row_seq;  // device, one row
     float *q_out;
-    float *kv;            // layer base of the f32 cache
+    void *kv;             // layer base of the cache (f16 when kv_f16, else f32)
+    int kv_f16;
     long long seq_stride, kv_half_stride, head_stride;
     int nq, nkv, hd;
     // QKVROPE unmerged LoRA: the lora_rows rows after the q/k/v rows (the
@@ -53,7 +54,8 @@ void launch_decode_gemv(Dt wt, int epi, const DecodeGemvArgs &a, hipStream_t s);
 
 struct AttnDecodeArgs {
     const float *q;       // [M, nq*hd]
-    const float *kv;      // layer base of the f32 cache
+    const void *kv;       // layer base of the cache (f16 when kv_f16, else f32)
+    int kv_f16;
     long long seq_stride, kv_half_stride, head_stride;
     const int32_t *row_pos, *row_seq;
     int seq1;             // >= 0: every row belongs to this sequence (row_seq unread)

@@ -22,10 +22,18 @@ template <> __device__ __forceinline__ float ld<uint16_t>(const uint16_t *p, siz
     return bf2f(p[i]);
 }
 
+template <> __device__ __forceinline__ float ld<_Float16>(const _Float16 *p, size_t i) {
+    return (float)p[i];
+}
+
 template <typename T> __device__ __forceinline__ void st(T *p, size_t i, float v);
 template <> __device__ __forceinline__ void st<float>(float *p, size_t i, float v) { p[i] = v; }
 template <> __device__ __forceinline__ void st<uint16_t>(uint16_t *p, size_t i, float v) {
     p[i] = f2bf(v);
+}
+// f32 -> f16, round to nearest even
+template <> __device__ __forceinline__ void st<_Float16>(_Float16 *p, size_t i, float v) {
+    p[i] = (_Float16)v;
 }
 
 // Store x into a split (hi/lo bf16 planes) matrix; `plane` = elements per plane.

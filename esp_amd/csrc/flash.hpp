@@ -7,7 +7,8 @@ namespace esp {
 
 struct FlashArgs {
     const float *q;    // [M, nq*hd] post-RoPE queries (f32)
-    const float *kv;   // layer base of the f32 cache
+    const void *kv;    // layer base of the cache (f16 when kv_f16, else f32)
+    int kv_f16;
     long long seq_stride, kv_half_stride, head_stride;
     int seq, p0;       // the rows are positions p0 .. p0+M-1 of sequence `seq`
     int M, nq, nkv, hd, window;

@@ -261,8 +261,8 @@ void launch_rope_kv(Dt wt, Dt kvdt, const RopeKvArgs &a, hipStream_t s) {
     while (rpb > 1 && rpb * per_row > lds_cap) rpb /= 2;
     const size_t shm = rpb * per_row;
     dim3 grid((a.rows.M + rpb - 1) / rpb, (a.nq + 2 * a.nkv + hpi - 1) / hpi);
-    if (wt == DT_BF16 && kvdt == DT_BF16)
-        rope_kv_k<uint16_t, uint16_t><<<grid, 256, shm, s>>>(a, rpb, t_lo, t_n);
+    if (wt == DT_BF16 && kvdt == DT_F16)
+        rope_kv_k<uint16_t, _Float16><<<grid, 256, shm, s>>>(a, rpb, t_lo, t_n);
     else if (wt == DT_BF16 && kvdt == DT_F32)
         rope_kv_k<uint16_t, float><<<grid, 256, shm, s>>>(a, rpb, t_lo, t_n);
     else if (wt == DT_F32 && kvdt == DT_F32)
@@ -413,18 +413,19 @@ void launch_attention(Dt kvdt, const AttnArgs &a, hipStream_t s) {
     size_t shm = sizeof(float) * ((size_t)G * a.hd + ATT_KT * (a.hd + 1) + ATT_KT * a.hd +
                                   (size_t)G * ATT_KT + 3 * G);
     dim3 grid(a.n_split, a.nkv, a.rows.M);
+    if (kvdt != DT_F16 && kvdt != DT_F32) fail(ESP_BACKEND, "attention: unsupported cache type");
     if (shm > 64 * 1024) {
         static bool set[2] = {false, false};
-        int i = kvdt == DT_BF16;
+        int i = kvdt == DT_F16;
         if (!set[i]) {
-            ESP_HIP(hipFuncSetAttribute(i ? (const void *)attn_split_k<uint16_t>
+            ESP_HIP(hipFuncSetAttribute(i ? (const void *)attn_split_k<_Float16>
                                           : (const void *)attn_split_k<float>,
                                         hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
             set[i] = true;
         }
     }
-    if (kvdt == DT_BF16)
-        attn_split_k<uint16_t><<<grid, 256, shm, s>>>(a);
+    if (kvdt == DT_F16)
+        attn_split_k<_Float16><<<grid, 256, shm, s>>>(a);
     else
         attn_split_k<float><<<grid, 256, shm, s>>>(a);
     dim3 g2(a.nq, a.rows.M);

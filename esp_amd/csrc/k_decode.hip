@@ -226,16 +226,26 @@ __global__ void __launch_bounds__(DG_THREADS) decode_gemv_k(DecodeGemvArgs a) {
                     a.q_out[r0] = o0;
                     a.q_out[r1] = o1;
                 } else {
-                    float *kc = a.kv + (size_t)seq * a.seq_stride +
-                                (size_t)(head - a.nq) * a.head_stride + (size_t)pos * hd;
-                    kc[d] = o0;
-                    kc[d + half] = o1;
+                    const size_t i = (size_t)seq * a.seq_stride +
+                                     (size_t)(head - a.nq) * a.head_stride + (size_t)pos * hd + d;
+                    if (a.kv_f16) {
+                        st((_Float16 *)a.kv, i, o0);
+                        st((_Float16 *)a.kv, i + half, o1);
+                    } else {
+                        ((float *)a.kv)[i] = o0;
+                        ((float *)a.kv)[i + half] = o1;
+                    }
                 }
             } else {
-                float *vc = a.kv + (size_t)seq * a.seq_stride + a.kv_half_stride +
-                            (size_t)(head - a.nq - a.nkv) * a.head_stride + (size_t)pos * hd;
-                vc[d] = v0;
-                vc[d + half] = v1;
+                const size_t i = (size_t)seq * a.seq_stride + a.kv_half_stride +
+                                 (size_t)(head - a.nq - a.nkv) * a.head_stride + (size_t)pos * hd + d;
+                if (a.kv_f16) {
+                    st((_Float16 *)a.kv, i, v0);
+                    st((_Float16 *)a.kv, i + half, v1);
+                } else {
+                    ((float *)a.kv)[i] = v0;
+                    ((float *)a.kv)[i + half] = v1;
+                }
             }
         }
     }
@@ -487,8 +497,23 @@ __device__ __forceinline__ void att_store(const AttnDecodeArgs &a, size_t i, flo
 // plain stores, then L1-bypassing loads in the merging block. With
 // xcd_nx == 0 the partials go through agent-scope (write-through) stores and
 // loads instead, which any placement tolerates.
-template <int HD, int GM, bool XCD, int NW = ATT_WAVES>
+// Keys and values as 4-dim slices: f32x4 (f32 cache) or four f16 in a u32x2.
+template <bool F16> struct KvSlice { typedef f32x4_t T; };
+template <> struct KvSlice<true> { typedef u32x2_t T; };
+__device__ __forceinline__ f32x4_t kv_f32(f32x4_t x) { return x; }
+__device__ __forceinline__ f32x4_t kv_f32(u32x2_t x) {
+    typedef _Float16 h4_t __attribute__((ext_vector_type(4)));
+    return __builtin_convertvector(__builtin_bit_cast(h4_t, x), f32x4_t);
+}
+__device__ __forceinline__ u32x2_t kv_f16(f32x4_t x) {
+    typedef _Float16 h4_t __attribute__((ext_vector_type(4)));
+    return __builtin_bit_cast(u32x2_t, __builtin_convertvector(x, h4_t));
+}
+
+template <int HD, int GM, bool XCD, int NW = ATT_WAVES, bool F16 = false>
 __global__ void __launch_bounds__(NW * 64) attn_decode_k(AttnDecodeArgs a) {
+    typedef typename KvSlice<F16>::T KR;
+    constexpr int ES = F16 ? 2 : 4;  // bytes per cached element
     constexpr int NT = NW * 64;
     constexpr int DPL = 8;               // dims per lane
     constexpr int LPK = HD / DPL;        // lanes per key
@@ -528,20 +553,21 @@ __global__ void __launch_bounds__(NW * 64) attn_decode_k(AttnDecodeArgs a) {
     const int seq = a.seq1 >= 0 ? a.seq1 : a.row_seq[row];
     const int s0 = split * a.split_len;
     const int s1 = min(s0 + a.split_len, a.max_t);
-    const float *kb = a.kv + (size_t)seq * a.seq_stride + (size_t)g * a.head_stride + sub * 4;
-    const float *vb = kb + a.kv_half_stride;
-    f32x4_t kk[NS][2], vv[NS][2];
-    f32x4_t kk2[NS][2], vv2[NS][2];  // the second buffer
+    const char *kb = (const char *)a.kv +
+                     ((size_t)seq * a.seq_stride + (size_t)g * a.head_stride + sub * 4) * ES;
+    const char *vb = kb + (size_t)a.kv_half_stride * ES;
+    KR kk[NS][2], vv[NS][2];
+    KR kk2[NS][2], vv2[NS][2];  // the second buffer
     // lanes past the chunk end re-read its last key (masked later)
-    auto issue = [&](f32x4_t (&K)[NS][2], f32x4_t (&V)[NS][2], int c0, int c1) {
+    auto issue = [&](KR (&K)[NS][2], KR (&V)[NS][2], int c0, int c1) {
 #pragma unroll
         for (int st = 0; st < NS; ++st) {
             if (c0 + st * STEP < c1) {  // block-uniform
                 const int t = min(c0 + st * STEP + wave * KPW + grp, c1 - 1);
-                K[st][0] = __builtin_nontemporal_load((const f32x4_t *)(kb + (size_t)t * HD));
-                K[st][1] = __builtin_nontemporal_load((const f32x4_t *)(kb + (size_t)t * HD + HALF));
-                V[st][0] = __builtin_nontemporal_load((const f32x4_t *)(vb + (size_t)t * HD));
-                V[st][1] = __builtin_nontemporal_load((const f32x4_t *)(vb + (size_t)t * HD + HALF));
+                K[st][0] = __builtin_nontemporal_load((const KR *)(kb + (size_t)t * HD * ES));
+                K[st][1] = __builtin_nontemporal_load((const KR *)(kb + ((size_t)t * HD + HALF) * ES));
+                V[st][0] = __builtin_nontemporal_load((const KR *)(vb + (size_t)t * HD * ES));
+                V[st][1] = __builtin_nontemporal_load((const KR *)(vb + ((size_t)t * HD + HALF) * ES));
             }
         }
     };
@@ -646,11 +672,16 @@ __global__ void __launch_bounds__(NW * 64) attn_decode_k(AttnDecodeArgs a) {
         for (int e = 0; e < DPL; ++e) acc[j][e] = 0.f;
     }
     // one chunk's keys [c0, c1) from a register buffer
-    auto consume = [&](f32x4_t (&kk)[NS][2], f32x4_t (&vv)[NS][2], int c0, int c1) {
+    auto consume = [&](const KR (&kr)[NS][2], const KR (&vr)[NS][2], int c0, int c1) {
+        f32x4_t kk[NS][2], vv[NS][2];
         bool ok[NS];
 #pragma unroll
         for (int st = 0; st < NS; ++st) {
             const int t = c0 + st * STEP + wave * KPW + grp;
+            kk[st][0] = kv_f32(kr[st][0]);
+            kk[st][1] = kv_f32(kr[st][1]);
+            vv[st][0] = kv_f32(vr[st][0]);
+            vv[st][1] = kv_f32(vr[st][1]);
             ok[st] = t >= lo && t < c1;
             if (!ok[st]) vv[st][0] = vv[st][1] = f32x4_t{0.f, 0.f, 0.f, 0.f};  // unread or unwritten rows
             if (kv_patch && t == pos && c0 + st * STEP < c1) {
@@ -662,11 +693,25 @@ __global__ void __launch_bounds__(NW * 64) attn_decode_k(AttnDecodeArgs a) {
                     vv[st][0][e] += vd[e];
                     vv[st][1][e] += vd[4 + e];
                 }
-                float *kr = (float *)kb + (size_t)pos * HD, *vr = (float *)vb + (size_t)pos * HD;
-                *(f32x4_t *)kr = kk[st][0];
-                *(f32x4_t *)(kr + HALF) = kk[st][1];
-                *(f32x4_t *)vr = vv[st][0];
-                *(f32x4_t *)(vr + HALF) = vv[st][1];
+                char *kw = (char *)kb + (size_t)pos * HD * ES, *vw = (char *)vb + (size_t)pos * HD * ES;
+                if constexpr (F16) {
+                    // what the cache holds is what every later step reads
+                    const u32x2_t k0 = kv_f16(kk[st][0]), k1 = kv_f16(kk[st][1]);
+                    const u32x2_t v0 = kv_f16(vv[st][0]), v1 = kv_f16(vv[st][1]);
+                    *(u32x2_t *)kw = k0;
+                    *(u32x2_t *)(kw + HALF * ES) = k1;
+                    *(u32x2_t *)vw = v0;
+                    *(u32x2_t *)(vw + HALF * ES) = v1;
+                    kk[st][0] = kv_f32(k0);
+                    kk[st][1] = kv_f32(k1);
+                    vv[st][0] = kv_f32(v0);
+                    vv[st][1] = kv_f32(v1);
+                } else {
+                    *(f32x4_t *)kw = kk[st][0];
+                    *(f32x4_t *)(kw + HALF * ES) = kk[st][1];
+                    *(f32x4_t *)vw = vv[st][0];
+                    *(f32x4_t *)(vw + HALF * ES) = vv[st][1];
+                }
             }
         }
 #pragma unroll
@@ -943,16 +988,21 @@ void launch_attn_decode(const AttnDecodeArgs &a0, hipStream_t s) {
     // four-wave blocks then let two blocks share a CU, so one block's loads
     // overlap the other's scores across the chunks of a long split.
     const bool narrow = U >= device_cus() && a.split_len > 2 * ATT_WAVES * 64 * 8 / a.hd;
-#define ATT_LAUNCH(HD_, GM_)                                                                   \
+#define ATT_LAUNCH_T(HD_, GM_, F16_)                                                           \
     do {                                                                                   \
         if (narrow) {                                                                      \
-            if (a.xcd_nx > 0) attn_decode_k<HD_, GM_, true, 4><<<grid, 4 * 64, 0, s>>>(a);   \
-            else attn_decode_k<HD_, GM_, false, 4><<<grid, 4 * 64, 0, s>>>(a);              \
+            if (a.xcd_nx > 0) attn_decode_k<HD_, GM_, true, 4, F16_><<<grid, 4 * 64, 0, s>>>(a);   \
+            else attn_decode_k<HD_, GM_, false, 4, F16_><<<grid, 4 * 64, 0, s>>>(a);              \
         } else if (a.xcd_nx > 0) {                                                         \
-            attn_decode_k<HD_, GM_, true><<<grid, ATT_WAVES * 64, 0, s>>>(a);                \
+            attn_decode_k<HD_, GM_, true, ATT_WAVES, F16_><<<grid, ATT_WAVES * 64, 0, s>>>(a);      \
         } else {                                                                           \
-            attn_decode_k<HD_, GM_, false><<<grid, ATT_WAVES * 64, 0, s>>>(a);               \
+            attn_decode_k<HD_, GM_, false, ATT_WAVES, F16_><<<grid, ATT_WAVES * 64, 0, s>>>(a);     \
         }                                                                                  \
+    } while (0)
+#define ATT_LAUNCH(HD_, GM_)                       \
+    do {                                           \
+        if (a.kv_f16) ATT_LAUNCH_T(HD_, GM_, true); \
+        else ATT_LAUNCH_T(HD_, GM_, false);        \
     } while (0)
     if (a.hd == 64) {
         if (G <= 4) ATT_LAUNCH(64, 4);
@@ -962,6 +1012,7 @@ void launch_attn_decode(const AttnDecodeArgs &a0, hipStream_t s) {
         else ATT_LAUNCH(128, 8);
     }
 #undef ATT_LAUNCH
+#undef ATT_LAUNCH_T
 }
 
 }  // namespace esp

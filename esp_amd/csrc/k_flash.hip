@@ -6,10 +6,13 @@
 // this kernel evaluates the same function tile by tile with an online
 // softmax (running max / sum per query row), never materialising scores.
 //
-// Precision: q, k, v (f32 in the cache) and the probabilities p are split
+// Precision: with an f32 cache, q, k, v and the probabilities p are split
 // into bf16 hi + lo parts (both round-to-nearest-even); each product uses
 // three bf16 MFMAs (hi.hi + hi.lo + lo.hi) accumulating in f32, which keeps
-// ~16 mantissa bits of each operand.
+// ~16 mantissa bits of each operand. With an f16 cache (F16), k and v are
+// exact f16 operands and only q and p are split, into f16 hi + lo: two f16
+// MFMAs per product (k.q_hi + k.q_lo, v.p_hi + v.p_lo), ~22 bits of q and p,
+// and one LDS plane per tile instead of two.
 //
 // Layout: a wave owns 32 query rows of one query head and computes the
 // transposed products S^T = K Q^T and O^T = V^T P^T with
@@ -26,6 +29,8 @@
 // K tiles are staged as [key][dim] and V tiles as V^T [dim][key], both
 // bf16 hi/lo planes in LDS; the next tile's f32 rows are loaded into
 // registers while the current tile is multiplied.
+#include <type_traits>
+
 #include "common.hpp"
 #include "dev.hpp"
 #include "flash.hpp"
@@ -39,15 +44,18 @@ typedef float ff32x4_t __attribute__((ext_vector_type(4)));
 typedef float ff32x2_t __attribute__((ext_vector_type(2)));
 typedef uint32_t fu32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t fu32x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 ff16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 ff16x2_t __attribute__((ext_vector_type(2)));
 
 constexpr int FA_BQ = 128, FA_BK = 32, FA_WQ = 32, FA_XCDS = 8;
 
-template <int HD> struct FaLds {
-    static constexpr int KLD = HD + 8;     // K rows [key][dim] (bf16), padded
-    static constexpr int VLD = FA_BK + 4;  // V^T rows [dim][key] (bf16), padded
+template <int HD, bool F16 = false> struct FaLds {
+    static constexpr int KLD = HD + 8;     // K rows [key][dim] (16-bit), padded
+    static constexpr int VLD = FA_BK + 4;  // V^T rows [dim][key] (16-bit), padded
     static constexpr int K_ELEMS = FA_BK * KLD;
     static constexpr int V_ELEMS = HD * VLD;
-    static constexpr size_t bytes = (size_t)(2 * K_ELEMS + 2 * V_ELEMS) * 2;
+    static constexpr int PLANES = F16 ? 1 : 2;  // hi (+ lo) per operand
+    static constexpr size_t bytes = (size_t)PLANES * (K_ELEMS + V_ELEMS) * 2;
     static constexpr int KCH = FA_BK * HD / 8 / 256;  // 8-dim K chunks per thread
     static constexpr int VCH = FA_BK * HD / 8 / 256;  // 4-key x 2-dim V units per thread
 };
@@ -61,6 +69,22 @@ __device__ __forceinline__ fu32x2_t split2(float x, float y) {
                     __builtin_bit_cast(uint32_t, __builtin_convertvector(r, fbf16x2_t))};
 }
 
+// two floats -> {packed f16 hi pair, packed f16 lo pair} (x = hi + lo)
+__device__ __forceinline__ fu32x2_t split2h(float x, float y) {
+    ff32x2_t v = {x, y};
+    ff16x2_t h = __builtin_convertvector(v, ff16x2_t);
+    ff32x2_t r = v - __builtin_convertvector(h, ff32x2_t);
+    return fu32x2_t{__builtin_bit_cast(uint32_t, h),
+                    __builtin_bit_cast(uint32_t, __builtin_convertvector(r, ff16x2_t))};
+}
+
+__device__ __forceinline__ void split8h(ff32x4_t x0, ff32x4_t x1, ff16x8_t &h, ff16x8_t &l) {
+    const fu32x2_t a = split2h(x0[0], x0[1]), b = split2h(x0[2], x0[3]);
+    const fu32x2_t c = split2h(x1[0], x1[1]), d = split2h(x1[2], x1[3]);
+    h = __builtin_bit_cast(ff16x8_t, fu32x4_t{a[0], b[0], c[0], d[0]});
+    l = __builtin_bit_cast(ff16x8_t, fu32x4_t{a[1], b[1], c[1], d[1]});
+}
+
 // eight floats -> bf16x8 hi and lo operands
 __device__ __forceinline__ void split8(ff32x4_t x0, ff32x4_t x1, fbf16x8_t &h, fbf16x8_t &l) {
     const fu32x2_t a = split2(x0[0], x0[1]), b = split2(x0[2], x0[3]);
@@ -69,14 +93,16 @@ __device__ __forceinline__ void split8(ff32x4_t x0, ff32x4_t x1, fbf16x8_t &h, f
     l = __builtin_bit_cast(fbf16x8_t, fu32x4_t{a[1], b[1], c[1], d[1]});
 }
 
-template <int HD>
+template <int HD, bool F16>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) flash_attn_k(FlashArgs a, int nqb) {
-    typedef FaLds<HD> Ly;
+    typedef FaLds<HD, F16> Ly;
+    typedef typename std::conditional<F16, ff16x8_t, fbf16x8_t>::type op8_t;  // MFMA operand
     constexpr int NKS = HD / 16;  // k-steps over head dims for S^T
     constexpr int NDT = HD / 32;  // 32-row output dim tiles of O^T
+    constexpr int ES = F16 ? 2 : 4;  // bytes per cached element
     extern __shared__ uint16_t fl[];
-    uint16_t *Kh = fl, *Kl = Kh + Ly::K_ELEMS;
-    uint16_t *Vh = Kl + Ly::K_ELEMS, *Vl = Vh + Ly::V_ELEMS;
+    uint16_t *Kh = fl, *Kl = Kh + Ly::K_ELEMS;  // Kl, Vl: f32 cache only
+    uint16_t *Vh = fl + Ly::PLANES * Ly::K_ELEMS, *Vl = Vh + Ly::V_ELEMS;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int half = lane >> 5, col = lane & 31;
 
@@ -95,7 +121,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
 
     // Q^T fragments (B operand): lane holds query row wq0 + col, dims
     // ks*16 + half*8 .. +8
-    fbf16x8_t qfh[NKS], qfl[NKS];
+    op8_t qfh[NKS], qfl[NKS];
     {
         const int r = wq0 + col;
         const float *qrow = a.q + (size_t)r * a.nq * HD + (size_t)qh * HD + half * 8;
@@ -106,7 +132,8 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
                 x0 = *(const ff32x4_t *)(qrow + ks * 16);
                 x1 = *(const ff32x4_t *)(qrow + ks * 16 + 4);
             }
-            split8(x0, x1, qfh[ks], qfl[ks]);
+            if constexpr (F16) split8h(x0, x1, qfh[ks], qfl[ks]);
+            else split8(x0, x1, qfh[ks], qfl[ks]);
         }
     }
     const int qp = a.p0 + wq0 + col;  // this lane's query position
@@ -121,21 +148,31 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
     const int kv_hi = a.p0 + last_row + 1;  // exclusive
     int kv_lo = a.window > 0 ? max(0, a.p0 + q0 - a.window + 1) : 0;
     kv_lo = kv_lo / FA_BK * FA_BK;
-    const float *kbase = a.kv + (size_t)a.seq * a.seq_stride + (size_t)kvh * a.head_stride;
-    const float *vbase = kbase + a.kv_half_stride;
+    const char *kbase = (const char *)a.kv +
+                        ((size_t)a.seq * a.seq_stride + (size_t)kvh * a.head_stride) * ES;
+    const char *vbase = kbase + (size_t)a.kv_half_stride * ES;
 
-    // register staging of one tile (rows beyond kv_hi are zero)
+    // register staging of one tile (rows beyond kv_hi are zero): 8 dims of a
+    // key per K chunk; 2 dims x 4 keys per V unit
     ff32x4_t kreg[Ly::KCH][2];
     ff32x2_t vreg[Ly::VCH][4];
+    fu32x4_t kreg16[Ly::KCH];
+    uint32_t vreg16[Ly::VCH][4];
     auto load_tile = [&](int k0) {
 #pragma unroll
         for (int c = 0; c < Ly::KCH; ++c) {
             const int idx = tid + c * 256, key = idx / (HD / 8), d = (idx % (HD / 8)) * 8;
             const int t = k0 + key;
-            kreg[c][0] = kreg[c][1] = ff32x4_t{0.f, 0.f, 0.f, 0.f};
-            if (t < kv_hi) {
-                kreg[c][0] = *(const ff32x4_t *)(kbase + (size_t)t * HD + d);
-                kreg[c][1] = *(const ff32x4_t *)(kbase + (size_t)t * HD + d + 4);
+            const char *p = kbase + ((size_t)t * HD + d) * ES;
+            if constexpr (F16) {
+                kreg16[c] = fu32x4_t{0u, 0u, 0u, 0u};
+                if (t < kv_hi) kreg16[c] = *(const fu32x4_t *)p;
+            } else {
+                kreg[c][0] = kreg[c][1] = ff32x4_t{0.f, 0.f, 0.f, 0.f};
+                if (t < kv_hi) {
+                    kreg[c][0] = *(const ff32x4_t *)p;
+                    kreg[c][1] = *(const ff32x4_t *)(p + 16);
+                }
             }
         }
 #pragma unroll
@@ -144,8 +181,14 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const int t = k0 + kq * 4 + j;
-                vreg[c][j] = ff32x2_t{0.f, 0.f};
-                if (t < kv_hi) vreg[c][j] = *(const ff32x2_t *)(vbase + (size_t)t * HD + dp * 2);
+                const char *p = vbase + ((size_t)t * HD + dp * 2) * ES;
+                if constexpr (F16) {
+                    vreg16[c][j] = 0u;
+                    if (t < kv_hi) vreg16[c][j] = *(const uint32_t *)p;
+                } else {
+                    vreg[c][j] = ff32x2_t{0.f, 0.f};
+                    if (t < kv_hi) vreg[c][j] = *(const ff32x2_t *)p;
+                }
             }
         }
     };
@@ -153,22 +196,35 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
 #pragma unroll
         for (int c = 0; c < Ly::KCH; ++c) {
             const int idx = tid + c * 256, key = idx / (HD / 8), d = (idx % (HD / 8)) * 8;
-            fbf16x8_t h, l;
-            split8(kreg[c][0], kreg[c][1], h, l);
-            *(fbf16x8_t *)(Kh + key * Ly::KLD + d) = h;
-            *(fbf16x8_t *)(Kl + key * Ly::KLD + d) = l;
+            if constexpr (F16) {
+                *(fu32x4_t *)(Kh + key * Ly::KLD + d) = kreg16[c];
+            } else {
+                fbf16x8_t h, l;
+                split8(kreg[c][0], kreg[c][1], h, l);
+                *(fbf16x8_t *)(Kh + key * Ly::KLD + d) = h;
+                *(fbf16x8_t *)(Kl + key * Ly::KLD + d) = l;
+            }
         }
 #pragma unroll
         for (int c = 0; c < Ly::VCH; ++c) {
             const int idx = tid + c * 256, dp = idx % (HD / 2), kq = idx / (HD / 2);
             // dims 2dp and 2dp+1, keys kq*4 .. +4
-            const fu32x2_t a = split2(vreg[c][0][0], vreg[c][1][0]), b = split2(vreg[c][2][0], vreg[c][3][0]);
-            const fu32x2_t e = split2(vreg[c][0][1], vreg[c][1][1]), f = split2(vreg[c][2][1], vreg[c][3][1]);
             const int o0 = (2 * dp) * Ly::VLD + kq * 4;
-            *(fu32x2_t *)(Vh + o0) = fu32x2_t{a[0], b[0]};
-            *(fu32x2_t *)(Vl + o0) = fu32x2_t{a[1], b[1]};
-            *(fu32x2_t *)(Vh + o0 + Ly::VLD) = fu32x2_t{e[0], f[0]};
-            *(fu32x2_t *)(Vl + o0 + Ly::VLD) = fu32x2_t{e[1], f[1]};
+            if constexpr (F16) {
+                // each u32 holds (dim 2dp, dim 2dp+1) of one key
+                const uint32_t *v = vreg16[c];
+                *(fu32x2_t *)(Vh + o0) = fu32x2_t{(v[0] & 0xffffu) | (v[1] << 16),
+                                                  (v[2] & 0xffffu) | (v[3] << 16)};
+                *(fu32x2_t *)(Vh + o0 + Ly::VLD) = fu32x2_t{(v[0] >> 16) | (v[1] & 0xffff0000u),
+                                                            (v[2] >> 16) | (v[3] & 0xffff0000u)};
+            } else {
+                const fu32x2_t a = split2(vreg[c][0][0], vreg[c][1][0]), b = split2(vreg[c][2][0], vreg[c][3][0]);
+                const fu32x2_t e = split2(vreg[c][0][1], vreg[c][1][1]), f = split2(vreg[c][2][1], vreg[c][3][1]);
+                *(fu32x2_t *)(Vh + o0) = fu32x2_t{a[0], b[0]};
+                *(fu32x2_t *)(Vl + o0) = fu32x2_t{a[1], b[1]};
+                *(fu32x2_t *)(Vh + o0 + Ly::VLD) = fu32x2_t{e[0], f[0]};
+                *(fu32x2_t *)(Vl + o0 + Ly::VLD) = fu32x2_t{e[1], f[1]};
+            }
         }
     };
 
@@ -186,11 +242,17 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
 #pragma unroll
         for (int ks = 0; ks < NKS; ++ks) {
             const int off = col * Ly::KLD + ks * 16 + half * 8;
-            fbf16x8_t kh = *(const fbf16x8_t *)(Kh + off);
-            fbf16x8_t kl = *(const fbf16x8_t *)(Kl + off);
-            sacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kh, qfh[ks], sacc, 0, 0, 0);
-            sacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kl, qfh[ks], sacc, 0, 0, 0);
-            sacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kh, qfl[ks], sacc, 0, 0, 0);
+            if constexpr (F16) {
+                const ff16x8_t kh = *(const ff16x8_t *)(Kh + off);
+                sacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(kh, qfh[ks], sacc, 0, 0, 0);
+                sacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(kh, qfl[ks], sacc, 0, 0, 0);
+            } else {
+                fbf16x8_t kh = *(const fbf16x8_t *)(Kh + off);
+                fbf16x8_t kl = *(const fbf16x8_t *)(Kl + off);
+                sacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kh, qfh[ks], sacc, 0, 0, 0);
+                sacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kl, qfh[ks], sacc, 0, 0, 0);
+                sacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kh, qfl[ks], sacc, 0, 0, 0);
+            }
         }
         // mask (only tiles that cross the diagonal / window / end), online softmax
         const bool full = k0 + FA_BK - 1 <= a.p0 + wq0 && k0 + FA_BK <= kv_hi &&
@@ -227,12 +289,13 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
                 for (int i = 0; i < 16; ++i) o[t][i] *= alpha;
         }
         // P^T as B operands (hi / lo) of the two 16-key steps
-        fbf16x8_t ph[2], pl[2];
+        op8_t ph[2], pl[2];
 #pragma unroll
         for (int kk = 0; kk < 2; ++kk) {
-            split8(ff32x4_t{sacc[kk * 8], sacc[kk * 8 + 1], sacc[kk * 8 + 2], sacc[kk * 8 + 3]},
-                   ff32x4_t{sacc[kk * 8 + 4], sacc[kk * 8 + 5], sacc[kk * 8 + 6], sacc[kk * 8 + 7]},
-                   ph[kk], pl[kk]);
+            const ff32x4_t p0 = {sacc[kk * 8], sacc[kk * 8 + 1], sacc[kk * 8 + 2], sacc[kk * 8 + 3]};
+            const ff32x4_t p1 = {sacc[kk * 8 + 4], sacc[kk * 8 + 5], sacc[kk * 8 + 6], sacc[kk * 8 + 7]};
+            if constexpr (F16) split8h(p0, p1, ph[kk], pl[kk]);
+            else split8(p0, p1, ph[kk], pl[kk]);
         }
         // O^T += V^T P^T
 #pragma unroll
@@ -242,12 +305,18 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
             for (int t = 0; t < NDT; ++t) {
                 const int vo = (t * 32 + col) * Ly::VLD;
                 fu32x2_t h0 = *(const fu32x2_t *)(Vh + vo + ka), h1 = *(const fu32x2_t *)(Vh + vo + kb);
-                fu32x2_t l0 = *(const fu32x2_t *)(Vl + vo + ka), l1 = *(const fu32x2_t *)(Vl + vo + kb);
-                fbf16x8_t vh = __builtin_bit_cast(fbf16x8_t, fu32x4_t{h0[0], h0[1], h1[0], h1[1]});
-                fbf16x8_t vl = __builtin_bit_cast(fbf16x8_t, fu32x4_t{l0[0], l0[1], l1[0], l1[1]});
-                o[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vh, ph[kk], o[t], 0, 0, 0);
-                o[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vl, ph[kk], o[t], 0, 0, 0);
-                o[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vh, pl[kk], o[t], 0, 0, 0);
+                if constexpr (F16) {
+                    const ff16x8_t vh = __builtin_bit_cast(ff16x8_t, fu32x4_t{h0[0], h0[1], h1[0], h1[1]});
+                    o[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vh, ph[kk], o[t], 0, 0, 0);
+                    o[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vh, pl[kk], o[t], 0, 0, 0);
+                } else {
+                    fu32x2_t l0 = *(const fu32x2_t *)(Vl + vo + ka), l1 = *(const fu32x2_t *)(Vl + vo + kb);
+                    fbf16x8_t vh = __builtin_bit_cast(fbf16x8_t, fu32x4_t{h0[0], h0[1], h1[0], h1[1]});
+                    fbf16x8_t vl = __builtin_bit_cast(fbf16x8_t, fu32x4_t{l0[0], l0[1], l1[0], l1[1]});
+                    o[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vh, ph[kk], o[t], 0, 0, 0);
+                    o[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vl, ph[kk], o[t], 0, 0, 0);
+                    o[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vh, pl[kk], o[t], 0, 0, 0);
+                }
             }
         }
     }
@@ -283,9 +352,11 @@ void launch_flash(const FlashArgs &a, hipStream_t s) {
     const int G = a.nq / a.nkv, ngroups = nqb * a.nkv;
     const int blocks = ((ngroups + FA_XCDS - 1) / FA_XCDS) * FA_XCDS * G;
     if (a.hd == 64) {
-        flash_attn_k<64><<<blocks, 256, FaLds<64>::bytes, s>>>(a, nqb);
+        if (a.kv_f16) flash_attn_k<64, true><<<blocks, 256, FaLds<64, true>::bytes, s>>>(a, nqb);
+        else flash_attn_k<64, false><<<blocks, 256, FaLds<64>::bytes, s>>>(a, nqb);
     } else if (a.hd == 128) {
-        flash_attn_k<128><<<blocks, 256, FaLds<128>::bytes, s>>>(a, nqb);
+        if (a.kv_f16) flash_attn_k<128, true><<<blocks, 256, FaLds<128, true>::bytes, s>>>(a, nqb);
+        else flash_attn_k<128, false><<<blocks, 256, FaLds<128>::bytes, s>>>(a, nqb);
     } else {
         fail(ESP_BACKEND, "flash attention: unsupported head_dim");
     }

@@ -731,7 +731,11 @@ Kv *create_kv(Model *m, uint32_t batch, uint32_t max_ctx) {
     kv->model = m;
     kv->batch = (int)batch;
     kv->max_ctx = (int)max_ctx;
-    kv->dt = DT_F32;  // keys/values keep f32 precision in every format
+    // bf16 weights: an f16 cache (11-bit significands: a CPU emulation of the
+    // f32 corridor at the 1B and 8B widths kept logits within 0.18 / 0.43 of
+    // the bf16-config tolerance, where bf16 keys and values broke it); the f32
+    // and packed formats keep f32 keys and values.
+    kv->dt = m->wt == DT_BF16 ? DT_F16 : DT_F32;
     kv->head_stride = (long long)max_ctx * m->hd;
     kv->half_stride = kv->head_stride * m->nkv;
     kv->layer_stride = kv->half_stride * 2;
@@ -748,6 +752,11 @@ Kv *create_kv(Model *m, uint32_t batch, uint32_t max_ctx) {
 }
 
 // ---------------------------------------------------------------- forward
+
+// Byte address of layer l's block in the cache (element type kv.dt).
+static void *kv_layer(Kv &kv, int l) {
+    return (char *)kv.cache.p + (size_t)l * kv.layer_stride * dt_size(kv.dt);
+}
 
 static const int kMaxRows = 4096;  // token rows per pass through the layers
 
@@ -844,7 +853,8 @@ static void attn_decode_rows(Model &m, Kv &kv, const Rows &rows, int Mc, int l, 
             if (w.lora_rank[j] && (w.lora_rank[j] % 8 || w.lora_t_col[j] % 4)) a.lora_vec = 0;
     }
     a.q = kv.q.as<float>();
-    a.kv = kv.cache.as<float>() + (size_t)l * kv.layer_stride;
+    a.kv = kv_layer(kv, l);
+    a.kv_f16 = kv.dt == DT_F16;
     a.seq_stride = kv.seq_stride;
     a.kv_half_stride = kv.half_stride;
     a.head_stride = kv.head_stride;
@@ -868,7 +878,7 @@ static void attn_decode_rows(Model &m, Kv &kv, const Rows &rows, int Mc, int l, 
 
 // Whether Mc rows take the split-K decode attention kernel.
 static bool use_attn_decode(const Model &m, const Kv &kv, int Mc) {
-    return kv.dt == DT_F32 && attn_decode_ok(m.hd, m.nq / m.nkv) &&
+    return (kv.dt == DT_F32 || kv.dt == DT_F16) && attn_decode_ok(m.hd, m.nq / m.nkv) &&
            (long long)Mc * m.nkv <= ATT_MAX_TICKETS;
 }
 
@@ -880,7 +890,7 @@ static void run_layer_decode(Model &m, Kv &kv, const Rows &rows, LayerW &w, int 
                              const Plan &plan) {
     hipStream_t s = kv.stream;
     const int H = m.H;
-    float *kvl = kv.cache.as<float>() + (size_t)l * kv.layer_stride;
+    void *kvl = kv_layer(kv, l);
     const bool lora = w.lora_rank[0] || w.lora_rank[1] || w.lora_rank[2];
     const bool attn_fast = attn_decode_ok(m.hd, m.nq / m.nkv);
     // LoRA deltas ride the decode attention, so a LoRA layer takes the fused
@@ -902,6 +912,7 @@ static void run_layer_decode(Model &m, Kv &kv, const Rows &rows, LayerW &w, int 
         g.row_seq = rows.row_seq;
         g.q_out = kv.q.as<float>();
         g.kv = kvl;
+        g.kv_f16 = kv.dt == DT_F16;
         g.seq_stride = kv.seq_stride;
         g.kv_half_stride = kv.half_stride;
         g.head_stride = kv.head_stride;
@@ -1144,7 +1155,7 @@ static void run_layers(Model &m, Kv &kv, const Rows &rows, int Mc, int max_t, in
                 r.lora_scale[j] = w.lora_scale[j];
             }
             r.rows = rows;
-            r.kv = (char *)kv.cache.p + (size_t)l * kv.layer_stride * dt_size(kv.dt);
+            r.kv = kv_layer(kv, l);
             r.seq_stride = kv.seq_stride;
             r.layer_stride = kv.layer_stride;
             r.kv_half_stride = kv.half_stride;
@@ -1164,7 +1175,8 @@ static void run_layers(Model &m, Kv &kv, const Rows &rows, int Mc, int max_t, in
             for (const Seg &g : *segs) {
                 FlashArgs f{};
                 f.q = kv.q.as<float>() + (size_t)g.row0 * m.qw;
-                f.kv = kv.cache.as<float>() + (size_t)l * kv.layer_stride;
+                f.kv = kv_layer(kv, l);
+                f.kv_f16 = kv.dt == DT_F16;
                 f.seq_stride = kv.seq_stride;
                 f.kv_half_stride = kv.half_stride;
                 f.head_stride = kv.head_stride;
@@ -1185,7 +1197,8 @@ static void run_layers(Model &m, Kv &kv, const Rows &rows, int Mc, int max_t, in
             // rows are consecutive positions of one sequence: tiled MFMA attention
             FlashArgs f{};
             f.q = kv.q.as<float>();
-            f.kv = kv.cache.as<float>() + (size_t)l * kv.layer_stride;
+            f.kv = kv_layer(kv, l);
+            f.kv_f16 = kv.dt == DT_F16;
             f.seq_stride = kv.seq_stride;
             f.kv_half_stride = kv.half_stride;
             f.head_stride = kv.head_stride;
@@ -1206,7 +1219,7 @@ static void run_layers(Model &m, Kv &kv, const Rows &rows, int Mc, int max_t, in
         } else {
             AttnArgs a{};
             a.q = kv.q.as<float>();
-            a.kv = (char *)kv.cache.p + (size_t)l * kv.layer_stride * dt_size(kv.dt);
+            a.kv = kv_layer(kv, l);
             a.seq_stride = kv.seq_stride;
             a.layer_stride = kv.layer_stride;
             a.kv_half_stride = kv.half_stride;
