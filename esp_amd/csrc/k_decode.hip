@@ -523,9 +523,11 @@ __global__ void __launch_bounds__(NW * 64) attn_decode_k(AttnDecodeArgs a) {
     // while the current one is consumed. Steps per buffer, measured on
     // MI355X: the narrow (4-wave, many-row) form at the C5 batch 65.0 us per
     // launch with two (66.4 with three, 69.9 with five, 70.7 single-
-    // buffered with five); the 8-wave form three (C2 decode 1327 vs
-    // 1287-1312 tok/s single-buffered with five).
-    constexpr int NS = NW == 4 ? 2 : 3;  // steps per chunk
+    // buffered with five); the 8-wave form three over an f32 cache (C2
+    // decode 1327 vs 1287-1312 tok/s single-buffered with five) and two over
+    // an f16 cache (163 VGPRs, three waves per SIMD: 15.2 vs 16.4 us per
+    // launch at hd 128, 4096 keys, 32 splits).
+    constexpr int NS = (NW == 4 || F16) ? 2 : 3;  // steps per chunk
     constexpr int CH = NS * STEP;        // keys per chunk
     constexpr int HALF = HD / 2;
     constexpr int STRIDE = HD + ATT_PART_PAD;
@@ -672,83 +674,99 @@ __global__ void __launch_bounds__(NW * 64) attn_decode_k(AttnDecodeArgs a) {
         for (int e = 0; e < DPL; ++e) acc[j][e] = 0.f;
     }
     // one chunk's keys [c0, c1) from a register buffer
-    auto consume = [&](const KR (&kr)[NS][2], const KR (&vr)[NS][2], int c0, int c1) {
-        f32x4_t kk[NS][2], vv[NS][2];
+    // Keys and values are widened to f32 one step at a time (scores from K,
+    // then the V accumulation), so no chunk is held twice in registers.
+    auto consume = [&](KR (&kr)[NS][2], KR (&vr)[NS][2], int c0, int c1) {
         bool ok[NS];
+        float sc[GM][NS];
 #pragma unroll
         for (int st = 0; st < NS; ++st) {
             const int t = c0 + st * STEP + wave * KPW + grp;
-            kk[st][0] = kv_f32(kr[st][0]);
-            kk[st][1] = kv_f32(kr[st][1]);
-            vv[st][0] = kv_f32(vr[st][0]);
-            vv[st][1] = kv_f32(vr[st][1]);
             ok[st] = t >= lo && t < c1;
-            if (!ok[st]) vv[st][0] = vv[st][1] = f32x4_t{0.f, 0.f, 0.f, 0.f};  // unread or unwritten rows
             if (kv_patch && t == pos && c0 + st * STEP < c1) {
                 // the new key's LoRA deltas, kept in the cache for later steps
+                f32x4_t k0 = kv_f32(kr[st][0]), k1 = kv_f32(kr[st][1]);
+                f32x4_t v0 = kv_f32(vr[st][0]), v1 = kv_f32(vr[st][1]);
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    kk[st][0][e] += kd[e];
-                    kk[st][1][e] += kd[4 + e];
-                    vv[st][0][e] += vd[e];
-                    vv[st][1][e] += vd[4 + e];
+                    k0[e] += kd[e];
+                    k1[e] += kd[4 + e];
+                    v0[e] += vd[e];
+                    v1[e] += vd[4 + e];
                 }
                 char *kw = (char *)kb + (size_t)pos * HD * ES, *vw = (char *)vb + (size_t)pos * HD * ES;
-                if constexpr (F16) {
-                    // what the cache holds is what every later step reads
-                    const u32x2_t k0 = kv_f16(kk[st][0]), k1 = kv_f16(kk[st][1]);
-                    const u32x2_t v0 = kv_f16(vv[st][0]), v1 = kv_f16(vv[st][1]);
-                    *(u32x2_t *)kw = k0;
-                    *(u32x2_t *)(kw + HALF * ES) = k1;
-                    *(u32x2_t *)vw = v0;
-                    *(u32x2_t *)(vw + HALF * ES) = v1;
-                    kk[st][0] = kv_f32(k0);
-                    kk[st][1] = kv_f32(k1);
-                    vv[st][0] = kv_f32(v0);
-                    vv[st][1] = kv_f32(v1);
+                if constexpr (F16) {  // what the cache holds is what every later step reads
+                    kr[st][0] = kv_f16(k0);
+                    kr[st][1] = kv_f16(k1);
+                    vr[st][0] = kv_f16(v0);
+                    vr[st][1] = kv_f16(v1);
                 } else {
-                    *(f32x4_t *)kw = kk[st][0];
-                    *(f32x4_t *)(kw + HALF * ES) = kk[st][1];
-                    *(f32x4_t *)vw = vv[st][0];
-                    *(f32x4_t *)(vw + HALF * ES) = vv[st][1];
+                    kr[st][0] = k0;
+                    kr[st][1] = k1;
+                    vr[st][0] = v0;
+                    vr[st][1] = v1;
                 }
+                *(KR *)kw = kr[st][0];
+                *(KR *)(kw + HALF * ES) = kr[st][1];
+                *(KR *)vw = vr[st][0];
+                *(KR *)(vw + HALF * ES) = vr[st][1];
+            }
+            if (c0 + st * STEP < c1) {  // block-uniform
+                const f32x4_t k0 = kv_f32(kr[st][0]), k1 = kv_f32(kr[st][1]);
+#pragma unroll
+                for (int j = 0; j < GM; ++j) {
+                    if (j >= G) break;
+                    const float d0 = q[j][0] * k0[0] + q[j][1] * k0[1];
+                    const float d1 = q[j][2] * k0[2] + q[j][3] * k0[3];
+                    const float d2 = q[j][4] * k1[0] + q[j][5] * k1[1];
+                    const float d3 = q[j][6] * k1[2] + q[j][7] * k1[3];
+                    const float d = group_sum<LPK>((d0 + d1) + (d2 + d3));
+                    sc[j][st] = ok[st] ? d * inv_scale : -INFINITY;
+                }
+            } else {
+#pragma unroll
+                for (int j = 0; j < GM; ++j) sc[j][st] = -INFINITY;
             }
         }
+        // online-softmax update per head; sc becomes the weights p (0 for a
+        // head with no key of this lane's group in the chunk yet)
 #pragma unroll
         for (int j = 0; j < GM; ++j) {
             if (j >= G) break;
-            float sc[NS];
             float mx = m[j];
 #pragma unroll
-            for (int st = 0; st < NS; ++st) {
-                float d = 0.f;
-                if (c0 + st * STEP < c1) {  // block-uniform
-                    const float d0 = q[j][0] * kk[st][0][0] + q[j][1] * kk[st][0][1];
-                    const float d1 = q[j][2] * kk[st][0][2] + q[j][3] * kk[st][0][3];
-                    const float d2 = q[j][4] * kk[st][1][0] + q[j][5] * kk[st][1][1];
-                    const float d3 = q[j][6] * kk[st][1][2] + q[j][7] * kk[st][1][3];
-                    d = group_sum<LPK>((d0 + d1) + (d2 + d3));
-                }
-                sc[st] = ok[st] ? d * inv_scale : -INFINITY;
-                mx = fmaxf(mx, sc[st]);
+            for (int st = 0; st < NS; ++st) mx = fmaxf(mx, sc[j][st]);
+            if (mx == -INFINITY) {
+#pragma unroll
+                for (int st = 0; st < NS; ++st) sc[j][st] = 0.f;
+                continue;
             }
-            if (mx == -INFINITY) continue;  // no key of this lane's group in the chunk yet
             const float al = __expf(m[j] - mx);
             l[j] *= al;
 #pragma unroll
             for (int e = 0; e < DPL; ++e) acc[j][e] *= al;
 #pragma unroll
             for (int st = 0; st < NS; ++st) {
-                if (c0 + st * STEP < c1) {
-                    const float p = __expf(sc[st] - mx);
-                    l[j] += p;
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) acc[j][e] += p * vv[st][0][e];
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) acc[j][4 + e] += p * vv[st][1][e];
-                }
+                sc[j][st] = __expf(sc[j][st] - mx);
+                l[j] += sc[j][st];
             }
             m[j] = mx;
+        }
+#pragma unroll
+        for (int st = 0; st < NS; ++st) {
+            if (c0 + st * STEP >= c1) continue;  // block-uniform
+            const f32x4_t z = {0.f, 0.f, 0.f, 0.f};
+            // unread or unwritten rows contribute nothing (their weight is 0)
+            const f32x4_t v0 = ok[st] ? kv_f32(vr[st][0]) : z, v1 = ok[st] ? kv_f32(vr[st][1]) : z;
+#pragma unroll
+            for (int j = 0; j < GM; ++j) {
+                if (j >= G) break;
+                const float pw = sc[j][st];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) acc[j][e] += pw * v0[e];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) acc[j][4 + e] += pw * v1[e];
+            }
         }
     };
     // chunks alternate between the buffers; each buffer is refilled only
@@ -824,23 +842,19 @@ __global__ void __launch_bounds__(NW * 64) attn_decode_k(AttnDecodeArgs a) {
     __syncthreads();
     if (!last) return;
     // Merge in the last block, splits in batches of ATT_MB: each thread owns
-    // four consecutive outputs of one head and issues its 16-byte partial
-    // loads of the batch first; the batch's (m, l) pairs are read once into
-    // LDS meanwhile. A running maximum carries across batches; splits are
-    // summed in order (deterministic). Offsets past the last split are
-    // clamped (their weight is zero), so the loads carry no predicates.
+    // one output of one head and issues its partial loads of the batch
+    // first; the batch's (m, l) pairs are read once into LDS meanwhile. A
+    // running maximum carries across batches; splits are summed in order
+    // (deterministic). Offsets past the last split are clamped (their weight
+    // is zero), so the loads carry no predicates.
     __shared__ float bm_[GM][ATT_MB], bl_[GM][ATT_MB];
     const float *pb = a.part + ((size_t)row * a.nq + (size_t)g * G) * ns * STRIDE;
-    const int o4 = tid * 4;
-    const bool own = o4 < G * HD;  // wave-uniform
-    const int j = own ? o4 / HD : 0, d = own ? o4 % HD : 0;
     // L1-bypassing (sc0) loads of this unit's partial rows
     const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
         (void *)pb, (short)0, G * ns * STRIDE * (int)sizeof(float), 0x00020000);
-    auto ld4 = [&](int off) -> f32x4_t {
-        if (XCD) return __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rs, off * 4, 0, 1));
-        const float *pp = pb + off;
-        return f32x4_t{ld_agent(pp), ld_agent(pp + 1), ld_agent(pp + 2), ld_agent(pp + 3)};
+    auto ld1 = [&](int off) -> float {
+        if (XCD) return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rs, off * 4, 0, 1));
+        return ld_agent(pb + off);
     };
     auto ld2 = [&](int off, float &x, float &y) {
         if (XCD) {
@@ -852,47 +866,43 @@ __global__ void __launch_bounds__(NW * 64) attn_decode_k(AttnDecodeArgs a) {
             y = ld_agent(pb + off + 1);
         }
     };
-    float M = -INFINITY, L = 0.f;
-    f32x4_t V = {0.f, 0.f, 0.f, 0.f};
-    for (int sp0 = 0; sp0 < ns; sp0 += ATT_MB) {
-        f32x4_t tv[ATT_MB];
-        if (own) {
+    for (int o = tid; o < ((G * HD + NT - 1) / NT) * NT; o += NT) {
+        const bool own = o < G * HD;  // wave-uniform
+        const int j = own ? o / HD : 0, d = own ? o % HD : 0;
+        float M = -INFINITY, L = 0.f, V = 0.f;
+        for (int sp0 = 0; sp0 < ns; sp0 += ATT_MB) {
+            float tv[ATT_MB];
+            if (own) {
 #pragma unroll
-            for (int q = 0; q < ATT_MB; ++q)
-                tv[q] = ld4((j * ns + min(sp0 + q, ns - 1)) * STRIDE + ATT_PART_PAD + d);
-        }
-        __syncthreads();  // previous batch's (m, l) reads are done
-        if (tid < G * ATT_MB) {
-            const int jj = tid / ATT_MB, q = tid % ATT_MB;
-            float mv, lv;
-            ld2((jj * ns + min(sp0 + q, ns - 1)) * STRIDE, mv, lv);
-            bm_[jj][q] = sp0 + q < ns ? mv : -INFINITY;
-            bl_[jj][q] = lv;
-        }
-        __syncthreads();
-        if (!own) continue;
-        float bmax = M;
+                for (int q = 0; q < ATT_MB; ++q)
+                    tv[q] = ld1((j * ns + min(sp0 + q, ns - 1)) * STRIDE + ATT_PART_PAD + d);
+            }
+            __syncthreads();  // previous batch's (m, l) reads are done
+            if (tid < G * ATT_MB) {
+                const int jj = tid / ATT_MB, q = tid % ATT_MB;
+                float mv, lv;
+                ld2((jj * ns + min(sp0 + q, ns - 1)) * STRIDE, mv, lv);
+                bm_[jj][q] = sp0 + q < ns ? mv : -INFINITY;
+                bl_[jj][q] = lv;
+            }
+            __syncthreads();
+            if (!own) continue;
+            float bmax = M;
 #pragma unroll
-        for (int q = 0; q < ATT_MB; ++q) bmax = fmaxf(bmax, bm_[j][q]);
-        if (bmax == -INFINITY) continue;
-        const float r = __expf(M - bmax);
-        L *= r;
-        V *= r;
+            for (int q = 0; q < ATT_MB; ++q) bmax = fmaxf(bmax, bm_[j][q]);
+            if (bmax == -INFINITY) continue;
+            const float r = __expf(M - bmax);
+            L *= r;
+            V *= r;
 #pragma unroll
-        for (int q = 0; q < ATT_MB; ++q) {
-            const float w = __expf(bm_[j][q] - bmax);
-            L += bl_[j][q] * w;
-            V += tv[q] * w;
+            for (int q = 0; q < ATT_MB; ++q) {
+                const float w = __expf(bm_[j][q] - bmax);
+                L += bl_[j][q] * w;
+                V += tv[q] * w;
+            }
+            M = bmax;
         }
-        M = bmax;
-    }
-    if (own) {
-        const size_t oi = (size_t)row * a.nq * HD + (size_t)g * G * HD + o4;
-        const float inv = 1.f / L;
-        att_store(a, oi, V.x * inv);
-        att_store(a, oi + 1, V.y * inv);
-        att_store(a, oi + 2, V.z * inv);
-        att_store(a, oi + 3, V.w * inv);
+        if (own) att_store(a, (size_t)row * a.nq * HD + (size_t)g * G * HD + o, V / L);
     }
 }
 
