@@ -120,9 +120,12 @@ def measured_traffic(name: str = "decode_gemv_mlp_c3_traffic.md"):
 
 
 def traffic_run(steps: int = 8) -> None:
-    """Workload for the FETCH_SIZE / WRITE_SIZE counter passes: one plain
-    device-to-device copy of known size (the calibration dispatch), then a
-    C3 prompt and `steps` eager decode steps (the SwiGLU GEMV dispatches)."""
+    """Workload for the counter passes (FETCH_SIZE, WRITE_SIZE, MFMA busy):
+    one plain device-to-device copy of known size (the calibration
+    dispatch), then on the C3 model a 2048-token prefill (the headline
+    prefill's GEMMs and attention), a 2016-token continuation over that
+    cache, and `steps` eager decode steps at 4064-4072 context (every decode
+    kernel of the headline, the SwiGLU GEMV among them)."""
     import torch
     from esp_amd import DecoderModel
     n = 64 << 20
@@ -132,12 +135,17 @@ def traffic_run(steps: int = 8) -> None:
     torch.cuda.synchronize()
     cfg = c3_config()
     model = DecoderModel.synthetic(cfg, seed=4321, std=0.02, fmt="bf16", **C3_LORA)
-    kv = model.new_cache(1, 600)
-    model.try_forward_cached_last(uniform_ids(42, 512, cfg.vocab_size), kv)
+    kv = model.new_cache(1, 4064 + steps)
+    prompt = uniform_ids(7, 4064, cfg.vocab_size)
+    print("traffic: model ready", file=sys.stderr, flush=True)
+    model.try_forward_cached_last(prompt[:2048], kv)
+    model.try_forward_cached_last(prompt[2048:], kv)
+    print("traffic: prefill done", file=sys.stderr, flush=True)
     for i in range(steps):
         model.try_forward_cached_last([i + 1], kv)
+    model.close()
     print(json.dumps({"copy_bytes": n * 4, "mlp_gemv_bytes": mlp_gemv_bytes(cfg),
-                      "decode_steps": steps}), flush=True)
+                      "prefill_rows": [2048, 2016], "decode_steps": steps}), flush=True)
 
 
 def prefill_flops(cfg, S: int) -> float:
