@@ -12,6 +12,8 @@ from .model import DecoderModel, KvCache  # noqa: F401
 from .generate import (TokenPicker, generate_constrained, generate_ids,  # noqa: F401
                        generate_ids_with)
 from .sample import Sampler  # noqa: F401
+from .provider import (DecoderProvider, GenerationCheckpoint, GenerationRequest,  # noqa: F401
+                       ScoreHealth)
 from .constraint import Constraint, Vocabulary  # noqa: F401
 from .streaming import (ArtifactSource, FnSource, LayerSource, StreamingOptions,  # noqa: F401
                         cache_verified_layers, split_checkpoint, with_expert_reader)

@@ -95,6 +95,7 @@ def load():
         "esp_kv_reset": (C.c_int, [vp, u32]),
         "esp_kv_position": (C.c_int, [vp, u32, P(u32)]),
         "esp_kv_stream": (C.c_int, [vp, P(vp)]),
+        "esp_kv_logits": (C.c_int, [vp, P(vp), P(u32)]),
         "esp_forward_last": (C.c_int, [vp, vp, u32, P(i32), u32, vp]),
         "esp_forward_batch": (C.c_int, [vp, vp, u32, P(u32), P(u32), P(i32), vp]),
         "esp_pick": (C.c_int, [vp, u32, vp, P(EspSampler), P(u32), P(C.c_uint8)]),
@@ -132,7 +133,7 @@ def load():
 
 EXPORTED = ["esp_last_error", "esp_version", "esp_model_load", "esp_model_create_synthetic",
             "esp_model_destroy", "esp_model_weight_bytes", "esp_kv_create", "esp_kv_destroy",
-            "esp_kv_reset", "esp_kv_position", "esp_kv_stream", "esp_forward_last",
+            "esp_kv_reset", "esp_kv_position", "esp_kv_stream", "esp_kv_logits", "esp_forward_last",
             "esp_forward_batch", "esp_pick", "esp_pick_constrained", "esp_pick_noalloc",
             "esp_generate_greedy",
             "esp_vocab_create", "esp_vocab_destroy", "esp_constraint_create",

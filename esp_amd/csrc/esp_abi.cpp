@@ -253,6 +253,15 @@ esp_status esp_kv_stream(const esp_kv *kv, void **stream) {
     });
 }
 
+esp_status esp_kv_logits(esp_kv *kv, float **rows_dev, uint32_t *n_rows) {
+    return guard([&] {
+        if (!kv) fail(ESP_INVALID_REQUEST, "null kv handle");
+        Kv &k = *(Kv *)kv;
+        if (rows_dev) *rows_dev = k.logits_rows ? k.logits.as<float>() : nullptr;
+        if (n_rows) *n_rows = (uint32_t)k.logits_rows;
+    });
+}
+
 static void copy_logits(Kv &kv, int rows, float *out) {
     if (!out) return;
     ESP_HIP(hipMemcpy(out, kv.logits.p, (size_t)rows * kv.model->V * 4, hipMemcpyDeviceToHost));
@@ -510,9 +519,28 @@ esp_status esp_generate_greedy(esp_model *model, esp_kv *kv, uint32_t seq, const
         Kv &k = *(Kv *)kv;
         if (k.model != &m) fail(ESP_INVALID_REQUEST, "kv handle belongs to another model");
         if (seq >= (uint32_t)k.batch) fail(ESP_INVALID_REQUEST, "sequence index out of range");
-        long long last_pos = (long long)n_prompt + (max_new ? max_new - 1 : 0);
-        if (last_pos > k.max_ctx || last_pos > (long long)m.cfg.max_position_embeddings)
+        // The reference grows its cache and refuses only a forward that
+        // would pass the window (model.rs:547-556): generation that stops at
+        // eos before then succeeds. So only the decode forwards that fit run
+        // (token i, 1-based, is fed at position n_prompt + i - 1); if no eos
+        // comes among the tokens they yield, the next forward is the one the
+        // reference refuses.
+        const long long lim =
+            std::min<long long>(k.max_ctx, (long long)m.cfg.max_position_embeddings);
+        if ((long long)n_prompt > lim)
             fail(ESP_INVALID_REQUEST, "cached input is empty or exceeds the context window");
+        const uint32_t fit =
+            max_new ? (uint32_t)std::min<long long>((long long)max_new - 1, lim - n_prompt) : 0;
+        const uint32_t gen_n = max_new ? fit + 1 : 0;  // tokens the fitting forwards yield
+        const long long last_pos = (long long)n_prompt + fit;
+        auto finish = [&](uint32_t n) {
+            // the KV holds exactly the fed tokens: every emitted id but the
+            // last of a full-length run (generate.rs:154-168)
+            k.pos[seq] = (int)(n_prompt + std::min<uint32_t>(n, max_new - 1));
+            if (n == gen_n && gen_n < max_new)
+                fail(ESP_INVALID_REQUEST, "cached input is empty or exceeds the context window");
+            if (n_out) *n_out = n;
+        };
         if (n_out) *n_out = 0;
         k.pos[seq] = 0;  // generate.rs:141 new_cache per generation
         forward(m, k, 1, &seq, &n_prompt, prompt);
@@ -539,22 +567,20 @@ esp_status esp_generate_greedy(esp_model *model, esp_kv *kv, uint32_t seq, const
         // a resident one, and its hit counter is set afterwards to the
         // forwards the reference takes (one per emitted token before the
         // last, generate.rs:154-168).
+        // The streamer's lock is taken before its cache is inspected and held
+        // to the end, so no other call can evict a layer in between.
+        std::shared_ptr<Streamer> keep = m.st;
+        std::unique_lock<std::recursive_mutex> st_lk;
+        if (keep) st_lk = std::unique_lock<std::recursive_mutex>(keep->mu);
         std::shared_ptr<Streamer> cached_st =
-            m.st && (int)m.st->cache.size() == m.L ? m.st : nullptr;
-        std::unique_lock<std::recursive_mutex> cached_lk;
-        uint64_t hits0 = 0;
-        if (cached_st) {
-            cached_lk = std::unique_lock<std::recursive_mutex>(cached_st->mu);
-            hits0 = cached_st->hits;
-        }
-        if (m.st && !cached_st) {
+            keep && (int)keep->cache.size() == m.L ? keep : nullptr;
+        const uint64_t hits0 = cached_st ? cached_st->hits : 0;
+        if (keep && !cached_st) {
             // Streamed layers are read between kernels: one host-driven step
             // per token, stopping at eos (generate.rs:154-168) so no layer
             // is read for a step the reference does not take.
-            std::shared_ptr<Streamer> keep = m.st;
-            std::lock_guard<std::recursive_mutex> lk(keep->mu);
-            uint32_t n = 0, fed = 0;
-            for (uint32_t i = 0; i < max_new; ++i) {
+            uint32_t n = 0;
+            for (uint32_t i = 0; i < gen_n; ++i) {
                 int32_t id = 0;
                 ESP_HIP(hipMemcpyAsync(&id, g + 8 + i, 4, hipMemcpyDeviceToHost, s));
                 ESP_HIP(hipStreamSynchronize(s));
@@ -564,13 +590,9 @@ esp_status esp_generate_greedy(esp_model *model, esp_kv *kv, uint32_t seq, const
                 if (stop) break;
                 if (out_ids) out_ids[n] = id;
                 ++n;
-                if (i + 1 < max_new) {
-                    decode_step_dev(m, k, (int)seq, max_t, g);
-                    ++fed;
-                }
+                if (i + 1 < gen_n) decode_step_dev(m, k, (int)seq, max_t, g);
             }
-            k.pos[seq] = (int)(n_prompt + fed);
-            if (n_out) *n_out = n;
+            finish(n);
             return;
         }
         // Multi-row MoE layers read their expert row counts back to the
@@ -581,7 +603,7 @@ esp_status esp_generate_greedy(esp_model *model, esp_kv *kv, uint32_t seq, const
         const bool has_moe = std::any_of(m.layers.begin(), m.layers.end(),
                                          [](const LayerW &w) { return w.moe; });
         const bool capturable = (!has_moe || moe_decode_ok(m)) && !(env && env[0] == '0');
-        uint32_t steps = max_new - 1;
+        uint32_t steps = fit;
         if (steps) {
             decode_step_dev(m, k, (int)seq, max_t, g);  // eager: sizes every scratch buffer
             --steps;
@@ -615,23 +637,22 @@ esp_status esp_generate_greedy(esp_model *model, esp_kv *kv, uint32_t seq, const
         } else {
             for (uint32_t i = 0; i < steps; ++i) decode_step_dev(m, k, (int)seq, max_t, g);
         }
-        std::vector<int32_t> list(max_new);
-        ESP_HIP(hipMemcpyAsync(list.data(), g + 8, (size_t)max_new * 4, hipMemcpyDeviceToHost, s));
+        std::vector<int32_t> list(gen_n);
+        ESP_HIP(hipMemcpyAsync(list.data(), g + 8, (size_t)gen_n * 4, hipMemcpyDeviceToHost, s));
         ESP_HIP(hipStreamSynchronize(s));
-        k.pos[seq] = (int)last_pos;
         uint32_t n = 0;
-        for (; n < max_new; ++n) {
+        for (; n < gen_n; ++n) {
             bool stop = false;
             for (uint32_t e = 0; e < n_eos; ++e) stop |= list[n] == eos[e];
             if (stop) break;
             if (out_ids) out_ids[n] = list[n];
         }
-        if (n_out) *n_out = n;
         if (cached_st) {
             stream_check(m);
             const uint64_t fwd = std::min<uint64_t>(n, max_new - 1);
             cached_st->hits = hits0 + fwd * (uint64_t)m.L;
         }
+        finish(n);
     });
 }
 

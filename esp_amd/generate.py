@@ -10,7 +10,6 @@ from __future__ import annotations
 
 from typing import Callable, List, Optional, Sequence, Tuple
 
-from .errors import InvalidRequest
 from .model import DecoderModel, KvCache
 from .sample import Sampler
 
@@ -57,8 +56,11 @@ def try_generate_ids_with(model: DecoderModel, prompt_ids: Sequence[int], max_ne
     and eos excluded."""
     if not prompt_ids:
         raise AssertionError("prompt must not be empty")
+    # The reference's cache grows; a forward past the window is refused when
+    # it is taken (model.rs:547-556), so a run that ends at eos first
+    # succeeds. The cache is sized to the window at most.
     need = len(prompt_ids) + max(0, max_new - 1)
-    cache = cache or model.new_cache(1, max(need, 1))
+    cache = cache or model.new_cache(1, max(1, min(need, model.config.max_position_embeddings)))
     if picker.sampler is None and on_token is None:
         return model.generate_greedy_device(cache, prompt_ids, max_new, eos)
     cache.reset(0)
@@ -84,39 +86,22 @@ def generate_constrained(model: DecoderModel, prompt_ids: Sequence[int], max_new
     Each turn either takes the grammar's forced span (constraint.rs:296-344;
     a sampled picker skips one draw per forced token, provider.rs:819-824)
     or picks one token from the logits masked on the device by the
-    constraint (provider.rs:744-817). Tokens are accepted into the
-    constraint; the loop ends when the grammar is complete or an eos id is
-    picked, and a token limit reached first is InvalidRequest
-    (provider.rs:874-878). Forced spans are evaluated as one block over the
-    warm cache. Returns (ids, complete)."""
+    constraint (provider.rs:744-817), with the reference's recovery from
+    non-finite scores (one recompute of the prefix, then Backend;
+    provider.rs:219-240). Tokens are accepted into the constraint; the loop
+    ends when the grammar is complete or an eos id is picked, and a token
+    limit reached first is InvalidRequest (provider.rs:874-878). Forced
+    spans are evaluated as one block over the warm cache. Returns
+    (ids, complete)."""
+    from .provider import DecoderProvider, GenerationCheckpoint
     if not prompt_ids:
         raise AssertionError("prompt must not be empty")
     need = len(prompt_ids) + max(0, max_new - 1)
-    cache = cache or model.new_cache(1, max(need, 1))
+    cache = cache or model.new_cache(1, max(1, min(need, model.config.max_position_embeddings)))
     cache.reset(0)
     model.try_forward_cached_last(list(prompt_ids), cache)
-    out: List[int] = []
-    sampler = picker.sampler
-    while len(out) < max_new:
-        forced = constraint.forced(tokenizer)
-        if not forced:
-            ids, _ = model.pick_constrained(cache, [constraint],
-                                            None if sampler is None else [sampler])
-            tokens = [int(ids[0])]
-        else:
-            if sampler is not None:
-                sampler.skip_draws(len(forced))
-            tokens = forced
-        evaluated: List[int] = []
-        for token in tokens[:max_new - len(out)]:
-            if token in eos:
-                return out, True
-            constraint.accept(token)
-            out.append(token)
-            evaluated.append(token)
-            if constraint.complete():
-                return out, True
-        if len(out) == max_new:
-            break
-        model.try_forward_cached_last(evaluated, cache)
-    raise InvalidRequest("token limit reached before output grammar completed")
+    provider = DecoderProvider(model, eos, tokenizer)
+    cp = GenerationCheckpoint(request=None, prompt_ids=list(prompt_ids), token_ids=[], draws=0,
+                              complete=False)
+    provider._token_loop(cache, cp, max_new, picker, constraint, lambda _: None, lambda: False)
+    return list(cp.token_ids), cp.complete

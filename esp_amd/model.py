@@ -117,6 +117,13 @@ class KvCache:
         _lib.check(_lib.load().esp_kv_stream(self._h, C.byref(s)))
         return s.value or 0
 
+    def logits_device(self) -> Tuple[int, int]:
+        """(device address, rows) of the last forward's f32 logits rows."""
+        p = C.c_void_p()
+        n = C.c_uint32()
+        _lib.check(_lib.load().esp_kv_logits(self._h, C.byref(p), C.byref(n)))
+        return p.value or 0, n.value
+
     def close(self) -> None:
         if getattr(self, "_h", None):
             _lib.load().esp_kv_destroy(self._h)
@@ -272,16 +279,17 @@ class DecoderModel:
             cache._h, n_rows, None if bits is None else bits.ctypes.data, *a))
 
     def pick_constrained(self, cache: KvCache, constraints: Sequence[Optional["Constraint"]],
-                         samplers: Optional[List[Optional[Sampler]]] = None
-                         ) -> Tuple[np.ndarray, np.ndarray]:
+                         samplers: Optional[List[Optional[Sampler]]] = None, check: bool = True):
         """provider.rs:740-817: pick with each row masked on the device by its
-        constraint (None = unconstrained). Constraint states are not advanced."""
+        constraint (None = unconstrained). Constraint states are not advanced.
+        Returns (ids, flags); with check=False, (ids, flags, status) and no
+        raise, so a caller can read the flags of a refused pick first."""
         from .constraint import constraint_handles
         arr, keep = constraint_handles(constraints)
         return self._pick(cache, len(constraints), samplers, lambda *a: _lib.load()
-                          .esp_pick_constrained(cache._h, len(keep), arr, *a))
+                          .esp_pick_constrained(cache._h, len(keep), arr, *a), check)
 
-    def _pick(self, cache: KvCache, n_rows: int, samplers, call) -> Tuple[np.ndarray, np.ndarray]:
+    def _pick(self, cache: KvCache, n_rows: int, samplers, call, check: bool = True):
         ids = np.zeros(n_rows, np.uint32)
         flags = np.zeros(n_rows, np.uint8)
         sarr = None
@@ -299,6 +307,8 @@ class DecoderModel:
             for i, s in enumerate(samplers):
                 if s is not None:
                     s.rng.state = sarr[i].state
+        if not check:
+            return ids, flags, status
         _lib.check(status)
         return ids, flags
 

@@ -160,6 +160,14 @@ esp_status esp_kv_reset(esp_kv *kv, uint32_t seq);
 esp_status esp_kv_position(const esp_kv *kv, uint32_t seq, uint32_t *position);
 /* The HIP stream (hipStream_t) this KV handle's work runs on. */
 esp_status esp_kv_stream(const esp_kv *kv, void **stream);
+/* Device address of the last forward's logits rows on this handle
+ * (row-major f32 [n_rows][vocab], valid until the next forward; NULL and 0
+ * before any forward), so a caller can read or post-process scores in
+ * place on the handle's stream before esp_pick. Stands where the reference
+ * hands its logits tensor to the provider (model.rs:502-539 return value,
+ * provider.rs:744-760 row read); the provider's test-only score faults
+ * (provider.rs:70-71, 755-762) are injected through it. */
+esp_status esp_kv_logits(esp_kv *kv, float **rows_dev, uint32_t *n_rows);
 
 /* model.rs:502-539 try_forward_cached_last for one sequence: consume `n`
  * ids at the sequence's position, extend its cache, and leave the
