@@ -91,6 +91,15 @@ struct GemmArgs {
     int M, N, K, ldc;
     float *ws;         // nullable split-K workspace
     size_t ws_bytes;
+    // Grouped launch (routed experts): the M rows are grp_n consecutive
+    // groups with row offsets grp_offs[0..grp_n] (device, ascending, written
+    // by the router on the stream, never read by the host); group e
+    // multiplies W + e * grp_w_stride (and W2 likewise, elements). The grid
+    // is sized for ceil(M / tile rows) + grp_n row tiles; the ones past the
+    // groups' last tile exit. nullptr = one group of M rows.
+    const int32_t *grp_offs;
+    int grp_n;
+    long long grp_w_stride;
 };
 void launch_gemm(Dt wt, GemmEpi epi, const GemmArgs &a, hipStream_t s);
 

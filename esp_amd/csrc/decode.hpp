@@ -34,7 +34,8 @@ struct DecodeGemvArgs {
     // routed experts (moe.rs:135-256, one row): with ex_sel set, SWIGLU
     // units are (slot, row) pairs, slot = unit / ex_rows, reading expert
     // ex_sel[slot] (clamped to [0, ex_count)) of the [E][rows][K] tensors;
-    // RESID reads expert ex_sel[ex_slot] and scales by ex_w[ex_slot].
+    // RESID and STORE read expert ex_sel[ex_slot]; RESID scales by
+    // ex_w[ex_slot] when ex_w is set.
     const int32_t *ex_sel;
     const float *ex_w;
     long long ex_stride;   // elements between consecutive experts

@@ -70,4 +70,34 @@ __device__ __forceinline__ float block_sum(float v, float *red) {
 
 __device__ __forceinline__ float silu(float x) { return x * (1.0f / (1.0f + expf(-x))); }
 
+// Row tile `slot` of a GEMM launch with tiles of BM rows. One group (offs
+// == nullptr): rows [slot * BM, M). Grouped: slots run through the groups in
+// order, ceil(n_e / BM) per group e of offs[e+1] - offs[e] rows (offsets
+// clamped into [0, M] and made ascending, so a corrupt table stays in
+// bounds); gives the tile's first row, its group's row end and the group,
+// or false past the last tile. Uniform across the block (scalar loads).
+__device__ __forceinline__ bool group_tile(const int32_t *offs, int n_groups, int M, int slot,
+                                           int BM, int &m0, int &mend, int &grp) {
+    if (!offs) {
+        m0 = slot * BM;
+        mend = M;
+        grp = 0;
+        return m0 < M;
+    }
+    int acc = 0, prev = min(max(offs[0], 0), M);
+    for (int e = 0; e < n_groups; ++e) {
+        const int nx = min(max(offs[e + 1], prev), M);
+        const int tiles = (nx - prev + BM - 1) / BM;
+        if (slot < acc + tiles) {
+            m0 = prev + (slot - acc) * BM;
+            mend = nx;
+            grp = e;
+            return true;
+        }
+        acc += tiles;
+        prev = nx;
+    }
+    return false;
+}
+
 }  // namespace esp

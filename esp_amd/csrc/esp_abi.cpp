@@ -21,6 +21,7 @@ Model *synthetic_model(const esp_config *cfg, uint64_t seed, float std, uint32_t
                        uint32_t lora_mask, float lora_a_std, float lora_b_std, float lora_scale);
 Kv *create_kv(Model *m, uint32_t batch, uint32_t max_ctx);
 void decode_step_dev(Model &m, Kv &kv, int seq, int max_t, int32_t *gen);
+void moe_check(Kv &kv);
 void launch_gen_step(const uint32_t *picked, int32_t *gen, hipStream_t s);
 }  // namespace esp
 
@@ -595,14 +596,11 @@ esp_status esp_generate_greedy(esp_model *model, esp_kv *kv, uint32_t seq, const
             finish(n);
             return;
         }
-        // Multi-row MoE layers read their expert row counts back to the
-        // host, which a captured graph cannot do; single-row decode routes on
-        // the device when the expert shapes fit the decode GEMV. ESP_GRAPHS=0
-        // replays eagerly (profilers).
+        // Every layer kind routes and groups on the device (MoE included), so
+        // the decode step is captured once and replayed. ESP_GRAPHS=0 replays
+        // eagerly (profilers).
         const char *env = getenv("ESP_GRAPHS");
-        const bool has_moe = std::any_of(m.layers.begin(), m.layers.end(),
-                                         [](const LayerW &w) { return w.moe; });
-        const bool capturable = (!has_moe || moe_decode_ok(m)) && !(env && env[0] == '0');
+        const bool capturable = !(env && env[0] == '0');
         uint32_t steps = fit;
         if (steps) {
             decode_step_dev(m, k, (int)seq, max_t, g);  // eager: sizes every scratch buffer
@@ -647,6 +645,7 @@ esp_status esp_generate_greedy(esp_model *model, esp_kv *kv, uint32_t seq, const
             if (stop) break;
             if (out_ids) out_ids[n] = list[n];
         }
+        moe_check(k);  // a step whose router failed fails the generation
         if (cached_st) {
             stream_check(m);
             const uint64_t fwd = std::min<uint64_t>(n, max_new - 1);

@@ -48,7 +48,7 @@ __global__ void __launch_bounds__(DG_THREADS) decode_gemv_k(DecodeGemvArgs a) {
     const void *W = a.w;
     const void *W2 = a.w2;
     size_t ex0 = 0;  // element offset of the routed expert (RESID)
-    if (EPI == DG_RESID && a.ex_sel)  // one routed expert's rows
+    if ((EPI == DG_RESID || EPI == DG_STORE) && a.ex_sel)  // one routed expert's rows
         ex0 = (size_t)min(max(a.ex_sel[a.ex_slot], 0), a.ex_count - 1) * a.ex_stride;
     // QKVROPE: N/2 rotary pairs, then the LoRA A rows in pairs
     const int units = EPI == DG_QKVROPE ? a.N / 2 + (a.lora_rows + 1) / 2 : a.N;

@@ -67,10 +67,13 @@ __global__ void __launch_bounds__(256, 2) gemm_mfma_k(GemmArgs g, float *ws, int
     const int total = mt * nt, per = (total + MF_XCDS - 1) / MF_XCDS;
     const int tile = (blockIdx.x % MF_XCDS) * per + blockIdx.x / MF_XCDS;
     if (tile >= total) return;
-    const int m0 = (tile % mt) * MF_BM, n0 = (tile / mt) * BN;
+    int m0, M, grp;  // M: end of this tile's group (rows >= M are not computed)
+    if (!group_tile(g.grp_offs, g.grp_n, g.M, tile % mt, MF_BM, m0, M, grp)) return;
+    const int n0 = (tile / mt) * BN;
+    const size_t woff = (size_t)grp * g.grp_w_stride;
     const uint16_t *Ah = (const uint16_t *)g.a, *Al = (const uint16_t *)g.a_lo;
-    const uint16_t *Wm[2] = {(const uint16_t *)g.w, (const uint16_t *)g.w2};
-    const int M = g.M, N = g.N, K = g.K;
+    const uint16_t *Wm[2] = {(const uint16_t *)g.w + woff, (const uint16_t *)g.w2 + woff};
+    const int N = g.N, K = g.K;
 
     f32x16_t acc[NB][2][NJ];
 #pragma unroll
@@ -207,7 +210,7 @@ __global__ void __launch_bounds__(256, 2) gemm_mfma_k(GemmArgs g, float *ws, int
                     if (row >= M) continue;
 #pragma unroll
                     for (int b = 0; b < NB; ++b)
-                        ws[(((size_t)blockIdx.z * NB + b) * M + row) * N + col] = acc[b][i][j][e];
+                        ws[(((size_t)blockIdx.z * NB + b) * g.M + row) * N + col] = acc[b][i][j][e];
                 }
                 continue;
             }
@@ -342,8 +345,11 @@ __global__ void __launch_bounds__(128 * BMW + (PROD ? 64 : 0), (BMW == 2 && STG 
     const int total = mt * nt, per = (total + MF_XCDS - 1) / MF_XCDS;
     const int tile = (blockIdx.x % MF_XCDS) * per + blockIdx.x / MF_XCDS;
     if (tile >= total) return;
-    const int m0 = (tile % mt) * F::BM, n0 = (tile / mt) * BN;
-    const int M = g.M, N = g.N, K = g.K;
+    int m0, M, grp;  // M: end of this tile's group (rows >= M are not computed)
+    if (!group_tile(g.grp_offs, g.grp_n, g.M, tile % mt, F::BM, m0, M, grp)) return;
+    const int n0 = (tile / mt) * BN;
+    const size_t woff = (size_t)grp * g.grp_w_stride;
+    const int N = g.N, K = g.K;
     const int kbeg = blockIdx.z * k_per_split;
     const int KT = (min(K, kbeg + k_per_split) - kbeg) / LS_BK;
 
@@ -361,7 +367,7 @@ __global__ void __launch_bounds__(128 * BMW + (PROD ? 64 : 0), (BMW == 2 && STG 
     for (int q = 0; q < F::QB; ++q) {
         const int sl = (wave * F::QB + q) * 64 + lane, r = sl >> 2, kc = (sl & 3) ^ ls_swz(r);
         const int b = r / BN, n = min(n0 + r % BN, N - 1);
-        bsrc[q] = (const uint16_t *)(b ? g.w2 : g.w) + (size_t)n * K + kbeg + kc * 8;
+        bsrc[q] = (const uint16_t *)(b ? g.w2 : g.w) + woff + (size_t)n * K + kbeg + kc * 8;
     }
     auto issue = [&](int kt) {
         char *base = lds_s + (kt % STAGES) * F::STAGE;
@@ -395,6 +401,7 @@ __global__ void __launch_bounds__(128 * BMW + (PROD ? 64 : 0), (BMW == 2 && STG 
                 boff[q] = (int)((size_t)min(n0 + r % BN, N - 1) * K + kbeg + kc * 8);
             }
             const uint16_t *pa = (const uint16_t *)g.a, *pl = (const uint16_t *)g.a_lo;
+            const uint16_t *pw0 = (const uint16_t *)g.w + woff, *pw1 = (const uint16_t *)g.w2 + woff;
             auto pissue = [&](int kt) {
                 char *base = lds_s + (kt % STAGES) * F::STAGE;
                 const int ko = kt * LS_BK;
@@ -405,7 +412,7 @@ __global__ void __launch_bounds__(128 * BMW + (PROD ? 64 : 0), (BMW == 2 && STG 
                 }
 #pragma unroll
                 for (int q = 0; q < BQ; ++q) {  // rows [16 q, 16 q + 16): gate rows, then up rows
-                    const uint16_t *pw = (const uint16_t *)(q * 16 < BN ? g.w : g.w2);
+                    const uint16_t *pw = q * 16 < BN ? pw0 : pw1;
                     __builtin_amdgcn_global_load_lds((gptr_t)(pw + boff[q] + ko), (lptr_t)(base + 2 * F::A + q * 1024), 16, 0, 0);
                 }
             };
@@ -503,7 +510,7 @@ __global__ void __launch_bounds__(128 * BMW + (PROD ? 64 : 0), (BMW == 2 && STG 
                     if (row >= M) continue;
 #pragma unroll
                     for (int b = 0; b < NB; ++b)
-                        ws[(((size_t)blockIdx.z * NB + b) * M + row) * N + col] = acc[b][i][j][e];
+                        ws[(((size_t)blockIdx.z * NB + b) * g.M + row) * N + col] = acc[b][i][j][e];
                 }
                 continue;
             }
@@ -542,7 +549,8 @@ static void mfma_launch_nj(const GemmArgs &a, float *ws, size_t ws_bytes, hipStr
                            int min_ks = 512) {
     constexpr size_t shm = mfma_lds_bytes<NB, NJ>();
     constexpr int BN = 64 * NJ;
-    const int gx = (a.N + BN - 1) / BN, gy = (a.M + MF_BM - 1) / MF_BM;
+    const int gx = (a.N + BN - 1) / BN,
+              gy = (a.M + MF_BM - 1) / MF_BM + (a.grp_offs ? a.grp_n : 0);
     const int blocks = MF_XCDS * ((gx * gy + MF_XCDS - 1) / MF_XCDS);
     // split K until the grid covers the chip twice
     int splits = 1;
@@ -574,7 +582,8 @@ static void lds_launch(const GemmArgs &a, float *ws, size_t ws_bytes, hipStream_
                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)F::LDS));
         attr = true;
     }
-    const int gx = (a.N + BN - 1) / BN, gy = (a.M + F::BM - 1) / F::BM;
+    const int gx = (a.N + BN - 1) / BN,
+              gy = (a.M + F::BM - 1) / F::BM + (a.grp_offs ? a.grp_n : 0);
     const int blocks = MF_XCDS * ((gx * gy + MF_XCDS - 1) / MF_XCDS);
     int splits = 1;
     while (gx * gy * splits < want_blocks && a.K / (splits * 2) >= min_ks &&

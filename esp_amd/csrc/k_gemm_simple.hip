@@ -15,9 +15,12 @@ __global__ void __launch_bounds__(256) gemm_simple_k(GemmArgs a) {
     __shared__ float Ws[NW][SG_BK][SG_BN + 4];
     const int tid = threadIdx.x;
     const int tx = tid % 16, ty = tid / 16;
-    const int m0 = blockIdx.y * SG_BM, n0 = blockIdx.x * SG_BN;
+    const int n0 = blockIdx.x * SG_BN;
+    int m0, mend, grp;
+    if (!group_tile(a.grp_offs, a.grp_n, a.M, blockIdx.y, SG_BM, m0, mend, grp)) return;
     const AT *A = (const AT *)a.a;
-    const WT *Wm[2] = {(const WT *)a.w, (const WT *)a.w2};
+    const size_t woff = (size_t)grp * a.grp_w_stride;
+    const WT *Wm[2] = {(const WT *)a.w + woff, (const WT *)a.w2 + woff};
     float acc[NW][4][4];
 #pragma unroll
     for (int w = 0; w < NW; ++w)
@@ -32,7 +35,7 @@ __global__ void __launch_bounds__(256) gemm_simple_k(GemmArgs a) {
             int r = e / SG_BK, kk = e % SG_BK;
             int gm = m0 + r, gk = k0 + kk;
             float av = 0.f;
-            if (gm < a.M && gk < a.K) {
+            if (gm < mend && gk < a.K) {
                 size_t ai = (size_t)gm * a.K + gk;
                 av = a.a_lo ? bf2f(((const uint16_t *)a.a)[ai]) + bf2f(((const uint16_t *)a.a_lo)[ai])
                             : ld(A, ai);
@@ -66,7 +69,7 @@ __global__ void __launch_bounds__(256) gemm_simple_k(GemmArgs a) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         int gm = m0 + ty * 4 + i;
-        if (gm >= a.M) continue;
+        if (gm >= mend) continue;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             int gn = n0 + tx * 4 + j;
@@ -93,7 +96,8 @@ __global__ void __launch_bounds__(256) gemm_simple_k(GemmArgs a) {
 
 template <typename AT, typename WT>
 static void simple_dispatch(GemmEpi epi, const GemmArgs &a, hipStream_t s) {
-    dim3 grid((a.N + SG_BN - 1) / SG_BN, (a.M + SG_BM - 1) / SG_BM);
+    dim3 grid((a.N + SG_BN - 1) / SG_BN,
+              (a.M + SG_BM - 1) / SG_BM + (a.grp_offs ? a.grp_n : 0));
     if (epi == GEMM_STORE) gemm_simple_k<AT, WT, GEMM_STORE><<<grid, 256, 0, s>>>(a);
     else if (epi == GEMM_RESIDUAL) gemm_simple_k<AT, WT, GEMM_RESIDUAL><<<grid, 256, 0, s>>>(a);
     else gemm_simple_k<AT, WT, GEMM_SWIGLU><<<grid, 256, 0, s>>>(a);

@@ -63,9 +63,17 @@ __global__ void __launch_bounds__(256) route_k(RouteArgs a) {
     }
     __syncthreads();
     if (status) {
+        // No expert gets a row; the grouped rows and the combine still index
+        // in bounds (identity slots). The sticky word reports the layer's
+        // failure to the host at the end of the forward.
         if (threadIdx.x == 0) {
             for (int e = 0; e <= E; ++e) a.offs[e] = 0;
             a.offs[E + 1] = status;
+            if (a.err) atomicMax(a.err, status);
+        }
+        for (int i = threadIdx.x; i < a.M * k; i += blockDim.x) {
+            a.slot[i] = i;
+            a.perm[i] = i / k;
         }
         return;
     }
@@ -81,12 +89,13 @@ __global__ void __launch_bounds__(256) route_k(RouteArgs a) {
     const int nt = blockDim.x, tid = threadIdx.x;
     if (E <= EMAX) {
         const int per = (R + nt - 1) / nt, b0 = min(R, tid * per), b1 = min(R, b0 + per);
+        const int nact = (R + per - 1) / per;  // threads holding selections
         for (int e = 0; e < E; ++e) tc[e][tid] = 0;
         for (int i = b0; i < b1; ++i) tc[a.sel[i]][tid] += 1;
         __syncthreads();
         if (tid < E) {  // exclusive scan of expert tid's counts over threads
             int acc = 0;
-            for (int t = 0; t < nt; ++t) {
+            for (int t = 0; t < nact; ++t) {
                 const int c = tc[tid][t];
                 tc[tid][t] = acc;
                 acc += c;
@@ -167,22 +176,26 @@ void launch_gather_rows(Dt dt, const void *src, const int32_t *perm, int rows, i
     else gather_k<float><<<rows, 256, 0, s>>>((const float *)src, perm, H, (float *)dst);
 }
 
+// One thread per (token, hidden element): every load of a thread is
+// independent, so a single decode row costs one memory round trip.
 __global__ void __launch_bounds__(256) combine_k(CombineArgs a) {
-    int t = blockIdx.x;
-    float g = 0.f;
-    if (a.sg) g = 1.0f / (1.0f + expf(-a.sg[t]));
-    for (int d = threadIdx.x; d < a.H; d += blockDim.x) {
-        float out = 0.f;
-        for (int j = 0; j < a.k; ++j) {
-            float y = a.y[(size_t)a.slot[(size_t)t * a.k + j] * a.H + d];
-            out = out + y * a.w[(size_t)t * a.k + j];
-        }
-        if (a.ys) out = out + g * a.ys[(size_t)t * a.H + d];
-        a.h[(size_t)t * a.H + d] += out;
+    const int t = blockIdx.x, d = blockIdx.y * blockDim.x + threadIdx.x;
+    if (d >= a.H) return;
+    float out = 0.f;
+    for (int j = 0; j < a.k; ++j) {
+        float y = a.y[(size_t)a.slot[(size_t)t * a.k + j] * a.H + d];
+        out = out + y * a.w[(size_t)t * a.k + j];
     }
+    if (a.ys) {
+        const float g = 1.0f / (1.0f + expf(-a.sg[t]));
+        out = out + g * a.ys[(size_t)t * a.H + d];
+    }
+    a.h[(size_t)t * a.H + d] += out;
 }
 
-void launch_combine(const CombineArgs &a, hipStream_t s) { combine_k<<<a.M, 256, 0, s>>>(a); }
+void launch_combine(const CombineArgs &a, hipStream_t s) {
+    combine_k<<<dim3(a.M, (a.H + 255) / 256), 256, 0, s>>>(a);
+}
 
 // --------------------------------------------------------------- fills
 

@@ -26,6 +26,7 @@ struct RouteArgs {
     int32_t *offs;   // [E + 1] expert row offsets; offs[E + 1] = status
     int32_t *perm;   // [M * k] token of each grouped row
     int32_t *slot;   // [M, k] grouped row of each selection
+    int32_t *err;    // nullable sticky status word: max(2 non-finite router, 3 bad top-k mass)
 };
 void launch_route(const RouteArgs &a, hipStream_t s);
 void launch_gather_rows(Dt dt, const void *src, const int32_t *perm, int rows, int H, void *dst,

@@ -1348,6 +1348,30 @@ static void ensure_scratch(Model &m, Kv &kv, int Mc, int n_seqs) {
     kv.rows_dev.ensure((size_t)(3 * kMaxRows + 2 * kv.batch + 64) * 4);
     if (Mc > 1 && (m.wt == DT_BF16 || dt_packed(m.wt)))
         kv.gemm_ws.ensure((size_t)256 << 20);  // split-K partials
+    if (m.E && !kv.moe_err.p) {
+        kv.moe_err.ensure(64);
+        launch_fill_const(kv.moe_err.as<float>(), 16, 0.f, kv.stream);
+    }
+}
+
+// The sticky router status word of this KV handle (moe.rs:160-171
+// refusals), raised by route_k; forward() clears it before its layers and
+// reads it back with the logits.
+static int32_t *moe_err_word(Kv &kv) { return kv.moe_err.as<int32_t>(); }
+
+static void moe_fail(int32_t status) {
+    if (status == 2) fail(ESP_BACKEND, "non-finite expert router");
+    if (status == 3) fail(ESP_BACKEND, "invalid top-k routing mass");
+    if (status) fail(ESP_BACKEND, "expert routing failed");
+}
+
+// After a device-resident generation loop: fail if any step's router did.
+void moe_check(Kv &kv) {
+    if (!kv.moe_err.p) return;
+    int32_t st = 0;
+    ESP_HIP(hipMemcpyAsync(&st, kv.moe_err.p, 4, hipMemcpyDeviceToHost, kv.stream));
+    ESP_HIP(hipStreamSynchronize(kv.stream));
+    moe_fail(st);
 }
 
 // Head on the last row of each sequence (model.rs:531-538): final RMSNorm
@@ -1445,7 +1469,9 @@ void forward(Model &m, Kv &kv, int n_seqs, const uint32_t *seqs, const uint32_t 
     }
     hipStream_t s = kv.stream;
     const int lastoff = 3 * kMaxRows;
+    const int erroff = lastoff + kv.batch + 8;  // pinned word: the router status read back
     ensure_pinned(kv, (size_t)(3 * kMaxRows + kv.batch + 64) * 4);
+    if (kv.moe_err.p) launch_fill_const(kv.moe_err.as<float>(), 1, 0.f, s);
     int32_t *pin = (int32_t *)kv.pinned;
     int32_t *dev = kv.rows_dev.as<int32_t>();
     float *hl = kv.last_h.as<float>();
@@ -1489,8 +1515,11 @@ void forward(Model &m, Kv &kv, int n_seqs, const uint32_t *seqs, const uint32_t 
     } else {
         run_head(m, kv, n_seqs, hl, nullptr);
     }
+    if (kv.moe_err.p)
+        ESP_HIP(hipMemcpyAsync(pin + erroff, kv.moe_err.p, 4, hipMemcpyDeviceToHost, s));
     ESP_HIP(hipStreamSynchronize(s));
     if (m.st) stream_check(m);  // a streamed layer that failed its device checks
+    if (kv.moe_err.p) moe_fail(pin[erroff]);
     for (int i = 0; i < n_seqs; ++i) kv.pos[seqs[i]] += (int)lens[i];
     kv.logits_rows = n_seqs;
 }
@@ -1581,9 +1610,11 @@ bool moe_decode_ok(const Model &m) {
 
 // moe.rs:135-256 for one decode row, entirely on the device (capturable):
 // router GEMV over RMSNorm(h), device top-k routing, one SwiGLU GEMV over
-// the k selected experts' gate/up rows (expert ids read on the device), then
-// per slot in ascending expert order a down GEMV that adds w_slot * y into
-// h, then the sigmoid-gated shared expert.
+// the k selected experts' gate/up rows (expert ids read on the device) and,
+// from the same pre-MoE h, the shared expert's gate and SwiGLU GEMVs; then a
+// down GEMV per slot and one for the shared expert, each storing its row,
+// and the combine that adds them into h in the reference's order (slots in
+// ascending expert order, then the sigmoid-gated shared expert).
 void moe_decode(Model &m, Kv &kv, LayerW &w, hipStream_t s) {
     const int H = m.H, E = m.E, k = m.topk;
     kv.moe_logits.ensure((size_t)E * 4);
@@ -1592,9 +1623,11 @@ void moe_decode(Model &m, Kv &kv, LayerW &w, hipStream_t s) {
     kv.moe_slot.ensure((size_t)k * 4);
     kv.moe_offs.ensure((size_t)(E + 2) * 4);
     kv.moe_perm.ensure((size_t)k * 4);
-    kv.moe_act.ensure((size_t)k * std::max(m.Fe, m.Fs) * 4);
+    kv.moe_act.ensure((size_t)(k * m.Fe + m.Fs) * 4);
+    kv.moe_y.ensure((size_t)k * H * 4);
+    kv.moe_ys.ensure((size_t)H * 4);
     kv.moe_sg.ensure(64);
-    const size_t wes = dt_size(m.wt);
+    float *act = kv.moe_act.as<float>(), *sh_act = act + (size_t)k * m.Fe;
     {
         DecodeGemvArgs r{};
         r.w = w.router;
@@ -1608,7 +1641,7 @@ void moe_decode(Model &m, Kv &kv, LayerW &w, hipStream_t s) {
         launch_decode_gemv(m.wt, DG_STORE, r, s);
         RouteArgs ra{kv.moe_logits.as<float>(), 1, E, k, m.norm_topk ? 1 : 0,
                      kv.moe_sel.as<int32_t>(), kv.moe_w.as<float>(), kv.moe_offs.as<int32_t>(),
-                     kv.moe_perm.as<int32_t>(), kv.moe_slot.as<int32_t>()};
+                     kv.moe_perm.as<int32_t>(), kv.moe_slot.as<int32_t>(), moe_err_word(kv)};
         launch_route(ra, s);
     }
     {
@@ -1618,7 +1651,7 @@ void moe_decode(Model &m, Kv &kv, LayerW &w, hipStream_t s) {
         g.x = kv.h.as<float>();
         g.gamma = w.post_norm;
         g.eps = m.cfg.rms_norm_eps;
-        g.y = kv.moe_act.as<float>();
+        g.y = act;
         g.N = k * m.Fe;
         g.K = H;
         g.ex_sel = kv.moe_sel.as<int32_t>();
@@ -1628,22 +1661,6 @@ void moe_decode(Model &m, Kv &kv, LayerW &w, hipStream_t s) {
         Prof p("gemv_mlp", s);
         launch_decode_gemv(m.wt, DG_SWIGLU, g, s);
     }
-    for (int j = 0; j < k; ++j) {
-        DecodeGemvArgs d{};
-        d.w = w.ex_down;
-        d.x = kv.moe_act.as<float>() + (size_t)j * m.Fe;
-        d.y = kv.h.as<float>();
-        d.N = H;
-        d.K = m.Fe;
-        d.ex_sel = kv.moe_sel.as<int32_t>();
-        d.ex_w = kv.moe_w.as<float>();
-        d.ex_stride = (long long)H * m.Fe;
-        d.ex_slot = j;
-        d.ex_count = E;
-        Prof p("gemv_down", s);
-        launch_decode_gemv(m.wt, DG_RESID, d, s);
-    }
-    (void)wes;
     if (m.Fs) {
         DecodeGemvArgs sg{};
         sg.w = w.shared_gate;
@@ -1659,27 +1676,57 @@ void moe_decode(Model &m, Kv &kv, LayerW &w, hipStream_t s) {
         g.x = kv.h.as<float>();
         g.gamma = w.post_norm;
         g.eps = m.cfg.rms_norm_eps;
-        g.y = kv.moe_act.as<float>();
+        g.y = sh_act;
         g.N = m.Fs;
         g.K = H;
-        DecodeGemvArgs d{};
-        d.w = w.sh_down;
-        d.x = kv.moe_act.as<float>();
-        d.y = kv.h.as<float>();
-        d.N = H;
-        d.K = m.Fs;
-        d.sig_scale = kv.moe_sg.as<float>();
         Prof p("moe", s);
         launch_decode_gemv(m.wt, DG_STORE, sg, s);
         launch_decode_gemv(m.wt, DG_SWIGLU, g, s);
-        launch_decode_gemv(m.wt, DG_RESID, d, s);
     }
+    for (int j = 0; j < k; ++j) {
+        DecodeGemvArgs d{};
+        d.w = w.ex_down;
+        d.x = act + (size_t)j * m.Fe;
+        d.y = kv.moe_y.as<float>() + (size_t)j * H;
+        d.N = H;
+        d.K = m.Fe;
+        d.ex_sel = kv.moe_sel.as<int32_t>();
+        d.ex_stride = (long long)H * m.Fe;
+        d.ex_slot = j;
+        d.ex_count = E;
+        Prof p("gemv_down", s);
+        launch_decode_gemv(m.wt, DG_STORE, d, s);
+    }
+    CombineArgs c{};
+    c.y = kv.moe_y.as<float>();
+    c.slot = kv.moe_slot.as<int32_t>();
+    c.w = kv.moe_w.as<float>();
+    c.h = kv.h.as<float>();
+    c.M = 1;
+    c.k = k;
+    c.H = H;
+    if (m.Fs) {
+        DecodeGemvArgs d{};
+        d.w = w.sh_down;
+        d.x = sh_act;
+        d.y = kv.moe_ys.as<float>();
+        d.N = H;
+        d.K = m.Fs;
+        Prof p("moe", s);
+        launch_decode_gemv(m.wt, DG_STORE, d, s);
+        c.ys = kv.moe_ys.as<float>();
+        c.sg = kv.moe_sg.as<float>();
+    }
+    Prof p("moe", s);
+    launch_combine(c, s);
 }
 
 // moe.rs:135-256 DecoderMlp::forward (Moe arm) for Mc rows: h += routed
-// experts (+ sigmoid-gated shared expert) of RMSNorm(h). Routing and the
-// combine run on the device; the per-expert row counts come back to the host
-// to size the per-expert GEMMs.
+// experts (+ sigmoid-gated shared expert) of RMSNorm(h). Routing, the row
+// grouping, both expert GEMMs and the combine run on the device with no host
+// round trip: the expert GEMMs are one grouped launch each over all experts,
+// their row ranges read from the router's offsets on the device, so the
+// block can be captured. A router failure is reported at the forward's end.
 void moe_block(Model &m, Kv &kv, LayerW &w, int Mc, hipStream_t s) {
     const Dt act = m.wt == DT_BF16 ? DT_SPLIT : DT_F32;
     const bool split = act == DT_SPLIT;
@@ -1713,18 +1760,10 @@ void moe_block(Model &m, Kv &kv, LayerW &w, int Mc, hipStream_t s) {
     }
     RouteArgs ra{kv.moe_logits.as<float>(), Mc, E, k, m.norm_topk ? 1 : 0,
                  kv.moe_sel.as<int32_t>(), kv.moe_w.as<float>(), kv.moe_offs.as<int32_t>(),
-                 kv.moe_perm.as<int32_t>(), kv.moe_slot.as<int32_t>()};
+                 kv.moe_perm.as<int32_t>(), kv.moe_slot.as<int32_t>(), moe_err_word(kv)};
     {
         Prof p("moe", s);
         launch_route(ra, s);
-    }
-    std::vector<int32_t> offs(E + 2);
-    ESP_HIP(hipMemcpyAsync(offs.data(), kv.moe_offs.p, (E + 2) * 4, hipMemcpyDeviceToHost, s));
-    ESP_HIP(hipStreamSynchronize(s));
-    if (offs[E + 1] == 2) fail(ESP_BACKEND, "non-finite expert router");
-    if (offs[E + 1] == 3) fail(ESP_BACKEND, "invalid top-k routing mass");
-    {
-        Prof p("moe", s);
         if (split) {
             const uint16_t *xs = kv.xn.as<uint16_t>();
             uint16_t *xd = kv.moe_x.as<uint16_t>();
@@ -1735,42 +1774,41 @@ void moe_block(Model &m, Kv &kv, LayerW &w, int Mc, hipStream_t s) {
             launch_gather_rows(DT_F32, kv.xn.p, kv.moe_perm.as<int32_t>(), R, H, kv.moe_x.p, s);
         }
     }
-    const size_t es = split ? 2 : 4;             // bytes per element of one plane
-    const size_t wes = dt_size(m.wt);
-    char *xh = (char *)kv.moe_x.p, *xl = split ? xh + (size_t)R * H * 2 : nullptr;
-    char *ah = (char *)kv.moe_act.p, *al = split ? ah + (size_t)R * m.Fe * 2 : nullptr;
-    for (int e = 0; e < E; ++e) {
-        int n = offs[e + 1] - offs[e];
-        if (!n) continue;
-        GemmArgs g{};
-        g.ws = kv.gemm_ws.as<float>();
-        g.ws_bytes = kv.gemm_ws.bytes;
-        g.a = xh + (size_t)offs[e] * H * es;
-        g.a_lo = split ? xl + (size_t)offs[e] * H * es : nullptr;
-        g.w = (char *)w.ex_gate + (size_t)e * m.Fe * H * wes;
-        g.w2 = (char *)w.ex_up + (size_t)e * m.Fe * H * wes;
-        g.c = ah + (size_t)offs[e] * m.Fe * es;
-        g.c_lo = split ? al + (size_t)offs[e] * m.Fe * es : nullptr;
-        g.M = n;
-        g.N = m.Fe;
-        g.K = H;
-        g.ldc = m.Fe;
-        {
-            Prof p("gemm", s);
-            launch_gemm(m.wt, GEMM_SWIGLU, g, s);
-        }
-        GemmArgs d{};
-        d.ws = kv.gemm_ws.as<float>();
-        d.ws_bytes = kv.gemm_ws.bytes;
-        d.a = g.c;
-        d.a_lo = g.c_lo;
-        d.w = (char *)w.ex_down + (size_t)e * H * m.Fe * wes;
-        d.c = kv.moe_y.as<float>() + (size_t)offs[e] * H;
-        d.M = n;
-        d.N = H;
-        d.K = m.Fe;
-        d.ldc = H;
+    const size_t es = split ? 2 : 4;  // bytes per element of one plane
+    char *xh = (char *)kv.moe_x.p, *ah = (char *)kv.moe_act.p;
+    GemmArgs g{};
+    g.ws = kv.gemm_ws.as<float>();
+    g.ws_bytes = kv.gemm_ws.bytes;
+    g.a = xh;
+    g.a_lo = split ? xh + (size_t)R * H * es : nullptr;
+    g.w = w.ex_gate;
+    g.w2 = w.ex_up;
+    g.c = ah;
+    g.c_lo = split ? ah + (size_t)R * m.Fe * es : nullptr;
+    g.M = R;
+    g.N = m.Fe;
+    g.K = H;
+    g.ldc = m.Fe;
+    g.grp_offs = kv.moe_offs.as<int32_t>();
+    g.grp_n = E;
+    g.grp_w_stride = (long long)m.Fe * H;
+    GemmArgs d{};
+    d.ws = kv.gemm_ws.as<float>();
+    d.ws_bytes = kv.gemm_ws.bytes;
+    d.a = g.c;
+    d.a_lo = g.c_lo;
+    d.w = w.ex_down;
+    d.c = kv.moe_y.as<float>();
+    d.M = R;
+    d.N = H;
+    d.K = m.Fe;
+    d.ldc = H;
+    d.grp_offs = g.grp_offs;
+    d.grp_n = E;
+    d.grp_w_stride = (long long)H * m.Fe;
+    {
         Prof p("gemm", s);
+        launch_gemm(m.wt, GEMM_SWIGLU, g, s);
         launch_gemm(m.wt, GEMM_STORE, d, s);
     }
     CombineArgs c{};

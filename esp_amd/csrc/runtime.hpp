@@ -111,6 +111,7 @@ struct Kv {
     DevMem tickets;  // zeroed counters for last-block merges (attention, head argmax)
     DevMem moe_logits, moe_sel, moe_w, moe_slot, moe_offs, moe_perm, moe_x, moe_y, moe_ys, moe_sg,
         moe_act;
+    DevMem moe_err;  // sticky router status of the forward in flight (0 = ok)
     int logits_rows = 0;  // rows valid in `logits`
     void *pinned = nullptr;
     size_t pinned_bytes = 0;
