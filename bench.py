@@ -618,7 +618,7 @@ def c4_bench(steps: int) -> dict:
     return res
 
 
-def c5_bench(steps: int, warmup: int = 2) -> dict:
+def c5_bench(steps: int, warmup: int = 2, kv_dtype: str = "f32") -> dict:
     """constrained decode on the 1B shape, 64 concurrent
     sequences at ~1024 context. Each step: every sequence whose index is
     congruent to the step mod 8 evaluates a forced 8-token block (a causal
@@ -634,7 +634,7 @@ def c5_bench(steps: int, warmup: int = 2) -> dict:
     B, ctx0, V = 64, 1024, cfg.vocab_size
     total = warmup + steps
     model = DecoderModel.synthetic(cfg, seed=1234, std=0.02, fmt="bf16")
-    kv = model.new_cache(B, ctx0 + 8 * total + 8)
+    kv = model.new_cache(B, ctx0 + 8 * total + 8, kv_dtype)
     model.forward_batch(kv, list(range(B)), [uniform_ids(5000 + i, ctx0, V) for i in range(B)],
                         want_logits=False)
     words = (V + 31) // 32
@@ -684,6 +684,7 @@ def c5_bench(steps: int, warmup: int = 2) -> dict:
            "ms_per_step": round(el / steps * 1e3, 3),
            "step_hbm_frac": round(step_bytes / (el / steps) / 1e9 / HBM_PEAK_GBS, 4),
            "step_bytes": step_bytes,
+           "kv_dtype": kv_dtype,
            "steps": steps}
     model.close()
     return res
@@ -822,7 +823,8 @@ def main():
         traffic_run()
         return
     only = {"c2": lambda: c2_bench(steps, args.warmup), "c4": lambda: c4_bench(steps),
-            "c5": lambda: c5_bench(16), "c5g": lambda: c5_grammar_bench(32),
+            "c5": lambda: {d: c5_bench(16, kv_dtype=d) for d in ("f32", "f16")},
+            "c5g": lambda: c5_grammar_bench(32),
             "stream": lambda: c3_stream_bench()}
     for leg, fn in only.items():
         if getattr(args, f"only_{leg}"):

@@ -91,6 +91,7 @@ def load():
         "esp_model_destroy": (C.c_int, [vp]),
         "esp_model_weight_bytes": (C.c_int, [vp, P(C.c_uint64)]),
         "esp_kv_create": (C.c_int, [vp, u32, u32, P(vp)]),
+        "esp_kv_create_ex": (C.c_int, [vp, u32, u32, u32, P(vp)]),
         "esp_kv_destroy": (C.c_int, [vp]),
         "esp_kv_reset": (C.c_int, [vp, u32]),
         "esp_kv_position": (C.c_int, [vp, u32, P(u32)]),
@@ -132,7 +133,8 @@ def load():
 
 
 EXPORTED = ["esp_last_error", "esp_version", "esp_model_load", "esp_model_create_synthetic",
-            "esp_model_destroy", "esp_model_weight_bytes", "esp_kv_create", "esp_kv_destroy",
+            "esp_model_destroy", "esp_model_weight_bytes", "esp_kv_create", "esp_kv_create_ex",
+            "esp_kv_destroy",
             "esp_kv_reset", "esp_kv_position", "esp_kv_stream", "esp_kv_logits", "esp_forward_last",
             "esp_forward_batch", "esp_pick", "esp_pick_constrained", "esp_pick_noalloc",
             "esp_generate_greedy",

@@ -19,7 +19,7 @@ Model *load_model(const esp_config *cfg, const uint8_t *bytes, size_t len,
                   const esp_lora *adapters, uint32_t n_adapters);
 Model *synthetic_model(const esp_config *cfg, uint64_t seed, float std, uint32_t lora_rank,
                        uint32_t lora_mask, float lora_a_std, float lora_b_std, float lora_scale);
-Kv *create_kv(Model *m, uint32_t batch, uint32_t max_ctx);
+Kv *create_kv(Model *m, uint32_t batch, uint32_t max_ctx, bool f16);
 void decode_step_dev(Model &m, Kv &kv, int seq, int max_t, int32_t *gen);
 void moe_check(Kv &kv);
 void launch_gen_step(const uint32_t *picked, int32_t *gen, hipStream_t s);
@@ -162,7 +162,7 @@ esp_status esp_stage_create(const esp_config *config, uint32_t first, uint32_t e
         st->model.reset(load_stage_model(config, first, end, source, options, shared, shared_len));
         st->head = shared != nullptr;
         const uint32_t ctx = max_ctx ? max_ctx : config->max_position_embeddings;
-        st->kv.reset(create_kv(st->model.get(), 1, ctx));
+        st->kv.reset(create_kv(st->model.get(), 1, ctx, false));
         *out = st.release();
     });
 }
@@ -214,7 +214,17 @@ esp_status esp_kv_create(esp_model *model, uint32_t batch, uint32_t max_ctx, esp
     return guard([&] {
         if (!out) fail(ESP_INVALID_REQUEST, "null output handle");
         *out = nullptr;
-        *out = (esp_kv *)create_kv((Model *)model, batch, max_ctx);
+        *out = (esp_kv *)create_kv((Model *)model, batch, max_ctx, false);
+    });
+}
+
+esp_status esp_kv_create_ex(esp_model *model, uint32_t batch, uint32_t max_ctx, uint32_t flags,
+                            esp_kv **out) {
+    return guard([&] {
+        if (!out) fail(ESP_INVALID_REQUEST, "null output handle");
+        *out = nullptr;
+        if (flags & ~(uint32_t)ESP_KV_F16) fail(ESP_INVALID_REQUEST, "kv: unknown flags");
+        *out = (esp_kv *)create_kv((Model *)model, batch, max_ctx, (flags & ESP_KV_F16) != 0);
     });
 }
 

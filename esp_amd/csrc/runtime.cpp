@@ -722,20 +722,22 @@ Model *synthetic_model(const esp_config *cfg, uint64_t seed, float std, uint32_t
 
 // ------------------------------------------------------------------- KV
 
-Kv *create_kv(Model *m, uint32_t batch, uint32_t max_ctx) {
+Kv *create_kv(Model *m, uint32_t batch, uint32_t max_ctx, bool f16) {
     if (!m) fail(ESP_MODEL_NOT_LOADED, "model not loaded");
     if (!batch || !max_ctx || max_ctx > m->cfg.max_position_embeddings)
         fail(ESP_INVALID_REQUEST, "kv: batch must be positive and max_ctx within "
                                   "max_position_embeddings");
+    if (f16 && m->wt != DT_BF16)
+        fail(ESP_UNSUPPORTED, "kv: half-precision keys and values need bf16 weights");
     std::unique_ptr<Kv> kv(new Kv());
     kv->model = m;
     kv->batch = (int)batch;
     kv->max_ctx = (int)max_ctx;
-    // bf16 weights: an f16 cache (11-bit significands: a CPU emulation of the
-    // f32 corridor at the 1B and 8B widths kept logits within 0.18 / 0.43 of
-    // the bf16-config tolerance, where bf16 keys and values broke it); the f32
-    // and packed formats keep f32 keys and values.
-    kv->dt = m->wt == DT_BF16 ? DT_F16 : DT_F32;
+    // f32 keys and values by default. The f16 cache (bf16 weights, on
+    // request) halves the bytes; a CPU emulation of the f32 corridor kept it
+    // within the bf16-config tolerance on 16-layer 1B-shape models (0.32-0.44
+    // of the bound) but not on 32-layer 8B-shape ones (1.3-1.6x).
+    kv->dt = f16 ? DT_F16 : DT_F32;
     kv->head_stride = (long long)max_ctx * m->hd;
     kv->half_stride = kv->head_stride * m->nkv;
     kv->layer_stride = kv->half_stride * 2;

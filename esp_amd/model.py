@@ -95,14 +95,20 @@ class LoraAdapter:
 class KvCache:
     """model.rs:671-681 KvCache for `batch` independent sequences."""
 
-    def __init__(self, model: "DecoderModel", batch: int, max_ctx: int):
+    def __init__(self, model: "DecoderModel", batch: int, max_ctx: int, kv_dtype: str = "f32"):
+        """kv_dtype "f32" (default) or "f16" (bf16 weights only: half the
+        bytes, outside the bf16 tolerance on deep models; esp_kv_create_ex)."""
         L = _lib.load()
         h = C.c_void_p()
-        _lib.check(L.esp_kv_create(model._h, batch, max_ctx, C.byref(h)))
+        if kv_dtype not in ("f32", "f16"):
+            raise InvalidRequest(f"kv_dtype must be f32 or f16, got {kv_dtype}")
+        _lib.check(L.esp_kv_create_ex(model._h, batch, max_ctx, 1 if kv_dtype == "f16" else 0,
+                                      C.byref(h)))
         self._h = h
         self.model = model
         self.batch = batch
         self.max_ctx = max_ctx
+        self.kv_dtype = kv_dtype
 
     def position(self, seq: int = 0) -> int:
         p = C.c_uint32()
@@ -238,9 +244,10 @@ class DecoderModel:
         _lib.check(_lib.load().esp_model_weight_bytes(self._h, C.byref(n)))
         return n.value
 
-    def new_cache(self, batch: int = 1, max_ctx: Optional[int] = None) -> KvCache:
+    def new_cache(self, batch: int = 1, max_ctx: Optional[int] = None,
+                  kv_dtype: str = "f32") -> KvCache:
         """model.rs:476-483"""
-        return KvCache(self, batch, max_ctx or self.config.max_position_embeddings)
+        return KvCache(self, batch, max_ctx or self.config.max_position_embeddings, kv_dtype)
 
     def try_forward_cached_last(self, ids: Sequence[int], cache: KvCache,
                                 seq: int = 0) -> np.ndarray:

@@ -153,6 +153,16 @@ esp_status esp_model_weight_bytes(const esp_model *model, uint64_t *bytes);
  * max_position_embeddings). Contiguous per-sequence f32 keys and values
  * (every weight format). */
 esp_status esp_kv_create(esp_model *model, uint32_t batch, uint32_t max_ctx, esp_kv **out);
+/* esp_kv_create with options. ESP_KV_F16 (bf16 weights only, else
+ * ESP_UNSUPPORTED): keys and values stored as IEEE half, half the cache
+ * bytes. No reference counterpart: the reference's cache holds the
+ * activation dtype. Half precision stays within the bf16-config tolerance
+ * of the f32 corridor on 16-layer 1B-shape models but not on 32-layer
+ * 8B-shape ones (CPU emulation of random-init models), so it is for
+ * callers that trade that margin for cache capacity and bandwidth. */
+#define ESP_KV_F16 1u
+esp_status esp_kv_create_ex(esp_model *model, uint32_t batch, uint32_t max_ctx, uint32_t flags,
+                            esp_kv **out);
 esp_status esp_kv_destroy(esp_kv *kv);
 /* Forget sequence `seq` (or every sequence when seq == UINT32_MAX). */
 esp_status esp_kv_reset(esp_kv *kv, uint32_t seq);

@@ -81,7 +81,8 @@ def test_generate_eos_and_callback_stop():
     assert got == full[:3] and seen == full[:3]
 
 
-def test_bf16_c2_slice_matches_oracle():
+@pytest.mark.parametrize("kv_dtype", ["f32", "f16"])
+def test_bf16_c2_slice_matches_oracle(kv_dtype):
     """Llama-3.2-1B shape (hidden 2048, 32q/8kv, hd 64, ffn 8192, vocab 128256,
     theta 5e5), 2-layer slice, bf16 weights: prefill 48 tokens + 6 decode steps
     teacher-forced; logits within 2e-2 relative + 1e-2 absolute."""
@@ -92,7 +93,7 @@ def test_bf16_c2_slice_matches_oracle():
     prompt = synth.uniform_ids(5, 48, cfg.vocab_size)
     model = DecoderModel.from_bytes(cfg, blob, "bf16")
     ref = oracle.OracleModel(cfg, tensors)
-    kv, rkv = model.new_cache(1, 128), ref.new_cache(128)
+    kv, rkv = model.new_cache(1, 128, kv_dtype), ref.new_cache(128)
     got = model.try_forward_cached_last(prompt, kv)
     want = ref.forward_last(rkv, prompt)
     assert _close_bf16(got, want), float(np.abs(got - want).max())
@@ -331,7 +332,8 @@ def test_bf16_prefill_odd_shapes_and_moe():
 
 
 @pytest.mark.parametrize("variant", ["llama_hd64", "gqa_hd128", "window_hd64"])
-def test_bf16_flash_prefill_chunks_match_oracle(variant):
+@pytest.mark.parametrize("kv_dtype", ["f32", "f16"])
+def test_bf16_flash_prefill_chunks_match_oracle(variant, kv_dtype):
     """MFMA prefill attention (bf16 format): a 140-token prefill, then a
     45-token block over the warm cache (rows start at position 140), then
     decode; logits within the bf16 tolerance of the oracle."""
@@ -345,7 +347,7 @@ def test_bf16_flash_prefill_chunks_match_oracle(variant):
     tensors = synth.make_tensors(cfg, 51, "bf16")
     model = DecoderModel.from_bytes(cfg, st.dump(tensors), "bf16")
     ref = oracle.OracleModel(cfg, tensors)
-    kv, rkv = model.new_cache(1, 256), ref.new_cache(256)
+    kv, rkv = model.new_cache(1, 256, kv_dtype), ref.new_cache(256)
     for block in (synth.uniform_ids(1, 140, 900), synth.uniform_ids(2, 45, 900), [7], [8]):
         got = model.try_forward_cached_last(block, kv)
         want = ref.forward_last(rkv, block)
@@ -369,7 +371,8 @@ def test_bf16_long_prefill_wide_gemm_tiles():
         assert _close_bf16(got, want), (len(block), float(np.abs(got - want).max()))
 
 
-def test_bf16_long_context_decode_splits():
+@pytest.mark.parametrize("kv_dtype", ["f32", "f16"])
+def test_bf16_long_context_decode_splits(kv_dtype):
     """Decode over 8.3k cached keys (hd 128, 4 query heads on one kv head):
     the key range is cut into one split per CU (up to 128 splits of at least
     65 keys; past 160 keys a split takes two load chunks) whose partials the last block merges;
@@ -379,7 +382,7 @@ def test_bf16_long_context_decode_splits():
     tensors = synth.make_tensors(cfg, 71, "bf16")
     model = DecoderModel.from_bytes(cfg, st.dump(tensors), "bf16")
     ref = oracle.OracleModel(cfg, tensors)
-    kv, rkv = model.new_cache(1, 8320), ref.new_cache(8320)
+    kv, rkv = model.new_cache(1, 8320, kv_dtype), ref.new_cache(8320)
     got = model.try_forward_cached_last(synth.uniform_ids(4, 8300, 500), kv)
     want = ref.forward_last(rkv, synth.uniform_ids(4, 8300, 500))
     assert _close_bf16(got, want), float(np.abs(got - want).max())

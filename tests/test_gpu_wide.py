@@ -150,7 +150,8 @@ def _bitmask(rng, n, vocab, frac):
 
 
 @pytest.mark.timeout(600)
-def test_c5_width_batch_masks_and_sampling():
+@pytest.mark.parametrize("kv_dtype", ["f32", "f16"])
+def test_c5_width_batch_masks_and_sampling(kv_dtype):
     """Llama-3.2-1B width (hidden 2048, 32 q / 8 kv, head_dim 64, ffn 8192,
     vocab 128256, tied head), 64 sequences: batched prompts, then one step
     of 56 decode rows + 8 forced 8-token blocks in the same forward, then a
@@ -166,8 +167,8 @@ def test_c5_width_batch_masks_and_sampling():
     model = DecoderModel.from_bytes(cfg, st.dump_buffer(tensors), "bf16")
     ref = oracle.OracleModel(cfg, tensors)
     prompts = [synth.uniform_ids(900 + i, 40 + (i * 37) % 72, cfg.vocab_size) for i in range(n)]
-    kv = model.new_cache(n, 256)
-    print("c5 width: batched prompts", flush=True)
+    kv = model.new_cache(n, 256, kv_dtype)
+    print(f"c5 width: batched prompts ({kv_dtype} cache)", flush=True)
     got = model.forward_batch(kv, list(range(n)), prompts)
     rkvs = [ref.new_cache(256) for _ in range(n)]
     for i in range(n):
