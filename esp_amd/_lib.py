@@ -57,8 +57,13 @@ LAYER_READ_FN = C.CFUNCTYPE(C.c_int, C.c_void_p, C.c_uint32, C.c_uint64, C.c_voi
                             C.c_uint64, C.POINTER(C.c_uint64))
 
 
+EXPERT_READ_FN = C.CFUNCTYPE(C.c_int, C.c_void_p, C.c_uint32, C.c_uint32, C.c_uint64,
+                             C.c_void_p, C.c_uint64, C.POINTER(C.c_uint64))
+
+
 class EspLayerSource(C.Structure):
-    _fields_ = [("read_layer", LAYER_READ_FN), ("user", C.c_void_p)]
+    _fields_ = [("read_layer", LAYER_READ_FN), ("user", C.c_void_p),
+                ("read_expert", EXPERT_READ_FN)]
 
 
 class EspStreamingStats(C.Structure):
@@ -66,7 +71,9 @@ class EspStreamingStats(C.Structure):
                 ("layer_reads", C.c_uint64), ("encoded_bytes_read", C.c_uint64),
                 ("largest_encoded_layer", C.c_uint64), ("cache_hits", C.c_uint64),
                 ("cache_misses", C.c_uint64), ("retained_payload_bytes", C.c_uint64),
-                ("payload_budget_bytes", C.c_uint64), ("cached_layers", C.c_uint64)]
+                ("payload_budget_bytes", C.c_uint64), ("cached_layers", C.c_uint64),
+                ("expert_reads", C.c_uint64), ("expert_encoded_bytes_read", C.c_uint64),
+                ("largest_encoded_expert", C.c_uint64)]
 
 
 _lib = None

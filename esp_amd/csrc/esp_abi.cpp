@@ -583,8 +583,10 @@ esp_status esp_generate_greedy(esp_model *model, esp_kv *kv, uint32_t seq, const
         std::shared_ptr<Streamer> keep = m.st;
         std::unique_lock<std::recursive_mutex> st_lk;
         if (keep) st_lk = std::unique_lock<std::recursive_mutex>(keep->mu);
+        // (routed experts are read per forward even for cached layers, so such
+        // a model keeps the host-driven loop)
         std::shared_ptr<Streamer> cached_st =
-            keep && (int)keep->cache.size() == m.L ? keep : nullptr;
+            keep && (int)keep->cache.size() == m.L && !m.E ? keep : nullptr;
         const uint64_t hits0 = cached_st ? cached_st->hits : 0;
         if (keep && !cached_st) {
             // Streamed layers are read between kernels: one host-driven step

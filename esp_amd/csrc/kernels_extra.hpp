@@ -42,7 +42,7 @@ struct CombineArgs {
 };
 void launch_combine(const CombineArgs &a, hipStream_t s);
 
-void moe_block(Model &m, Kv &kv, LayerW &w, int Mc, hipStream_t s);
+void moe_block(Model &m, Kv &kv, LayerW &w, int Mc, hipStream_t s, int l);
 // one decode row through the routed experts without host round trips
 bool moe_decode_ok(const Model &m);
 void moe_decode(Model &m, Kv &kv, LayerW &w, hipStream_t s);

@@ -527,9 +527,6 @@ Model *load_streamed_model(const esp_config *cfg, const uint8_t *shared, size_t 
         if (kv.first != "model.embed_tokens.weight" && kv.first != "model.norm.weight" &&
             kv.first != "lm_head.weight")
             fail(ESP_INVALID_WEIGHTS, "unexpected tensor in shared artifact");
-    if (m.E)
-        fail(ESP_UNSUPPORTED, "native expert streaming: routed-expert layers are not streamed by "
-                              "this library");
     check_packed(m, 0);
     // the geometry every staged block binds (scratch buffers are sized from it)
     for (auto &w : m.layers) w.qkv_rows = m.qw + 2 * m.kvw;
@@ -567,9 +564,6 @@ Model *load_stage_model(const esp_config *cfg, uint32_t first, uint32_t end,
     std::unique_ptr<Model> mp(new Model());
     Model &m = *mp;
     init_model_shape(m, c);
-    if (m.E)
-        fail(ESP_UNSUPPORTED, "native expert streaming: routed-expert layers are not streamed by "
-                              "this library");
     check_packed(m, 0);
     for (auto &w : m.layers) w.qkv_rows = m.qw + 2 * m.kvw;
     if (shared) {  // stage.rs:384-413 with_output: the final range owns norm and head
@@ -1033,8 +1027,8 @@ static void run_layer_decode(Model &m, Kv &kv, const Rows &rows, LayerW &w, int 
     };
     resid("gemv_o", w.o, w.o_s, kv.attn.as<float>(), w.o_bias, H, m.qw);
     if (w.moe) {
-        if (moe_decode_ok(m)) moe_decode(m, kv, w, s);
-        else moe_block(m, kv, w, 1, s);
+        if (moe_decode_ok(m) && w.ex_gate) moe_decode(m, kv, w, s);
+        else moe_block(m, kv, w, 1, s, l);
         return;
     }
     if (decode_gemv_ok(H)) {
@@ -1268,7 +1262,7 @@ static void run_layers(Model &m, Kv &kv, const Rows &rows, int Mc, int max_t, in
         }
         // ---- MLP block (layer.rs:147-151)
         if (w.moe) {
-            moe_block(m, kv, w, Mc, s);
+            moe_block(m, kv, w, Mc, s, l);
         } else if (single) {
             GemvArgs g{};
             g.w = w.gate;
@@ -1729,7 +1723,7 @@ void moe_decode(Model &m, Kv &kv, LayerW &w, hipStream_t s) {
 // round trip: the expert GEMMs are one grouped launch each over all experts,
 // their row ranges read from the router's offsets on the device, so the
 // block can be captured. A router failure is reported at the forward's end.
-void moe_block(Model &m, Kv &kv, LayerW &w, int Mc, hipStream_t s) {
+void moe_block(Model &m, Kv &kv, LayerW &w, int Mc, hipStream_t s, int l) {
     const Dt act = m.wt == DT_BF16 ? DT_SPLIT : DT_F32;
     const bool split = act == DT_SPLIT;
     const int H = m.H, E = m.E, k = m.topk, R = Mc * k;
@@ -1808,10 +1802,46 @@ void moe_block(Model &m, Kv &kv, LayerW &w, int Mc, hipStream_t s) {
     d.grp_offs = g.grp_offs;
     d.grp_n = E;
     d.grp_w_stride = (long long)H * m.Fe;
-    {
+    if (w.ex_gate) {
         Prof p("gemm", s);
         launch_gemm(m.wt, GEMM_SWIGLU, g, s);
         launch_gemm(m.wt, GEMM_STORE, d, s);
+    } else {
+        // Streamed experts (moe.rs:183-243): the router's choice comes back
+        // to the host, then only the chosen experts are read, in ascending
+        // order, each staged on the copy stream while the previous one's
+        // GEMMs run over its own rows.
+        if (!m.st) fail(ESP_BACKEND, "routed layer without experts");
+        std::vector<int32_t> offs(E + 2);
+        ESP_HIP(hipMemcpyAsync(offs.data(), kv.moe_offs.p, (size_t)(E + 2) * 4,
+                               hipMemcpyDeviceToHost, s));
+        ESP_HIP(hipStreamSynchronize(s));
+        moe_fail(offs[E + 1]);
+        for (int e = 0; e < E; ++e) {
+            const int n = offs[e + 1] - offs[e];
+            if (n <= 0) continue;
+            const ExpertW x = stream_expert(m, s, l, e);
+            GemmArgs ge = g, de = d;
+            ge.grp_offs = de.grp_offs = nullptr;
+            ge.a = xh + (size_t)offs[e] * H * es;
+            ge.a_lo = split ? (char *)g.a_lo + (size_t)offs[e] * H * es : nullptr;
+            ge.w = x.gate;
+            ge.w2 = x.up;
+            ge.c = ah + (size_t)offs[e] * m.Fe * es;
+            ge.c_lo = split ? (char *)g.c_lo + (size_t)offs[e] * m.Fe * es : nullptr;
+            ge.M = n;
+            de.a = ge.c;
+            de.a_lo = ge.c_lo;
+            de.w = x.down;
+            de.c = kv.moe_y.as<float>() + (size_t)offs[e] * H;
+            de.M = n;
+            {
+                Prof p("gemm", s);
+                launch_gemm(m.wt, GEMM_SWIGLU, ge, s);
+                launch_gemm(m.wt, GEMM_STORE, de, s);
+            }
+            stream_expert_release(m, s);
+        }
     }
     CombineArgs c{};
     c.y = kv.moe_y.as<float>();

@@ -26,8 +26,11 @@ Streamer::~Streamer() {
     if (copy) (void)hipStreamSynchronize(copy);
     for (int i = 0; i < 2; ++i) {
         if (stage[i]) (void)hipHostFree(stage[i]);
+        if (estage[i]) (void)hipHostFree(estage[i]);
         if (copied[i]) (void)hipEventDestroy(copied[i]);
         if (freed[i]) (void)hipEventDestroy(freed[i]);
+        if (ecopied[i]) (void)hipEventDestroy(ecopied[i]);
+        if (efreed[i]) (void)hipEventDestroy(efreed[i]);
     }
     if (copy) (void)hipStreamDestroy(copy);
 }
@@ -42,7 +45,7 @@ static size_t proj_bytes(const Model &m, uint64_t rows, uint64_t cols, size_t *s
     return *scales_at + n / 32 * 4;
 }
 
-static BlockLayout block_layout(const Model &m) {
+static BlockLayout block_layout(const Model &m, bool moe) {
     BlockLayout b;
     size_t o = 0;
     auto f32 = [&](size_t n) {
@@ -70,16 +73,36 @@ static BlockLayout block_layout(const Model &m) {
         b.q_norm = f32(m.hd);
         b.k_norm = f32(m.hd);
     }
-    b.gate = proj(m.F, H, b.gate_s);
-    b.up = proj(m.F, H, b.up_s);
-    b.down = proj(H, m.F, b.down_s);
+    if (!moe) {
+        b.gate = proj(m.F, H, b.gate_s);
+        b.up = proj(m.F, H, b.up_s);
+        b.down = proj(H, m.F, b.down_s);
+    } else {  // routed-expert core: no packed formats (refused at load)
+        size_t unused = 0;
+        b.router = proj(m.E, H, unused);
+        if (m.Fs) {
+            b.shared_gate = proj(1, H, unused);
+            b.sh_gate = proj(m.Fs, H, unused);
+            b.sh_up = proj(m.Fs, H, unused);
+            b.sh_down = proj(H, m.Fs, unused);
+        }
+    }
     b.total = o;
     return b;
+}
+
+// Bytes of one expert block: gate [Fe, H], up [Fe, H], down [H, Fe], each
+// region 256-byte aligned.
+static size_t expert_part(const Model &m) { return up256((size_t)m.Fe * m.H * dt_size(m.wt)); }
+
+static const BlockLayout &layout_of(const Model &m, const Streamer &st, int l) {
+    return m.layers[l].moe ? st.lay_moe : st.lay;
 }
 
 static LayerW bind(const Model &m, const BlockLayout &b, char *base, int l) {
     LayerW w;
     w.window = m.layers[l].window;
+    w.moe = m.layers[l].moe;
     const bool pk = dt_packed(m.wt);
     w.in_norm = (float *)(base + b.in_norm);
     w.post_norm = (float *)(base + b.post_norm);
@@ -91,6 +114,16 @@ static LayerW bind(const Model &m, const BlockLayout &b, char *base, int l) {
     if (m.cfg.qk_norm) {
         w.q_norm = (float *)(base + b.q_norm);
         w.k_norm = (float *)(base + b.k_norm);
+    }
+    if (w.moe) {  // experts are read per forward (ex_* stay null)
+        w.router = base + b.router;
+        if (m.Fs) {
+            w.shared_gate = base + b.shared_gate;
+            w.sh_gate = base + b.sh_gate;
+            w.sh_up = base + b.sh_up;
+            w.sh_down = base + b.sh_down;
+        }
+        return w;
     }
     w.gate = base + b.gate;
     w.up = base + b.up;
@@ -105,17 +138,28 @@ static LayerW bind(const Model &m, const BlockLayout &b, char *base, int l) {
     return w;
 }
 
-// loader.rs:48-85 layer_core_tensor_names for a dense layer.
-static std::vector<std::string> core_names(const Model &m) {
+// loader.rs:48-85 layer_core_tensor_names: a routed-expert layer's core
+// holds the router and the shared expert (when the configuration declares
+// one, as the resident loader requires) in place of the dense MLP; its
+// experts live in separate artifacts.
+static std::vector<std::string> core_names(const Model &m, bool moe) {
     std::vector<std::string> n = {"input_layernorm.weight",
                                   "post_attention_layernorm.weight",
                                   "self_attn.q_proj.weight",
                                   "self_attn.k_proj.weight",
                                   "self_attn.v_proj.weight",
-                                  "self_attn.o_proj.weight",
-                                  "mlp.gate_proj.weight",
-                                  "mlp.up_proj.weight",
-                                  "mlp.down_proj.weight"};
+                                  "self_attn.o_proj.weight"};
+    if (!moe) {
+        for (const char *x : {"mlp.gate_proj.weight", "mlp.up_proj.weight", "mlp.down_proj.weight"})
+            n.push_back(x);
+    } else {
+        n.push_back("mlp.gate.weight");
+        if (m.Fs)
+            for (const char *x : {"mlp.shared_expert_gate.weight", "mlp.shared_expert.gate_proj.weight",
+                                  "mlp.shared_expert.up_proj.weight",
+                                  "mlp.shared_expert.down_proj.weight"})
+                n.push_back(x);
+    }
     if (m.cfg.qkv_bias)
         for (const char *s : {"self_attn.q_proj.bias", "self_attn.k_proj.bias", "self_attn.v_proj.bias"})
             n.push_back(s);
@@ -157,9 +201,10 @@ struct Plan {
 static Plan plan_layer(const Model &m, const Streamer &st,
                        const std::map<std::string, StTensor> &t, int l) {
     const std::string p = "model.layers." + std::to_string(l) + ".";
+    const bool moe = m.layers[l - st.first].moe;
     {
         std::set<std::string> want;
-        for (auto &s : core_names(m)) want.insert(p + s);
+        for (auto &s : core_names(m, moe)) want.insert(p + s);
         bool same = want.size() == t.size();
         for (auto &kv : t) same = same && want.count(kv.first);
         if (!same)
@@ -176,7 +221,7 @@ static Plan plan_layer(const Model &m, const Streamer &st,
         if (pl.payload > UINT64_MAX - n) fail(ESP_INVALID_WEIGHTS, "layer payload size overflow");
         pl.payload += n;
     }
-    const BlockLayout &b = st.lay;
+    const BlockLayout &b = moe ? st.lay_moe : st.lay;
     // an f32 region: in place when the artifact holds f32, else widened
     // from the raw area
     auto f32_region = [&](const StTensor &s, uint64_t n, size_t dst, int tag) {
@@ -250,10 +295,56 @@ static Plan plan_layer(const Model &m, const Streamer &st,
         vec("self_attn.q_norm.weight", (uint64_t)m.hd, b.q_norm);
         vec("self_attn.k_norm.weight", (uint64_t)m.hd, b.k_norm);
     }
-    projs({{"mlp.gate_proj.weight", (uint64_t)m.F}}, H, b.gate, b.gate_s);
-    projs({{"mlp.up_proj.weight", (uint64_t)m.F}}, H, b.up, b.up_s);
-    projs({{"mlp.down_proj.weight", H}}, (uint64_t)m.F, b.down, b.down_s);
+    if (!moe) {
+        projs({{"mlp.gate_proj.weight", (uint64_t)m.F}}, H, b.gate, b.gate_s);
+        projs({{"mlp.up_proj.weight", (uint64_t)m.F}}, H, b.up, b.up_s);
+        projs({{"mlp.down_proj.weight", H}}, (uint64_t)m.F, b.down, b.down_s);
+    } else {
+        projs({{"mlp.gate.weight", (uint64_t)m.E}}, H, b.router, 0);
+        if (m.Fs) {
+            projs({{"mlp.shared_expert_gate.weight", 1}}, H, b.shared_gate, 0);
+            projs({{"mlp.shared_expert.gate_proj.weight", (uint64_t)m.Fs}}, H, b.sh_gate, 0);
+            projs({{"mlp.shared_expert.up_proj.weight", (uint64_t)m.Fs}}, H, b.sh_up, 0);
+            projs({{"mlp.shared_expert.down_proj.weight", H}}, (uint64_t)m.Fs, b.sh_down, 0);
+        }
+    }
     if ((int)pl.checks.size() > kStreamMaxChecks) fail(ESP_BACKEND, "layer plan: too many regions");
+    return pl;
+}
+
+// An expert artifact (loader.rs:137-168 load_expert): exactly the three
+// projections of expert e of layer l ([Fe, H], [Fe, H], [H, Fe]), admitted
+// like the layer's own projections; tag 3 * e + part.
+static Plan plan_expert(const Model &m, const std::map<std::string, StTensor> &t, int l, int e) {
+    const std::string p = "model.layers." + std::to_string(l) + ".mlp.experts." + std::to_string(e) + ".";
+    static const char *parts[3] = {"gate_proj.weight", "up_proj.weight", "down_proj.weight"};
+    {
+        bool same = t.size() == 3;
+        for (const char *x : parts) same = same && t.count(p + x);
+        if (!same) fail(ESP_INVALID_WEIGHTS, "expert artifact names disagree with layer/expert selection");
+    }
+    Plan pl;
+    const uint64_t H = m.H, Fe = m.Fe;
+    const size_t part = expert_part(m);
+    for (int i = 0; i < 3; ++i) {
+        const std::string name = p + parts[i];
+        const uint64_t rows = i < 2 ? Fe : H, cols = i < 2 ? H : Fe, n = rows * cols;
+        const StTensor &s = expect_tensor(t, name, {rows, cols});
+        check_tensor_dtype(m, name, s, false);
+        const size_t dst = (size_t)i * part;
+        if (m.wt == DT_BF16) {
+            pl.pieces.push_back({s.data, n * 2, dst, false});
+            pl.checks.push_back({dst, 0, n, SC_BF16, 3 * e + i});
+        } else if (s.dtype == "F32") {
+            pl.pieces.push_back({s.data, n * 4, dst, false});
+            pl.checks.push_back({dst, 0, n, SC_F32, 3 * e + i});
+        } else {  // f32 model, half-precision artifact: widened on the device
+            pl.pieces.push_back({s.data, s.bytes, pl.raw_used, true});
+            pl.checks.push_back({pl.raw_used, dst, n, s.dtype == "BF16" ? SC_BF16_F32 : SC_F16_F32,
+                                 3 * e + i});
+            pl.raw_used = up256(pl.raw_used + s.bytes);
+        }
+    }
     return pl;
 }
 
@@ -263,12 +354,29 @@ void streamer_init(Model &m, const esp_layer_source &src, const esp_streaming_op
     st->first = first;
     st->src = src;
     st->opt = opt;
-    st->lay = block_layout(m);
+    st->lay = block_layout(m, false);
+    st->lay_moe = block_layout(m, true);
+    size_t widest = 0, f32e = 0;
+    for (int l = 0; l < m.L; ++l) {
+        const BlockLayout &b = layout_of(m, *st, l);
+        widest = std::max(widest, b.total);
+        f32e = std::max(f32e, b.f32_elems);
+    }
     // The device block is at least as wide as any admissible encoding of
     // its tensors, so a valid artifact fits in the block size plus its
     // header.
-    st->stage_cap = (size_t)std::min<uint64_t>(opt.max_layer_bytes, st->lay.total + (1u << 20));
-    st->raw_cap = st->lay.f32_elems * 2 + kStreamMaxChecks * 256;
+    st->stage_cap = (size_t)std::min<uint64_t>(opt.max_layer_bytes, widest + (1u << 20));
+    st->raw_cap = f32e * 2 + kStreamMaxChecks * 256;
+    if (m.E) {
+        st->eblock_bytes = 3 * expert_part(m);
+        st->estage_cap = (size_t)std::min<uint64_t>(opt.max_layer_bytes, st->eblock_bytes + (1u << 20));
+        st->eraw_cap = m.wt == DT_F32 ? 3 * expert_part(m) / 2 + 3 * 256 : 0;
+        for (int i = 0; i < 2; ++i) {
+            ESP_HIP(hipEventCreateWithFlags(&st->ecopied[i], hipEventDisableTiming));
+            ESP_HIP(hipEventCreateWithFlags(&st->efreed[i], hipEventDisableTiming));
+        }
+        st->ebad.alloc((size_t)m.L * 4);
+    }
     ESP_HIP(hipStreamCreateWithFlags(&st->copy, hipStreamNonBlocking));
     for (int i = 0; i < 2; ++i) {
         ESP_HIP(hipEventCreateWithFlags(&st->copied[i], hipEventDisableTiming));
@@ -277,6 +385,8 @@ void streamer_init(Model &m, const esp_layer_source &src, const esp_streaming_op
     st->bad.alloc((size_t)m.L * 4);
     std::vector<int> clean(m.L, INT_MAX);
     ESP_HIP(hipMemcpy(st->bad.p, clean.data(), (size_t)m.L * 4, hipMemcpyHostToDevice));
+    if (st->ebad.p)
+        ESP_HIP(hipMemcpy(st->ebad.p, clean.data(), (size_t)m.L * 4, hipMemcpyHostToDevice));
     m.st = st;
 }
 
@@ -312,13 +422,15 @@ static LayerW stage_layer(Model &m, hipStream_t compute, int l, DevMem *perm, ui
         fail(ESP_INVALID_WEIGHTS, "layer " + std::to_string(gl) + ": " + e.msg);
     }
     Plan pl = plan_layer(m, st, t, gl);
-    if (st.tag_names.empty()) {
-        st.tag_names = pl.tags;
-        st.tag_scales = pl.tag_scales;
+    const int kind = m.layers[l].moe ? 1 : 0;
+    if (st.tag_names[kind].empty()) {
+        st.tag_names[kind] = pl.tags;
+        st.tag_scales[kind] = pl.tag_scales;
     }
     *payload = pl.payload;
-    if (perm) perm->alloc(st.lay.total);
-    else if (!st.block[sl].p) st.block[sl].alloc(st.lay.total);
+    const BlockLayout &lay = layout_of(m, st, l);
+    if (perm) perm->alloc(lay.total);
+    else if (!st.block[sl].p) st.block[sl].alloc(std::max(st.lay.total, st.lay_moe.total));
     char *base = (char *)(perm ? perm->p : st.block[sl].p);
     if (pl.raw_used && !st.raw[sl].p) st.raw[sl].alloc(st.raw_cap);
     char *raw = (char *)st.raw[sl].p;
@@ -343,7 +455,73 @@ static LayerW stage_layer(Model &m, hipStream_t compute, int l, DevMem *perm, ui
     launch_stream_check(c, st.bad.as<int>() + l, compute);
     st.pending = true;
     st.cur_slot = sl;
-    return bind(m, st.lay, base, l);
+    return bind(m, lay, base, l);
+}
+
+ExpertW stream_expert(Model &m, hipStream_t compute, int l, int e) {
+    Streamer &st = *m.st;
+    const int gl = l + st.first;
+    if (!st.src.read_expert) fail(ESP_INVALID_WEIGHTS, "layer source has no expert reader");
+    const int sl = st.enext;
+    st.enext ^= 1;
+    ESP_HIP(hipEventSynchronize(st.ecopied[sl]));  // this staging buffer's last transfer is done
+    if (!st.estage[sl])
+        ESP_HIP(hipHostMalloc((void **)&st.estage[sl], st.estage_cap, hipHostMallocDefault));
+    uint64_t len = 0;
+    const int rc = (int)st.src.read_expert(st.src.user, (uint32_t)gl, (uint32_t)e,
+                                           st.opt.max_layer_bytes, st.estage[sl], st.estage_cap, &len);
+    if (rc != ESP_OK)
+        fail(rc > 0 && rc <= ESP_UNSUPPORTED ? (esp_status)rc : ESP_BACKEND,
+             "layer " + std::to_string(gl) + " expert " + std::to_string(e) +
+                 ": expert source read failed");
+    if (len > st.opt.max_layer_bytes)  // moe.rs:214-218
+        fail(ESP_INVALID_WEIGHTS, "expert source exceeded artifact budget");
+    if (len > st.estage_cap)
+        fail(ESP_INVALID_WEIGHTS, "layer " + std::to_string(gl) + " expert " + std::to_string(e) +
+                                      ": artifact exceeds the declared expert's encoded size");
+    ++st.ereads;
+    st.ebytes += len;
+    st.elargest = std::max<uint64_t>(st.elargest, len);
+    std::map<std::string, StTensor> t;
+    try {
+        t = parse_safetensors(st.estage[sl], (size_t)len);
+    } catch (const Error &err) {
+        fail(ESP_INVALID_WEIGHTS, "layer " + std::to_string(gl) + " expert " + std::to_string(e) +
+                                      ": " + err.msg);
+    }
+    Plan pl = plan_expert(m, t, gl, e);
+    if (!st.eblock[sl].p) st.eblock[sl].alloc(st.eblock_bytes);
+    if (pl.raw_used && !st.eraw[sl].p) st.eraw[sl].alloc(st.eraw_cap);
+    char *base = (char *)st.eblock[sl].p, *raw = (char *)st.eraw[sl].p;
+    // the transfer waits until the expert that last used this slot is done
+    ESP_HIP(hipStreamWaitEvent(st.copy, st.efreed[sl], 0));
+    for (const Piece &pc : pl.pieces)
+        ESP_HIP(hipMemcpyAsync((pc.raw ? raw : base) + pc.dst, pc.src, pc.bytes,
+                               hipMemcpyHostToDevice, st.copy));
+    ESP_HIP(hipEventRecord(st.ecopied[sl], st.copy));
+    ESP_HIP(hipStreamWaitEvent(compute, st.ecopied[sl], 0));
+    StreamChecks c{};
+    c.n = (int)pl.checks.size();
+    for (int i = 0; i < c.n; ++i) {
+        const PlanCheck &k = pl.checks[i];
+        const bool widen = k.op == SC_BF16_F32 || k.op == SC_F16_F32;
+        c.d[i].src = widen ? (const void *)(raw + k.src) : (const void *)(base + k.src);
+        c.d[i].dst = widen ? (float *)(base + k.dst) : nullptr;
+        c.d[i].n = k.n;
+        c.d[i].op = k.op;
+        c.d[i].tag = k.tag;
+    }
+    launch_stream_check(c, st.ebad.as<int>() + l, compute);
+    st.pending = true;
+    st.ecur = sl;
+    const size_t part = expert_part(m);
+    return ExpertW{base, base + part, base + 2 * part};
+}
+
+void stream_expert_release(Model &m, hipStream_t compute) {
+    Streamer &st = *m.st;
+    if (st.ecur >= 0) (void)hipEventRecord(st.efreed[st.ecur], compute);
+    st.ecur = -1;
 }
 
 LayerW stream_acquire(Model &m, Kv &kv, int l) {
@@ -362,10 +540,11 @@ LayerW stream_acquire(Model &m, Kv &kv, int l) {
     uint64_t payload = 0;
     LayerW w = stage_layer(m, kv.stream, l, nullptr, &payload);
     if (st.cache_on && st.cache.size() < 128 && payload <= st.budget - st.payload) {
-        std::unique_ptr<DevMem> mem(new DevMem(st.lay.total));
-        ESP_HIP(hipMemcpyAsync(mem->p, st.block[st.cur_slot].p, st.lay.total,
+        const BlockLayout &lay = layout_of(m, st, l);
+        std::unique_ptr<DevMem> mem(new DevMem(lay.total));
+        ESP_HIP(hipMemcpyAsync(mem->p, st.block[st.cur_slot].p, lay.total,
                                hipMemcpyDeviceToDevice, kv.stream));
-        LayerW kept = bind(m, st.lay, (char *)mem->p, l);
+        LayerW kept = bind(m, lay, (char *)mem->p, l);
         st.payload += payload;
         StreamEntry e;
         e.layer = l;
@@ -388,9 +567,19 @@ void stream_check(Model &m) {
     Streamer &st = *m.st;
     if (!st.pending) return;
     st.pending = false;
-    std::vector<int> bad(m.L);
+    std::vector<int> bad(m.L), ebad(m.L, INT_MAX);
     ESP_HIP(hipMemcpy(bad.data(), st.bad.p, (size_t)m.L * 4, hipMemcpyDeviceToHost));
+    if (st.ebad.p) ESP_HIP(hipMemcpy(ebad.data(), st.ebad.p, (size_t)m.L * 4, hipMemcpyDeviceToHost));
     for (int l = 0; l < m.L; ++l) {
+        if (ebad[l] != INT_MAX) {  // an expert that failed its checks (never kept)
+            std::vector<int> clean(m.L, INT_MAX);
+            ESP_HIP(hipMemcpy(st.ebad.p, clean.data(), (size_t)m.L * 4, hipMemcpyHostToDevice));
+            static const char *parts[3] = {"gate_proj", "up_proj", "down_proj"};
+            fail(ESP_INVALID_WEIGHTS, "weight format: non-finite weight in model.layers." +
+                                          std::to_string(l + st.first) + ".mlp.experts." +
+                                          std::to_string(ebad[l] / 3) + "." + parts[ebad[l] % 3] +
+                                          ".weight");
+        }
         if (bad[l] == INT_MAX) continue;
         for (auto it = st.cache.begin(); it != st.cache.end(); ++it)
             if (it->layer == l) {  // errors are never cached (streaming.rs:101-110)
@@ -400,10 +589,10 @@ void stream_check(Model &m) {
             }
         std::vector<int> clean(m.L, INT_MAX);
         ESP_HIP(hipMemcpy(st.bad.p, clean.data(), (size_t)m.L * 4, hipMemcpyHostToDevice));
-        const int tag = bad[l];
+        const int tag = bad[l], kind = m.layers[l].moe ? 1 : 0;
         const std::string name = "model.layers." + std::to_string(l + st.first) + "." +
-                                 (tag < (int)st.tag_names.size() ? st.tag_names[tag] : "?");
-        if (tag < (int)st.tag_scales.size() && st.tag_scales[tag])
+                                 (tag < (int)st.tag_names[kind].size() ? st.tag_names[kind][tag] : "?");
+        if (tag < (int)st.tag_scales[kind].size() && st.tag_scales[kind][tag])
             fail(ESP_INVALID_WEIGHTS, "weight format: packed projection byte count or block scales "
                                       "are invalid (" + name + ")");
         fail(ESP_INVALID_WEIGHTS, "weight format: non-finite weight in " + name);
@@ -430,14 +619,33 @@ void stream_make_resident(Model &m) {
         ws.push_back(stage_layer(m, st.copy, l, blocks.back().get(), &payload));
         ESP_HIP(hipEventRecord(st.freed[st.cur_slot], st.copy));
         st.cur_slot = -1;
+        if (!ws.back().moe) continue;
+        // loader.rs:196-210 ExpertMode::Resident: every expert read once and
+        // kept, in the resident loader's [E][Fe][H] / [E][H][Fe] layout
+        const size_t part = (size_t)m.Fe * m.H * dt_size(m.wt);
+        blocks.emplace_back(new DevMem(3 * part * m.E));
+        char *kept = (char *)blocks.back()->p;
+        for (int e = 0; e < m.E; ++e) {
+            ExpertW x = stream_expert(m, st.copy, l, e);
+            for (int i = 0; i < 3; ++i)
+                ESP_HIP(hipMemcpyAsync(kept + ((size_t)i * m.E + e) * part,
+                                       i == 0 ? x.gate : i == 1 ? x.up : x.down, part,
+                                       hipMemcpyDeviceToDevice, st.copy));
+            stream_expert_release(m, st.copy);
+        }
+        ws.back().ex_gate = kept;
+        ws.back().ex_up = kept + part * m.E;
+        ws.back().ex_down = kept + 2 * part * m.E;
     }
     ESP_HIP(hipStreamSynchronize(st.copy));
     stream_check(m);
     for (int l = 0; l < m.L; ++l) {
         ws[l].window = m.layers[l].window;
         m.layers[l] = ws[l];
-        m.weight_bytes += blocks[l]->bytes;
-        m.mem.push_back(std::move(blocks[l]));
+    }
+    for (auto &b : blocks) {
+        m.weight_bytes += b->bytes;
+        m.mem.push_back(std::move(b));
     }
     m.st.reset();
 }
@@ -450,6 +658,9 @@ void stream_stats(const Model &m, esp_streaming_stats *o) {
     o->layer_reads = st.reads;
     o->encoded_bytes_read = st.bytes;
     o->largest_encoded_layer = st.largest;
+    o->expert_reads = st.ereads;
+    o->expert_encoded_bytes_read = st.ebytes;
+    o->largest_encoded_expert = st.elargest;
     if (st.cache_on) {
         o->device_cache = 1;
         o->cache_hits = st.hits;

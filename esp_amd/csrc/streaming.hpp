@@ -45,8 +45,17 @@ struct BlockLayout {
     size_t in_norm = 0, post_norm = 0, qkv = 0, qkv_s = 0, qkv_bias = 0, o = 0, o_s = 0,
            o_bias = 0, q_norm = 0, k_norm = 0, gate = 0, gate_s = 0, up = 0, up_s = 0, down = 0,
            down_s = 0;
+    // a routed-expert layer's core (loader.rs:66-85): router, shared expert
+    // gate and shared expert projections in place of the dense MLP
+    size_t router = 0, shared_gate = 0, sh_gate = 0, sh_up = 0, sh_down = 0;
     size_t total = 0;
     size_t f32_elems = 0;  // elements of f32 regions (bound on widening sources)
+};
+
+// One routed expert staged in HBM: [Fe, H], [Fe, H], [H, Fe] in the model's
+// weight type.
+struct ExpertW {
+    void *gate = nullptr, *up = nullptr, *down = nullptr;
 };
 
 struct StreamEntry {
@@ -60,16 +69,17 @@ struct Streamer {
     esp_layer_source src{};
     int first = 0;  // global index of local layer 0 (a stage's range start)
     esp_streaming_options opt{};
-    BlockLayout lay;
+    BlockLayout lay, lay_moe;  // dense and routed-expert layer blocks
     // logical verified reads (streaming.rs:228-252)
     uint64_t reads = 0, bytes = 0, largest = 0;
     // device layer cache (model.rs:336-362, 560-646)
     bool cache_on = false;
     uint64_t budget = 0, payload = 0, hits = 0, misses = 0;
     std::vector<StreamEntry> cache;
-    // the tensor suffix of each check tag (the same for every dense layer)
-    std::vector<std::string> tag_names;
-    std::vector<int> tag_scales;  // 1 when the tag checks packed block scales
+    // the tensor suffix of each check tag (the same for every layer of one
+    // kind: [0] dense, [1] routed-expert core)
+    std::vector<std::string> tag_names[2];
+    std::vector<int> tag_scales[2];  // 1 when the tag checks packed block scales
     // pipeline
     uint8_t *stage[2] = {nullptr, nullptr};
     size_t stage_cap = 0;
@@ -80,6 +90,17 @@ struct Streamer {
     int next = 0, cur_slot = -1;
     bool pending = false;  // device checks queued since the last stream_check
     DevMem bad;  // int[L], INT_MAX when clean
+    // routed experts (moe.rs:207-243, streaming.rs:252-260): read per forward
+    // through src.read_expert for the experts the router chose, two staging
+    // slots alternating on the copy stream; checks report 3 * expert + part
+    // into ebad[l]
+    size_t eblock_bytes = 0, estage_cap = 0, eraw_cap = 0;
+    uint8_t *estage[2] = {nullptr, nullptr};
+    DevMem eblock[2], eraw[2];
+    hipEvent_t ecopied[2] = {nullptr, nullptr}, efreed[2] = {nullptr, nullptr};
+    int enext = 0, ecur = -1;
+    uint64_t ereads = 0, ebytes = 0, elargest = 0;
+    DevMem ebad;  // int[L], INT_MAX when clean
     std::recursive_mutex mu;
     ~Streamer();
 };
@@ -94,6 +115,11 @@ void stream_release(Model &m, Kv &kv);
 // After the forward's stream has drained: report (and evict from the
 // cache) the first layer whose device checks failed.
 void stream_check(Model &m);
+// Expert e of local layer l, read through the source and staged for the
+// kernels on `compute` (moe.rs:207-243); stream_expert_release marks the end
+// of the kernels that read it.
+ExpertW stream_expert(Model &m, hipStream_t compute, int l, int e);
+void stream_expert_release(Model &m, hipStream_t compute);
 void stream_set_cache(Model &m, uint64_t budget);
 void stream_make_resident(Model &m);
 void stream_stats(const Model &m, esp_streaming_stats *out);

@@ -192,7 +192,7 @@ class DecoderModel:
         L = _lib.load()
         c, keep = esp_config(config, fmt)
         bridge = SourceBridge(source)
-        src = _lib.EspLayerSource(bridge.fn, None)
+        src = _lib.EspLayerSource(bridge.fn, None, bridge.efn)
         opt = _lib.EspStreamingOptions(options.query_chunk, options.max_layer_bytes,
                                        options.max_shared_bytes)
         buf = (C.c_uint8 * len(shared)).from_buffer_copy(shared) if shared else None
@@ -224,7 +224,10 @@ class DecoderModel:
         bridge = getattr(self, "_bridge", None)
         out = StreamingReadStats(layer_reads=s.layer_reads, encoded_bytes_read=s.encoded_bytes_read,
                                  largest_encoded_layer=s.largest_encoded_layer,
-                                 verified_cache=bridge.source.cache_stats() if bridge else None)
+                                 verified_cache=bridge.source.cache_stats() if bridge else None,
+                                 expert_reads=s.expert_reads,
+                                 expert_encoded_bytes_read=s.expert_encoded_bytes_read,
+                                 largest_encoded_expert=s.largest_encoded_expert)
         if s.device_cache:
             out.device_cache = DeviceLayerCacheStats(s.cache_hits, s.cache_misses,
                                                      s.retained_payload_bytes,

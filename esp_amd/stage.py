@@ -187,7 +187,7 @@ class DecoderStage(StageExecutor):
         options.validate()
         c, keep = esp_config(config, fmt)
         bridge = SourceBridge(source)
-        src = _lib.EspLayerSource(bridge.fn, None)
+        src = _lib.EspLayerSource(bridge.fn, None, bridge.efn)
         opt = _lib.EspStreamingOptions(options.query_chunk, options.max_layer_bytes,
                                        options.max_shared_bytes)
         buf = (C.c_uint8 * len(shared)).from_buffer_copy(shared) if shared else None

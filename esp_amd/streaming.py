@@ -202,8 +202,10 @@ class ArtifactSource(LayerSource):
     byte size is checked against ``limit`` before the bytes are handed out,
     and against the bytes themselves."""
 
-    def __init__(self, artifacts: Sequence[bytes]):
+    def __init__(self, artifacts: Sequence[bytes],
+                 experts: Optional[Dict[Tuple[int, int], bytes]] = None):
         self._artifacts = list(artifacts)
+        self._experts = experts
 
     def read_layer(self, index: int, limit: int) -> bytes:
         if index >= len(self._artifacts):
@@ -211,6 +213,17 @@ class ArtifactSource(LayerSource):
         data = self._artifacts[index]
         if len(data) > limit:
             raise InvalidWeights("layer library: layer artifact identity, schema or byte limit "
+                                 "mismatch")
+        return data
+
+    def read_expert(self, layer: int, expert: int, limit: int) -> bytes:
+        if self._experts is None:
+            return super().read_expert(layer, expert, limit)
+        data = self._experts.get((layer, expert))
+        if data is None:
+            raise InvalidWeights(f"layer library: missing expert artifact {layer}/{expert}")
+        if len(data) > limit:
+            raise InvalidWeights("layer library: expert artifact identity, schema or byte limit "
                                  "mismatch")
         return data
 
@@ -263,21 +276,41 @@ def layer_tensor_names(config: DecoderConfig) -> List[str]:
     return names
 
 
+def layer_core_tensor_names(config: DecoderConfig, index: int) -> List[str]:
+    """loader.rs:66-85: a routed-expert layer's core artifact holds the
+    router and the shared expert (when the configuration declares one) in
+    place of the dense MLP; its experts are separate artifacts."""
+    names = layer_tensor_names(config)
+    if config.layer_is_moe(index):
+        names = [n for n in names if not n.startswith("mlp.")] + ["mlp.gate.weight"]
+        if config.moe.shared_expert_intermediate_size:
+            names += ["mlp.shared_expert_gate.weight", "mlp.shared_expert.gate_proj.weight",
+                      "mlp.shared_expert.up_proj.weight", "mlp.shared_expert.down_proj.weight"]
+    return names
+
+
+def expert_tensor_names(layer: int, expert: int) -> List[str]:
+    """loader.rs:87-91"""
+    return [f"model.layers.{layer}.mlp.experts.{expert}.{n}.weight"
+            for n in ("gate_proj", "up_proj", "down_proj")]
+
+
 class CheckpointReader:
     """checkpoint.rs:47-293 over one safetensors checkpoint held in memory:
-    the declared names are checked once, then the shared artifact and each
-    layer's artifact are packed on request within a byte limit."""
+    the declared names are checked once, then the shared artifact, each
+    layer's core artifact and each routed expert's artifact are packed on
+    request within a byte limit."""
 
     def __init__(self, checkpoint: bytes, config: DecoderConfig):
-        if config.moe is not None:
-            raise InvalidConfig("checkpoint: routed-expert layers are split by the expert "
-                                "reader, which this library does not stream")
         self._buf = memoryview(checkpoint)
         self._header, self._start = read_header(self._buf)
         self._config = config
         want = {"model.embed_tokens.weight", "model.norm.weight"}
         for i in range(config.num_hidden_layers):
-            want |= {f"model.layers.{i}.{s}" for s in layer_tensor_names(config)}
+            want |= {f"model.layers.{i}.{s}" for s in layer_core_tensor_names(config, i)}
+            if config.layer_is_moe(i):
+                for e in range(config.moe.num_experts):
+                    want |= set(expert_tensor_names(i, e))
         if not config.tie_word_embeddings or "lm_head.weight" in self._header:
             want.add("lm_head.weight")
         have = {n for n in self._header if not n.endswith(".rotary_emb.inv_freq")}
@@ -307,8 +340,16 @@ class CheckpointReader:
         return self._pack(names, limit)
 
     def layer_bytes(self, index: int, limit: int) -> bytes:
-        return self._pack([f"model.layers.{index}.{s}" for s in layer_tensor_names(self._config)],
-                          limit)
+        return self._pack([f"model.layers.{index}.{s}"
+                           for s in layer_core_tensor_names(self._config, index)], limit)
+
+    def expert_bytes(self, layer: int, expert: int, limit: int) -> bytes:
+        """checkpoint.rs:231-244"""
+        c = self._config
+        if (layer >= c.num_hidden_layers or not c.layer_is_moe(layer)
+                or expert >= c.moe.num_experts):
+            raise InvalidWeights("checkpoint: expert outside the declared sparse layer")
+        return self._pack(expert_tensor_names(layer, expert), limit)
 
 
 def split_checkpoint(checkpoint: bytes, config: DecoderConfig,
@@ -320,6 +361,18 @@ def split_checkpoint(checkpoint: bytes, config: DecoderConfig,
     r = CheckpointReader(checkpoint, config)
     return (r.shared_bytes(options.max_shared_bytes),
             [r.layer_bytes(i, options.max_layer_bytes) for i in range(config.num_hidden_layers)])
+
+
+def split_experts(checkpoint: bytes, config: DecoderConfig,
+                  options: Optional[StreamingOptions] = None) -> Dict[Tuple[int, int], bytes]:
+    """One artifact per routed expert, keyed (layer, expert), each within
+    the options' layer limit (checkpoint.rs:231-244)."""
+    options = options or StreamingOptions()
+    options.validate()
+    r = CheckpointReader(checkpoint, config)
+    return {(i, e): r.expert_bytes(i, e, options.max_layer_bytes)
+            for i in range(config.num_hidden_layers) if config.layer_is_moe(i)
+            for e in range(config.moe.num_experts)}
 
 
 # ---- the C callback behind esp_model_load_streamed ----
@@ -337,10 +390,19 @@ class SourceBridge:
         self.error: Optional[BaseException] = None
         self._pool = ThreadPoolExecutor(8)
         self.fn = _lib.LAYER_READ_FN(self._read)
+        self.efn = _lib.EXPERT_READ_FN(self._read_expert)
 
     def _read(self, user, index, limit, dst, cap, plen):
+        return self._fill(lambda: self.source.read_layer_shared(int(index), int(limit)),
+                          dst, cap, plen)
+
+    def _read_expert(self, user, layer, expert, limit, dst, cap, plen):
+        return self._fill(lambda: self.source.read_expert(int(layer), int(expert), int(limit)),
+                          dst, cap, plen)
+
+    def _fill(self, read, dst, cap, plen):
         try:
-            data = self.source.read_layer_shared(int(index), int(limit))
+            data = read()
             n = len(data)
             plen[0] = n
             if n <= cap:

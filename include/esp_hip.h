@@ -257,9 +257,18 @@ typedef struct esp_streaming_options {
  * on the thread running the forward, one call at a time. */
 typedef esp_status (*esp_layer_read_fn)(void *user, uint32_t index, uint64_t limit, uint8_t *dst,
                                         uint64_t cap, uint64_t *len);
+/* streaming.rs:26-66 LayerSource::read_expert in the same fill form: the
+ * artifact of routed expert `expert` of layer `layer`, holding exactly
+ * model.layers.{layer}.mlp.experts.{expert}.{gate,up,down}_proj.weight
+ * (loader.rs:137-168). NULL = the source has no expert reader
+ * (ESP_INVALID_WEIGHTS "layer source has no expert reader" when a routed
+ * layer runs). */
+typedef esp_status (*esp_expert_read_fn)(void *user, uint32_t layer, uint32_t expert,
+                                         uint64_t limit, uint8_t *dst, uint64_t cap, uint64_t *len);
 typedef struct esp_layer_source {
     esp_layer_read_fn read_layer;
     void *user;
+    esp_expert_read_fn read_expert; /* nullable */
 } esp_layer_source;
 
 /* provider.rs:370-426 from_layer_source_with_format + model.rs:268-312
@@ -272,9 +281,13 @@ typedef struct esp_layer_source {
  * the artifact must hold exactly model.layers.{i}.* of the declared block
  * (loader.rs:830-848), is staged into HBM on a copy stream while the
  * previous layer computes, and is checked on the device (dtype admission,
- * finiteness, packed block scales) before its results are used. `source`
- * is copied; its `user` must outlive the model. MoE configurations ->
- * ESP_UNSUPPORTED. */
+ * finiteness, packed block scales) before its results are used. A routed
+ * layer's artifact holds its core (attention, norms, router, shared expert:
+ * loader.rs:66-85); its experts are read per forward through read_expert,
+ * only those the router chose, in ascending order (moe.rs:183-243), each
+ * staged while the previous one computes. Routed experts run in the f32
+ * and bf16 formats (packed -> ESP_UNSUPPORTED). `source` is copied; its
+ * `user` must outlive the model. */
 esp_status esp_model_load_streamed(const esp_config *config, const uint8_t *shared,
                                    size_t shared_len, const esp_layer_source *source,
                                    const esp_streaming_options *options, esp_model **out);
@@ -287,8 +300,9 @@ esp_status esp_model_load_streamed(const esp_config *config, const uint8_t *shar
 esp_status esp_model_layer_cache(esp_model *model, uint64_t budget);
 
 /* model.rs:384-415 with_resident_layers: read every layer once through
- * the source and keep all of them in HBM; the model then no longer
- * streams. A model that does not stream is left unchanged. */
+ * the source, and every routed expert once through read_expert
+ * (loader.rs:196-210), and keep all of them in HBM; the model then no
+ * longer streams. A model that does not stream is left unchanged. */
 esp_status esp_model_resident_layers(esp_model *model);
 
 /* streaming.rs:228-252 StreamingReadStats (logical verified reads) and
@@ -300,6 +314,8 @@ typedef struct esp_streaming_stats {
     uint64_t layer_reads, encoded_bytes_read, largest_encoded_layer;
     uint64_t cache_hits, cache_misses, retained_payload_bytes, payload_budget_bytes;
     uint64_t cached_layers;
+    /* streaming.rs:242-252, 305-312: routed experts read per forward */
+    uint64_t expert_reads, expert_encoded_bytes_read, largest_encoded_expert;
 } esp_streaming_stats;
 esp_status esp_model_streaming_stats(const esp_model *model, esp_streaming_stats *out);
 
