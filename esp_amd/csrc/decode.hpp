@@ -64,7 +64,15 @@ struct AttnDecodeArgs {
     int max_t;            // plan bound: every row's position is below it
     int n_split, split_len;
     float *part;          // [M, nq, n_split, hd + 4]
-    int32_t *ticket;      // [M, nkv] zero-initialised
+    // [M, nkv] zero-initialised merge tickets: bits 0-7 count the splits
+    // that arrived, bits 8 + 7x the ones that ran on XCD x
+    unsigned long long *ticket;
+    int32_t *xcd_err;     // set to 1 when a unit's splits ran on several XCDs
+    // set by the launcher from ESP_ATT_XCD_MISPLACE=1: blocks take the
+    // linear (unit, split) order under the XCD-local protocol, so the
+    // placement check fires (exercises the fallback; every access stays
+    // in bounds)
+    int misplace;
     float *out;           // [M, nq*hd] f32, or the bf16 hi plane when out_lo is set
     uint16_t *out_lo;     // nullable: bf16 lo plane (split activation output)
     int xcd_nx;           // set by the launcher: merge protocol (0 = agent scope)
@@ -92,5 +100,8 @@ void launch_attn_decode(const AttnDecodeArgs &a, hipStream_t s);
 // XCD count of the XCD-local split merge, or 0 for the agent-scope merge
 // (probed once per process; environment ESP_ATT_XCD=0 forces 0)
 int attn_xcd_mode();
+// Switch the XCD-local merge off for the process (a launch found a unit's
+// splits on several XCDs).
+void attn_xcd_disable();
 
 }  // namespace esp

@@ -22,6 +22,7 @@ Model *synthetic_model(const esp_config *cfg, uint64_t seed, float std, uint32_t
 Kv *create_kv(Model *m, uint32_t batch, uint32_t max_ctx, bool f16);
 void decode_step_dev(Model &m, Kv &kv, int seq, int max_t, int32_t *gen);
 void moe_check(Kv &kv);
+bool xcd_merge_failed(Kv &kv);
 void launch_gen_step(const uint32_t *picked, int32_t *gen, hipStream_t s);
 }  // namespace esp
 
@@ -552,10 +553,14 @@ esp_status esp_generate_greedy(esp_model *model, esp_kv *kv, uint32_t seq, const
                 fail(ESP_INVALID_REQUEST, "cached input is empty or exceeds the context window");
             if (n_out) *n_out = n;
         };
+        // One pass of the generation; true when a decode-attention launch
+        // found its splits on several XCDs (the XCD-local merge is then off
+        // for the process and the pass runs again).
+        auto pass = [&]() -> bool {
         if (n_out) *n_out = 0;
         k.pos[seq] = 0;  // generate.rs:141 new_cache per generation
         forward(m, k, 1, &seq, &n_prompt, prompt);
-        if (max_new == 0) return;
+        if (max_new == 0) return false;
         hipStream_t s = k.stream;
         // gen layout: [0] fed token, [1] step, [2] row_seq, [3] row_pos, [8..] list
         DevMem gen((size_t)(8 + max_new) * 4);
@@ -605,8 +610,9 @@ esp_status esp_generate_greedy(esp_model *model, esp_kv *kv, uint32_t seq, const
                 ++n;
                 if (i + 1 < gen_n) decode_step_dev(m, k, (int)seq, max_t, g);
             }
+            if (xcd_merge_failed(k)) return true;
             finish(n);
-            return;
+            return false;
         }
         // Every layer kind routes and groups on the device (MoE included), so
         // the decode step is captured once and replayed. ESP_GRAPHS=0 replays
@@ -650,6 +656,7 @@ esp_status esp_generate_greedy(esp_model *model, esp_kv *kv, uint32_t seq, const
         std::vector<int32_t> list(gen_n);
         ESP_HIP(hipMemcpyAsync(list.data(), g + 8, (size_t)gen_n * 4, hipMemcpyDeviceToHost, s));
         ESP_HIP(hipStreamSynchronize(s));
+        if (xcd_merge_failed(k)) return true;
         uint32_t n = 0;
         for (; n < gen_n; ++n) {
             bool stop = false;
@@ -664,6 +671,10 @@ esp_status esp_generate_greedy(esp_model *model, esp_kv *kv, uint32_t seq, const
             cached_st->hits = hits0 + fwd * (uint64_t)m.L;
         }
         finish(n);
+        return false;
+        };
+        if (pass() && pass())
+            fail(ESP_BACKEND, "decode attention: split placement check failed with the agent-scope merge");
     });
 }
 

@@ -538,15 +538,15 @@ __global__ void __launch_bounds__(NW * 64) attn_decode_k(AttnDecodeArgs a) {
     int unit, split;
     {
         const int b = blockIdx.x;
-        if (XCD) {
+        if (XCD && !a.misplace) {
             const int x = b % a.xcd_nx, i = b / a.xcd_nx;
             unit = x + a.xcd_nx * (i / ns);
             split = i % ns;
-            if (unit >= U) return;  // padding block of a short residue class
         } else {
             unit = b / ns;
             split = b % ns;
         }
+        if (unit >= U) return;  // padding block of a short residue class
     }
     const int g = unit % a.nkv, row = unit / a.nkv;
     const int G = a.nq / a.nkv;
@@ -834,10 +834,17 @@ __global__ void __launch_bounds__(NW * 64) attn_decode_k(AttnDecodeArgs a) {
     wait_stores();
     __syncthreads();
     if (tid == 0) {
-        int *tk = a.ticket + unit;
-        const int t = atomicAdd(tk, 1);
-        last = t == ns - 1;
-        if (last) *tk = 0;
+        // one device-scope add counts the split and the XCD it ran on
+        const unsigned xcc = XCD ? __builtin_amdgcn_s_getreg((3 << 11) | (0 << 6) | 20) & 7u : 0u;
+        unsigned long long *tk = a.ticket + unit;
+        const unsigned long long t = atomicAdd(tk, 1ull + (1ull << (8 + 7 * xcc)));
+        last = (int)(t & 0xffu) == ns - 1;
+        if (last) {
+            *tk = 0;
+            // every earlier split must have run on this block's XCD, or its
+            // plain stores may still sit in another XCD's L2
+            if (XCD && (int)((t >> (8 + 7 * xcc)) & 0x7fu) != ns - 1) atomicOr(a.xcd_err, 1);
+        }
     }
     __syncthreads();
     if (!last) return;
@@ -949,8 +956,13 @@ __global__ void xcc_probe_k(int32_t *out) {
     if (threadIdx.x == 0) out[blockIdx.x] = (int32_t)x;
 }
 
+static int g_xcd_off = 0;  // set once a launch reported a split across XCDs
+
+void attn_xcd_disable() { g_xcd_off = 1; }
+
 int attn_xcd_mode() {
     static int mode = -1;
+    if (g_xcd_off) return 0;
     if (mode < 0) {
         int dev = 0, nx = 0;
         ESP_HIP(hipGetDevice(&dev));
@@ -990,6 +1002,10 @@ void launch_attn_decode(const AttnDecodeArgs &a0, hipStream_t s) {
     if (a.n_split > 1 && U > ATT_MAX_TICKETS)
         fail(ESP_BACKEND, "attn_decode: too many (row, kv head) merges");
     a.xcd_nx = a.n_split > 1 ? attn_xcd_mode() : 0;
+    {
+        const char *mp = getenv("ESP_ATT_XCD_MISPLACE");
+        a.misplace = a.xcd_nx > 0 && mp && mp[0] == '1';
+    }
     long long nb = a.xcd_nx > 0 ? (long long)a.xcd_nx * ((U + a.xcd_nx - 1) / a.xcd_nx) * a.n_split
                                 : U * a.n_split;
     if (nb > 0x7fffffffLL) fail(ESP_BACKEND, "attn_decode: grid too large");

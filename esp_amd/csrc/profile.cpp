@@ -61,6 +61,11 @@ void prof_record(const char *family, hipEvent_t start, hipEvent_t end) {
     if (f.pending.size() > 4096) drain(f);
 }
 
+void prof_count(const char *family) {
+    std::lock_guard<std::mutex> g(mu);
+    ++fams[family].launches;
+}
+
 int prof_enable(const char *family, int on) {
     std::lock_guard<std::mutex> g(mu);
     Fam &f = fams[family];

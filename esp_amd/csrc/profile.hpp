@@ -34,6 +34,9 @@ struct Prof {
     }
 };
 
+// Count one occurrence of a host-side event under `family` (read back as
+// its launch count, total time 0), whether or not timing is enabled.
+void prof_count(const char *family);
 int prof_enable(const char *family, int on);
 int prof_read(const char *family, unsigned long long *launches, double *total_ms);
 

@@ -21,7 +21,11 @@
 namespace esp {
 
 // words of Kv::tickets (128-byte multiple)
-static const int kTicketWords = (4096 + 8 + 2 * DG_MAX_PART + 8 + 31) / 32 * 32;
+// [0, 2 * ATT_MAX_TICKETS): 64-bit attention merge tickets; then the head
+// ticket, the XCD placement flag, the argmax partials and the picked id
+static const int kHeadTicket = 2 * ATT_MAX_TICKETS;
+static const int kXcdErr = kHeadTicket + 4;
+static const int kTicketWords = (kHeadTicket + 8 + 2 * DG_MAX_PART + 8 + 31) / 32 * 32;
 
 struct Rows;
 
@@ -781,7 +785,14 @@ static Plan attn_plan(const Model &m, int rows, int max_t) {
     return Plan{ns, sl};
 }
 
-static int32_t *att_tickets(Kv &kv) { return kv.tickets.as<int32_t>(); }
+static unsigned long long *att_tickets(Kv &kv) { return kv.tickets.as<unsigned long long>(); }
+
+// The XCD-local attention merge assumes every split of a (row, kv head)
+// runs on one XCD (attn_xcd_mode's probe). Each launch checks that
+// placement on the device; a violation sets this flag, read back when the
+// forward's stream drains: the forward is then computed again with the
+// agent-scope merge, which every placement tolerates (xcd_merge_failed).
+static int32_t *xcd_err_word(Kv &kv) { return kv.tickets.as<int32_t>() + kXcdErr; }
 
 // lo plane of a split activation buffer holding rows x cols (nullptr for f32)
 static void *lo_plane(Dt act, const DevMem &b, int rows, int cols) {
@@ -867,6 +878,7 @@ static void attn_decode_rows(Model &m, Kv &kv, const Rows &rows, int Mc, int l, 
     a.split_len = plan.split_len;
     a.part = kv.part.as<float>();
     a.ticket = att_tickets(kv);
+    a.xcd_err = xcd_err_word(kv);
     a.out = kv.attn.as<float>();
     a.out_lo = (uint16_t *)lo_plane(out_dt, kv.attn, Mc, m.qw);
     launch_attn_decode(a, kv.stream);
@@ -1387,10 +1399,10 @@ static void run_head(Model &m, Kv &kv, int n_seqs, const float *h_src, const int
         g.y = kv.logits.as<float>();
         g.N = m.V;
         g.K = m.H;
-        g.ticket = t + 4096;
-        g.part_v = (float *)(t + 4096 + 8);
-        g.part_i = t + 4096 + 8 + DG_MAX_PART;
-        g.picked = (uint32_t *)(t + 4096 + 8 + 2 * DG_MAX_PART);
+        g.ticket = t + kHeadTicket;
+        g.part_v = (float *)(t + kHeadTicket + 8);
+        g.part_i = t + kHeadTicket + 8 + DG_MAX_PART;
+        g.picked = (uint32_t *)(t + kHeadTicket + 8 + 2 * DG_MAX_PART);
         g.gen = gen;
         Prof p("gemv_head", s);
         launch_decode_gemv(m.ht, DG_HEAD, g, s);
@@ -1429,8 +1441,34 @@ static void run_head(Model &m, Kv &kv, int n_seqs, const float *h_src, const int
     launch_gemm(gemm_dt(m.ht), GEMM_STORE, g, s);
 }
 
+// After a stream has drained: whether a decode-attention launch since the
+// last check found a (row, kv head)'s splits on several XCDs. The flag is
+// cleared and the XCD-local merge switched off for the process.
+bool xcd_merge_failed(Kv &kv) {
+    int32_t flag = 0;
+    ESP_HIP(hipMemcpy(&flag, xcd_err_word(kv), 4, hipMemcpyDeviceToHost));
+    if (!flag) return false;
+    const int32_t zero = 0;
+    ESP_HIP(hipMemcpy(xcd_err_word(kv), &zero, 4, hipMemcpyHostToDevice));
+    attn_xcd_disable();
+    prof_count("attn_xcd_fallback");
+    return true;
+}
+
+static bool forward_pass(Model &m, Kv &kv, int n_seqs, const uint32_t *seqs, const uint32_t *lens,
+                         const int32_t *ids);
+
+// One forward; computed again with the agent-scope attention merge when the
+// XCD-local merge's placement check failed (positions only move after a
+// pass that succeeded).
 void forward(Model &m, Kv &kv, int n_seqs, const uint32_t *seqs, const uint32_t *lens,
              const int32_t *ids) {
+    if (forward_pass(m, kv, n_seqs, seqs, lens, ids) && forward_pass(m, kv, n_seqs, seqs, lens, ids))
+        fail(ESP_BACKEND, "decode attention: split placement check failed with the agent-scope merge");
+}
+
+static bool forward_pass(Model &m, Kv &kv, int n_seqs, const uint32_t *seqs, const uint32_t *lens,
+                         const int32_t *ids) {
     if (n_seqs <= 0) fail(ESP_INVALID_REQUEST, "cached input is empty or exceeds the context window");
     std::unique_lock<std::recursive_mutex> streaming;
     if (m.st) streaming = std::unique_lock<std::recursive_mutex>(m.st->mu);
@@ -1513,22 +1551,36 @@ void forward(Model &m, Kv &kv, int n_seqs, const uint32_t *seqs, const uint32_t 
     }
     if (kv.moe_err.p)
         ESP_HIP(hipMemcpyAsync(pin + erroff, kv.moe_err.p, 4, hipMemcpyDeviceToHost, s));
+    ESP_HIP(hipMemcpyAsync(pin + erroff + 1, xcd_err_word(kv), 4, hipMemcpyDeviceToHost, s));
     ESP_HIP(hipStreamSynchronize(s));
     if (m.st) stream_check(m);  // a streamed layer that failed its device checks
     if (kv.moe_err.p) moe_fail(pin[erroff]);
+    if (pin[erroff + 1] && xcd_merge_failed(kv)) return true;
     for (int i = 0; i < n_seqs; ++i) kv.pos[seqs[i]] += (int)lens[i];
     kv.logits_rows = n_seqs;
+    return false;
 }
 
 // A stage's forward (stage.rs:471-527): `hidden` [S, H] f32 enters the
 // range's first layer at absolute positions start..start+S of sequence 0;
 // `out` receives the last layer's hidden rows [S, H], or with `logits` the
 // final norm + head on the last row ([V] f32).
+static bool forward_hidden_pass(Model &m, Kv &kv, const float *hidden, int S, int start,
+                                float *out, bool logits);
+
 void forward_hidden(Model &m, Kv &kv, const float *hidden, int S, int start, float *out,
                     bool logits) {
+    if (forward_hidden_pass(m, kv, hidden, S, start, out, logits) &&
+        forward_hidden_pass(m, kv, hidden, S, start, out, logits))
+        fail(ESP_BACKEND, "decode attention: split placement check failed with the agent-scope merge");
+}
+
+static bool forward_hidden_pass(Model &m, Kv &kv, const float *hidden, int S, int start,
+                                float *out, bool logits) {
     hipStream_t s = kv.stream;
     const int H = m.H;
     ensure_scratch(m, kv, std::min(S, kMaxRows), 1);
+    if (kv.moe_err.p) launch_fill_const(kv.moe_err.as<float>(), 1, 0.f, s);
     const int lastoff = 3 * kMaxRows;
     ensure_pinned(kv, (size_t)(3 * kMaxRows + kv.batch + 64) * 4);
     int32_t *pin = (int32_t *)kv.pinned;
@@ -1557,8 +1609,11 @@ void forward_hidden(Model &m, Kv &kv, const float *hidden, int S, int start, flo
         }
     }
     ESP_HIP(hipStreamSynchronize(s));
+    if (kv.moe_err.p) moe_check(kv);
+    if (xcd_merge_failed(kv)) return true;
     kv.pos[0] = start + S;
     kv.logits_rows = logits ? 1 : 0;
+    return false;
 }
 
 }  // namespace esp

@@ -407,7 +407,11 @@ esp_status esp_pick_constrained(esp_kv *kv, uint32_t n_rows, esp_constraint *con
 
 /* Kernel timing (measurement support, no reference counterpart): while
  * enabled, every launch of the named kernel family records HIP events on
- * its stream; read returns launches and total milliseconds since enable. */
+ * its stream; read returns launches and total milliseconds since enable.
+ * The family "attn_xcd_fallback" counts (always, time 0) the forwards
+ * computed again because a decode-attention launch found a (row, kv
+ * head)'s key splits on several XCDs, after which the process uses the
+ * agent-scope merge. */
 esp_status esp_profile_enable(const char *kernel, int enable);
 esp_status esp_profile_read(const char *kernel, uint64_t *launches, double *total_ms);
 

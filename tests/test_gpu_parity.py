@@ -492,6 +492,25 @@ def test_decode_attention_merge_protocols(protocol, monkeypatch):
         want = ref.forward_last(rkv, [t])
 
 
+def test_decode_attention_placement_fallback():
+    """The XCD-local merge checks, per launch, that every split of a (row,
+    kv head) ran on one XCD; forced to fail from the host
+    (ESP_ATT_XCD_MISPLACE=1), the forward and the device greedy loop are
+    computed again with the agent-scope merge and match the oracle
+    (tests/xcd_fallback_case.py, in a child process because the fallback
+    is process-wide)."""
+    import os
+    import subprocess
+    import sys
+    env = dict(os.environ, ESP_ATT_XCD_MISPLACE="1")
+    env.pop("ESP_ATT_XCD", None)
+    case = os.path.join(os.path.dirname(os.path.abspath(__file__)), "xcd_fallback_case.py")
+    r = subprocess.run([sys.executable, "-u", case], env=env, capture_output=True, text=True,
+                       timeout=300)
+    print(r.stdout[-2000:], r.stderr[-2000:])
+    assert r.returncode == 0
+
+
 def test_bf16_batch_decode_rows_match_oracle():
     """Multi-sequence rows (decode rows of six sequences + an 8-token forced
     block of a seventh) through the split-K decode attention with split
