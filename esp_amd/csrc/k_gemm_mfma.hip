@@ -465,33 +465,92 @@ __global__ void __launch_bounds__(128 * BMW + (PROD ? 64 : 0), (BMW == 2 && STG 
         }
         const char *base = lds_s + (kt % STAGES) * F::STAGE;
         const char *ah = base, *al = base + F::A, *bb = base + 2 * F::A;
+        // Form with register room (no producer wave: at most two waves per
+        // SIMD): both 16-deep k-steps' fragments are read before their
+        // MFMAs, and the schedule interleaves the second step's LDS reads
+        // with the first step's MFMAs, so only the first reads' latency is
+        // exposed per stage (at most 12 reads in flight: lgkmcnt counts
+        // 15). The producer form (up to three waves per SIMD, ~170
+        // registers) reads each step's fragments just before its MFMAs.
+        constexpr int KS = LS_BK / 16;
+        static_assert(KS == 2, "two k-steps per stage");
+        if constexpr (!PROD) {
+            constexpr int RD = 4 + NB * NJ;      // LDS reads per k-step
+            constexpr int MF = 2 * NB * 2 * NJ;  // MFMAs per k-step
+            bf16x8_t fh[KS][2], fl[KS][2], fb[KS][NB][NJ];
 #pragma unroll
-        for (int ks = 0; ks < LS_BK / 16; ++ks) {
-            const int c = 2 * ks + (lane >> 5);
-            bf16x8_t fh[2], fl[2], fb[NB][NJ];
+            for (int ks = 0; ks < KS; ++ks) {
+                const int c = 2 * ks + (lane >> 5);
 #pragma unroll
-            for (int i = 0; i < 2; ++i) {
-                const int r = wm * 64 + i * 32 + (lane & 31);
-                const int off = r * LS_ROWB + ((c ^ ls_swz(r)) << 4);
-                fh[i] = *(const bf16x8_t *)(ah + off);
-                fl[i] = *(const bf16x8_t *)(al + off);
-            }
-#pragma unroll
-            for (int b = 0; b < NB; ++b)
-#pragma unroll
-                for (int j = 0; j < NJ; ++j) {
-                    const int r = b * BN + wn * (BN / 2) + j * 32 + (lane & 31);
-                    fb[b][j] = *(const bf16x8_t *)(bb + r * LS_ROWB + ((c ^ ls_swz(r)) << 4));
+                for (int i = 0; i < 2; ++i) {
+                    const int r = wm * 64 + i * 32 + (lane & 31);
+                    const int off = r * LS_ROWB + ((c ^ ls_swz(r)) << 4);
+                    fh[ks][i] = *(const bf16x8_t *)(ah + off);
+                    fl[ks][i] = *(const bf16x8_t *)(al + off);
                 }
 #pragma unroll
-            for (int b = 0; b < NB; ++b)
-#pragma unroll
-                for (int i = 0; i < 2; ++i)
+                for (int b = 0; b < NB; ++b)
 #pragma unroll
                     for (int j = 0; j < NJ; ++j) {
-                        acc[b][i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fh[i], fb[b][j], acc[b][i][j], 0, 0, 0);
-                        acc[b][i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fl[i], fb[b][j], acc[b][i][j], 0, 0, 0);
+                        const int r = b * BN + wn * (BN / 2) + j * 32 + (lane & 31);
+                        fb[ks][b][j] = *(const bf16x8_t *)(bb + r * LS_ROWB + ((c ^ ls_swz(r)) << 4));
                     }
+            }
+            // hi products of every accumulator, then the lo ones:
+            // consecutive MFMAs never chain on one accumulator
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+                for (int p = 0; p < 2; ++p)
+#pragma unroll
+                    for (int b = 0; b < NB; ++b)
+#pragma unroll
+                        for (int i = 0; i < 2; ++i)
+#pragma unroll
+                            for (int j = 0; j < NJ; ++j)
+                                acc[b][i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                                    p ? fl[ks][i] : fh[ks][i], fb[ks][b][j], acc[b][i][j], 0, 0, 0);
+            // step 0's reads, then step 0's MFMAs with one of step 1's reads
+            // after every MF / RD of them, then step 1's MFMAs (the one-row-
+            // tile form, 5 reads for 4 MFMAs, keeps the default order)
+            if constexpr (MF % RD == 0) {
+                __builtin_amdgcn_sched_group_barrier(0x100, RD, 0);
+#pragma unroll
+                for (int q = 0; q < RD; ++q) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, MF / RD, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                }
+                __builtin_amdgcn_sched_group_barrier(0x008, MF, 0);
+            }
+        } else {
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) {
+                const int c = 2 * ks + (lane >> 5);
+                bf16x8_t fh[2], fl[2], fb[NB][NJ];
+#pragma unroll
+                for (int i = 0; i < 2; ++i) {
+                    const int r = wm * 64 + i * 32 + (lane & 31);
+                    const int off = r * LS_ROWB + ((c ^ ls_swz(r)) << 4);
+                    fh[i] = *(const bf16x8_t *)(ah + off);
+                    fl[i] = *(const bf16x8_t *)(al + off);
+                }
+#pragma unroll
+                for (int b = 0; b < NB; ++b)
+#pragma unroll
+                    for (int j = 0; j < NJ; ++j) {
+                        const int r = b * BN + wn * (BN / 2) + j * 32 + (lane & 31);
+                        fb[b][j] = *(const bf16x8_t *)(bb + r * LS_ROWB + ((c ^ ls_swz(r)) << 4));
+                    }
+#pragma unroll
+                for (int b = 0; b < NB; ++b)
+#pragma unroll
+                    for (int i = 0; i < 2; ++i)
+#pragma unroll
+                        for (int j = 0; j < NJ; ++j) {
+                            acc[b][i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fh[i], fb[b][j], acc[b][i][j], 0, 0, 0);
+                            acc[b][i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fl[i], fb[b][j], acc[b][i][j], 0, 0, 0);
+                        }
+            }
         }
     }
 
