@@ -130,8 +130,9 @@ void launch_rmsnorm(const float *x, const float *gamma, float eps, int M, int H,
 // attention.rs:306-326: q/k/v projections (+bias, + unmerged LoRA as in
 // lora.rs:93-97), optional QK RMSNorm over head_dim (:312-319), split-half
 // RoPE at the row's absolute position (:99-123), then K/V appended to the
-// cache (:126-148). A block owns a group of heads (one thread per head
-// element) and up to ROPE_ROWS consecutive token rows: every row's loads
+// cache (:126-148). General form (any head_dim up to 256, mixed adapter
+// ranks): a block owns a group of heads (one thread per head element) and
+// up to ROPE_ROWS consecutive token rows: every row's loads
 // are issued before any is used, each thread's LoRA-B row (first ROPE_BREG
 // ranks) is loaded once into registers, and the rows' LoRA t values are
 // staged in LDS.
@@ -240,8 +241,168 @@ __global__ void __launch_bounds__(256) rope_kv_k(RopeKvArgs a, int rows_per_bloc
     }
 }
 
+
+// Pair form (head_dim 128, every adapter of the layer of rank R or none):
+// a thread owns the RoPE pair (d, d + 64) of one head, so the rotation
+// needs no exchange, and a head is exactly one wave, so its target (q, k or
+// v) and the row's LoRA t values are wave-uniform and the QK RMSNorm is a
+// wave reduction. B's two rows per thread sit in registers. Rows go RK2_RB
+// at a time, every load of a batch issued before its first use.
+constexpr int RK2_RB = 8;
+
+template <int R, typename WT> __device__ __forceinline__ void rk2_brow(const WT *B, size_t row, float *b) {
+    if constexpr (sizeof(WT) == 2) {
+        const uint4 *p = (const uint4 *)((const uint16_t *)B + row * R);
+#pragma unroll
+        for (int k = 0; k < R / 8; ++k) {
+            const uint4 u = p[k];
+            const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+            for (int e = 0; e < 8; ++e) b[k * 8 + e] = __uint_as_float((e & 1 ? w[e >> 1] >> 16 : w[e >> 1] & 0xffffu) << 16);
+        }
+    } else {
+        const float4 *p = (const float4 *)((const float *)B + row * R);
+#pragma unroll
+        for (int k = 0; k < R / 4; ++k) {
+            const float4 u = p[k];
+            b[k * 4] = u.x; b[k * 4 + 1] = u.y; b[k * 4 + 2] = u.z; b[k * 4 + 3] = u.w;
+        }
+    }
+}
+
+template <typename WT, typename KT, int R>
+__global__ void __launch_bounds__(256) rope_kv2_k(const RopeKvArgs a, int rows_per_block) {
+    constexpr int HD = 128, HALF = 64;
+    const int p = threadIdx.x & 63;
+    const int head = blockIdx.y * 4 + (threadIdx.x >> 6);
+    const int total = a.nq + 2 * a.nkv;
+    if (head >= total) return;  // no barriers below
+    const int target = __builtin_amdgcn_readfirstlane(head < a.nq ? 0 : (head < a.nq + a.nkv ? 1 : 2));
+    const int hbase = target == 0 ? 0 : (target == 1 ? a.nq : a.nq + a.nkv);
+    const int qw = a.nq * HD, kvw = a.nkv * HD;
+    const int off = target == 0 ? 0 : (target == 1 ? qw : qw + kvw);
+    const int hl = head - hbase;  // head within its target
+    const int c0 = off + hl * HD + p, c1 = c0 + HALF;
+    const float *__restrict__ qkv = a.qkv;
+    const float *__restrict__ cs = a.rope_cos;
+    const float *__restrict__ sn = a.rope_sin;
+    const int32_t *__restrict__ rpos = a.rows.row_pos;
+    const int32_t *__restrict__ rseq = a.rows.row_seq;
+    KT *__restrict__ cache = (KT *)a.kv;
+
+    const WT *B = R ? (const WT *)a.lora_b[target] : nullptr;
+    const bool lora = R && B && a.lora_rank[target] == R;
+    const int tcol = a.lora_t_col[target];
+    const float lsc = a.lora_scale[target];
+    float b0[R ? R : 1], b1[R ? R : 1];
+    if constexpr (R > 0) {
+        if (lora) {
+            rk2_brow<R>(B, (size_t)(c0 - off), b0);
+            rk2_brow<R>(B, (size_t)(c1 - off), b1);
+        }
+    }
+    const float *g = target == 0 ? a.q_norm : (target == 1 ? a.k_norm : nullptr);
+    const float g0 = g ? g[p] : 0.f, g1 = g ? g[p + HALF] : 0.f;
+
+    const int m0 = blockIdx.x * rows_per_block;
+    const int nr = min(a.rows.M - m0, rows_per_block);
+    for (int rb = 0; rb < nr; rb += RK2_RB) {
+        float x0[RK2_RB], x1[RK2_RB];
+        int pos[RK2_RB], sq[RK2_RB];
+#pragma unroll
+        for (int r = 0; r < RK2_RB; ++r) {
+            const int m = m0 + min(rb + r, nr - 1);
+            x0[r] = qkv[(size_t)m * a.ldq + c0];
+            x1[r] = qkv[(size_t)m * a.ldq + c1];
+            pos[r] = rpos[m];
+            sq[r] = rseq[m];
+        }
+        // LoRA: x += scale * B t (the row's t values are uniform loads)
+        if constexpr (R > 0) {
+            if (lora) {
+#pragma unroll
+                for (int r = 0; r < RK2_RB; ++r) {
+                    const int m = m0 + min(rb + r, nr - 1);
+                    const float *__restrict__ t = qkv + (size_t)m * a.ldq + tcol;
+                    float acc0 = 0.f, acc1 = 0.f;
+#pragma unroll
+                    for (int i = 0; i < R; ++i) {
+                        const float ti = t[i];
+                        acc0 += b0[i] * ti;
+                        acc1 += b1[i] * ti;
+                    }
+                    x0[r] = x0[r] + acc0 * lsc;
+                    x1[r] = x1[r] + acc1 * lsc;
+                }
+            }
+        }
+        // QK RMSNorm over the head's 128 values: a wave reduction
+        if (g) {
+#pragma unroll
+            for (int r = 0; r < RK2_RB; ++r) {
+                float ss = x0[r] * x0[r] + x1[r] * x1[r];
+#pragma unroll
+                for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
+                const float rms = sqrtf(ss / (float)HD + a.eps);
+                x0[r] = (x0[r] / rms) * g0;
+                x1[r] = (x1[r] / rms) * g1;
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < RK2_RB; ++r) {
+            if (rb + r >= nr) break;
+            const int m = m0 + rb + r;
+            if (target < 2) {
+                const size_t tb = (size_t)pos[r] * HD + p;
+                const float y0 = x0[r] * cs[tb] + (-x1[r]) * sn[tb];
+                const float y1 = x1[r] * cs[tb + HALF] + x0[r] * sn[tb + HALF];
+                if (target == 0) {
+                    float *q = a.q_out + (size_t)m * qw + head * HD;
+                    q[p] = y0;
+                    q[p + HALF] = y1;
+                } else {
+                    const size_t ci = (size_t)sq[r] * a.seq_stride + (size_t)hl * a.head_stride + (size_t)pos[r] * HD + p;
+                    st(cache, ci, y0);
+                    st(cache, ci + HALF, y1);
+                }
+            } else {
+                const size_t ci = (size_t)sq[r] * a.seq_stride + a.kv_half_stride + (size_t)hl * a.head_stride +
+                                  (size_t)pos[r] * HD + p;
+                st(cache, ci, x0[r]);
+                st(cache, ci + HALF, x1[r]);
+            }
+        }
+    }
+}
+
+template <typename WT, typename KT>
+static bool rope_kv2_launch(const RopeKvArgs &a, hipStream_t s) {
+    int rank = 0;
+    for (int j = 0; j < 3; ++j) {
+        if (!a.lora_b[j] || !a.lora_rank[j]) continue;
+        if (rank && a.lora_rank[j] != rank) return false;
+        rank = a.lora_rank[j];
+    }
+    const int rpb = a.rows.M >= 1024 ? 32 : (a.rows.M >= 128 ? 8 : 1);
+    dim3 grid((a.rows.M + rpb - 1) / rpb, (a.nq + 2 * a.nkv + 3) / 4);
+    switch (rank) {
+    case 0: rope_kv2_k<WT, KT, 0><<<grid, 256, 0, s>>>(a, rpb); return true;
+    case 8: rope_kv2_k<WT, KT, 8><<<grid, 256, 0, s>>>(a, rpb); return true;
+    case 16: rope_kv2_k<WT, KT, 16><<<grid, 256, 0, s>>>(a, rpb); return true;
+    case 32: rope_kv2_k<WT, KT, 32><<<grid, 256, 0, s>>>(a, rpb); return true;
+    default: return false;
+    }
+}
+
 void launch_rope_kv(Dt wt, Dt kvdt, const RopeKvArgs &a, hipStream_t s) {
     if (a.hd > 256) fail(ESP_UNSUPPORTED, "head_dim: values above 256 are not implemented");
+    if (a.hd == 128) {
+        bool done = false;
+        if (wt == DT_BF16 && kvdt == DT_F16) done = rope_kv2_launch<uint16_t, _Float16>(a, s);
+        else if (wt == DT_BF16 && kvdt == DT_F32) done = rope_kv2_launch<uint16_t, float>(a, s);
+        else if (wt == DT_F32 && kvdt == DT_F32) done = rope_kv2_launch<float, float>(a, s);
+        if (done) return;
+    }
     const int hpi = 256 / a.hd;
     // contiguous span of LoRA t columns read by this layer
     int t_lo = 0, t_hi = 0;

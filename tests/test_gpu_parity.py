@@ -275,6 +275,7 @@ DECODE_VARIANTS = {
     "qwen3_qknorm": ({"model_type": "qwen3", "architectures": ["Qwen3ForCausalLM"],
                       "layer_types": ["sliding_attention", "full_attention"],
                       "sliding_window": 4, "use_sliding_window": True}, 64, 8, 2),
+    "qwen3_qknorm_hd128": ({"model_type": "qwen3", "architectures": ["Qwen3ForCausalLM"]}, 128, 4, 2),
     "llama_tied": ({"tie_word_embeddings": True}, 64, 4, 4),
 }
 
@@ -462,6 +463,33 @@ def test_lora_unmerged_matches_merged_oracle(fmt, prompt_len):
         ids.append(int(np.argmax(logits)))
         logits = model.try_forward_cached_last([ids[-1]], kv2)
     assert model.generate_greedy_device(model.new_cache(1, ctx), prompt, 6, eos=[]) == ids
+
+
+@pytest.mark.parametrize("fmt", ["f32", "bf16"])
+@pytest.mark.parametrize("rank", [8, 16, 32])
+def test_lora_head_dim_128_pair_form(fmt, rank):
+    """The head-dim-128 rotary/KV kernel (one wave per head, adapter rows in
+    registers, one instantiation per rank) with one adapter on q, k and v:
+    prefills of 300 rows (eight-row blocks) and 1100 rows (32-row blocks)
+    against the oracle's merged weights (lora.rs:99-217)."""
+    from esp_amd.model import LoraAdapter
+    cfg = synth.llama_config(2, 256, 4, 2, 320, 500, head_dim=128, max_pos=1200)
+    tensors = synth.make_tensors(cfg, 67, fmt, std=0.05)
+    targets = ["q_proj", "k_proj", "v_proj"]
+    ad = _adapter(cfg, rank, targets, 3, fmt)
+    model = DecoderModel.from_bytes(cfg, st.dump(tensors), fmt,
+                                    adapters=[LoraAdapter(rank, 2.0 * rank, targets, st.dump(ad))])
+    merged = oracle.apply_lora(cfg, tensors, {"rank": rank, "alpha": 2.0 * rank, "targets": targets,
+                                              "tensors": ad})
+    ref = oracle.OracleModel(cfg, merged)
+    for n in (300, 1100):
+        prompt = synth.uniform_ids(9 + n, n, cfg.vocab_size)
+        got = model.try_forward_cached_last(prompt, model.new_cache(1, n + 4))
+        want = ref.forward_last(ref.new_cache(n + 4), prompt)
+        if fmt == "f32":
+            assert np.abs(got - want).max() <= 1e-4 * float(np.abs(want).max()), n
+        else:
+            assert _close_bf16(got, want), (n, float(np.abs(got - want).max()))
 
 
 @pytest.mark.parametrize("protocol", ["xcd", "agent"])
