@@ -242,12 +242,14 @@ __global__ void __launch_bounds__(256) rope_kv_k(RopeKvArgs a, int rows_per_bloc
 }
 
 
-// Pair form (head_dim 128, every adapter of the layer of rank R or none):
-// a thread owns the RoPE pair (d, d + 64) of one head, so the rotation
-// needs no exchange, and a head is exactly one wave, so its target (q, k or
-// v) and the row's LoRA t values are wave-uniform and the QK RMSNorm is a
-// wave reduction. B's two rows per thread sit in registers. Rows go RK2_RB
-// at a time, every load of a batch issued before its first use.
+// Pair form (head_dim 64 or 128, every adapter of the layer of rank R or
+// none): a thread owns the RoPE pair (d, d + hd/2) of one head, so the
+// rotation needs no exchange. A head is one wave (hd 128) or half of one
+// (hd 64, the query and kv head counts even, so the two heads of a wave
+// share their target): the target (q, k or v) and the row's LoRA t values
+// are wave-uniform, and the QK RMSNorm is a reduction within the head's
+// lanes. B's two rows per thread sit in registers. Rows go RK2_RB at a
+// time, every load of a batch issued before its first use.
 constexpr int RK2_RB = 8;
 
 template <int R, typename WT> __device__ __forceinline__ void rk2_brow(const WT *B, size_t row, float *b) {
@@ -270,11 +272,11 @@ template <int R, typename WT> __device__ __forceinline__ void rk2_brow(const WT 
     }
 }
 
-template <typename WT, typename KT, int R>
+template <typename WT, typename KT, int R, int HD>
 __global__ void __launch_bounds__(256) rope_kv2_k(const RopeKvArgs a, int rows_per_block) {
-    constexpr int HD = 128, HALF = 64;
-    const int p = threadIdx.x & 63;
-    const int head = blockIdx.y * 4 + (threadIdx.x >> 6);
+    constexpr int HALF = HD / 2, HPB = 256 / HALF;  // lanes per head, heads per block
+    const int p = threadIdx.x % HALF;
+    const int head = blockIdx.y * HPB + threadIdx.x / HALF;
     const int total = a.nq + 2 * a.nkv;
     if (head >= total) return;  // no barriers below
     const int target = __builtin_amdgcn_readfirstlane(head < a.nq ? 0 : (head < a.nq + a.nkv ? 1 : 2));
@@ -336,13 +338,13 @@ __global__ void __launch_bounds__(256) rope_kv2_k(const RopeKvArgs a, int rows_p
                 }
             }
         }
-        // QK RMSNorm over the head's 128 values: a wave reduction
+        // QK RMSNorm over the head's values: a reduction within its lanes
         if (g) {
 #pragma unroll
             for (int r = 0; r < RK2_RB; ++r) {
                 float ss = x0[r] * x0[r] + x1[r] * x1[r];
 #pragma unroll
-                for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
+                for (int o = HALF / 2; o > 0; o >>= 1) ss += __shfl_xor(ss, o, HALF);
                 const float rms = sqrtf(ss / (float)HD + a.eps);
                 x0[r] = (x0[r] / rms) * g0;
                 x1[r] = (x1[r] / rms) * g1;
@@ -375,8 +377,10 @@ __global__ void __launch_bounds__(256) rope_kv2_k(const RopeKvArgs a, int rows_p
     }
 }
 
-template <typename WT, typename KT>
+template <typename WT, typename KT, int HD>
 static bool rope_kv2_launch(const RopeKvArgs &a, hipStream_t s) {
+    constexpr int HPB = 256 / (HD / 2);
+    if (HD == 64 && (a.nq % 2 || a.nkv % 2)) return false;  // two heads per wave share a target
     int rank = 0;
     for (int j = 0; j < 3; ++j) {
         if (!a.lora_b[j] || !a.lora_rank[j]) continue;
@@ -384,25 +388,29 @@ static bool rope_kv2_launch(const RopeKvArgs &a, hipStream_t s) {
         rank = a.lora_rank[j];
     }
     const int rpb = a.rows.M >= 1024 ? 32 : (a.rows.M >= 128 ? 8 : 1);
-    dim3 grid((a.rows.M + rpb - 1) / rpb, (a.nq + 2 * a.nkv + 3) / 4);
+    dim3 grid((a.rows.M + rpb - 1) / rpb, (a.nq + 2 * a.nkv + HPB - 1) / HPB);
     switch (rank) {
-    case 0: rope_kv2_k<WT, KT, 0><<<grid, 256, 0, s>>>(a, rpb); return true;
-    case 8: rope_kv2_k<WT, KT, 8><<<grid, 256, 0, s>>>(a, rpb); return true;
-    case 16: rope_kv2_k<WT, KT, 16><<<grid, 256, 0, s>>>(a, rpb); return true;
-    case 32: rope_kv2_k<WT, KT, 32><<<grid, 256, 0, s>>>(a, rpb); return true;
+    case 0: rope_kv2_k<WT, KT, 0, HD><<<grid, 256, 0, s>>>(a, rpb); return true;
+    case 8: rope_kv2_k<WT, KT, 8, HD><<<grid, 256, 0, s>>>(a, rpb); return true;
+    case 16: rope_kv2_k<WT, KT, 16, HD><<<grid, 256, 0, s>>>(a, rpb); return true;
+    case 32: rope_kv2_k<WT, KT, 32, HD><<<grid, 256, 0, s>>>(a, rpb); return true;
     default: return false;
     }
 }
 
 void launch_rope_kv(Dt wt, Dt kvdt, const RopeKvArgs &a, hipStream_t s) {
     if (a.hd > 256) fail(ESP_UNSUPPORTED, "head_dim: values above 256 are not implemented");
+    bool done = false;
     if (a.hd == 128) {
-        bool done = false;
-        if (wt == DT_BF16 && kvdt == DT_F16) done = rope_kv2_launch<uint16_t, _Float16>(a, s);
-        else if (wt == DT_BF16 && kvdt == DT_F32) done = rope_kv2_launch<uint16_t, float>(a, s);
-        else if (wt == DT_F32 && kvdt == DT_F32) done = rope_kv2_launch<float, float>(a, s);
-        if (done) return;
+        if (wt == DT_BF16 && kvdt == DT_F16) done = rope_kv2_launch<uint16_t, _Float16, 128>(a, s);
+        else if (wt == DT_BF16 && kvdt == DT_F32) done = rope_kv2_launch<uint16_t, float, 128>(a, s);
+        else if (wt == DT_F32 && kvdt == DT_F32) done = rope_kv2_launch<float, float, 128>(a, s);
+    } else if (a.hd == 64) {
+        if (wt == DT_BF16 && kvdt == DT_F16) done = rope_kv2_launch<uint16_t, _Float16, 64>(a, s);
+        else if (wt == DT_BF16 && kvdt == DT_F32) done = rope_kv2_launch<uint16_t, float, 64>(a, s);
+        else if (wt == DT_F32 && kvdt == DT_F32) done = rope_kv2_launch<float, float, 64>(a, s);
     }
+    if (done) return;
     const int hpi = 256 / a.hd;
     // contiguous span of LoRA t columns read by this layer
     int t_lo = 0, t_hi = 0;

@@ -467,13 +467,14 @@ def test_lora_unmerged_matches_merged_oracle(fmt, prompt_len):
 
 @pytest.mark.parametrize("fmt", ["f32", "bf16"])
 @pytest.mark.parametrize("rank", [8, 16, 32])
-def test_lora_head_dim_128_pair_form(fmt, rank):
-    """The head-dim-128 rotary/KV kernel (one wave per head, adapter rows in
-    registers, one instantiation per rank) with one adapter on q, k and v:
-    prefills of 300 rows (eight-row blocks) and 1100 rows (32-row blocks)
-    against the oracle's merged weights (lora.rs:99-217)."""
+@pytest.mark.parametrize("hd", [64, 128])
+def test_lora_pair_form(fmt, rank, hd):
+    """The pair-form rotary/KV kernel (a head per wave or half-wave, adapter
+    rows in registers, one instantiation per rank) with one adapter on q, k
+    and v: prefills of 300 rows (eight-row blocks) and 1100 rows (32-row
+    blocks) against the oracle's merged weights (lora.rs:99-217)."""
     from esp_amd.model import LoraAdapter
-    cfg = synth.llama_config(2, 256, 4, 2, 320, 500, head_dim=128, max_pos=1200)
+    cfg = synth.llama_config(2, 256, 4, 2, 320, 500, head_dim=hd, max_pos=1200)
     tensors = synth.make_tensors(cfg, 67, fmt, std=0.05)
     targets = ["q_proj", "k_proj", "v_proj"]
     ad = _adapter(cfg, rank, targets, 3, fmt)
