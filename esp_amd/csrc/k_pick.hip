@@ -50,7 +50,8 @@ struct PickRow {
     int flags;
 };
 
-// Per-call scratch: [n][cap] sorted candidates | [n][cap] weights |
+// Per-call scratch: [n][cap] sorted candidates | [n][cap] weights (first
+// pick_k's list of the ids it weighs, then the sorted weights) |
 // big-bucket temp [cap] | [n][PB_BINS] bucket start | [n][PB_BINS] bucket
 // count | [n] PickRow | small, medium and big bucket lists [n * PB_BINS]
 // each | counters [4] (small, big, medium).
@@ -152,23 +153,6 @@ __device__ void bitonic(Cand *buf, int n) {
     }
 }
 
-// row[i4 + q] = v[q] for ids below V (rows of ps.wts are cap-aligned).
-__device__ __forceinline__ void store4(float *row, int V, int i4, const float (&v)[4]) {
-    typedef float f4_t __attribute__((ext_vector_type(4)));
-    if (i4 + 3 < V) {
-        f4_t x;
-        x.x = v[0];
-        x.y = v[1];
-        x.z = v[2];
-        x.w = v[3];
-        *(f4_t *)(row + i4) = x;
-    } else {
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-            if (i4 + q < V) row[i4 + q] = v[q];
-    }
-}
-
 // v[q] = row[i4 + q] for ids below V (row 16-byte aligned when V % 4 == 0).
 __device__ __forceinline__ void load4(const float *row, int V, int i4, float (&v)[4]) {
     typedef float f4_t __attribute__((ext_vector_type(4)));
@@ -188,18 +172,27 @@ __global__ void __launch_bounds__(PICK_THREADS) pick_k(PickArgs a) {
     extern __shared__ Cand lds[];
     __shared__ float red_f[32];
     __shared__ int red_i[32];
-    __shared__ int s_count, s_zmax, s_bad, s_elig, s_wbase, s_mbase;
+    __shared__ int s_count, s_zmax, s_bad, s_elig, s_wbase, s_mbase, s_ncand;
     __shared__ int s_scan[33];
     const int row = blockIdx.x;
     const int V = a.V;
     const float *L = a.logits + (size_t)row * V;
     const uint32_t *bits = a.allowed ? a.allowed + (size_t)row * ((V + 31) / 32) : nullptr;
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const esp_sampler *smp = a.samplers ? a.samplers + row : nullptr;
+    const bool sampled = smp && smp->temperature > 0.f;
+    // sampled rows list the ids whose weight pass 2 computes (every id not
+    // masked to -inf), in the row's weight scratch; the later passes walk
+    // that list instead of the vocabulary
+    int32_t *list = sampled ? (int32_t *)(pick_layout(a.scratch, a.n, V).wts +
+                                          (size_t)row * pick_cap(V))
+                            : nullptr;
     if (tid == 0) {
         s_count = 0;
         s_zmax = -1;
         s_bad = 0;
         s_elig = 0;
+        s_ncand = 0;
     }
     __syncthreads();
     // pass 1: mask, finiteness, greedy best and max. Each thread takes four
@@ -207,22 +200,41 @@ __global__ void __launch_bounds__(PICK_THREADS) pick_k(PickArgs a) {
     // two groups in flight.
     float best = -INFINITY;
     int best_id = 0x7fffffff;
-    int bad = 0, elig = 0;
+    int bad = 0, elig = 0, zmax = -1;
     auto scan4 = [&](int i4, const float (&v4)[4]) {
         const uint32_t bw = bits && i4 < V ? bits[i4 >> 5] : 0u;
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             const int i = i4 + q;
-            if (i >= V) break;
+            const bool in = i < V;
             float v = v4[q];
             bool fin = isfinite(v);
-            bad |= !fin;
             bool allowed = bits ? ((bw >> (i & 31)) & 1u) : true;
-            if (bits ? (!allowed || !fin) : isnan(v)) v = -INFINITY;
-            elig += (allowed && fin);
-            if (v > best || (v == best && i < best_id)) {
-                best = v;
-                best_id = i;
+            // pass 2's value: masked or non-finite ids of a masked row are -inf
+            const float v2 = bits && (!allowed || !fin) ? -INFINITY : v;
+            if (in) {
+                bad |= !fin;
+                if (bits ? (!allowed || !fin) : isnan(v)) v = -INFINITY;
+                elig += (allowed && fin);
+                if (v > best || (v == best && i < best_id)) {
+                    best = v;
+                    best_id = i;
+                }
+            }
+            if (list) {
+                // weight 0 without an exp: the largest such id is the
+                // fall-through of an uncut list; every other id is listed
+                const bool cand = in && v2 != -INFINITY;
+                if (in && !cand) zmax = i;  // ids rise along this thread's walk
+                const uint64_t bm = __ballot(cand);
+                if (bm) {
+                    const uint64_t act = __ballot(1);
+                    const int leader = __ffsll((unsigned long long)act) - 1;
+                    int base = 0;
+                    if (lane == leader) base = atomicAdd(&s_ncand, __popcll(bm));
+                    base = __shfl(base, leader);
+                    if (cand) list[base + __popcll(bm & ((1ull << lane) - 1ull))] = i;
+                }
             }
         }
     };
@@ -260,8 +272,6 @@ __global__ void __launch_bounds__(PICK_THREADS) pick_k(PickArgs a) {
     const float mx = red_f[0];
     uint8_t flags = (s_bad ? ESP_PICK_NONFINITE : 0) |
                     ((bits && s_elig == 0) ? ESP_PICK_NO_ELIGIBLE : 0);
-    const esp_sampler *smp = a.samplers ? a.samplers + row : nullptr;
-    const bool sampled = smp && smp->temperature > 0.f;
     if (!sampled || (bits && s_elig == 0)) {
         if (tid == 0) {
             a.ids_out[row] = (bits && s_elig == 0) ? 0u : (uint32_t)(red_i[0] == 0x7fffffff ? 0 : red_i[0]);
@@ -270,45 +280,27 @@ __global__ void __launch_bounds__(PICK_THREADS) pick_k(PickArgs a) {
         }
         return;
     }
-    // pass 2: every weight once (stored per row), the candidate count, the
-    // largest zero-weight id (the fall-through of an uncut list) and the
-    // weight-bucket histogram of the candidates
+    // pass 2 over the listed ids: their weights (the exp is recomputed,
+    // bit for bit, wherever a weight is needed again), the candidate count
+    // (weights > 0), the largest zero-weight id (pass 1's, or an exp that
+    // underflows) and the weight-bucket histogram of the candidates
     const float inv_t = 1.0f / smp->temperature;
     const PickScratch ps = pick_layout(a.scratch, a.n, V);
-    float *wrow = ps.wts + (size_t)row * ps.cap;
+    const int ncand = s_ncand;
+    auto weight = [&](int i) { return (float)exp((double)((L[i] - mx) * inv_t)); };
     int *hist = (int *)lds, *cur = hist + PB_BINS;
     for (int d = tid; d < PB_BINS; d += blockDim.x) hist[d] = 0;
     __syncthreads();
-    int cnt = 0, zmax = -1;
-    auto weigh4 = [&](int i4, const float (&v4)[4]) {
-        if (i4 >= V) return;
-        const uint32_t bw = bits ? bits[i4 >> 5] : 0u;
-        float w4[4];
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const int i = i4 + q;
-            float v = v4[q];
-            bool allowed = bits ? ((bw >> (i & 31)) & 1u) : true;
-            if (bits && (!allowed || !isfinite(v))) v = -INFINITY;
-            const float w = v == -INFINITY ? 0.f : (float)exp((double)((v - mx) * inv_t));
-            w4[q] = w;
-            if (i < V) {
-                if (w > 0.f) {
-                    ++cnt;
-                    atomicAdd(&hist[wbucket(w)], 1);
-                } else if (w == 0.f) {
-                    zmax = i;  // ids rise along this thread's walk
-                }
-            }
+    int cnt = 0;
+    for (int k = tid; k < ncand; k += blockDim.x) {
+        const int i = list[k];
+        const float w = weight(i);
+        if (w > 0.f) {
+            ++cnt;
+            atomicAdd(&hist[wbucket(w)], 1);
+        } else if (w == 0.f) {
+            zmax = max(zmax, i);
         }
-        store4(wrow, V, i4, w4);
-    };
-    for (int i4 = tid * 4; i4 < V; i4 += 8 * (int)blockDim.x) {
-        float a4[4], b4[4];
-        load4(L, V, i4, a4);
-        load4(L, V, i4 + 4 * (int)blockDim.x, b4);
-        weigh4(i4, a4);
-        weigh4(i4 + 4 * (int)blockDim.x, b4);
     }
     cnt = (int)wave_sum((float)cnt);
 #pragma unroll
@@ -395,16 +387,10 @@ __global__ void __launch_bounds__(PICK_THREADS) pick_k(PickArgs a) {
         }
         __syncthreads();
         Cand *dst = ps.cand + (size_t)row * ps.cap;
-        for (int i4 = tid * 4; i4 < V; i4 += 8 * (int)blockDim.x) {
-            float a4[4], b4[4];
-            load4(wrow, V, i4, a4);
-            load4(wrow, V, i4 + 4 * (int)blockDim.x, b4);
-#pragma unroll
-            for (int q = 0; q < 8; ++q) {
-                const int i = (q < 4 ? i4 : i4 + 4 * (int)blockDim.x) + (q & 3);
-                const float w = q < 4 ? a4[q & 3] : b4[q & 3];
-                if (i < V && w > 0.f) dst[atomicAdd(&cur[wbucket(w)], 1)] = Cand{w, i};
-            }
+        for (int k = tid; k < ncand; k += blockDim.x) {
+            const int i = list[k];
+            const float w = weight(i);
+            if (w > 0.f) dst[atomicAdd(&cur[wbucket(w)], 1)] = Cand{w, i};
         }
         if (tid == 0) ps.info[row] = PickRow{C, s_zmax, 1, flags};
         return;
@@ -415,12 +401,10 @@ __global__ void __launch_bounds__(PICK_THREADS) pick_k(PickArgs a) {
     __syncthreads();
     if (tid == 0) s_count = 0;
     __syncthreads();
-    for (int i4 = tid * 4; i4 < V; i4 += 4 * (int)blockDim.x) {
-        float w4[4];
-        load4(wrow, V, i4, w4);
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-            if (i4 + q < V && w4[q] > 0.f) buf[atomicAdd(&s_count, 1)] = Cand{w4[q], i4 + q};
+    for (int k = tid; k < ncand; k += blockDim.x) {
+        const int i = list[k];
+        const float w = weight(i);
+        if (w > 0.f) buf[atomicAdd(&s_count, 1)] = Cand{w, i};
     }
     __syncthreads();
     for (int i = C + tid; i < n2; i += blockDim.x) buf[i] = Cand{-1.f, 0x7fffffff};
