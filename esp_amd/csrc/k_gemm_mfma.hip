@@ -16,6 +16,7 @@
 // 80 bytes) from register prefetches issued one k-tile ahead. Epilogues:
 // STORE (+bias), RESIDUAL (+=), SWIGLU (out = silu(g) * u).
 #include <cstdlib>
+#include <utility>
 
 #include "common.hpp"
 #include "dev.hpp"
@@ -685,6 +686,228 @@ static void lds_launch(const GemmArgs &a, float *ws, size_t ws_bytes, hipStream_
     mfma_reduce_k<EPI, NB><<<rblocks, 256, 0, s>>>(a, ws, splits);
 }
 
+// ---------------------------------------------------------------------------
+// Skinny streamed form (one row tile of M <= 32 * RB rows, no groups): each
+// block owns 32 * NW weight columns per matrix and one k range. The
+// activation rows of each 32-key stage go global -> LDS (direct loads into a
+// ring of D + 1 stages, read by every wave); each wave streams the weight
+// rows of its own 32 columns global -> registers, D stages ahead, and
+// multiplies them by all 32 * RB rows. The weights then need no LDS room or
+// LDS bandwidth, and the bytes in flight per CU (NW * D * NB * 2 KB per
+// block) are set by registers, not by the stage ring. The k range of a block
+// is a multiple of D stages: every stage of a steady group issues stage
+// kt + D unconditionally and the last group issues none, so every vmcnt wait
+// is an exact constant (conditional loads would make the compiler wait for
+// all loads in flight at each group's first use).
+template <int N, typename F, int... I>
+__device__ __forceinline__ void static_for_impl(F &&f, std::integer_sequence<int, I...>) {
+    (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, typename F> __device__ __forceinline__ void static_for(F &&f) {
+    static_for_impl<N>(f, std::make_integer_sequence<int, N>{});
+}
+
+template <int EPI, int NB, int RB, int NW, int D>
+__global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
+    gemm_skinny_k(GemmArgs g, float *ws, int k_per_split) {
+    constexpr int ROWS = 32 * RB;
+    constexpr int APL = ROWS * LS_ROWB;  // one A plane of a stage
+    constexpr int AST = 2 * APL;         // one stage (hi + lo planes)
+    constexpr int AQ = 4 * RB;           // 1 KB direct loads per stage
+    static_assert(AQ % NW == 0, "the stage's A loads split evenly over the waves");
+    constexpr int LA = AQ / NW;          // A loads per wave and stage
+    constexpr int LPS = LA + 2 * NB;     // loads per wave and stage
+    static_assert(D >= 2 && (D - 1) * LPS < 64, "waits count up to D - 1 later stages");
+    extern __shared__ __attribute__((aligned(16))) char lds_s[];
+    const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+    const int M = g.M, N = g.N, K = g.K;
+    const int n0 = blockIdx.x * 32 * NW;
+    const int kbeg = blockIdx.z * k_per_split;
+    const int KT = (min(K, kbeg + k_per_split) - kbeg) / LS_BK;  // a multiple of D
+
+    // A: wave-instruction q covers slots (q mod 2RB) * 64 + lane of plane
+    // q / 2RB (16 rows x 4 chunks, chunk c of row r at slot c ^ swz(r));
+    // rows past M re-read row M - 1
+    const uint16_t *asrc[LA];
+    int adst[LA];
+#pragma unroll
+    for (int j = 0; j < LA; ++j) {
+        const int q = wave * LA + j, p = q / (2 * RB), qq = q % (2 * RB);
+        const int sl = qq * 64 + lane, r = sl >> 2, kc = (sl & 3) ^ ls_swz(r);
+        asrc[j] = (const uint16_t *)(p ? g.a_lo : g.a) + (size_t)min(r, M - 1) * K + kbeg + kc * 8;
+        adst[j] = p * APL + qq * 1024;
+    }
+    // weights: the MFMA B-operand layout, lane = (column lane & 31, keys
+    // 8 * (lane >> 5) .. + 8 of each 16-key step); columns past N re-read N - 1
+    const uint16_t *wsrc[NB];
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+        const int n = min(n0 + wave * 32 + (lane & 31), N - 1);
+        wsrc[b] = (const uint16_t *)(b ? g.w2 : g.w) + (size_t)n * K + kbeg + (lane >> 5) * 8;
+    }
+    auto issue_a = [&](int kt, int slot) {
+        char *base = lds_s + slot * AST;
+#pragma unroll
+        for (int j = 0; j < LA; ++j)
+            __builtin_amdgcn_global_load_lds((gptr_t)(asrc[j] + kt * LS_BK), (lptr_t)(base + adst[j]), 16, 0, 0);
+    };
+    auto issue_w = [&](int kt, bf16x8_t (&r)[NB][2]) {
+#pragma unroll
+        for (int b = 0; b < NB; ++b)
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks) r[b][ks] = *(const bf16x8_t *)(wsrc[b] + kt * LS_BK + ks * 16);
+    };
+
+    f32x16_t acc[NB][RB];
+#pragma unroll
+    for (int b = 0; b < NB; ++b)
+#pragma unroll
+        for (int i = 0; i < RB; ++i)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[b][i][e] = 0.f;
+
+    auto stage = [&](int slot, int nslot, bf16x8_t (&w)[NB][2], auto later_c, auto more_c, int kt) {
+        constexpr int LATER = decltype(later_c)::value;
+        constexpr bool MORE = decltype(more_c)::value;
+        // this stage's loads are done once at most LATER stages' remain
+        __builtin_amdgcn_s_waitcnt(vm_imm(LATER * LPS));
+        // every wave's A loads of this stage landed; the previous slot is free
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (MORE) issue_a(kt + D, nslot);
+        __builtin_amdgcn_sched_barrier(0);
+        const char *ah = lds_s + slot * AST, *al = ah + APL;
+        // a k-step's fragment reads, then its MFMAs (both k-steps' reads
+        // first when the registers allow: one matrix)
+        constexpr int KG = NB == 1 ? 2 : 1;
+#pragma unroll
+        for (int g0 = 0; g0 < 2; g0 += KG) {
+            bf16x8_t fh[KG][RB], fl[KG][RB];
+#pragma unroll
+            for (int kk = 0; kk < KG; ++kk) {
+                const int c = 2 * (g0 + kk) + (lane >> 5);
+#pragma unroll
+                for (int i = 0; i < RB; ++i) {
+                    const int r = i * 32 + (lane & 31);
+                    const int off = r * LS_ROWB + ((c ^ ls_swz(r)) << 4);
+                    fh[kk][i] = *(const bf16x8_t *)(ah + off);
+                    fl[kk][i] = *(const bf16x8_t *)(al + off);
+                }
+            }
+            // hi products of every accumulator, then the lo ones
+#pragma unroll
+            for (int kk = 0; kk < KG; ++kk) {
+#pragma unroll
+                for (int b = 0; b < NB; ++b)
+#pragma unroll
+                    for (int i = 0; i < RB; ++i)
+                        acc[b][i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fh[kk][i], w[b][g0 + kk], acc[b][i], 0, 0, 0);
+#pragma unroll
+                for (int b = 0; b < NB; ++b)
+#pragma unroll
+                    for (int i = 0; i < RB; ++i)
+                        acc[b][i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fl[kk][i], w[b][g0 + kk], acc[b][i], 0, 0, 0);
+            }
+            __builtin_amdgcn_sched_group_barrier(0x100, 2 * KG * RB, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, 2 * KG * RB * NB, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (MORE) issue_w(kt + D, w);
+        __builtin_amdgcn_sched_barrier(0);
+    };
+
+    // prologue: stages 0 .. D-1, A then weights per stage
+    bf16x8_t wr[D][NB][2];
+#pragma unroll
+    for (int s = 0; s < D; ++s) {
+        issue_a(s, s);
+        issue_w(s, wr[s]);
+    }
+    int kt = 0, aslot = 0;  // aslot: ring slot of stage kt (D + 1 slots)
+    for (; kt + D < KT; kt += D) {
+#pragma unroll
+        for (int s = 0; s < D; ++s) {
+            const int nslot = aslot == 0 ? D : aslot - 1;  // (kt + s + D) mod (D + 1)
+            stage(aslot, nslot, wr[s], std::integral_constant<int, D - 1>{}, std::true_type{}, kt + s);
+            aslot = aslot == D ? 0 : aslot + 1;
+        }
+    }
+    // last group: no further loads; stage s waits for D - 1 - s later stages
+    static_for<D>([&](auto sc) {
+        constexpr int s = decltype(sc)::value;
+        stage(aslot, 0, wr[s], std::integral_constant<int, D - 1 - s>{}, std::false_type{}, kt + s);
+        aslot = aslot == D ? 0 : aslot + 1;
+    });
+
+    // epilogue: lane holds column (lane & 31) of each 32 x 32 block, rows
+    // (e / 4) * 8 + (lane >> 5) * 4 + e % 4
+    const int col = n0 + wave * 32 + (lane & 31);
+    if (col >= N) return;
+#pragma unroll
+    for (int i = 0; i < RB; ++i)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            const int row = i * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3);
+            if (row >= M) continue;
+            if (EPI == MF_PARTIAL) {
+#pragma unroll
+                for (int b = 0; b < NB; ++b)
+                    ws[(((size_t)blockIdx.z * NB + b) * M + row) * N + col] = acc[b][i][e];
+                continue;
+            }
+            float *c = (float *)g.c + (size_t)row * g.ldc + col;
+            if (EPI == GEMM_SWIGLU) {
+                const float y = silu(acc[0][i][e]) * acc[NB - 1][i][e];
+                if (g.c_lo) {
+                    const size_t ci = (size_t)row * g.ldc + col;
+                    uint16_t h = f2bf(y);
+                    ((uint16_t *)g.c)[ci] = h;
+                    ((uint16_t *)g.c_lo)[ci] = f2bf(y - bf2f(h));
+                } else {
+                    *c = y;
+                }
+            } else {
+                float v = g.bias ? acc[0][i][e] + g.bias[col] : acc[0][i][e];
+                if (EPI == GEMM_RESIDUAL) *c = *c + v;
+                else *c = v;
+            }
+        }
+}
+
+// k split as for the streamed form; each split's range is a multiple of
+// D stages (K % (32 D) == 0 is checked by the caller)
+template <int EPI, int NB, int RB, int NW, int D>
+static void skinny_launch(const GemmArgs &a, float *ws, size_t ws_bytes, hipStream_t s,
+                          int want_blocks, int min_ks) {
+    constexpr size_t LDSB = (size_t)(D + 1) * 2 * 32 * RB * LS_ROWB;
+    static bool attr = false;
+    if (!attr) {
+        ESP_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(gemm_skinny_k<EPI, NB, RB, NW, D>),
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, (int)LDSB));
+        ESP_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(gemm_skinny_k<MF_PARTIAL, NB, RB, NW, D>),
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, (int)LDSB));
+        attr = true;
+    }
+    constexpr int BN = 32 * NW, KU = LS_BK * D;
+    if (a.K % KU != 0 || a.M > 32 * RB) fail(ESP_BACKEND, "skinny GEMM: shape outside the form");
+    const int gx = (a.N + BN - 1) / BN;
+    int splits = 1;
+    while (gx * splits < want_blocks && a.K / (splits * 2) >= min_ks &&
+           (size_t)(splits * 2) * NB * a.M * a.N * 4 <= ws_bytes)
+        splits *= 2;
+    int kps = (a.K + splits - 1) / splits;
+    kps = (kps + KU - 1) / KU * KU;
+    splits = (a.K + kps - 1) / kps;
+    if (splits == 1) {
+        gemm_skinny_k<EPI, NB, RB, NW, D><<<dim3(gx, 1, 1), 64 * NW, LDSB, s>>>(a, nullptr, a.K);
+        return;
+    }
+    gemm_skinny_k<MF_PARTIAL, NB, RB, NW, D><<<dim3(gx, 1, splits), 64 * NW, LDSB, s>>>(a, ws, kps);
+    size_t mn = (size_t)a.M * a.N;
+    const int rblocks = (int)std::min<size_t>((mn + 255) / 256, (size_t)g_cus * 8);
+    mfma_reduce_k<EPI, NB><<<rblocks, 256, 0, s>>>(a, ws, splits);
+}
+
 template <int EPI> static void mfma_launch(const GemmArgs &a, float *ws, size_t ws_bytes,
                                            hipStream_t s) {
     constexpr int NB = EPI == GEMM_SWIGLU ? 2 : 1;
@@ -702,6 +925,25 @@ template <int EPI> static void mfma_launch(const GemmArgs &a, float *ws, size_t 
         if (NB == 1) lds_launch<EPI, NB, 4>(a, ws, ws_bytes, s, g_cus);
         else lds_launch<EPI, NB, 2>(a, ws, ws_bytes, s, 2 * g_cus);
         return;
+    }
+    if (a.M <= MF_BM && !a.grp_offs) {
+        // skinny streamed form (measured on MI355X, 1B / 8B shapes): a
+        // weight matrix wide enough to fill the chip with one k range (the
+        // 128256-column output head) takes 256 columns per block, two
+        // stages ahead (64 rows: 240 -> 138 us); 64 rows or fewer take 128
+        // columns per block, four stages ahead (16 rows: down 18.0 -> 12.3
+        // us, gate/up 26.1 -> 19.7 us). 65 - 128 rows of narrower matrices
+        // keep the streamed form below, which measured faster there.
+        const bool wide = (a.N + 255) / 256 >= g_cus;
+        if (wide && a.K % (LS_BK * 2) == 0) {
+            if (a.M <= 64) skinny_launch<EPI, NB, 2, 8, 2>(a, ws, ws_bytes, s, g_cus, 256);
+            else skinny_launch<EPI, NB, 4, 8, 2>(a, ws, ws_bytes, s, g_cus, 256);
+            return;
+        }
+        if (a.M <= 64 && a.K % (LS_BK * 4) == 0) {
+            skinny_launch<EPI, NB, 2, 4, 4>(a, ws, ws_bytes, s, g_cus, 256);
+            return;
+        }
     }
     if (a.K % LS_BK == 0 && a.M <= MF_BM && !getenv("ESP_SKINNY_REG")) {
         // one row tile (decode batches, forced blocks): 64 weight columns per
