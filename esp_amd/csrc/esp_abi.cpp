@@ -336,8 +336,20 @@ static void pick_rows(Kv &k, uint32_t n_rows, const uint32_t *allowed_bits,
     k.pick_io.ensure(off_out + out_b);
     char *io = (char *)k.pick_io.p;
     hipStream_t s = k.stream;
-    if (allowed_bits)
-        ESP_HIP(hipMemcpyAsync(io + off_mask, allowed_bits, mask_b, hipMemcpyHostToDevice, s));
+    // pinned staging with the device layout: [mask | samplers | ids, states, flags]
+    if (k.pick_pinned_bytes < off_out + out_b) {
+        if (k.pick_pinned) ESP_HIP(hipHostFree(k.pick_pinned));
+        k.pick_pinned = nullptr;
+        k.pick_pinned_bytes = 0;
+        ESP_HIP(hipHostMalloc(&k.pick_pinned, off_out + out_b, hipHostMallocDefault));
+        k.pick_pinned_bytes = off_out + out_b;
+    }
+    char *pin = (char *)k.pick_pinned;
+    if (allowed_bits) memcpy(pin + off_mask, allowed_bits, mask_b);
+    if (smp_b) memcpy(pin + off_smp, samplers, smp_b);
+    // one upload of what the host supplies (constraint rows are written on the device)
+    if (allowed_bits) ESP_HIP(hipMemcpyAsync(io, pin, off_smp + smp_b, hipMemcpyHostToDevice, s));
+    else if (smp_b) ESP_HIP(hipMemcpyAsync(io + off_smp, pin + off_smp, smp_b, hipMemcpyHostToDevice, s));
     if (cs) {
         uint32_t *m = (uint32_t *)(io + off_mask);
         for (uint32_t i = 0; i < n_rows; ++i) {
@@ -352,7 +364,6 @@ static void pick_rows(Kv &k, uint32_t n_rows, const uint32_t *allowed_bits,
         Prof p("cmask", s);
         run_cmask(*k.cmask, con.data(), con_mask.data(), (int)con.size(), s);
     }
-    if (smp_b) ESP_HIP(hipMemcpyAsync(io + off_smp, samplers, smp_b, hipMemcpyHostToDevice, s));
     bool any_sampled = false;
     for (uint32_t i = 0; samplers && i < n_rows; ++i) any_sampled |= samplers[i].temperature > 0.f;
     size_t scr = any_sampled ? pick_scratch_bytes((int)n_rows, V) : 0;
@@ -377,13 +388,14 @@ static void pick_rows(Kv &k, uint32_t n_rows, const uint32_t *allowed_bits,
         Prof p("pick", s);
         launch_pick(a, s);
     }
-    std::vector<uint64_t> states(n_rows);
-    std::vector<uint8_t> flags(n_rows);
-    ESP_HIP(hipMemcpyAsync(ids_out, d_ids, (size_t)n_rows * 4, hipMemcpyDeviceToHost, s));
-    ESP_HIP(hipMemcpyAsync(states.data(), d_state, (size_t)n_rows * 8, hipMemcpyDeviceToHost, s));
-    ESP_HIP(hipMemcpyAsync(flags.data(), d_flags, n_rows, hipMemcpyDeviceToHost, s));
+    // one readback of ids, states and flags (contiguous in the io buffer)
+    const size_t res_b = (size_t)((char *)(d_flags + n_rows) - (char *)d_ids);
+    ESP_HIP(hipMemcpyAsync(pin + off_out, d_ids, res_b, hipMemcpyDeviceToHost, s));
     if (!con.empty()) check_cmask(*k.cmask, s);
     ESP_HIP(hipStreamSynchronize(s));
+    memcpy(ids_out, pin + off_out, (size_t)n_rows * 4);
+    const uint64_t *states = (const uint64_t *)(pin + off_out + ((char *)d_state - (char *)d_ids));
+    const uint8_t *flags = (const uint8_t *)(pin + off_out + ((char *)d_flags - (char *)d_ids));
     bool none = false;
     for (uint32_t i = 0; i < n_rows; ++i) {
         if (flags_out) flags_out[i] = flags[i];

@@ -32,6 +32,7 @@ struct Rows;
 Kv::~Kv() {
     if (gen_exec) (void)hipGraphExecDestroy(gen_exec);
     if (pinned) (void)hipHostFree(pinned);
+    if (pick_pinned) (void)hipHostFree(pick_pinned);
     if (stream) (void)hipStreamDestroy(stream);
 }
 

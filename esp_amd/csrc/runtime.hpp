@@ -115,6 +115,10 @@ struct Kv {
     int logits_rows = 0;  // rows valid in `logits`
     void *pinned = nullptr;
     size_t pinned_bytes = 0;
+    // esp_pick's host staging (masks and samplers in, ids / states / flags
+    // out): one DMA each way instead of copies from pageable memory
+    void *pick_pinned = nullptr;
+    size_t pick_pinned_bytes = 0;
     // generation graph
     hipGraphExec_t gen_exec = nullptr;
     // grammar mask buffers of esp_pick_constrained

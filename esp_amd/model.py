@@ -17,6 +17,10 @@ from .config import DecoderConfig
 from .errors import InvalidRequest
 from .sample import Sampler
 
+# numpy view of esp_sampler (float temperature, float top_p, uint64 state)
+_SAMPLER_DT = np.dtype([("temperature", "<f4"), ("top_p", "<f4"), ("state", "<u8")], align=True)
+assert _SAMPLER_DT.itemsize == C.sizeof(_lib.EspSampler)
+
 # weight_format.rs:34-49 names (short and versioned)
 FORMATS = {"f32": _lib.ESP_FORMAT_F32, "bf16": _lib.ESP_FORMAT_BF16,
            "q8-block32": _lib.ESP_FORMAT_Q8, "q8-k32-f32-scale-f16-shared-v1": _lib.ESP_FORMAT_Q8,
@@ -302,21 +306,19 @@ class DecoderModel:
     def _pick(self, cache: KvCache, n_rows: int, samplers, call, check: bool = True):
         ids = np.zeros(n_rows, np.uint32)
         flags = np.zeros(n_rows, np.uint8)
-        sarr = None
+        sarr = sptr = None
         if samplers is not None:
-            sarr = (_lib.EspSampler * n_rows)()
-            for i, s in enumerate(samplers):
-                if s is None:
-                    sarr[i] = _lib.EspSampler(0.0, -1.0, 0)
-                else:
-                    sarr[i] = _lib.EspSampler(s.temperature,
-                                              -1.0 if s.top_p is None else s.top_p, s.rng.state)
-        status = call(sarr, ids.ctypes.data_as(C.POINTER(C.c_uint32)),
+            # esp_sampler rows (temperature, top_p, state) built in one pass
+            sarr = np.fromiter(((0.0, -1.0, 0) if s is None else
+                                (s.temperature, -1.0 if s.top_p is None else s.top_p, s.rng.state)
+                                for s in samplers), dtype=_SAMPLER_DT, count=n_rows)
+            sptr = sarr.ctypes.data_as(C.POINTER(_lib.EspSampler))
+        status = call(sptr, ids.ctypes.data_as(C.POINTER(C.c_uint32)),
                       flags.ctypes.data_as(C.POINTER(C.c_uint8)))
         if samplers is not None:
-            for i, s in enumerate(samplers):
+            for s, st in zip(samplers, sarr["state"].tolist()):
                 if s is not None:
-                    s.rng.state = sarr[i].state
+                    s.rng.state = st
         if not check:
             return ids, flags, status
         _lib.check(status)
