@@ -59,6 +59,13 @@ void launch_embed(Dt wt, const void *embed, const int32_t *ids, int M, int H, fl
 
 // out[M,H] (dt out) = x / sqrt(mean(x^2)+eps) * gamma ; rows selected by
 // row_index (nullable = identity).
+// x[m] += bias + sum_z ws[z][m] (the split-K partials of a RESIDUAL
+// projection, summed in split order as the GEMM reduction does), then
+// out = RMSNorm(x[m]) * gamma in out_dt (DT_SPLIT: hi/lo planes of M rows).
+// H <= 8192, H % 4 == 0 (resid_norm_ok).
+bool resid_norm_ok(int H);
+void launch_resid_norm(const float *ws, int splits, int M, int H, const float *bias, float *x,
+                       const float *gamma, float eps, Dt out_dt, void *out, hipStream_t s);
 void launch_rmsnorm(const float *x, const float *gamma, float eps, int M, int H, Dt out_dt,
                     void *out, const int32_t *row_index, hipStream_t s);
 
@@ -100,6 +107,12 @@ struct GemmArgs {
     const int32_t *grp_offs;
     int grp_n;
     long long grp_w_stride;
+    // Nullable host word. When set, a launch that splits K leaves the
+    // partial sums in ws ([splits][M][N] f32) and stores the split count
+    // here instead of running the reduction and epilogue (the consumer sums
+    // them, in split order); a launch without splits applies the epilogue and
+    // stores 0.
+    int *defer_splits;
 };
 void launch_gemm(Dt wt, GemmEpi epi, const GemmArgs &a, hipStream_t s);
 
@@ -121,7 +134,17 @@ struct RopeKvArgs {
     void *kv;           // cache base (kv dt)
     long long seq_stride, layer_stride, kv_half_stride, head_stride;  // elements
     int nq, nkv, hd;
+    // Nullable: the q/k/v projection's split-K partial sums [splits][M][ldq]
+    // (qkv is then unread), summed in split order, + part_bias (nullable).
+    // Pair form only (rope_kv_fusable).
+    const float *part;
+    int splits;
+    const float *part_bias;
 };
+// Whether launch_rope_kv takes `part` for these shapes: the pair form's
+// dtype pairs, head_dim 64 (even head counts) or 128, and no LoRA adapter
+// (its t columns are read raw).
+bool rope_kv_fusable(Dt wt, Dt kvdt, int hd, int nq, int nkv, bool lora);
 void launch_rope_kv(Dt wt, Dt kvdt, const RopeKvArgs &a, hipStream_t s);
 
 // Attention over the cache for each row (causal, optional sliding window).

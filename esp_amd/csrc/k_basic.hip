@@ -126,6 +126,97 @@ void launch_rmsnorm(const float *x, const float *gamma, float eps, int M, int H,
         rmsnorm_k<float, false><<<M, 256, 0, s>>>(x, gamma, eps, H, (float *)out, row_index);
 }
 
+// Split-K partial sums of a RESIDUAL projection fused with the RMSNorm that
+// follows it (layer.rs:120-151: the o_proj residual before post-attention
+// norm, the down_proj residual before the next layer's input norm). One
+// block per row; thread t owns elements 4 (t + 256 i) .. + 4. The partials
+// are summed from 0 in split order, eight loads in flight, then + bias and
+// added to x, exactly as the GEMM reduction does; the norm is then that of
+// rmsnorm_k on the new row.
+template <typename OT, bool SPLIT, int NQ>
+__global__ void __launch_bounds__(256) resid_norm_k(const float *ws, int splits, int M, int H,
+                                                    const float *bias, float *x, const float *gamma,
+                                                    float eps, OT *out) {
+    __shared__ float red[4];
+    const int m = blockIdx.x, tid = threadIdx.x;
+    const size_t MH = (size_t)M * H;
+    f32x4 v[NQ];
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < NQ; ++i) {
+        const int j = (tid + 256 * i) * 4;
+        v[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+        if (j >= H) continue;
+        const size_t o = (size_t)m * H + j;
+        f32x4 t = {0.f, 0.f, 0.f, 0.f};
+        for (int z0 = 0; z0 < splits; z0 += 8) {
+            f32x4 pz[8];
+#pragma unroll
+            for (int q = 0; q < 8; ++q)
+                pz[q] = z0 + q < splits ? *(const f32x4 *)(ws + (size_t)(z0 + q) * MH + o) : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int q = 0; q < 8; ++q)
+                if (z0 + q < splits) t += pz[q];
+        }
+        if (bias) t = t + *(const f32x4 *)(bias + j);
+        const f32x4 xv = *(const f32x4 *)(x + o) + t;
+        *(f32x4 *)(x + o) = xv;
+        v[i] = xv;
+        ss += xv[0] * xv[0] + xv[1] * xv[1] + xv[2] * xv[2] + xv[3] * xv[3];
+    }
+    ss = wave_sum(ss);
+    if ((tid & 63) == 0) red[tid >> 6] = ss;
+    __syncthreads();
+    ss = (red[0] + red[1]) + (red[2] + red[3]);
+    const float rms = sqrtf(ss / (float)H + eps);
+#pragma unroll
+    for (int i = 0; i < NQ; ++i) {
+        const int j = (tid + 256 * i) * 4;
+        if (j >= H) continue;
+        const f32x4 gv = *(const f32x4 *)(gamma + j);
+        float y[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) y[e] = (v[i][e] / rms) * gv[e];
+        const size_t o = (size_t)m * H + j;
+        if (SPLIT) {
+            uint16_t hi[4], lo[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                hi[e] = f2bf(y[e]);
+                lo[e] = f2bf(y[e] - bf2f(hi[e]));
+            }
+            *(uint2 *)((uint16_t *)out + o) = make_uint2(hi[0] | ((uint32_t)hi[1] << 16), hi[2] | ((uint32_t)hi[3] << 16));
+            *(uint2 *)((uint16_t *)out + MH + o) =
+                make_uint2(lo[0] | ((uint32_t)lo[1] << 16), lo[2] | ((uint32_t)lo[3] << 16));
+        } else {
+            *(f32x4 *)((float *)out + o) = f32x4{y[0], y[1], y[2], y[3]};
+        }
+    }
+}
+
+bool resid_norm_ok(int H) { return H > 0 && H % 4 == 0 && H <= 8192; }
+
+void launch_resid_norm(const float *ws, int splits, int M, int H, const float *bias, float *x,
+                       const float *gamma, float eps, Dt out_dt, void *out, hipStream_t s) {
+    if (!resid_norm_ok(H) || splits < 1 || (out_dt != DT_SPLIT && out_dt != DT_F32))
+        fail(ESP_BACKEND, "resid_norm: unsupported shape");
+    const int nq = (H / 4 + 255) / 256;
+#define RN_LAUNCH(NQ_)                                                                                    \
+    do {                                                                                                  \
+        if (out_dt == DT_SPLIT)                                                                           \
+            resid_norm_k<uint16_t, true, NQ_><<<M, 256, 0, s>>>(ws, splits, M, H, bias, x, gamma, eps,    \
+                                                                 (uint16_t *)out);                        \
+        else                                                                                              \
+            resid_norm_k<float, false, NQ_><<<M, 256, 0, s>>>(ws, splits, M, H, bias, x, gamma, eps,      \
+                                                               (float *)out);                             \
+    } while (0)
+    if (nq <= 1) RN_LAUNCH(1);
+    else if (nq <= 2) RN_LAUNCH(2);
+    else if (nq <= 4) RN_LAUNCH(4);
+    else RN_LAUNCH(8);
+#undef RN_LAUNCH
+}
+
 // ----------------------------------------------------------------- rope_kv
 // attention.rs:306-326: q/k/v projections (+bias, + unmerged LoRA as in
 // lora.rs:93-97), optional QK RMSNorm over head_dim (:312-319), split-half
@@ -286,6 +377,7 @@ __global__ void __launch_bounds__(256) rope_kv2_k(const RopeKvArgs a, int rows_p
     const int hl = head - hbase;  // head within its target
     const int c0 = off + hl * HD + p, c1 = c0 + HALF;
     const float *__restrict__ qkv = a.qkv;
+    const float *__restrict__ part = a.part;
     const float *__restrict__ cs = a.rope_cos;
     const float *__restrict__ sn = a.rope_sin;
     const int32_t *__restrict__ rpos = a.rows.row_pos;
@@ -314,10 +406,46 @@ __global__ void __launch_bounds__(256) rope_kv2_k(const RopeKvArgs a, int rows_p
 #pragma unroll
         for (int r = 0; r < RK2_RB; ++r) {
             const int m = m0 + min(rb + r, nr - 1);
-            x0[r] = qkv[(size_t)m * a.ldq + c0];
-            x1[r] = qkv[(size_t)m * a.ldq + c1];
+            if (!part) {
+                x0[r] = qkv[(size_t)m * a.ldq + c0];
+                x1[r] = qkv[(size_t)m * a.ldq + c1];
+            }
             pos[r] = rpos[m];
             sq[r] = rseq[m];
+        }
+        if (part) {
+            // the projection's split-K partials, summed from 0 in split order
+            // (eight loads in flight), then + bias, as the GEMM reduction does
+            const size_t MN = (size_t)a.rows.M * a.ldq;
+#pragma unroll
+            for (int r = 0; r < RK2_RB; ++r) {
+                const int m = m0 + min(rb + r, nr - 1);
+                float t0 = 0.f, t1 = 0.f;
+                if (rb + r < nr) {  // block-uniform
+                    const float *__restrict__ p = part + (size_t)m * a.ldq;
+                    for (int z0 = 0; z0 < a.splits; z0 += 8) {
+                        float p0[8], p1[8];
+#pragma unroll
+                        for (int q = 0; q < 8; ++q) {
+                            const size_t zo = (size_t)min(z0 + q, a.splits - 1) * MN;
+                            p0[q] = p[zo + c0];
+                            p1[q] = p[zo + c1];
+                        }
+#pragma unroll
+                        for (int q = 0; q < 8; ++q)
+                            if (z0 + q < a.splits) {
+                                t0 += p0[q];
+                                t1 += p1[q];
+                            }
+                    }
+                    if (a.part_bias) {
+                        t0 = t0 + a.part_bias[c0];
+                        t1 = t1 + a.part_bias[c1];
+                    }
+                }
+                x0[r] = t0;
+                x1[r] = t1;
+            }
         }
         // LoRA: x += scale * B t (the row's t values are uniform loads)
         if constexpr (R > 0) {
@@ -398,8 +526,19 @@ static bool rope_kv2_launch(const RopeKvArgs &a, hipStream_t s) {
     }
 }
 
+bool rope_kv_fusable(Dt wt, Dt kvdt, int hd, int nq, int nkv, bool lora) {
+    const bool dts = (wt == DT_BF16 && (kvdt == DT_F16 || kvdt == DT_F32)) || (wt == DT_F32 && kvdt == DT_F32);
+    return dts && !lora && (hd == 128 || (hd == 64 && nq % 2 == 0 && nkv % 2 == 0));
+}
+
 void launch_rope_kv(Dt wt, Dt kvdt, const RopeKvArgs &a, hipStream_t s) {
     if (a.hd > 256) fail(ESP_UNSUPPORTED, "head_dim: values above 256 are not implemented");
+    if (a.part) {
+        bool lora = false;
+        for (int j = 0; j < 3; ++j) lora |= a.lora_b[j] && a.lora_rank[j];
+        if (!rope_kv_fusable(wt, kvdt, a.hd, a.nq, a.nkv, lora) || a.splits < 1)
+            fail(ESP_BACKEND, "rope_kv: split-K partials need the pair form");
+    }
     bool done = false;
     if (a.hd == 128) {
         if (wt == DT_BF16 && kvdt == DT_F16) done = rope_kv2_launch<uint16_t, _Float16, 128>(a, s);
@@ -411,6 +550,7 @@ void launch_rope_kv(Dt wt, Dt kvdt, const RopeKvArgs &a, hipStream_t s) {
         else if (wt == DT_F32 && kvdt == DT_F32) done = rope_kv2_launch<float, float, 64>(a, s);
     }
     if (done) return;
+    if (a.part) fail(ESP_BACKEND, "rope_kv: split-K partials need the pair form");
     const int hpi = 256 / a.hd;
     // contiguous span of LoRA t columns read by this layer
     int t_lo = 0, t_hi = 0;

@@ -624,6 +624,10 @@ static void mfma_launch_nj(const GemmArgs &a, float *ws, size_t ws_bytes, hipStr
         return;
     }
     gemm_mfma_k<MF_PARTIAL, NB, NJ><<<dim3(blocks, 1, splits), 256, shm, s>>>(a, ws, kps, gy, gx);
+    if (a.defer_splits) {
+        *a.defer_splits = splits;
+        return;
+    }
     size_t mn = (size_t)a.M * a.N;
     const int rblocks = (int)std::min<size_t>((mn + 255) / 256, (size_t)g_cus * 8);
     mfma_reduce_k<EPI, NB><<<rblocks, 256, 0, s>>>(a, ws, splits);
@@ -670,6 +674,10 @@ static void lds_launch(const GemmArgs &a, float *ws, size_t ws_bytes, hipStream_
                 return;
             }
             gemm_lds_k<MF_PARTIAL, NB, BMW, BROWS, STG, true><<<dim3(blocks, 1, splits), F::NT + 64, F::LDS, s>>>(a, ws, kps, gy, gx);
+            if (a.defer_splits) {
+                *a.defer_splits = splits;
+                return;
+            }
             size_t mn = (size_t)a.M * a.N;
             const int rblocks = (int)std::min<size_t>((mn + 255) / 256, (size_t)g_cus * 8);
             mfma_reduce_k<EPI, NB><<<rblocks, 256, 0, s>>>(a, ws, splits);
@@ -681,6 +689,10 @@ static void lds_launch(const GemmArgs &a, float *ws, size_t ws_bytes, hipStream_
         return;
     }
     gemm_lds_k<MF_PARTIAL, NB, BMW, BROWS, STG><<<dim3(blocks, 1, splits), F::NT, F::LDS, s>>>(a, ws, kps, gy, gx);
+    if (a.defer_splits) {
+        *a.defer_splits = splits;
+        return;
+    }
     size_t mn = (size_t)a.M * a.N;
     const int rblocks = (int)std::min<size_t>((mn + 255) / 256, (size_t)g_cus * 8);
     mfma_reduce_k<EPI, NB><<<rblocks, 256, 0, s>>>(a, ws, splits);
@@ -903,6 +915,10 @@ static void skinny_launch(const GemmArgs &a, float *ws, size_t ws_bytes, hipStre
         return;
     }
     gemm_skinny_k<MF_PARTIAL, NB, RB, NW, D><<<dim3(gx, 1, splits), 64 * NW, LDSB, s>>>(a, ws, kps);
+    if (a.defer_splits) {
+        *a.defer_splits = splits;
+        return;
+    }
     size_t mn = (size_t)a.M * a.N;
     const int rblocks = (int)std::min<size_t>((mn + 255) / 256, (size_t)g_cus * 8);
     mfma_reduce_k<EPI, NB><<<rblocks, 256, 0, s>>>(a, ws, splits);

@@ -1103,6 +1103,12 @@ static void run_layers(Model &m, Kv &kv, const Rows &rows, int Mc, int max_t, in
             if (m.st) stream_release(m, kv);
         }
     };
+    // Split-K partial sums are consumed by the kernel that follows the
+    // projection when it can take them (bf16 activations): the q/k/v sums by
+    // the rotary/KV kernel, the o_proj and down_proj residual sums by a row
+    // kernel that also applies the next RMSNorm (post-attention, or the next
+    // resident layer's input norm: `pre_normed`).
+    bool pre_normed = false;
     for (int l = 0; l < m.L; ++l) {
         LayerW staged;
         if (m.st) staged = stream_acquire(m, kv, l);
@@ -1112,6 +1118,9 @@ static void run_layers(Model &m, Kv &kv, const Rows &rows, int Mc, int max_t, in
             run_layer_decode(m, kv, rows, w, l, plan);
             continue;
         }
+        bool lora_any = false;
+        for (int j = 0; j < 3; ++j) lora_any |= w.lora_b[j] && w.lora_rank[j];
+        int qkv_splits = 0, o_splits = 0;
         // ---- attention block (layer.rs:120-131)
         if (single) {
             GemvArgs g{};
@@ -1126,7 +1135,7 @@ static void run_layers(Model &m, Kv &kv, const Rows &rows, int Mc, int max_t, in
             Prof p("gemv", s);
             launch_gemv(m.wt, GEMV_STORE, g, s);
         } else {
-            {
+            if (!pre_normed) {
                 Prof p("rmsnorm", s);
                 launch_rmsnorm(kv.h.as<float>(), w.in_norm, m.cfg.rms_norm_eps, Mc, H, act,
                                kv.xn.p, nullptr, s);
@@ -1143,10 +1152,13 @@ static void run_layers(Model &m, Kv &kv, const Rows &rows, int Mc, int max_t, in
             g.N = w.qkv_rows;
             g.K = H;
             g.ldc = w.qkv_rows;
+            if (act == DT_SPLIT && rope_kv_fusable(lora_dt(m.wt), kv.dt, m.hd, m.nq, m.nkv, lora_any))
+                g.defer_splits = &qkv_splits;
             Prof p("gemm_qkv", s);
             widen_k(m, kv, g);
             launch_gemm(layer_gemm_dt(m.wt), GEMM_STORE, g, s);
         }
+        pre_normed = false;
         {
             RopeKvArgs r{};
             r.qkv = kv.qkv.as<float>();
@@ -1172,6 +1184,11 @@ static void run_layers(Model &m, Kv &kv, const Rows &rows, int Mc, int max_t, in
             r.nq = m.nq;
             r.nkv = m.nkv;
             r.hd = m.hd;
+            if (qkv_splits > 1) {
+                r.part = kv.gemm_ws.as<float>();
+                r.splits = qkv_splits;
+                r.part_bias = w.qkv_bias;
+            }
             Prof p("rope_kv", s);
             launch_rope_kv(lora_dt(m.wt), kv.dt, r, s);
         }
@@ -1269,6 +1286,7 @@ static void run_layers(Model &m, Kv &kv, const Rows &rows, int Mc, int max_t, in
             g.N = H;
             g.K = m.qw;
             g.ldc = H;
+            if (!w.moe && act == DT_SPLIT && resid_norm_ok(H)) g.defer_splits = &o_splits;
             Prof p("gemm_o", s);
             widen_k(m, kv, g);
             launch_gemm(layer_gemm_dt(m.wt), GEMM_RESIDUAL, g, s);
@@ -1299,7 +1317,11 @@ static void run_layers(Model &m, Kv &kv, const Rows &rows, int Mc, int max_t, in
             Prof p("gemv", s);
             launch_gemv(m.wt, GEMV_RESIDUAL, d, s);
         } else {
-            {
+            if (o_splits > 1) {
+                Prof p("resid_norm", s);
+                launch_resid_norm(kv.gemm_ws.as<float>(), o_splits, Mc, H, w.o_bias, kv.h.as<float>(),
+                                  w.post_norm, m.cfg.rms_norm_eps, act, kv.xn.p, s);
+            } else {
                 Prof p("rmsnorm", s);
                 launch_rmsnorm(kv.h.as<float>(), w.post_norm, m.cfg.rms_norm_eps, Mc, H, act,
                                kv.xn.p, nullptr, s);
@@ -1333,9 +1355,21 @@ static void run_layers(Model &m, Kv &kv, const Rows &rows, int Mc, int max_t, in
             d.N = H;
             d.K = m.F;
             d.ldc = H;
-            Prof p("gemm_down", s);
-            widen_k(m, kv, d);
-            launch_gemm(layer_gemm_dt(m.wt), GEMM_RESIDUAL, d, s);
+            // the next resident layer's input norm takes the partial sums
+            int d_splits = 0;
+            const bool next_norm = l + 1 < m.L && !m.st && act == DT_SPLIT && resid_norm_ok(H);
+            if (next_norm) d.defer_splits = &d_splits;
+            {
+                Prof p("gemm_down", s);
+                widen_k(m, kv, d);
+                launch_gemm(layer_gemm_dt(m.wt), GEMM_RESIDUAL, d, s);
+            }
+            if (d_splits > 1) {
+                Prof p("resid_norm", s);
+                launch_resid_norm(kv.gemm_ws.as<float>(), d_splits, Mc, H, nullptr, kv.h.as<float>(),
+                                  m.layers[l + 1].in_norm, m.cfg.rms_norm_eps, act, kv.xn.p, s);
+                pre_normed = true;
+            }
         }
     }
 }
