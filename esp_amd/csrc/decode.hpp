@@ -92,6 +92,11 @@ struct AttnDecodeArgs {
 };
 
 bool attn_decode_ok(int hd, int G);
+// The matrix-core form of attn_decode_k for batches without key splits
+// (k_attn_mfma.hip): one wave per (row, kv head), up to 16 query heads per
+// kv head, hd 64 (f16 or f32 cache) or 128 (f16 cache), no LoRA.
+bool attn_rows_mfma_ok(const AttnDecodeArgs &a);
+void launch_attn_rows_mfma(const AttnDecodeArgs &a, hipStream_t s);
 // key splits and keys per split for M decode rows over max_t cached keys
 int attn_decode_splits(int hd, int nkv, int G, int M, int max_t, int *split_len);
 constexpr int ATT_MAX_TICKETS = 4096;  // (row, kv head) merge tickets at the start of Kv::tickets

@@ -1001,6 +1001,15 @@ void launch_attn_decode(const AttnDecodeArgs &a0, hipStream_t s) {
     const long long U = (long long)a.M * a.nkv;
     if (a.n_split > 1 && U > ATT_MAX_TICKETS)
         fail(ESP_BACKEND, "attn_decode: too many (row, kv head) merges");
+    {
+        // batches whose units fill the chip without key splits: matrix cores
+        // (ESP_ATT_MFMA=0 keeps the vector form, for comparison)
+        const char *am = getenv("ESP_ATT_MFMA");
+        if (U >= device_cus() && attn_rows_mfma_ok(a) && !(am && am[0] == '0')) {
+            launch_attn_rows_mfma(a, s);
+            return;
+        }
+    }
     a.xcd_nx = a.n_split > 1 ? attn_xcd_mode() : 0;
     {
         const char *mp = getenv("ESP_ATT_XCD_MISPLACE");

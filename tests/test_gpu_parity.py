@@ -591,3 +591,44 @@ def test_bf16_moe_decode_on_device_matches_oracle():
         want = ref.forward_last(rkv, [t])
     dev = model.generate_greedy_device(model.new_cache(1, 100), prompt, 8, eos=[])
     assert dev == ids
+
+
+ROWS_MFMA_VARIANTS = {
+    # name: (nq, nkv, head_dim, extra config)
+    "hd64_g1": (8, 8, 64, {}),
+    "hd64_g4": (16, 4, 64, {}),
+    "hd64_g16": (32, 2, 64, {}),
+    "hd128_g2": (8, 4, 128, {}),
+    "hd64_window": (8, 4, 64, {"model_type": "mistral", "architectures": ["MistralForCausalLM"],
+                               "sliding_window": 37}),
+}
+
+
+@pytest.mark.parametrize("variant", sorted(ROWS_MFMA_VARIANTS))
+@pytest.mark.parametrize("kv_dtype", ["f32", "f16"])
+def test_batch_rows_attention_matches_oracle(variant, kv_dtype):
+    """Forty sequences with prompts of 1-150 tokens prefilled in one batch
+    (rows of short and long prompts mixed: per-row decode attention), then a
+    step of 26 decode rows and 14 forced 8-token blocks: with (rows x kv
+    heads) >= the CU count and no key splits these take the matrix-core
+    row attention (hd 64 over f16 and f32 caches, hd 128 over f16; up to 16
+    query heads per kv head; partial 32-key tiles; a sliding window). Every
+    sequence's logits within the bf16 tolerance of the oracle run alone."""
+    nq, nkv, hd, extra = ROWS_MFMA_VARIANTS[variant]
+    cfg = synth.llama_config(2, 256, nq, nkv, 384, 300, head_dim=hd, max_pos=512, extra=extra)
+    tensors = synth.make_tensors(cfg, 83, "bf16")
+    model = DecoderModel.from_bytes(cfg, st.dump(tensors), "bf16")
+    ref = oracle.OracleModel(cfg, tensors)
+    n = 40
+    prompts = [synth.uniform_ids(1000 + i, 1 + (37 * i) % 150, cfg.vocab_size) for i in range(n)]
+    kv = model.new_cache(n, 200, kv_dtype)
+    first = model.forward_batch(kv, list(range(n)), prompts)
+    blocks = [synth.uniform_ids(2000 + i, 8, cfg.vocab_size) if i % 3 == 0 else [(7 * i + 2) % cfg.vocab_size]
+              for i in range(n)]
+    got = model.forward_batch(kv, list(range(n)), blocks)
+    for i in range(n):
+        rkv = ref.new_cache(200)
+        want0 = ref.forward_last(rkv, prompts[i])
+        assert _close_bf16(first[i], want0), (variant, "prefill", i, float(np.abs(first[i] - want0).max()))
+        want = ref.forward_last(rkv, blocks[i])
+        assert _close_bf16(got[i], want), (variant, "step", i, float(np.abs(got[i] - want).max()))
