@@ -269,14 +269,17 @@ esp_status esp_kv_logits(esp_kv *kv, float **rows_dev, uint32_t *n_rows) {
     return guard([&] {
         if (!kv) fail(ESP_INVALID_REQUEST, "null kv handle");
         Kv &k = *(Kv *)kv;
+        ESP_HIP(hipStreamSynchronize(k.stream));  // the last forward has finished
         if (rows_dev) *rows_dev = k.logits_rows ? k.logits.as<float>() : nullptr;
         if (n_rows) *n_rows = (uint32_t)k.logits_rows;
     });
 }
 
+// the forward may still be in flight on the handle's (non-blocking) stream
 static void copy_logits(Kv &kv, int rows, float *out) {
     if (!out) return;
-    ESP_HIP(hipMemcpy(out, kv.logits.p, (size_t)rows * kv.model->V * 4, hipMemcpyDeviceToHost));
+    ESP_HIP(hipMemcpyAsync(out, kv.logits.p, (size_t)rows * kv.model->V * 4, hipMemcpyDeviceToHost, kv.stream));
+    ESP_HIP(hipStreamSynchronize(kv.stream));
 }
 
 esp_status esp_forward_last(esp_model *model, esp_kv *kv, uint32_t seq, const int32_t *ids,

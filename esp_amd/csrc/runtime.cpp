@@ -882,6 +882,7 @@ static void attn_decode_rows(Model &m, Kv &kv, const Rows &rows, int Mc, int l, 
     a.xcd_err = xcd_err_word(kv);
     a.out = kv.attn.as<float>();
     a.out_lo = (uint16_t *)lo_plane(out_dt, kv.attn, Mc, m.qw);
+    if (plan.n_split > 1) kv.att_merged = true;
     launch_attn_decode(a, kv.stream);
 }
 
@@ -1521,6 +1522,7 @@ static bool forward_pass(Model &m, Kv &kv, int n_seqs, const uint32_t *seqs, con
     for (long long r = 0; r < M; ++r)
         if (ids[r] < 0 || ids[r] >= m.V) fail(ESP_INVALID_REQUEST, "token id outside the vocabulary");
     ensure_scratch(m, kv, (int)std::min<long long>(M, kMaxRows), n_seqs);
+    kv.att_merged = false;
     // host row descriptors
     std::vector<int32_t> rseq(M), rpos(M);
     std::vector<int32_t> last(n_seqs);
@@ -1584,13 +1586,19 @@ static bool forward_pass(Model &m, Kv &kv, int n_seqs, const uint32_t *seqs, con
     } else {
         run_head(m, kv, n_seqs, hl, nullptr);
     }
-    if (kv.moe_err.p)
-        ESP_HIP(hipMemcpyAsync(pin + erroff, kv.moe_err.p, 4, hipMemcpyDeviceToHost, s));
-    ESP_HIP(hipMemcpyAsync(pin + erroff + 1, xcd_err_word(kv), 4, hipMemcpyDeviceToHost, s));
-    ESP_HIP(hipStreamSynchronize(s));
-    if (m.st) stream_check(m);  // a streamed layer that failed its device checks
-    if (kv.moe_err.p) moe_fail(pin[erroff]);
-    if (pin[erroff + 1] && xcd_merge_failed(kv)) return true;
+    // The pass is left in flight (later calls on this stream, and reads of
+    // the logits, are ordered after it) unless something must be read back:
+    // the router status of MoE layers, a streamed layer's device checks, or
+    // the placement word of a split-merging attention.
+    if (kv.moe_err.p || m.st || kv.att_merged) {
+        if (kv.moe_err.p)
+            ESP_HIP(hipMemcpyAsync(pin + erroff, kv.moe_err.p, 4, hipMemcpyDeviceToHost, s));
+        ESP_HIP(hipMemcpyAsync(pin + erroff + 1, xcd_err_word(kv), 4, hipMemcpyDeviceToHost, s));
+        ESP_HIP(hipStreamSynchronize(s));
+        if (m.st) stream_check(m);  // a streamed layer that failed its device checks
+        if (kv.moe_err.p) moe_fail(pin[erroff]);
+        if (pin[erroff + 1] && xcd_merge_failed(kv)) return true;
+    }
     for (int i = 0; i < n_seqs; ++i) kv.pos[seqs[i]] += (int)lens[i];
     kv.logits_rows = n_seqs;
     return false;

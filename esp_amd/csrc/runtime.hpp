@@ -113,6 +113,9 @@ struct Kv {
         moe_act;
     DevMem moe_err;  // sticky router status of the forward in flight (0 = ok)
     int logits_rows = 0;  // rows valid in `logits`
+    // set when a decode attention launch of the forward in flight merged key
+    // splits (its XCD placement word must then be read back)
+    bool att_merged = false;
     void *pinned = nullptr;
     size_t pinned_bytes = 0;
     // esp_pick's host staging (masks and samplers in, ids / states / flags

@@ -178,6 +178,7 @@ esp_status esp_kv_stream(const esp_kv *kv, void **stream);
  * provider.rs:744-760 row read); the provider's test-only score faults
  * (provider.rs:70-71, 755-762) are injected through it. */
 esp_status esp_kv_logits(esp_kv *kv, float **rows_dev, uint32_t *n_rows);
+/* (esp_kv_logits returns once the last forward on the handle has finished.) */
 
 /* model.rs:502-539 try_forward_cached_last for one sequence: consume `n`
  * ids at the sequence's position, extend its cache, and leave the
@@ -192,7 +193,13 @@ esp_status esp_forward_last(esp_model *model, esp_kv *kv, uint32_t seq, const in
  * consumes seq_lens[i] ids (ids concatenated in order). Decode steps are
  * seq_len 1; grammar-forced spans are short blocks over a warm cache
  * (provider.rs:865-872). Each sequence's result equals its own
- * esp_forward_last. Last-position logits land as rows 0..n_seqs-1. */
+ * esp_forward_last. Last-position logits land as rows 0..n_seqs-1.
+ * Without logits_out the call may return while the pass still runs on the
+ * handle's stream (esp_kv_stream): every later call on the handle is
+ * ordered after it, esp_kv_logits waits for it, and a device failure of the
+ * pass is reported by the next call that waits (esp_pick). Passes that must
+ * read back a status (routed experts, streamed layers, split-merging
+ * attention) still finish before returning. */
 esp_status esp_forward_batch(esp_model *model, esp_kv *kv, uint32_t n_seqs, const uint32_t *seqs,
                              const uint32_t *seq_lens, const int32_t *ids, float *logits_out);
 
