@@ -18,6 +18,7 @@
 // split), online softmax in registers; the last split to finish for a
 // (row, kv head) merges the partials in split order (deterministic).
 #include <algorithm>
+#include <type_traits>
 #include <cstdlib>
 #include <vector>
 
@@ -28,22 +29,22 @@
 
 namespace esp {
 
-// NCH = 8-element chunks per lane and row in this wave's quarter of K
-// (K <= 4 * 64 * 8 * NCH). The first iteration's weight loads are issued
+// NCH = 8-element chunks per lane and row in this wave's share (1 / NW) of K
+// (K <= NW * 64 * 8 * NCH). The first iteration's weight loads are issued
 // before x is read and normalised, and each iteration issues the next
 // one's loads before reducing its own sums.
-template <typename WT, int EPI, int RB, int NCH>
-__global__ void __launch_bounds__(DG_THREADS) decode_gemv_k(DecodeGemvArgs a) {
+template <typename WT, int EPI, int RB, int NCH, int NW = DG_WAVES>
+__global__ void __launch_bounds__(NW * 64) decode_gemv_k(DecodeGemvArgs a) {
     constexpr int RU = RowsPerUnit<EPI>::v;
     constexpr int R = RB * RU;  // weight rows per block iteration
-    __shared__ float red[DG_MAX_IT][R][DG_WAVES];
-    __shared__ float ssq[DG_WAVES];
-    __shared__ float best_v[DG_WAVES];
-    __shared__ int best_i[DG_WAVES];
+    __shared__ float red[DG_MAX_IT][R][NW];
+    __shared__ float ssq[NW];
+    __shared__ float best_v[NW];
+    __shared__ int best_i[NW];
     __shared__ int last;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     constexpr int CW = Chunk<WT>::W;  // weights per chunk
-    const int K = a.K, kq = K / DG_WAVES, nch = kq / CW;  // chunks in this wave's quarter
+    const int K = a.K, kq = K / NW, nch = kq / CW;  // chunks in this wave's quarter
     const int k0 = wave * kq;
     const void *W = a.w;
     const void *W2 = a.w2;
@@ -128,7 +129,7 @@ __global__ void __launch_bounds__(DG_THREADS) decode_gemv_k(DecodeGemvArgs a) {
         __syncthreads();
         float tot = 0.f;
 #pragma unroll
-        for (int w = 0; w < DG_WAVES; ++w) tot += ssq[w];
+        for (int w = 0; w < NW; ++w) tot += ssq[w];
         const float rms = sqrtf(tot / (float)K + a.eps);
 #pragma unroll
         for (int c = 0; c < NCH; ++c) {
@@ -184,7 +185,7 @@ __global__ void __launch_bounds__(DG_THREADS) decode_gemv_k(DecodeGemvArgs a) {
         for (int j = 0; j < RU; ++j) {
             float t = 0.f;
 #pragma unroll
-            for (int w = 0; w < DG_WAVES; ++w) t += red[it][r * RU + j][w];
+            for (int w = 0; w < NW; ++w) t += red[it][r * RU + j][w];
             y[j] = t;
         }
         if (EPI == DG_RESID) {
@@ -268,7 +269,7 @@ __global__ void __launch_bounds__(DG_THREADS) decode_gemv_k(DecodeGemvArgs a) {
     if (tid == 0) {
         float b = best_v[0];
         int bj = best_i[0];
-        for (int w = 1; w < DG_WAVES; ++w)
+        for (int w = 1; w < NW; ++w)
             if (best_v[w] > b || (best_v[w] == b && best_i[w] < bj)) {
                 b = best_v[w];
                 bj = best_i[w];
@@ -284,12 +285,12 @@ __global__ void __launch_bounds__(DG_THREADS) decode_gemv_k(DecodeGemvArgs a) {
     // last block: reduce the partials in block order (deterministic)
     float b = -INFINITY;
     int bj = 0x7fffffff;
-    constexpr int PER = DG_MAX_PART / DG_THREADS;
+    constexpr int PER = DG_MAX_PART / (NW * 64);
     float pvs[PER];
     int pis[PER];
 #pragma unroll
     for (int q = 0; q < PER; ++q) {  // independent loads, issued together
-        int k = tid + q * DG_THREADS;
+        int k = tid + q * (NW * 64);
         pvs[q] = k < (int)gridDim.x ? ld_agent(a.part_v + k) : -INFINITY;
         pis[q] = k < (int)gridDim.x ? ld_agent(a.part_i + k) : 0x7fffffff;
     }
@@ -316,7 +317,7 @@ __global__ void __launch_bounds__(DG_THREADS) decode_gemv_k(DecodeGemvArgs a) {
     if (tid == 0) {
         b = best_v[0];
         bj = best_i[0];
-        for (int w = 1; w < DG_WAVES; ++w)
+        for (int w = 1; w < NW; ++w)
             if (best_v[w] > b || (best_v[w] == b && best_i[w] < bj)) {
                 b = best_v[w];
                 bj = best_i[w];
@@ -334,12 +335,12 @@ __global__ void __launch_bounds__(DG_THREADS) decode_gemv_k(DecodeGemvArgs a) {
     }
 }
 
-template <typename WT, int EPI, int RB, int NCH>
+template <typename WT, int EPI, int RB, int NCH, int NW = DG_WAVES>
 static void dg_launch_nch(const DecodeGemvArgs &a, int cus, hipStream_t s) {
     static int per_cu = 0;  // resident blocks per CU for this instance
     if (!per_cu) {
         ESP_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(
-            &per_cu, reinterpret_cast<const void *>(decode_gemv_k<WT, EPI, RB, NCH>), DG_THREADS, 0));
+            &per_cu, reinterpret_cast<const void *>(decode_gemv_k<WT, EPI, RB, NCH, NW>), NW * 64, 0));
         if (per_cu <= 0) per_cu = 1;
     }
     const int units = EPI == DG_QKVROPE ? a.N / 2 + (a.lora_rows + 1) / 2 : a.N;
@@ -353,7 +354,7 @@ static void dg_launch_nch(const DecodeGemvArgs &a, int cus, hipStream_t s) {
     if (blocks < need) blocks = need;
     if (EPI == DG_HEAD && a.ticket && blocks > DG_MAX_PART)
         fail(ESP_UNSUPPORTED, "decode head: vocabulary above the argmax partial capacity");
-    decode_gemv_k<WT, EPI, RB, NCH><<<blocks, DG_THREADS, 0, s>>>(a);
+    decode_gemv_k<WT, EPI, RB, NCH, NW><<<blocks, NW * 64, 0, s>>>(a);
 }
 
 template <typename WT, int EPI>
@@ -365,6 +366,15 @@ static void dg_launch(const DecodeGemvArgs &a, int cus, hipStream_t s) {
     // rows per block (measured at H 2048: 90.6 vs 97.4 us for 128256 rows)
     if (EPI == DG_HEAD && nch <= 1) {
         dg_launch_nch<WT, EPI, 4, 1>(a, cus, s);
+        return;
+    }
+    // bf16 rows wider than 8k (down_proj at F 14336): eight waves split K,
+    // four chunks per lane instead of eight (111 instead of 155 VGPRs: four
+    // waves per SIMD instead of three). Measured at C3 decode: 3.35 -> 3.30
+    // ms per token; seven waves (exactly four chunks per lane) 3.32 ms.
+    // ESP_DG_4W=1 keeps the four-wave form, for comparison.
+    if (std::is_same<WT, uint16_t>::value && nch > 4 && a.K % (8 * 64) == 0 && !getenv("ESP_DG_4W")) {
+        dg_launch_nch<WT, EPI, 2, DG_MAXC / 2, 8>(a, cus, s);
         return;
     }
     if (nch <= 1) dg_launch_nch<WT, EPI, 2, 1>(a, cus, s);
