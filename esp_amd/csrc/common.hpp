@@ -51,6 +51,12 @@ struct Rows {
     const int32_t *row_pos;  // [M]
     int M;
     int seq1 = -1;           // >= 0: every row belongs to this sequence
+    // nullable: groups of consecutive rows of one sequence (consecutive
+    // positions), row0 | (rows << 16) each, for attention kernels that read
+    // a sequence's keys once per group
+    const int32_t *grp = nullptr;
+    int ngrp = 0;
+    int grp_rows = 0;        // rows per full group
 };
 
 // h[M,H] (f32) = embed[ids[m]] (wt)

@@ -89,6 +89,10 @@ struct AttnDecodeArgs {
     int lora_rank[3];
     float lora_scale[3];
     const float *rope_cos, *rope_sin;  // [max_pos, hd]
+    // nullable (attn_rows_mfma_k only): row groups (Rows::grp); one unit
+    // per (group, kv head) instead of per (row, kv head)
+    const int32_t *grp;
+    int ngrp;
 };
 
 bool attn_decode_ok(int hd, int G);

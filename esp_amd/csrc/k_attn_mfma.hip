@@ -4,8 +4,11 @@
 // over the row's cached keys), for batches whose (row, kv head) units fill
 // the chip on their own.
 //
-// One wave per (row, kv head) unit; its G query heads are the 16 columns of
-// v_mfma_f32_16x16x32 products (heads past G are zero columns):
+// One wave per (row group, kv head) unit: a group is up to 16 / G rows of
+// one sequence at consecutive positions (a forced block's rows), so the
+// group's key tiles are read once; its rows' G query heads are the 16
+// columns of v_mfma_f32_16x16x32 products (column c = row c / G, head c % G;
+// unused columns are zero), each column masked to its own row's keys:
 //   S^T = K Q^T   A = K (16 keys x 32 dims), B = Q^T
 //   O^T = V^T P^T A = V^T (16 dims x 32 keys, through LDS), B = P^T
 // In the 16 x 16 accumulator layout lane l holds column l % 16 (= its query
@@ -89,14 +92,29 @@ __global__ void __launch_bounds__(AM_WAVES * 64) attn_rows_mfma_k(AttnDecodeArgs
     // the unit, its row range and the buffer descriptors are wave-uniform
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int unit = blockIdx.x * AM_WAVES + wave;
-    if (unit >= a.M * a.nkv) return;  // no barriers below
-    const int g = unit % a.nkv, row = unit / a.nkv;
+    if (unit >= (a.grp ? a.ngrp : a.M) * a.nkv) return;  // no barriers below
+    const int g = unit % a.nkv, gi = unit / a.nkv;
     const int G = a.nq / a.nkv;
     const int col = lane & 15, grp = lane >> 4;
-    const int seq = a.seq1 >= 0 ? a.seq1 : a.row_seq[row];
-    const int pos = a.row_pos[row];
-    const int lo = a.window > 0 ? max(0, pos - a.window + 1) : 0;
-    const int hi = min(pos + 1, a.max_t);
+    // the unit's rows: one group of nr consecutive positions of a sequence
+    // (or a single row); column col is row j = col / G, query head col % G
+    int r0 = gi, nr = 1;
+    if (a.grp) {
+        const int e = a.grp[gi];
+        r0 = e & 0xffff;
+        nr = e >> 16;
+    }
+    const int j = col / G, hq = col % G;
+    const bool cvalid = j < nr;
+    const int row_c = r0 + (cvalid ? j : 0);
+    const int seq = a.seq1 >= 0 ? a.seq1 : a.row_seq[r0];
+    const int pos_c = a.row_pos[row_c];  // this lane's row
+    const int pos0 = a.row_pos[r0], posn = a.row_pos[r0 + nr - 1];
+    const int lo_c = a.window > 0 ? max(0, pos_c - a.window + 1) : 0;
+    const int hi_c = min(pos_c + 1, a.max_t);
+    // the key range every column needs: [lo of the first row, end of the last)
+    const int lo = a.window > 0 ? max(0, pos0 - a.window + 1) : 0;
+    const int hi = min(posn + 1, a.max_t);
     const char *kb = (const char *)a.kv + ((size_t)seq * a.seq_stride + (size_t)g * a.head_stride) * ES;
     const char *vb = kb + (size_t)a.kv_half_stride * ES;
     uint16_t *vt = lds + wave * S::LDSW;
@@ -104,12 +122,12 @@ __global__ void __launch_bounds__(AM_WAVES * 64) attn_rows_mfma_k(AttnDecodeArgs
     // q of this lane's head (zero columns past G), pre-split
     am_u4 qh[S::KS], ql[S::KS];
     {
-        const float *qr = a.q + (size_t)row * a.nq * HD + (size_t)(g * G + min(col, G - 1)) * HD + grp * S::KD;
+        const float *qr = a.q + (size_t)row_c * a.nq * HD + (size_t)(g * G + hq) * HD + grp * S::KD;
 #pragma unroll
         for (int s = 0; s < S::KS; ++s) {
             const am_f4 x0 = *(const am_f4 *)(qr + 8 * s), x1 = *(const am_f4 *)(qr + 8 * s + 4);
             float x[8] = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
-            if (col >= G) {
+            if (!cvalid) {
 #pragma unroll
                 for (int j = 0; j < 8; ++j) x[j] = 0.f;
             }
@@ -228,7 +246,7 @@ __global__ void __launch_bounds__(AM_WAVES * 64) attn_rows_mfma_k(AttnDecodeArgs
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int key = t0 + 16 * h + 4 * grp + i;
-                sc[4 * h + i] = key < hi ? sa[h][i] * cscale : -INFINITY;
+                sc[4 * h + i] = key >= lo_c && key < hi_c ? sa[h][i] * cscale : -INFINITY;
             }
         float mx = sc[0];
 #pragma unroll
@@ -300,8 +318,8 @@ __global__ void __launch_bounds__(AM_WAVES * 64) attn_rows_mfma_k(AttnDecodeArgs
     // the head's sum over the four lane groups, then O / sum
     l += __shfl_xor(l, 16, 64);
     l += __shfl_xor(l, 32, 64);
-    if (col >= G) return;
-    const size_t ob = (size_t)row * a.nq * HD + (size_t)(g * G + col) * HD;
+    if (!cvalid) return;
+    const size_t ob = (size_t)row_c * a.nq * HD + (size_t)(g * G + hq) * HD;
 #pragma unroll
     for (int d = 0; d < HD / 16; ++d)
 #pragma unroll
@@ -327,7 +345,7 @@ bool attn_rows_mfma_ok(const AttnDecodeArgs &a) {
 void launch_attn_rows_mfma(const AttnDecodeArgs &a, hipStream_t s) {
     if (!attn_rows_mfma_ok(a)) fail(ESP_BACKEND, "attn_rows_mfma: unsupported shape");
     if (a.max_t < 1) fail(ESP_BACKEND, "attn_rows_mfma: empty key range");
-    const long long units = (long long)a.M * a.nkv;
+    const long long units = (long long)(a.grp ? a.ngrp : a.M) * a.nkv;
     const unsigned blocks = (unsigned)((units + AM_WAVES - 1) / AM_WAVES);
     if (a.hd == 64) {
         if (a.kv_f16) attn_rows_mfma_k<64, true><<<blocks, AM_WAVES * 64, 0, s>>>(a);

@@ -1015,7 +1015,8 @@ void launch_attn_decode(const AttnDecodeArgs &a0, hipStream_t s) {
         // batches whose units fill the chip without key splits: matrix cores
         // (ESP_ATT_MFMA=0 keeps the vector form, for comparison)
         const char *am = getenv("ESP_ATT_MFMA");
-        if (U >= device_cus() && attn_rows_mfma_ok(a) && !(am && am[0] == '0')) {
+        const long long Ur = (long long)(a.grp ? a.ngrp : a.M) * a.nkv;  // its units: row groups
+        if (Ur >= device_cus() && attn_rows_mfma_ok(a) && !(am && am[0] == '0')) {
             launch_attn_rows_mfma(a, s);
             return;
         }

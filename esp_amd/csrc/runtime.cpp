@@ -869,6 +869,8 @@ static void attn_decode_rows(Model &m, Kv &kv, const Rows &rows, int Mc, int l, 
     a.row_pos = rows.row_pos;
     a.row_seq = rows.row_seq;
     a.seq1 = rows.seq1;
+    a.grp = rows.grp;
+    a.ngrp = rows.ngrp;
     a.M = Mc;
     a.nq = m.nq;
     a.nkv = m.nkv;
@@ -1389,7 +1391,7 @@ static void ensure_scratch(Model &m, Kv &kv, int Mc, int n_seqs) {
     kv.act.ensure((size_t)Mc * fmax * 4);
     kv.last_h.ensure((size_t)n_seqs * H * 4);
     kv.logits.ensure((size_t)std::max(n_seqs, kv.batch) * m.V * 4);
-    kv.rows_dev.ensure((size_t)(3 * kMaxRows + 2 * kv.batch + 64) * 4);
+    kv.rows_dev.ensure((size_t)(4 * kMaxRows + 2 * kv.batch + 64) * 4);
     if (Mc > 1 && (m.wt == DT_BF16 || dt_packed(m.wt)))
         kv.gemm_ws.ensure((size_t)256 << 20);  // split-K partials
     if (m.E && !kv.moe_err.p) {
@@ -1541,7 +1543,10 @@ static bool forward_pass(Model &m, Kv &kv, int n_seqs, const uint32_t *seqs, con
     hipStream_t s = kv.stream;
     const int lastoff = 3 * kMaxRows;
     const int erroff = lastoff + kv.batch + 8;  // pinned word: the router status read back
-    ensure_pinned(kv, (size_t)(3 * kMaxRows + kv.batch + 64) * 4);
+    const int grpoff = lastoff + kv.batch + 32;  // row groups of the row attention
+    ensure_pinned(kv, (size_t)(4 * kMaxRows + kv.batch + 64) * 4);
+    // rows of one sequence that the matrix-core row attention serves per wave
+    const int G = m.nq / m.nkv, grp_rows = G >= 1 && G <= 16 ? 16 / G : 1;
     if (kv.moe_err.p) launch_fill_const(kv.moe_err.as<float>(), 1, 0.f, s);
     int32_t *pin = (int32_t *)kv.pinned;
     int32_t *dev = kv.rows_dev.as<int32_t>();
@@ -1554,16 +1559,11 @@ static bool forward_pass(Model &m, Kv &kv, int n_seqs, const uint32_t *seqs, con
         memcpy(pin + kMaxRows, rseq.data() + c0, Mc * 4);
         memcpy(pin + 2 * kMaxRows, rpos.data() + c0, Mc * 4);
         memcpy(pin + lastoff, last.data(), n_seqs * 4);
-        ESP_HIP(hipMemcpyAsync(dev, pin, (size_t)(lastoff + n_seqs) * 4, hipMemcpyHostToDevice, s));
-        Rows rows{dev, dev + kMaxRows, dev + 2 * kMaxRows, Mc, n_seqs == 1 ? (int)seqs[0] : -1};
-        {
-            Prof p("embed", s);
-            launch_embed(m.et, m.embed, rows.ids, Mc, m.H, kv.h.as<float>(), s);
-        }
-        if (n_seqs == 1) {
-            run_layers(m, kv, rows, Mc, max_t, (int)seqs[0], rpos[c0]);
-        } else {
-            std::vector<Seg> segs;
+        // segments: runs of consecutive positions of one sequence; each is
+        // cut into row groups of up to grp_rows rows
+        std::vector<Seg> segs;
+        int ngrp = 0;
+        if (n_seqs > 1) {
             for (int r = 0; r < Mc; ++r) {
                 const long long g = c0 + r;
                 if (segs.empty() || rseq[g] != segs.back().seq ||
@@ -1571,8 +1571,24 @@ static bool forward_pass(Model &m, Kv &kv, int n_seqs, const uint32_t *seqs, con
                     segs.push_back(Seg{rseq[g], r, 0, rpos[g]});
                 segs.back().len++;
             }
-            run_layers(m, kv, rows, Mc, max_t, -1, 0, &segs);
+            for (const Seg &sg : segs)
+                for (int r = 0; r < sg.len; r += grp_rows)
+                    pin[grpoff + ngrp++] = (sg.row0 + r) | (std::min(grp_rows, sg.len - r) << 16);
         }
+        ESP_HIP(hipMemcpyAsync(dev, pin, (size_t)(ngrp ? grpoff + ngrp : lastoff + n_seqs) * 4,
+                               hipMemcpyHostToDevice, s));
+        Rows rows{dev, dev + kMaxRows, dev + 2 * kMaxRows, Mc, n_seqs == 1 ? (int)seqs[0] : -1};
+        if (ngrp) {
+            rows.grp = dev + grpoff;
+            rows.ngrp = ngrp;
+            rows.grp_rows = grp_rows;
+        }
+        {
+            Prof p("embed", s);
+            launch_embed(m.et, m.embed, rows.ids, Mc, m.H, kv.h.as<float>(), s);
+        }
+        if (n_seqs == 1) run_layers(m, kv, rows, Mc, max_t, (int)seqs[0], rpos[c0]);
+        else run_layers(m, kv, rows, Mc, max_t, -1, 0, &segs);
         if (one_chunk) break;
         // keep the hidden state of every sequence's last row in this chunk
         for (int i = 0; i < n_seqs; ++i)

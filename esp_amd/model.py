@@ -8,6 +8,7 @@ libesp_hip.so; this module converts arguments and errors only.
 from __future__ import annotations
 
 import ctypes as C
+import itertools
 from typing import List, Optional, Sequence, Tuple
 
 import numpy as np
@@ -270,8 +271,8 @@ class DecoderModel:
                       blocks: Sequence[Sequence[int]], want_logits: bool = True) -> Optional[np.ndarray]:
         """Several sequences' blocks in one pass; row i = last logits of seqs[i]."""
         seqs_a = np.ascontiguousarray(seqs, dtype=np.uint32)
-        lens = np.ascontiguousarray([len(b) for b in blocks], dtype=np.uint32)
-        ids = np.ascontiguousarray([t for b in blocks for t in b], dtype=np.int32)
+        lens = np.fromiter(map(len, blocks), dtype=np.uint32, count=len(blocks))
+        ids = np.fromiter(itertools.chain.from_iterable(blocks), dtype=np.int32, count=int(lens.sum()))
         out = np.empty((len(seqs_a), self.config.vocab_size), np.float32) if want_logits else None
         self._check(_lib.load().esp_forward_batch(
             self._h, cache._h, len(seqs_a), seqs_a.ctypes.data_as(C.POINTER(C.c_uint32)),
