@@ -967,6 +967,16 @@ template <int EPI> static void mfma_launch(const GemmArgs &a, float *ws, size_t 
         lds_launch<EPI, NB, 2, 64 * NB, 6>(a, ws, ws_bytes, s, g_cus, 256);
         return;
     }
+    if (a.K % LS_BK == 0 && a.M > MF_BM && a.M < 1024 && !getenv("ESP_MID_REG")) {
+        // 129 - 1023 rows (grammar-forced spans in a batch, short prompts):
+        // the streamed form, 128-row tiles of 128 weight rows per matrix,
+        // three stages (measured on the C5 grammar batch: 4.87 -> 4.47 ms
+        // per step against the register-staged tiles; 64 weight rows and
+        // six stages 4.55, the 256-row prefill tiles 4.80).
+        // ESP_MID_REG=1 keeps the register-staged form, for comparison.
+        lds_launch<EPI, NB, 2, 128 * NB, 3>(a, ws, ws_bytes, s, g_cus, 256);
+        return;
+    }
     if (a.M <= MF_BM) {
         // 64-column register-staged tiles, k splits down to 128 keys
         mfma_launch_nj<EPI, NB, 1>(a, ws, ws_bytes, s, 128);
