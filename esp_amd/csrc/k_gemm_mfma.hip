@@ -304,9 +304,10 @@ constexpr int LS_ROWB = LS_BK * 2;                 // bytes per tile row
 // BMW waves along M (block rows 64 * BMW) x 2 along N, BROWS weight rows
 // per stage (all matrices), STG stages: 128-row blocks with 256 weight rows
 // keep two stages (64 KB) so two blocks share a CU; 256-row blocks (eight
-// waves) keep three (144 KB); skinny row counts (M <= 128) use 64 weight
-// rows per matrix and six stages in flight (one block per CU), since their
-// time is the latency of the weight stream, not the matrix cores.
+// waves) keep three (144 KB); one row tile (M <= 128) uses 64 weight rows
+// per matrix and three stages, and 129-1023 rows 128 weight rows per
+// matrix and three stages (the stage count and tile widths for these row
+// ranges were chosen by measurement on the C5 and C2 shapes).
 template <int BMW, int BROWS = 256, int STG = (BMW == 2 ? 2 : 3)> struct LsForm {
     static constexpr int BM = 64 * BMW, NT = 128 * BMW;
     static constexpr int A = BM * LS_ROWB;                       // one A plane per stage
@@ -963,8 +964,9 @@ template <int EPI> static void mfma_launch(const GemmArgs &a, float *ws, size_t 
     }
     if (a.K % LS_BK == 0 && a.M <= MF_BM && !getenv("ESP_SKINNY_REG")) {
         // one row tile (decode batches, forced blocks): 64 weight columns per
-        // matrix, six stages in flight, k splits down to 256 keys
-        lds_launch<EPI, NB, 2, 64 * NB, 6>(a, ws, ws_bytes, s, g_cus, 256);
+        // matrix, three stages (60 KB of LDS; measured on the C5 step: 3.28
+        // -> 3.19 ms against six stages), k splits down to 256 keys
+        lds_launch<EPI, NB, 2, 64 * NB, 3>(a, ws, ws_bytes, s, g_cus, 256);
         return;
     }
     if (a.K % LS_BK == 0 && a.M > MF_BM && a.M < 1024 && !getenv("ESP_MID_REG")) {
