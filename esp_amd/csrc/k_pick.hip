@@ -750,7 +750,7 @@ __global__ void __launch_bounds__(GC_THREADS) pick_chain_k(PickArgs a, PickScrat
     __shared__ float s_x;
     __shared__ int s_i, s_ev, s_stop;
     __shared__ float s_wev;
-    __shared__ float s_w[GC_SERIAL];
+    __shared__ __attribute__((aligned(16))) float s_w[GC_SERIAL];
     __shared__ int ck_i[GC_CK];
     __shared__ float ck_x[GC_CK];
     __shared__ int s_nck;
@@ -811,21 +811,44 @@ __global__ void __launch_bounds__(GC_THREADS) pick_chain_k(PickArgs a, PickScrat
                 for (int r = tid; r < len; r += GC_THREADS) s_w[r] = w[i + r];
                 __syncthreads();
                 if (tid == 0) {
+                    // Terms are positive, so the running value is monotone
+                    // (up for sums, down for the walk): a batch of eight whose
+                    // end value has not reached the stop condition never
+                    // reached it inside, and is added plainly; the batch that
+                    // reaches it is replayed term by term from its start
+                    // value (identical arithmetic either way).
+                    auto reached = [&](float v) {
+                        return walk ? v <= 0.0f : (use_target && v >= target);
+                    };
                     float y = x;
                     int k = 0, stop = 0;
-                    for (; k < len; ++k) {
+                    for (; k + 8 <= len; k += 8) {
+                        const float4 b0 = *(const float4 *)&s_w[k];
+                        const float4 b1 = *(const float4 *)&s_w[k + 4];
+                        float z = y;
                         if (!walk) {
-                            y += s_w[k];
-                            if (use_target && y >= target) {
-                                stop = 1;
-                                break;
-                            }
+                            z += b0.x; z += b0.y; z += b0.z; z += b0.w;
+                            z += b1.x; z += b1.y; z += b1.z; z += b1.w;
                         } else {
-                            y -= s_w[k];
-                            if (y <= 0.0f) {
-                                stop = 1;
-                                break;
-                            }
+                            z -= b0.x; z -= b0.y; z -= b0.z; z -= b0.w;
+                            z -= b1.x; z -= b1.y; z -= b1.z; z -= b1.w;
+                        }
+                        if (!reached(z)) {
+                            y = z;
+                            continue;
+                        }
+                        stop = 1;
+                        break;
+                    }
+                    // the reaching batch (stop) or the tail past the last
+                    // whole batch, term by term
+                    const int end = stop ? k + 8 : len;
+                    stop = 0;
+                    for (; k < end; ++k) {
+                        y = walk ? y - s_w[k] : y + s_w[k];
+                        if (reached(y)) {
+                            stop = 1;
+                            break;
                         }
                     }
                     s_x = y;
