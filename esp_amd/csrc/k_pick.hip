@@ -717,35 +717,67 @@ __device__ __forceinline__ uint64_t grid_ceil(float t, int ue) {
     return qc;
 }
 
-// Exclusive prefix sum of a u64 over the block; *total gets the sum.
-__device__ uint64_t block_scan_u64(uint64_t v, uint64_t *tmp, uint64_t *total) {
+// grid_units in 32 bits for the scan windows, values saturated at GC_SAT:
+// a term of 2^24 grid units or more leaves the binade (or passes the walk's
+// floor), so it is an event, and before a window's first event every prefix
+// stays below 2^24 (no wrap-around reaches the first event).
+constexpr uint32_t GC_SAT = 1u << 25;
+__device__ __forceinline__ uint32_t grid_units32(uint32_t wb, int ue, bool &tie, uint32_t &qc) {
+    const int ew = (int)((wb >> 23) & 0xff);
+    uint32_t m = wb & 0x7fffff;
+    int e;
+    if (ew == 0) {
+        e = -149;
+    } else {
+        m |= 0x800000;
+        e = ew - 150;
+    }
+    const int sh = ue - e;
+    tie = false;
+    if (sh <= 0) {  // -sh >= 2 only for normal terms (m >= 2^23): >= 2^25 units
+        qc = -sh >= 2 ? GC_SAT : m << (-sh);
+        return qc;
+    }
+    if (sh >= 25) {  // m < 2^24 <= half: rounds to 0, never a tie
+        qc = m != 0;
+        return 0;
+    }
+    const uint32_t q = m >> sh, r = m & ((1u << sh) - 1), half = 1u << (sh - 1);
+    qc = q + (r != 0);
+    if (r > half) return q + 1;
+    tie = r == half;
+    return q;
+}
+
+// Exclusive prefix sum of a u32 over the block (wrapping); *total gets the sum.
+__device__ uint32_t block_scan_u32(uint32_t v, uint32_t *tmp, uint32_t *total) {
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, nw = blockDim.x >> 6;
-    uint64_t x = v;
+    uint32_t x = v;
 #pragma unroll
     for (int d = 1; d < 64; d <<= 1) {
-        const uint64_t y = __shfl_up(x, d);
+        const uint32_t y = __shfl_up(x, d);
         if (lane >= d) x += y;
     }
     if (lane == 63) tmp[wv] = x;
     __syncthreads();
     if (threadIdx.x == 0) {
-        uint64_t run = 0;
+        uint32_t run = 0;
         for (int w = 0; w < nw; ++w) {
-            const uint64_t t = tmp[w];
+            const uint32_t t = tmp[w];
             tmp[w] = run;
             run += t;
         }
         tmp[32] = run;
     }
     __syncthreads();
-    const uint64_t r = tmp[wv] + x - v;
+    const uint32_t r = tmp[wv] + x - v;
     *total = tmp[32];
     __syncthreads();
     return r;
 }
 
 __global__ void __launch_bounds__(GC_THREADS) pick_chain_k(PickArgs a, PickScratch ps) {
-    __shared__ uint64_t s_tmp[33];
+    __shared__ uint32_t s_tmp[33];
     __shared__ uint64_t s_pref;
     __shared__ float s_x;
     __shared__ int s_i, s_ev, s_stop;
@@ -863,10 +895,13 @@ __global__ void __launch_bounds__(GC_THREADS) pick_chain_k(PickArgs a, PickScrat
             W = min(W, n - i);
             const int ipt = (W + GC_THREADS - 1) / GC_THREADS;
             const int base = i + tid * ipt;
-            uint64_t q[GC_IPT], qc[GC_IPT];
+            // 32-bit grid values (see grid_units32); the bounds below lim
+            const uint32_t K32 = (uint32_t)K, lim32 = (uint32_t)lim, low32 = (uint32_t)(low ? low : 1);
+            const uint32_t T32 = (uint32_t)min<uint64_t>(T, lim);
+            uint32_t q[GC_IPT], qc[GC_IPT];
             float wv[GC_IPT];
             bool tie[GC_IPT];
-            uint64_t lsum = 0;
+            uint32_t lsum = 0;
 #pragma unroll
             for (int r = 0; r < GC_IPT; ++r) {
                 const int j = base + r;
@@ -875,24 +910,24 @@ __global__ void __launch_bounds__(GC_THREADS) pick_chain_k(PickArgs a, PickScrat
                 wv[r] = 0.f;
                 if (r < ipt && j < i + W) {
                     wv[r] = w[j];
-                    q[r] = grid_units(__float_as_uint(wv[r]), ue, tie[r], qc[r]);
+                    q[r] = grid_units32(__float_as_uint(wv[r]), ue, tie[r], qc[r]);
                     lsum += q[r];
                 }
             }
-            uint64_t tot;
-            uint64_t E = block_scan_u64(lsum, s_tmp, &tot);
+            uint32_t tot;
+            uint32_t E = block_scan_u32(lsum, s_tmp, &tot);
             if (tid == 0) s_ev = 0x7fffffff;
             __syncthreads();
             int mine = 0x7fffffff;
-            uint64_t mine_pref = 0;
+            uint32_t mine_pref = 0;
             float mine_w = 0.f;
 #pragma unroll
             for (int r = 0; r < GC_IPT; ++r) {
                 const int j = base + r;
                 if (r < ipt && j < i + W && mine == 0x7fffffff) {
                     bool ev = tie[r];
-                    if (!walk) ev = ev || K + E + q[r] >= lim || (use_target && K + E + q[r] >= T);
-                    else ev = ev || E + qc[r] + (low ? low : 1) > K;
+                    if (!walk) ev = ev || K32 + E + q[r] >= lim32 || (use_target && K32 + E + q[r] >= T32);
+                    else ev = ev || E + qc[r] + low32 > K32;
                     if (ev) {
                         mine = j - i;
                         mine_pref = E;
