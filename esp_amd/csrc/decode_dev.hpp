@@ -1,5 +1,5 @@
-// Device helpers shared by the single-token kernels (k_decode.hip) and the
-// persistent decode-step kernel (k_step.hip).
+// Device helpers of the single-token kernels (k_decode.hip): cross-block
+// hand-off stores and loads, and the packed weight formats.
 #pragma once
 
 #include "common.hpp"
