@@ -286,6 +286,75 @@ __global__ void __launch_bounds__(256) mfma_reduce_k(GemmArgs g, const float *ws
     }
 }
 
+// mfma_reduce_k over four consecutive columns per thread (N and ldc
+// multiples of 4): 16-byte partial loads, every split's load of the group in
+// flight before the sums, and the same per-element arithmetic (splits
+// summed from 0 in split order, then the epilogue).
+template <int EPI, int NB>
+__global__ void __launch_bounds__(256) mfma_reduce4_k(GemmArgs g, const float *ws, int splits) {
+    const size_t MN = (size_t)g.M * g.N, MN4 = MN / 4;
+    for (size_t q = blockIdx.x * (size_t)blockDim.x + threadIdx.x; q < MN4;
+         q += (size_t)gridDim.x * blockDim.x) {
+        const size_t idx = q * 4;
+        const int row = (int)(idx / g.N), col = (int)(idx % g.N);
+        float4 v[NB];
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+            float4 t = make_float4(0.f, 0.f, 0.f, 0.f);
+            for (int z0 = 0; z0 < splits; z0 += 8) {
+                float4 pz[8];
+#pragma unroll
+                for (int u = 0; u < 8; ++u)
+                    if (z0 + u < splits) pz[u] = *(const float4 *)(ws + ((size_t)(z0 + u) * NB + b) * MN + idx);
+#pragma unroll
+                for (int u = 0; u < 8; ++u)
+                    if (z0 + u < splits) {
+                        t.x += pz[u].x;
+                        t.y += pz[u].y;
+                        t.z += pz[u].z;
+                        t.w += pz[u].w;
+                    }
+            }
+            v[b] = t;
+        }
+        const size_t ci = (size_t)row * g.ldc + col;
+        if (EPI == GEMM_SWIGLU) {
+            const float y[4] = {silu(v[0].x) * v[NB - 1].x, silu(v[0].y) * v[NB - 1].y,
+                                silu(v[0].z) * v[NB - 1].z, silu(v[0].w) * v[NB - 1].w};
+            if (g.c_lo) {
+                uint16_t h[4], l[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    h[e] = f2bf(y[e]);
+                    l[e] = f2bf(y[e] - bf2f(h[e]));
+                }
+                *(uint2 *)((uint16_t *)g.c + ci) = make_uint2(pack2(h[0], h[1]), pack2(h[2], h[3]));
+                *(uint2 *)((uint16_t *)g.c_lo + ci) = make_uint2(pack2(l[0], l[1]), pack2(l[2], l[3]));
+            } else {
+                *(float4 *)((float *)g.c + ci) = make_float4(y[0], y[1], y[2], y[3]);
+            }
+        } else {
+            float4 y = v[0];
+            if (g.bias) {
+                const float4 bb = *(const float4 *)(g.bias + col);
+                y.x += bb.x;
+                y.y += bb.y;
+                y.z += bb.z;
+                y.w += bb.w;
+            }
+            float4 *c = (float4 *)((float *)g.c + ci);
+            if (EPI == GEMM_RESIDUAL) {
+                const float4 o = *c;
+                y.x = o.x + y.x;
+                y.y = o.y + y.y;
+                y.z = o.z + y.z;
+                y.w = o.w + y.w;
+            }
+            *c = y;
+        }
+    }
+}
+
 // ---------------------------------------------------------------------------
 // Streamed form (K a multiple of 32): the same 128 x 256 block tile, but the
 // A planes and weight rows go global -> LDS directly (global_load_lds, 16
@@ -602,6 +671,23 @@ __global__ void __launch_bounds__(128 * BMW + (PROD ? 64 : 0), (BMW == 2 && STG 
 
 static int g_cus = 0;
 
+// The split-K reduction launch: four columns per thread when the shapes
+// and pointers allow 16-byte access, else one.
+template <int EPI, int NB>
+static void launch_reduce(const GemmArgs &a, const float *ws, int splits, hipStream_t s) {
+    const size_t mn = (size_t)a.M * a.N;
+    auto al16 = [](const void *p) { return ((uintptr_t)p & 15) == 0; };
+    const bool v4 = a.N % 4 == 0 && a.ldc % 4 == 0 && al16(ws) && al16(a.c) &&
+                    (!a.c_lo || al16(a.c_lo)) && (!a.bias || al16(a.bias));
+    if (v4) {
+        const int rblocks = (int)std::min<size_t>((mn / 4 + 255) / 256, (size_t)g_cus * 8);
+        mfma_reduce4_k<EPI, NB><<<rblocks, 256, 0, s>>>(a, ws, splits);
+        return;
+    }
+    const int rblocks = (int)std::min<size_t>((mn + 255) / 256, (size_t)g_cus * 8);
+    mfma_reduce_k<EPI, NB><<<rblocks, 256, 0, s>>>(a, ws, splits);
+}
+
 // min_ks: smallest k range a split may get (the weight tile each block
 // streams shrinks with it, so skinny row counts use short splits to put the
 // weight stream on every CU)
@@ -629,9 +715,7 @@ static void mfma_launch_nj(const GemmArgs &a, float *ws, size_t ws_bytes, hipStr
         *a.defer_splits = splits;
         return;
     }
-    size_t mn = (size_t)a.M * a.N;
-    const int rblocks = (int)std::min<size_t>((mn + 255) / 256, (size_t)g_cus * 8);
-    mfma_reduce_k<EPI, NB><<<rblocks, 256, 0, s>>>(a, ws, splits);
+    launch_reduce<EPI, NB>(a, ws, splits, s);
 }
 
 template <int EPI, int NB, int BMW, int BROWS = 256, int STG = (BMW == 2 ? 2 : 3)>
@@ -679,9 +763,7 @@ static void lds_launch(const GemmArgs &a, float *ws, size_t ws_bytes, hipStream_
                 *a.defer_splits = splits;
                 return;
             }
-            size_t mn = (size_t)a.M * a.N;
-            const int rblocks = (int)std::min<size_t>((mn + 255) / 256, (size_t)g_cus * 8);
-            mfma_reduce_k<EPI, NB><<<rblocks, 256, 0, s>>>(a, ws, splits);
+            launch_reduce<EPI, NB>(a, ws, splits, s);
             return;
         }
     }
@@ -694,9 +776,7 @@ static void lds_launch(const GemmArgs &a, float *ws, size_t ws_bytes, hipStream_
         *a.defer_splits = splits;
         return;
     }
-    size_t mn = (size_t)a.M * a.N;
-    const int rblocks = (int)std::min<size_t>((mn + 255) / 256, (size_t)g_cus * 8);
-    mfma_reduce_k<EPI, NB><<<rblocks, 256, 0, s>>>(a, ws, splits);
+    launch_reduce<EPI, NB>(a, ws, splits, s);
 }
 
 // ---------------------------------------------------------------------------
@@ -920,9 +1000,7 @@ static void skinny_launch(const GemmArgs &a, float *ws, size_t ws_bytes, hipStre
         *a.defer_splits = splits;
         return;
     }
-    size_t mn = (size_t)a.M * a.N;
-    const int rblocks = (int)std::min<size_t>((mn + 255) / 256, (size_t)g_cus * 8);
-    mfma_reduce_k<EPI, NB><<<rblocks, 256, 0, s>>>(a, ws, splits);
+    launch_reduce<EPI, NB>(a, ws, splits, s);
 }
 
 template <int EPI> static void mfma_launch(const GemmArgs &a, float *ws, size_t ws_bytes,
