@@ -140,13 +140,15 @@ __global__ void __launch_bounds__(256) resid_norm_k(const float *ws, int splits,
     __shared__ float red[4];
     const int m = blockIdx.x, tid = threadIdx.x;
     const size_t MH = (size_t)M * H;
-    f32x4 v[NQ];
+    f32x4 v[NQ], gv[NQ];
     float ss = 0.f;
 #pragma unroll
     for (int i = 0; i < NQ; ++i) {
         const int j = (tid + 256 * i) * 4;
         v[i] = f32x4{0.f, 0.f, 0.f, 0.f};
         if (j >= H) continue;
+        // gamma now, with the partials: no memory wait after the barrier
+        gv[i] = *(const f32x4 *)(gamma + j);
         const size_t o = (size_t)m * H + j;
         f32x4 t = {0.f, 0.f, 0.f, 0.f};
         for (int z0 = 0; z0 < splits; z0 += 8) {
@@ -173,10 +175,9 @@ __global__ void __launch_bounds__(256) resid_norm_k(const float *ws, int splits,
     for (int i = 0; i < NQ; ++i) {
         const int j = (tid + 256 * i) * 4;
         if (j >= H) continue;
-        const f32x4 gv = *(const f32x4 *)(gamma + j);
         float y[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) y[e] = (v[i][e] / rms) * gv[e];
+        for (int e = 0; e < 4; ++e) y[e] = (v[i][e] / rms) * gv[i][e];
         const size_t o = (size_t)m * H + j;
         if (SPLIT) {
             uint16_t hi[4], lo[4];
