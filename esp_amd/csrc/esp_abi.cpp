@@ -8,6 +8,7 @@
 #include <string>
 #include <vector>
 
+#include "decode.hpp"
 #include "kernels_extra.hpp"
 #include "profile.hpp"
 #include "constraint.hpp"
@@ -22,6 +23,8 @@ Model *synthetic_model(const esp_config *cfg, uint64_t seed, float std, uint32_t
 Kv *create_kv(Model *m, uint32_t batch, uint32_t max_ctx, bool f16);
 void decode_step_dev(Model &m, Kv &kv, int seq, int max_t, int32_t *gen);
 void moe_check(Kv &kv);
+void moe_steps_reset(Kv &kv);
+void moe_check_steps(Kv &kv, uint32_t n);
 bool xcd_merge_failed(Kv &kv);
 void launch_gen_step(const uint32_t *picked, int32_t *gen, hipStream_t s);
 }  // namespace esp
@@ -578,7 +581,9 @@ esp_status esp_generate_greedy(esp_model *model, esp_kv *kv, uint32_t seq, const
         if (max_new == 0) return false;
         hipStream_t s = k.stream;
         // gen layout: [0] fed token, [1] step, [2] row_seq, [3] row_pos, [8..] list
-        DevMem gen((size_t)(8 + max_new) * 4);
+        // (gen_n <= the context window + 1 slots: only the fitting forwards'
+        // tokens are ever written)
+        DevMem gen((8 + (size_t)gen_n) * 4);
         int32_t *g = gen.as<int32_t>();
         int32_t init[4] = {0, 0, (int32_t)seq, (int32_t)n_prompt - 1};
         ESP_HIP(hipMemcpyAsync(g, init, sizeof(init), hipMemcpyHostToDevice, s));
@@ -608,6 +613,11 @@ esp_status esp_generate_greedy(esp_model *model, esp_kv *kv, uint32_t seq, const
         std::shared_ptr<Streamer> cached_st =
             keep && (int)keep->cache.size() == m.L && !m.E ? keep : nullptr;
         const uint64_t hits0 = cached_st ? cached_st->hits : 0;
+        auto is_eos = [&](int32_t id) {
+            for (uint32_t e = 0; e < n_eos; ++e)
+                if (id == eos[e]) return true;
+            return false;
+        };
         if (keep && !cached_st) {
             // Streamed layers are read between kernels: one host-driven step
             // per token, stopping at eos (generate.rs:154-168) so no layer
@@ -618,77 +628,97 @@ esp_status esp_generate_greedy(esp_model *model, esp_kv *kv, uint32_t seq, const
                 ESP_HIP(hipMemcpyAsync(&id, g + 8 + i, 4, hipMemcpyDeviceToHost, s));
                 ESP_HIP(hipStreamSynchronize(s));
                 stream_check(m);
-                bool stop = false;
-                for (uint32_t e = 0; e < n_eos; ++e) stop |= id == eos[e];
-                if (stop) break;
+                if (is_eos(id)) break;
                 if (out_ids) out_ids[n] = id;
                 ++n;
-                if (i + 1 < gen_n) decode_step_dev(m, k, (int)seq, max_t, g);
+                if (i + 1 < gen_n) {
+                    prof_count("greedy_forwards");
+                    decode_step_dev(m, k, (int)seq, max_t, g);
+                }
             }
             if (xcd_merge_failed(k)) return true;
             finish(n);
             return false;
         }
         // Every layer kind routes and groups on the device (MoE included), so
-        // the decode step is captured once and replayed. ESP_GRAPHS=0 replays
-        // eagerly (profilers).
+        // the decode step is captured once and replayed, in chunks of 4, 8,
+        // 16, 32, then 64 forwards: between chunks the host reads the new
+        // ids and stops at eos (generate.rs:154-168), so the forwards run are
+        // those the reference runs plus at most the rest of the last chunk.
+        // ESP_GRAPHS=0 replays eagerly (profilers).
         const char *env = getenv("ESP_GRAPHS");
         const bool capturable = !(env && env[0] == '0');
-        uint32_t steps = fit;
-        if (steps) {
-            decode_step_dev(m, k, (int)seq, max_t, g);  // eager: sizes every scratch buffer
-            --steps;
-        }
-        if (steps && capturable) {
-            hipGraph_t graph = nullptr;
-            hipGraphExec_t exec = nullptr;
-            ESP_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
-            g_capturing = true;
-            try {
-                decode_step_dev(m, k, (int)seq, max_t, g);
-            } catch (...) {
-                g_capturing = false;
-                (void)hipStreamEndCapture(s, &graph);
-                if (graph) (void)hipGraphDestroy(graph);
-                throw;
+        struct Exec {
+            hipGraphExec_t x = nullptr;
+            ~Exec() {
+                if (x) (void)hipGraphExecDestroy(x);
             }
-            g_capturing = false;
-            ESP_HIP(hipStreamEndCapture(s, &graph));
-            hipError_t ie = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
-            (void)hipGraphDestroy(graph);
-            ESP_HIP(ie);
-            for (uint32_t i = 0; i < steps; ++i) {
-                hipError_t le = hipGraphLaunch(exec, s);
-                if (le != hipSuccess) {
-                    (void)hipGraphExecDestroy(exec);
-                    ESP_HIP(le);
-                }
-            }
-            (void)hipGraphExecDestroy(exec);
-        } else {
-            for (uint32_t i = 0; i < steps; ++i) decode_step_dev(m, k, (int)seq, max_t, g);
-        }
+        } exec;
+        moe_steps_reset(k);
         std::vector<int32_t> list(gen_n);
-        ESP_HIP(hipMemcpyAsync(list.data(), g + 8, (size_t)gen_n * 4, hipMemcpyDeviceToHost, s));
-        ESP_HIP(hipStreamSynchronize(s));
-        if (xcd_merge_failed(k)) return true;
-        uint32_t n = 0;
-        for (; n < gen_n; ++n) {
-            bool stop = false;
-            for (uint32_t e = 0; e < n_eos; ++e) stop |= list[n] == eos[e];
-            if (stop) break;
-            if (out_ids) out_ids[n] = list[n];
+        uint32_t seen = 0, avail = 1, fwd = 0, n = gen_n, chunk = 4;
+        // reads list[seen, avail): true once an eos or the last fitting
+        // token has been seen
+        auto scan = [&]() -> bool {
+            ESP_HIP(hipMemcpyAsync(list.data() + seen, g + 8 + seen, (size_t)(avail - seen) * 4,
+                                   hipMemcpyDeviceToHost, s));
+            ESP_HIP(hipStreamSynchronize(s));
+            for (; seen < avail; ++seen)
+                if (is_eos(list[seen])) {
+                    n = seen;
+                    return true;
+                }
+            return avail == gen_n;
+        };
+        while (!scan()) {
+            uint32_t c = std::min(chunk, fit - fwd);
+            chunk = std::min<uint32_t>(chunk * 2, 64);
+            for (uint32_t i = 0; i < c; ++i) prof_count("greedy_forwards");
+            fwd += c;
+            avail += c;
+            if (fwd == c) {
+                decode_step_dev(m, k, (int)seq, max_t, g);  // eager: sizes every scratch buffer
+                --c;
+            }
+            if (c && capturable && !exec.x) {
+                hipGraph_t graph = nullptr;
+                ESP_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
+                g_capturing = true;
+                try {
+                    decode_step_dev(m, k, (int)seq, max_t, g);
+                } catch (...) {
+                    g_capturing = false;
+                    (void)hipStreamEndCapture(s, &graph);
+                    if (graph) (void)hipGraphDestroy(graph);
+                    throw;
+                }
+                g_capturing = false;
+                ESP_HIP(hipStreamEndCapture(s, &graph));
+                hipError_t ie = hipGraphInstantiate(&exec.x, graph, nullptr, nullptr, 0);
+                (void)hipGraphDestroy(graph);
+                ESP_HIP(ie);
+            }
+            for (uint32_t i = 0; i < c; ++i) {
+                if (exec.x) ESP_HIP(hipGraphLaunch(exec.x, s));
+                else decode_step_dev(m, k, (int)seq, max_t, g);
+            }
         }
-        moe_check(k);  // a step whose router failed fails the generation
+        if (xcd_merge_failed(k)) return true;
+        if (out_ids)
+            for (uint32_t i = 0; i < n; ++i) out_ids[i] = list[i];
+        moe_check_steps(k, n);  // a forward the reference runs whose router failed
         if (cached_st) {
             stream_check(m);
-            const uint64_t fwd = std::min<uint64_t>(n, max_new - 1);
-            cached_st->hits = hits0 + fwd * (uint64_t)m.L;
+            const uint64_t fw = std::min<uint64_t>(n, max_new - 1);
+            cached_st->hits = hits0 + fw * (uint64_t)m.L;
         }
         finish(n);
         return false;
         };
-        if (pass() && pass())
+        const StreamMark mark = stream_mark(m);
+        if (!pass()) return;
+        stream_rewind(m, mark);
+        if (pass())
             fail(ESP_BACKEND, "decode attention: split placement check failed with the agent-scope merge");
     });
 }
@@ -704,7 +734,12 @@ esp_status esp_profile_read(const char *kernel, uint64_t *launches, double *tota
     return guard([&] {
         if (!kernel) fail(ESP_INVALID_REQUEST, "null kernel name");
         unsigned long long n = 0;
-        prof_read(kernel, &n, total_ms);
+        if (!strcmp(kernel, "attn_xcd_mode")) {  // the decode attention's merge mode
+            n = (unsigned long long)attn_xcd_mode();
+            if (total_ms) *total_ms = 0.0;
+        } else {
+            prof_read(kernel, &n, total_ms);
+        }
         if (launches) *launches = n;
     });
 }

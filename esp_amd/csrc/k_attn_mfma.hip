@@ -27,8 +27,10 @@
 // each product takes three MFMAs (hi.hi + hi.lo + lo.hi). The running max
 // moves only when a tile's max passes it by more than 8 (log2 units), so the
 // probabilities stay below 2^8. Tiles are double-buffered in registers: the
-// next tile's loads (clamped to the last valid key) are issued before the
-// current tile is used.
+// next tile's loads are issued before the current tile is used; they are
+// buffer loads whose range check covers the whole offset (the tile start is
+// part of the per-lane offset), so keys at or past the row's end read as 0
+// and nothing past the unit's rows is fetched.
 #include <type_traits>
 
 #include "common.hpp"
@@ -141,8 +143,10 @@ __global__ void __launch_bounds__(AM_WAVES * 64) attn_rows_mfma_k(AttnDecodeArgs
     }
 
     // Tile loads are buffer loads over this unit's K and V rows [0, hi):
-    // keys past the row's range read as 0 (and are masked below), the tile
-    // start is the scalar offset and each lane's row offsets are constants.
+    // keys past the row's range read as 0 (and are masked below). The tile
+    // start is added to each lane's constant row offset (the per-lane offset
+    // is what the range check compares with the descriptor's size; the
+    // scalar offset is left 0).
     constexpr int ROWB = HD * ES;
     const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc((void *)kb, (short)0, hi * ROWB, 0x00020000);
     const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc((void *)vb, (short)0, hi * ROWB, 0x00020000);
@@ -161,15 +165,15 @@ __global__ void __launch_bounds__(AM_WAVES * 64) attn_rows_mfma_k(AttnDecodeArgs
         for (int h = 0; h < 2; ++h)
 #pragma unroll
             for (int q = 0; q < S::KL; ++q)
-                b.k[h][q] = __builtin_bit_cast(am_u4, __builtin_amdgcn_raw_buffer_load_b128(rk, kofs[h] + 16 * q, so, 0));
+                b.k[h][q] = __builtin_bit_cast(am_u4, __builtin_amdgcn_raw_buffer_load_b128(rk, so + kofs[h] + 16 * q, 0, 0));
 #pragma unroll
         for (int u = 0; u < S::VU; ++u)
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 if constexpr (F16)
-                    b.v[u][e] = __builtin_amdgcn_raw_buffer_load_b32(rv, vofs[u] + e * ROWB, so, 0);
+                    b.v[u][e] = __builtin_amdgcn_raw_buffer_load_b32(rv, so + vofs[u] + e * ROWB, 0, 0);
                 else
-                    b.v[u][e] = __builtin_bit_cast(am_u2, __builtin_amdgcn_raw_buffer_load_b64(rv, vofs[u] + e * ROWB, so, 0));
+                    b.v[u][e] = __builtin_bit_cast(am_u2, __builtin_amdgcn_raw_buffer_load_b64(rv, so + vofs[u] + e * ROWB, 0, 0));
             }
     };
 
@@ -301,7 +305,7 @@ __global__ void __launch_bounds__(AM_WAVES * 64) attn_rows_mfma_k(AttnDecodeArgs
     };
 
     // tiles alternate between two register buffers; every prefetch is
-    // issued (clamped past the last key), so the waits are exact
+    // issued (a tile past the last key reads zeros), so the waits are exact
     T b0, b1;
     int t = lo;
     load(b0, t);

@@ -70,6 +70,7 @@ __global__ void __launch_bounds__(256) route_k(RouteArgs a) {
             for (int e = 0; e <= E; ++e) a.offs[e] = 0;
             a.offs[E + 1] = status;
             if (a.err) atomicMax(a.err, status);
+            if (a.err && a.step) atomicMin(a.err + 1, (a.step[0] << 2) | status);
         }
         for (int i = threadIdx.x; i < a.M * k; i += blockDim.x) {
             a.slot[i] = i;

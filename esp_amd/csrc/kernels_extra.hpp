@@ -27,6 +27,9 @@ struct RouteArgs {
     int32_t *perm;   // [M * k] token of each grouped row
     int32_t *slot;   // [M, k] grouped row of each selection
     int32_t *err;    // nullable sticky status word: max(2 non-finite router, 3 bad top-k mass)
+    // nullable: the device generation loop's step counter (emitted tokens so
+    // far); a failing route then also records min(step << 2 | status) in err[1]
+    const int32_t *step;
 };
 void launch_route(const RouteArgs &a, hipStream_t s);
 void launch_gather_rows(Dt dt, const void *src, const int32_t *perm, int rows, int H, void *dst,

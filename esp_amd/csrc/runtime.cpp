@@ -1411,13 +1411,32 @@ static void moe_fail(int32_t status) {
     if (status) fail(ESP_BACKEND, "expert routing failed");
 }
 
-// After a device-resident generation loop: fail if any step's router did.
+// After a forward whose status word was not read back with its results.
 void moe_check(Kv &kv) {
     if (!kv.moe_err.p) return;
     int32_t st = 0;
     ESP_HIP(hipMemcpyAsync(&st, kv.moe_err.p, 4, hipMemcpyDeviceToHost, kv.stream));
     ESP_HIP(hipStreamSynchronize(kv.stream));
     moe_fail(st);
+}
+
+// Before a device-resident generation loop: no step has failed yet.
+void moe_steps_reset(Kv &kv) {
+    if (!kv.moe_err.p) return;
+    static const int32_t none = INT32_MAX;
+    ESP_HIP(hipMemcpyAsync(kv.moe_err.as<int32_t>() + 1, &none, 4, hipMemcpyHostToDevice, kv.stream));
+    ESP_HIP(hipStreamSynchronize(kv.stream));
+}
+
+// After a device-resident generation loop: fail if the router failed in a
+// forward the reference runs, i.e. one that fed token i < n (its step word
+// is i + 1); later forwards of the last replayed chunk do not count.
+void moe_check_steps(Kv &kv, uint32_t n) {
+    if (!kv.moe_err.p) return;
+    int32_t v = INT32_MAX;
+    ESP_HIP(hipMemcpyAsync(&v, kv.moe_err.as<int32_t>() + 1, 4, hipMemcpyDeviceToHost, kv.stream));
+    ESP_HIP(hipStreamSynchronize(kv.stream));
+    if (v != INT32_MAX && (uint32_t)(v >> 2) <= n) moe_fail(v & 3);
 }
 
 // Head on the last row of each sequence (model.rs:531-538): final RMSNorm
@@ -1501,7 +1520,12 @@ static bool forward_pass(Model &m, Kv &kv, int n_seqs, const uint32_t *seqs, con
 // pass that succeeded).
 void forward(Model &m, Kv &kv, int n_seqs, const uint32_t *seqs, const uint32_t *lens,
              const int32_t *ids) {
-    if (forward_pass(m, kv, n_seqs, seqs, lens, ids) && forward_pass(m, kv, n_seqs, seqs, lens, ids))
+    std::unique_lock<std::recursive_mutex> streaming;
+    if (m.st) streaming = std::unique_lock<std::recursive_mutex>(m.st->mu);
+    const StreamMark mark = stream_mark(m);
+    if (!forward_pass(m, kv, n_seqs, seqs, lens, ids)) return;
+    stream_rewind(m, mark);
+    if (forward_pass(m, kv, n_seqs, seqs, lens, ids))
         fail(ESP_BACKEND, "decode attention: split placement check failed with the agent-scope merge");
 }
 
@@ -1685,6 +1709,11 @@ namespace esp {
 void decode_step_dev(Model &m, Kv &kv, int seq, int max_t, int32_t *gen) {
     hipStream_t s = kv.stream;
     ensure_scratch(m, kv, 1, 1);
+    struct StepWord {
+        Kv &k;
+        StepWord(Kv &k_, const int32_t *w) : k(k_) { k.gen_step = w; }
+        ~StepWord() { k.gen_step = nullptr; }
+    } step_word(kv, gen + 1);
     Rows rows{gen, gen + 2, gen + 3, 1, seq};
     {
         Prof p("embed", s);
@@ -1751,7 +1780,7 @@ void moe_decode(Model &m, Kv &kv, LayerW &w, hipStream_t s) {
         launch_decode_gemv(m.wt, DG_STORE, r, s);
         RouteArgs ra{kv.moe_logits.as<float>(), 1, E, k, m.norm_topk ? 1 : 0,
                      kv.moe_sel.as<int32_t>(), kv.moe_w.as<float>(), kv.moe_offs.as<int32_t>(),
-                     kv.moe_perm.as<int32_t>(), kv.moe_slot.as<int32_t>(), moe_err_word(kv)};
+                     kv.moe_perm.as<int32_t>(), kv.moe_slot.as<int32_t>(), moe_err_word(kv), kv.gen_step};
         launch_route(ra, s);
     }
     {
@@ -1870,7 +1899,7 @@ void moe_block(Model &m, Kv &kv, LayerW &w, int Mc, hipStream_t s, int l) {
     }
     RouteArgs ra{kv.moe_logits.as<float>(), Mc, E, k, m.norm_topk ? 1 : 0,
                  kv.moe_sel.as<int32_t>(), kv.moe_w.as<float>(), kv.moe_offs.as<int32_t>(),
-                 kv.moe_perm.as<int32_t>(), kv.moe_slot.as<int32_t>(), moe_err_word(kv)};
+                 kv.moe_perm.as<int32_t>(), kv.moe_slot.as<int32_t>(), moe_err_word(kv), kv.gen_step};
     {
         Prof p("moe", s);
         launch_route(ra, s);

@@ -112,6 +112,9 @@ struct Kv {
     DevMem moe_logits, moe_sel, moe_w, moe_slot, moe_offs, moe_perm, moe_x, moe_y, moe_ys, moe_sg,
         moe_act;
     DevMem moe_err;  // sticky router status of the forward in flight (0 = ok)
+    // during esp_generate_greedy's device steps: the step counter (gen[1]),
+    // so a router failure records the step it happened in (moe_err[1])
+    const int32_t *gen_step = nullptr;
     int logits_rows = 0;  // rows valid in `logits`
     // set when a decode attention launch of the forward in flight merged key
     // splits (its XCD placement word must then be read back)

@@ -650,6 +650,41 @@ void stream_make_resident(Model &m) {
     m.st.reset();
 }
 
+StreamMark stream_mark(const Model &m) {
+    StreamMark k{};
+    if (!m.st) return k;
+    const Streamer &st = *m.st;
+    k.reads = st.reads;
+    k.bytes = st.bytes;
+    k.largest = st.largest;
+    k.ereads = st.ereads;
+    k.ebytes = st.ebytes;
+    k.elargest = st.elargest;
+    k.payload = st.payload;
+    k.hits = st.hits;
+    k.misses = st.misses;
+    k.cached = st.cache.size();
+    return k;
+}
+
+void stream_rewind(Model &m, const StreamMark &k) {
+    if (!m.st) return;
+    Streamer &st = *m.st;
+    // the pass ran to its end (no check failed, so nothing was evicted): the
+    // layers it admitted are the entries after the mark
+    ESP_HIP(hipStreamSynchronize(st.copy));
+    while (st.cache.size() > k.cached) st.cache.pop_back();
+    st.reads = k.reads;
+    st.bytes = k.bytes;
+    st.largest = k.largest;
+    st.ereads = k.ereads;
+    st.ebytes = k.ebytes;
+    st.elargest = k.elargest;
+    st.payload = k.payload;
+    st.hits = k.hits;
+    st.misses = k.misses;
+}
+
 void stream_stats(const Model &m, esp_streaming_stats *o) {
     memset(o, 0, sizeof(*o));
     if (!m.st) return;

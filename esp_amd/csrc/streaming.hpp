@@ -123,5 +123,14 @@ void stream_expert_release(Model &m, hipStream_t compute);
 void stream_set_cache(Model &m, uint64_t budget);
 void stream_make_resident(Model &m);
 void stream_stats(const Model &m, esp_streaming_stats *out);
+// The read and cache counters (and cache size) before a pass that may have
+// to run again; stream_rewind restores them and drops the layers the pass
+// admitted, so a repeated pass counts as the one forward it stands for.
+struct StreamMark {
+    uint64_t reads, bytes, largest, ereads, ebytes, elargest, payload, hits, misses;
+    size_t cached;
+};
+StreamMark stream_mark(const Model &m);
+void stream_rewind(Model &m, const StreamMark &k);
 
 }  // namespace esp

@@ -330,7 +330,8 @@ class DecoderModel:
         """generate.rs:134-170 with the greedy picker, run as a device loop."""
         p = np.ascontiguousarray(prompt, dtype=np.int32)
         e = np.ascontiguousarray(list(eos) or [0], dtype=np.int32)
-        out = np.zeros(max(1, max_new), np.int32)
+        window = min(cache.max_ctx, self.config.max_position_embeddings)
+        out = np.zeros(max(1, min(max_new, window - len(p) + 1)), np.int32)
         n = C.c_uint32()
         P = C.POINTER(C.c_int32)
         self._check(_lib.load().esp_generate_greedy(

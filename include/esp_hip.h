@@ -234,9 +234,17 @@ esp_status esp_pick_noalloc(esp_kv *kv, uint32_t n_rows, const uint32_t *allowed
 
 /* generate.rs:134-170 try_generate_ids_with + TokenPicker::Greedy, run on
  * the device: prefill `prompt`, then up to max_new greedy steps, stopping
- * at (and excluding) any id in `eos`. Writes generated ids to out_ids
- * [max_new] and their count to n_out. The per-step token never leaves the
- * device; decode steps replay one captured HIP graph. */
+ * at (and excluding) any id in `eos`. Writes generated ids to out_ids and
+ * their count to n_out; at most min(max_new, W - n_prompt + 1) ids, where
+ * W = min(the KV handle's max_ctx, max_position_embeddings), so out_ids
+ * needs that many slots (any max_new, up to UINT32_MAX, is accepted). A
+ * run that yields that many ids without eos while max_new asks for more
+ * fails as the reference's next forward past the window does. The
+ * per-step token never leaves the device; decode steps replay one
+ * captured HIP graph in chunks of 4, 8, 16, 32 and then 64 forwards, the
+ * host checking the new ids for eos between chunks, so an early eos ends
+ * the call after at most the rest of its chunk. A router failure counts
+ * only in a forward the reference runs (one feeding a token before eos). */
 esp_status esp_generate_greedy(esp_model *model, esp_kv *kv, uint32_t seq, const int32_t *prompt,
                                uint32_t n_prompt, uint32_t max_new, const int32_t *eos,
                                uint32_t n_eos, int32_t *out_ids, uint32_t *n_out);
@@ -418,7 +426,10 @@ esp_status esp_pick_constrained(esp_kv *kv, uint32_t n_rows, esp_constraint *con
  * The family "attn_xcd_fallback" counts (always, time 0) the forwards
  * computed again because a decode-attention launch found a (row, kv
  * head)'s key splits on several XCDs, after which the process uses the
- * agent-scope merge. */
+ * agent-scope merge. "greedy_forwards" counts (always) the decode
+ * forwards esp_generate_greedy issues. The name "attn_xcd_mode" reads (launches) the
+ * merge the decode attention uses on the current device: 0 agent-scope,
+ * 1 a single XCD, N > 1 XCD-local over N XCDs. */
 esp_status esp_profile_enable(const char *kernel, int enable);
 esp_status esp_profile_read(const char *kernel, uint64_t *launches, double *total_ms);
 

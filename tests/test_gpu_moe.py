@@ -23,7 +23,7 @@ QWEN2_MOE = {"model_type": "qwen2_moe", "architectures": ["Qwen2MoeForCausalLM"]
 def _close(got, want, fmt):
     if fmt == "bf16":
         return np.all(np.abs(got - want) <= 1e-2 + 2e-2 * np.abs(want))
-    return np.all(np.abs(got - want) <= 1e-4 * max(1.0, float(np.abs(want).max())))
+    return np.all(np.abs(got - want) <= 1e-4 * float(np.abs(want).max()))
 
 
 def _f32(arr, dt):

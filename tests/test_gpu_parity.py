@@ -31,7 +31,8 @@ def test_arch_golden(case):
     cache = model.new_cache()
     logits = model.try_forward_cached_last(row["input_ids"], cache)
     err = np.abs(logits - np.array(row["last_logits"], np.float32)).max()
-    assert err < 1e-4, f"{case}: max logits error {err}"
+    print(f"  logits max error {err:.3g}", flush=True)
+    assert err < 2e-5, f"{case}: max logits error {err}"  # architecture_tests.rs:244-247
     gen = []
     for step in range(4):
         if step:
@@ -537,6 +538,9 @@ def test_decode_attention_placement_fallback():
     r = subprocess.run([sys.executable, "-u", case], env=env, capture_output=True, text=True,
                        timeout=300)
     print(r.stdout[-2000:], r.stderr[-2000:])
+    if r.returncode == 77:
+        pytest.skip("the device gives the XCD-local merge no placement to check "
+                    "(one XCD, or its dispatch-order probe failed)")
     assert r.returncode == 0
 
 

@@ -27,7 +27,7 @@ def _case(art, layers=3, tensors=False):
 def _close(got, want, fmt):
     if fmt == "bf16":
         return np.all(np.abs(got - want) <= 1e-2 + 2e-2 * np.abs(want))
-    return np.all(np.abs(got - want) <= 1e-4 * max(1.0, float(np.abs(want).max())))
+    return np.all(np.abs(got - want) <= 1e-4 * float(np.abs(want).max()))
 
 
 @pytest.mark.parametrize("fmt", ["f32", "bf16"])

@@ -79,7 +79,7 @@ def test_streamed_matches_resident_bit_exactly(fmt, art, extra, bias):
         if fmt == "bf16":
             assert np.all(np.abs(g - want) <= 1e-2 + 2e-2 * np.abs(want)), i
         else:
-            assert np.abs(g - want).max() <= 1e-4 * max(1.0, float(np.abs(want).max())), i
+            assert np.abs(g - want).max() <= 1e-4 * float(np.abs(want).max()), i
 
 
 def test_streamed_batch_and_long_prompt_match_resident():
@@ -288,7 +288,7 @@ def _moe_case(fmt, seed=31):
 def _close(got, want, fmt):
     if fmt == "bf16":
         return np.all(np.abs(got - want) <= 1e-2 + 2e-2 * np.abs(want))
-    return np.abs(got - want).max() <= 1e-4 * max(1.0, float(np.abs(want).max()))
+    return np.abs(got - want).max() <= 1e-4 * float(np.abs(want).max())
 
 
 @pytest.mark.parametrize("fmt", ["f32", "bf16"])
