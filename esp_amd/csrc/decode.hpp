@@ -31,6 +31,10 @@ struct DecodeGemvArgs {
     // scale * B t (lora.rs:93-97) to q, k and v.
     int lora_rows;
     float *lora_t_out;
+    // QKVROPE, nullable: block 0 also copies the rope rows at the row's
+    // position here (cos then sin, hd floats each), so the attention that
+    // follows reads them from a fixed address instead of after the position
+    float *rope_row;
     // routed experts (moe.rs:135-256, one row): with ex_sel set, SWIGLU
     // units are (slot, row) pairs, slot = unit / ex_rows, reading expert
     // ex_sel[slot] (clamped to [0, ex_count)) of the [E][rows][K] tensors;
@@ -89,6 +93,12 @@ struct AttnDecodeArgs {
     int lora_rank[3];
     float lora_scale[3];
     const float *rope_cos, *rope_sin;  // [max_pos, hd]
+    // With lora_fast (lora_vec, every rank <= 16, rope_row set): the deltas'
+    // operands (B rows, the rope rows copied by the QKV launch) are loaded
+    // before the block's first keys and the deltas are exchanged through LDS
+    // without waiting for those keys.
+    int lora_fast;
+    const float *rope_row;
     // nullable (attn_rows_mfma_k only): row groups (Rows::grp); one unit
     // per (group, kv head) instead of per (row, kv head)
     const int32_t *grp;

@@ -26,6 +26,7 @@
 #include "dev.hpp"
 #include "decode.hpp"
 #include "decode_dev.hpp"
+#include "attn_dev.hpp"
 
 namespace esp {
 
@@ -119,6 +120,40 @@ __global__ void __launch_bounds__(NW * 64) decode_gemv_k(DecodeGemvArgs a) {
                 xr[c][4 * q + 2] = p.z;
                 xr[c][4 * q + 3] = p.w;
             }
+        }
+    }
+    // The epilogue's memory operands for this thread's unit (the residual
+    // row and bias; the rotary row at the decode position), loaded here so
+    // they arrive with the first weight rows instead of as dependent round
+    // trips (position, then the rope row) after the last ones. Thread t owns
+    // epilogue unit t (at most DG_MAX_IT * RB <= blockDim.x units per block).
+    const int n_it = (int)blockIdx.x * RB < units
+                         ? (units - (int)blockIdx.x * RB + (int)gridDim.x * RB - 1) / ((int)gridDim.x * RB)
+                         : 0;
+    const int pe_u = (int)blockIdx.x * RB + (tid / RB) * (int)gridDim.x * RB + tid % RB;
+    const bool pe = tid < n_it * RB && pe_u < units;
+    float pf[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    if (EPI == DG_RESID && pe) {
+        pf[0] = a.y[pe_u];
+        if (a.bias) pf[1] = a.bias[pe_u];
+    } else if (EPI == DG_QKVROPE && pe && pe_u < a.N / 2) {
+        const int half = a.hd / 2, head = pe_u / half, d = pe_u % half;
+        const int r0 = head * a.hd + d;
+        if (a.bias) {
+            pf[0] = a.bias[r0];
+            pf[1] = a.bias[r0 + half];
+        }
+        if (head < a.nq + a.nkv) {
+            const size_t ro = (size_t)a.row_pos[0] * a.hd + d;
+            pf[2] = a.rope_cos[ro];
+            pf[3] = a.rope_cos[ro + half];
+            pf[4] = a.rope_sin[ro];
+            pf[5] = a.rope_sin[ro + half];
+        }
+    }
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+        if (lane + 64 * c < nch) {
 #pragma unroll
             for (int i = 0; i < CW; ++i) ss += xr[c][i] * xr[c][i];
         }
@@ -188,11 +223,12 @@ __global__ void __launch_bounds__(NW * 64) decode_gemv_k(DecodeGemvArgs a) {
             for (int w = 0; w < NW; ++w) t += red[it][r * RU + j][w];
             y[j] = t;
         }
+        const bool mine = e == tid;  // the unit whose operands were prefetched
         if (EPI == DG_RESID) {
-            float v = a.bias ? y[0] + a.bias[u] : y[0];
+            float v = a.bias ? y[0] + (mine ? pf[1] : a.bias[u]) : y[0];
             if (a.ex_w) v = v * a.ex_w[a.ex_slot];
             if (a.sig_scale) v = v * (1.f / (1.f + expf(-a.sig_scale[0])));
-            a.y[u] = a.y[u] + v;
+            a.y[u] = (mine ? pf[0] : a.y[u]) + v;
         } else if (EPI == DG_STORE) {
             a.y[u] = a.bias ? y[0] + a.bias[u] : y[0];
         } else if (EPI == DG_HEAD) {
@@ -214,15 +250,17 @@ __global__ void __launch_bounds__(NW * 64) decode_gemv_k(DecodeGemvArgs a) {
             const int r0 = head * hd + d, r1 = r0 + half;
             float v0 = y[0], v1 = y[1];
             if (a.bias) {
-                v0 = v0 + a.bias[r0];
-                v1 = v1 + a.bias[r1];
+                v0 = v0 + (mine ? pf[0] : a.bias[r0]);
+                v1 = v1 + (mine ? pf[1] : a.bias[r1]);
             }
             const int pos = a.row_pos[0], seq = a.row_seq[0];
             const float *cs = a.rope_cos + (size_t)pos * hd;
             const float *sn = a.rope_sin + (size_t)pos * hd;
             if (head < a.nq + a.nkv) {
-                float o0 = v0 * cs[d] + (-v1) * sn[d];
-                float o1 = v1 * cs[d + half] + v0 * sn[d + half];
+                const float c0 = mine ? pf[2] : cs[d], c1 = mine ? pf[3] : cs[d + half];
+                const float s0 = mine ? pf[4] : sn[d], s1 = mine ? pf[5] : sn[d + half];
+                float o0 = v0 * c0 + (-v1) * s0;
+                float o1 = v1 * c1 + v0 * s1;
                 if (head < a.nq) {
                     a.q_out[r0] = o0;
                     a.q_out[r1] = o1;
@@ -248,6 +286,13 @@ __global__ void __launch_bounds__(NW * 64) decode_gemv_k(DecodeGemvArgs a) {
                     ((float *)a.kv)[i + half] = v1;
                 }
             }
+        }
+    }
+    if (EPI == DG_QKVROPE && a.rope_row && blockIdx.x == 0) {
+        const size_t ro = (size_t)a.row_pos[0] * a.hd;
+        for (int d = tid; d < a.hd; d += blockDim.x) {
+            a.rope_row[d] = a.rope_cos[ro + d];
+            a.rope_row[a.hd + d] = a.rope_sin[ro + d];
         }
     }
     if (EPI != DG_HEAD || !a.ticket) return;
@@ -423,57 +468,6 @@ void launch_decode_gemv(Dt wt, int epi, const DecodeGemvArgs &a, hipStream_t s) 
 
 // ------------------------------------------------------------ attention
 
-constexpr int ATT_MAX_SPLIT = 128;
-constexpr int ATT_WAVES = 8;      // waves per attention block (two per SIMD)
-constexpr int ATT_MB = 32;        // splits whose partials one merge batch loads at once
-
-// Steps (of ATT_WAVES * 64 * 8 / HD keys) whose K/V loads a block keeps in
-// flight together: 16 VGPRs per step and lane.
-
-// Both values of the lane pair (lane, lane ^ X), lower lane first, in every
-// lane of the pair: X = 32 and 16 with the gfx950 permlane swaps, X = 8 with
-// a DPP rotate by 8 inside each 16-lane row.
-template <int X> __device__ __forceinline__ void lane_pair(float v, float &lo, float &hi) {
-    if constexpr (X == 32) {
-        const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-        lo = __uint_as_float(r[0]);
-        hi = __uint_as_float(r[1]);
-    } else if constexpr (X == 16) {
-        const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-        lo = __uint_as_float(r[0]);
-        hi = __uint_as_float(r[1]);
-    } else {
-        static_assert(X == 8, "lane_pair: X = 8, 16 or 32");
-        const float o = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x128, 0xF, 0xF, false));
-        const bool low = (threadIdx.x & 8) == 0;
-        lo = low ? v : o;
-        hi = low ? o : v;
-    }
-}
-
-// Merges the online-softmax states (m, l, acc[8]) of lane pairs (lane, lane ^ X).
-template <int X, int GM>
-__device__ __forceinline__ void att_pair_merge(int G, float (&m)[GM], float (&l)[GM], float (&acc)[GM][8]) {
-#pragma unroll
-    for (int j = 0; j < GM; ++j) {
-        if (j >= G) break;
-        float m0, m1, l0, l1;
-        lane_pair<X>(m[j], m0, m1);
-        lane_pair<X>(l[j], l0, l1);
-        const float mn = fmaxf(m0, m1);
-        const float w0 = mn == -INFINITY ? 0.f : __expf(m0 - mn);
-        const float w1 = mn == -INFINITY ? 0.f : __expf(m1 - mn);
-        l[j] = l0 * w0 + l1 * w1;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            float a0, a1;
-            lane_pair<X>(acc[j][i], a0, a1);
-            acc[j][i] = a0 * w0 + a1 * w1;
-        }
-        m[j] = mn;
-    }
-}
-
 __device__ __forceinline__ void att_store(const AttnDecodeArgs &a, size_t i, float v) {
     if (a.out_lo) {
         const uint16_t h = f2bf(v);
@@ -490,11 +484,11 @@ __device__ __forceinline__ void att_store(const AttnDecodeArgs &a, size_t i, flo
 // [4 sub, 4 sub + 4) and [hd/2 + 4 sub, hd/2 + 4 sub + 4), so each 16-byte
 // load of the group covers a contiguous hd/2 * 4 bytes of the key row, and
 // a dot product is finished with DPP swaps inside the group. The loads of
-// the first chunk of the split (one buffer's steps) are issued before the
-// row's position is known: they cover the split's planned range (clamped to
-// max_t, the plan's key bound; lanes past the range load nothing) and keys
-// past the position are masked afterwards, so the position read and the K/V
-// stream overlap. The softmax update runs once per chunk (one exp per key).
+// the first two chunks of the split (both buffers) are issued right after
+// q's, before the row's position is known: they cover the split's planned
+// range (clamped to max_t, the plan's key bound; lanes past the range re-read
+// its last key) and keys past the position are masked afterwards, so the
+// position read and the K/V stream overlap. The softmax update runs once per chunk (one exp per key).
 // The key groups of a wave merge through lane-pair swaps, the waves through
 // LDS; the last split to finish for a (row, kv head) merges the partials in
 // split order (deterministic), each thread one output with every partial
@@ -507,19 +501,6 @@ __device__ __forceinline__ void att_store(const AttnDecodeArgs &a, size_t i, flo
 // plain stores, then L1-bypassing loads in the merging block. With
 // xcd_nx == 0 the partials go through agent-scope (write-through) stores and
 // loads instead, which any placement tolerates.
-// Keys and values as 4-dim slices: f32x4 (f32 cache) or four f16 in a u32x2.
-template <bool F16> struct KvSlice { typedef f32x4_t T; };
-template <> struct KvSlice<true> { typedef u32x2_t T; };
-__device__ __forceinline__ f32x4_t kv_f32(f32x4_t x) { return x; }
-__device__ __forceinline__ f32x4_t kv_f32(u32x2_t x) {
-    typedef _Float16 h4_t __attribute__((ext_vector_type(4)));
-    return __builtin_convertvector(__builtin_bit_cast(h4_t, x), f32x4_t);
-}
-__device__ __forceinline__ u32x2_t kv_f16(f32x4_t x) {
-    typedef _Float16 h4_t __attribute__((ext_vector_type(4)));
-    return __builtin_bit_cast(u32x2_t, __builtin_convertvector(x, h4_t));
-}
-
 template <int HD, int GM, bool XCD, int NW = ATT_WAVES, bool F16 = false>
 __global__ void __launch_bounds__(NW * 64) attn_decode_k(AttnDecodeArgs a) {
     typedef typename KvSlice<F16>::T KR;
@@ -583,7 +564,6 @@ __global__ void __launch_bounds__(NW * 64) attn_decode_k(AttnDecodeArgs a) {
             }
         }
     };
-    issue(kk, vv, s0, min(s0 + CH, s1));
     // q for the group's heads: this lane's 8 dims
     float q[GM][DPL];
     const float *qrow = a.q + (size_t)row * a.nq * HD + (size_t)g * G * HD + sub * 4;
@@ -595,6 +575,41 @@ __global__ void __launch_bounds__(NW * 64) attn_decode_k(AttnDecodeArgs a) {
             q[j][0] = v0.x; q[j][1] = v0.y; q[j][2] = v0.z; q[j][3] = v0.w;
             q[j][4] = v1.x; q[j][5] = v1.y; q[j][6] = v1.z; q[j][7] = v1.w;
         }
+    // Fast LoRA path: this thread's delta outputs o = tid + k NT, k < KO
+    // (head j = o / HD, dim d = o % HD; rows of the key and value heads
+    // whatever the position), B rows (rank <= 16) and the lane's rope dims
+    // loaded before the first keys, so they return first.
+    constexpr bool FASTOK = GM <= 4;  // eight heads per kv head would spill
+    constexpr int KO = FASTOK ? ((GM + 2) * HD + NT - 1) / NT : 1;
+    const bool fast = FASTOK && a.lora_on && a.lora_fast;  // block-uniform
+    u32x4_t lb[KO][2];
+    f32x4_t rr[4];  // cos lo, cos hi, sin lo, sin hi at this lane's dims
+    // A wave's outputs share their head (HD is a multiple of 64), so the
+    // target and its kernel arguments are wave-uniform (scalar reads).
+    auto lsel = [&](int tg, auto p0, auto p1, auto p2) { return tg == 0 ? p0 : tg == 1 ? p1 : p2; };
+    if (fast) {
+#pragma unroll
+        for (int k = 0; k < KO; ++k) {
+            lb[k][0] = lb[k][1] = u32x4_t{0u, 0u, 0u, 0u};
+            const int o = tid + k * NT;
+            const int j = __builtin_amdgcn_readfirstlane(o / HD), d = o % HD;
+            if (j >= G + 2) continue;
+            const int tg = j < G ? 0 : j - G + 1;
+            const void *bp = lsel(tg, a.lora_b[0], a.lora_b[1], a.lora_b[2]);
+            if (!bp) continue;
+            const size_t brow = j < G ? (size_t)(g * G + j) * HD + d : (size_t)g * HD + d;
+            const int rank = lsel(tg, a.lora_rank[0], a.lora_rank[1], a.lora_rank[2]);
+            const u32x4_t *B = (const u32x4_t *)((const uint16_t *)bp + brow * rank);
+            lb[k][0] = B[0];
+            if (rank > 8) lb[k][1] = B[1];
+        }
+        rr[0] = *(const f32x4_t *)(a.rope_row + sub * 4);
+        rr[1] = *(const f32x4_t *)(a.rope_row + HALF + sub * 4);
+        rr[2] = *(const f32x4_t *)(a.rope_row + HD + sub * 4);
+        rr[3] = *(const f32x4_t *)(a.rope_row + HD + HALF + sub * 4);
+    }
+    issue(kk, vv, s0, min(s0 + CH, s1));
+    if (s0 + CH < s1) issue(kk2, vv2, s0 + CH, min(s0 + 2 * CH, s1));
     const int pos = a.row_pos[row];
     // Unmerged LoRA of a single decode row: c = scale * B t for the group's
     // query heads (and, in the block whose split holds the new key, for this
@@ -604,7 +619,59 @@ __global__ void __launch_bounds__(NW * 64) attn_decode_k(AttnDecodeArgs a) {
     __shared__ float lc[GM + 2][HD];
     float kd[DPL], vd[DPL];
     bool kv_patch = false;
-    if (a.lora_on) {  // block-uniform
+    if (fast) {
+        const bool own = pos >= s0 && pos < s1;
+#pragma unroll
+        for (int k = 0; k < KO; ++k) {
+            const int o = tid + k * NT;
+            const int j = __builtin_amdgcn_readfirstlane(o / HD), d = o % HD;
+            if (j >= G + 2) break;
+            const int tg = j < G ? 0 : j - G + 1;
+            float c = 0.f;
+            if (lsel(tg, a.lora_b[0], a.lora_b[1], a.lora_b[2])) {
+                const float *t = lsel(tg, a.lora_t[0], a.lora_t[1], a.lora_t[2]);
+                const int rank = lsel(tg, a.lora_rank[0], a.lora_rank[1], a.lora_rank[2]);
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    if (h * 8 >= rank) break;
+                    const u32x4_t b = lb[k][h];
+                    const float *tt = t + 8 * h;
+                    c += __uint_as_float(b.x << 16) * tt[0] + __uint_as_float(b.x & 0xffff0000u) * tt[1] +
+                         __uint_as_float(b.y << 16) * tt[2] + __uint_as_float(b.y & 0xffff0000u) * tt[3] +
+                         __uint_as_float(b.z << 16) * tt[4] + __uint_as_float(b.z & 0xffff0000u) * tt[5] +
+                         __uint_as_float(b.w << 16) * tt[6] + __uint_as_float(b.w & 0xffff0000u) * tt[7];
+                }
+                c = c * lsel(tg, a.lora_scale[0], a.lora_scale[1], a.lora_scale[2]);
+            }
+            lc[j][d] = c;
+        }
+        lds_barrier();
+        auto rot = [&](const float *c, float *out) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float x0 = c[sub * 4 + e], x1 = c[HALF + sub * 4 + e];
+                out[e] = x0 * rr[0][e] + (-x1) * rr[2][e];
+                out[4 + e] = x1 * rr[1][e] + x0 * rr[3][e];
+            }
+        };
+#pragma unroll
+        for (int j = 0; j < GM; ++j) {
+            if (j >= G) break;
+            float dq[DPL];
+            rot(lc[j], dq);
+#pragma unroll
+            for (int e = 0; e < DPL; ++e) q[j][e] += dq[e];
+        }
+        if (own && (a.lora_b[1] || a.lora_b[2])) {
+            kv_patch = true;
+            rot(lc[G], kd);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                vd[e] = lc[G + 1][sub * 4 + e];
+                vd[4 + e] = lc[G + 1][HALF + sub * 4 + e];
+            }
+        }
+    } else if (a.lora_on) {  // block-uniform
         const bool own = pos >= s0 && pos < s1;
         for (int o = tid; o < (G + 2) * HD; o += NT) {
             const int j = o / HD, d = o % HD;
@@ -779,16 +846,20 @@ __global__ void __launch_bounds__(NW * 64) attn_decode_k(AttnDecodeArgs a) {
             }
         }
     };
-    // chunks alternate between the buffers; each buffer is refilled only
-    // after it has been consumed, with exactly the range consumed from it
+    // Chunks alternate between the buffers. Both first chunks were issued
+    // before q and the position were read; a buffer is refilled with the
+    // chunk two ahead right after it has been consumed. Loads cover the
+    // split's planned range (keys past the row's position are masked), so
+    // chunk k always starts at s0 + k CH.
     for (int c0 = s0; c0 < hi;) {
         const int c1 = min(c0 + CH, hi);
-        if (c1 < hi) issue(kk2, vv2, c1, min(c1 + CH, hi));
         consume(kk, vv, c0, c1);
         if (c1 >= hi) break;
+        if (c0 + 2 * CH < s1) issue(kk, vv, c0 + 2 * CH, min(c0 + 3 * CH, s1));
         const int c2 = min(c1 + CH, hi);
-        if (c2 < hi) issue(kk, vv, c2, min(c2 + CH, hi));
         consume(kk2, vv2, c1, c2);
+        if (c2 >= hi) break;
+        if (c1 + 2 * CH < s1) issue(kk2, vv2, c1 + 2 * CH, min(c1 + 3 * CH, s1));
         c0 = c2;
     }
     // merge the KPW key groups of the wave: lane pairs at distance LPK .. 32

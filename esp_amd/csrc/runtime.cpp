@@ -748,6 +748,7 @@ Kv *create_kv(Model *m, uint32_t batch, uint32_t max_ctx, bool f16) {
     // partials (values, ids) and the picked id
     kv->tickets.alloc((size_t)kTicketWords * 4);
     ESP_HIP(hipMemset(kv->tickets.p, 0, kv->tickets.bytes));
+    kv->rope_row.alloc((size_t)2 * m->hd * 4);
     (void)attn_xcd_mode();  // one-time dispatch probe, outside any graph capture
     return kv.release();
 }
@@ -841,8 +842,8 @@ static Dt lora_dt(Dt wt) { return dt_packed(wt) ? DT_F32 : wt; }
 // into kv.attn (f32), with the plan from attn_decode_splits.
 // With `lora` (a single decode row whose QKV launch stored the LoRA t rows),
 // the attention adds the adapters' deltas to q and to the new key/value row.
-static void attn_decode_rows(Model &m, Kv &kv, const Rows &rows, int Mc, int l, const LayerW &w,
-                             const Plan &plan, Dt out_dt = DT_F32, bool lora = false) {
+static AttnDecodeArgs attn_decode_args(Model &m, Kv &kv, const Rows &rows, int Mc, int l,
+                                       const LayerW &w, const Plan &plan, Dt out_dt, bool lora) {
     AttnDecodeArgs a{};
     if (lora) {
         a.lora_on = 1;
@@ -859,6 +860,11 @@ static void attn_decode_rows(Model &m, Kv &kv, const Rows &rows, int Mc, int l, 
         a.lora_vec = !a.lora_b_f32;
         for (int j = 0; j < 3; ++j)
             if (w.lora_rank[j] && (w.lora_rank[j] % 8 || w.lora_t_col[j] % 4)) a.lora_vec = 0;
+        // the QKV launch copied the position's rope rows (single decode row)
+        a.lora_fast = a.lora_vec && Mc == 1 && kv.rope_row.p && m.hd % 64 == 0;
+        for (int j = 0; j < 3; ++j)
+            if (w.lora_rank[j] > 16) a.lora_fast = 0;
+        a.rope_row = kv.rope_row.as<float>();
     }
     a.q = kv.q.as<float>();
     a.kv = kv_layer(kv, l);
@@ -884,6 +890,12 @@ static void attn_decode_rows(Model &m, Kv &kv, const Rows &rows, int Mc, int l, 
     a.xcd_err = xcd_err_word(kv);
     a.out = kv.attn.as<float>();
     a.out_lo = (uint16_t *)lo_plane(out_dt, kv.attn, Mc, m.qw);
+    return a;
+}
+
+static void attn_decode_rows(Model &m, Kv &kv, const Rows &rows, int Mc, int l, const LayerW &w,
+                             const Plan &plan, Dt out_dt = DT_F32, bool lora = false) {
+    AttnDecodeArgs a = attn_decode_args(m, kv, rows, Mc, l, w, plan, out_dt, lora);
     if (plan.n_split > 1) kv.att_merged = true;
     launch_attn_decode(a, kv.stream);
 }
@@ -934,6 +946,7 @@ static void run_layer_decode(Model &m, Kv &kv, const Rows &rows, LayerW &w, int 
         if (lora) {  // t = A . norm(x) rows, in their qkv-buffer columns
             g.lora_rows = w.qkv_rows - qkv_n;
             g.lora_t_out = kv.qkv.as<float>() + qkv_n;
+            g.rope_row = kv.rope_row.as<float>();
         }
         Prof p("gemv_qkv", s);
         launch_decode_gemv(m.wt, DG_QKVROPE, g, s);

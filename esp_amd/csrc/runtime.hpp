@@ -109,6 +109,9 @@ struct Kv {
     DevMem deq[2];   // packed formats: dequantized weights of the GEMMs in flight
     DevMem wide;     // packed formats: activation planes widened to the doubled K
     DevMem tickets;  // zeroed counters for last-block merges (attention, head argmax)
+    // the decode position's rope rows (cos then sin, hd floats each), written
+    // by the single-row QKV launch for the attention's LoRA deltas
+    DevMem rope_row;
     DevMem moe_logits, moe_sel, moe_w, moe_slot, moe_offs, moe_perm, moe_x, moe_y, moe_ys, moe_sg,
         moe_act;
     DevMem moe_err;  // sticky router status of the forward in flight (0 = ok)
