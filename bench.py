@@ -59,6 +59,34 @@ def llama_config(layers, hidden, heads, kv_heads, ffn, vocab, theta=10000.0, max
     return DecoderConfig.from_json_bytes(json.dumps(raw).encode())
 
 
+def llama_sized_table(seed: int = 11, n: int = 128256):
+    """Every single byte, then random multi-byte tokens: ASCII words and
+    punctuation, quotes and backslashes, whole and split UTF-8 sequences,
+    control bytes; empty entries stand for added tokens."""
+    rng = np.random.default_rng(seed)
+    pieces = [bytes([b]) for b in range(256)]
+    ascii_ = np.frombuffer(b"abcdefghijklmnopqrstuvwxyz _-:,{}[]\"\\0123456789./", np.uint8)
+    utf = ["é", "→", "日", "\U0001F600", "ü", "ß"]
+    while len(pieces) < n - 256:
+        k = int(min(1 + rng.geometric(0.22), 24))
+        out = bytearray()
+        while len(out) < k:
+            r = rng.random()
+            if r < 0.8:
+                out.append(int(rng.choice(ascii_)))
+            elif r < 0.92:
+                out += utf[int(rng.integers(len(utf)))].encode()
+            elif r < 0.97:
+                s = utf[int(rng.integers(len(utf)))].encode()
+                cut = int(rng.integers(1, len(s))) if len(s) > 1 else 1
+                out += s[:cut] if rng.random() < 0.5 else s[cut:]
+            else:
+                out.append(int(rng.integers(0, 256)))
+        pieces.append(bytes(out))
+    pieces += [b""] * (n - len(pieces))
+    return pieces
+
+
 def c2_config(max_pos=2048):
     return llama_config(16, 2048, 32, 8, 8192, 128256, theta=500000.0, max_pos=max_pos,
                         extra={"tie_word_embeddings": True})
@@ -732,7 +760,6 @@ def c5_grammar_bench(steps: int, warmup: int = 2) -> dict:
     from esp_amd import DecoderModel, Sampler
     from esp_amd.constraint import Constraint, Vocabulary
     from esp_amd.model import profile_enable, profile_read
-    from tests.grammar_cases import llama_sized_table
     cfg = c2_config(max_pos=4096)
     B, ctx0, V = 64, 1024, cfg.vocab_size
     total = warmup + steps

@@ -46,7 +46,6 @@ typedef float am_f2 __attribute__((ext_vector_type(2)));
 typedef uint32_t am_u4 __attribute__((ext_vector_type(4)));
 typedef uint32_t am_u2 __attribute__((ext_vector_type(2)));
 
-constexpr int AM_WAVES = 4;        // units per block
 constexpr int AM_BK = 32;          // keys per tile
 constexpr int AM_VLD = AM_BK + 4;  // V^T row stride in LDS (16-bit elements)
 
@@ -85,16 +84,20 @@ __device__ __forceinline__ am_u2 am_split_h(float x, float y) {
     return am_u2{__builtin_bit_cast(uint32_t, h), __builtin_bit_cast(uint32_t, __builtin_convertvector(r, am_h2))};
 }
 
+// One unit per block (one wave), so a batch's units spread over every CU:
+// four units per block put the C5 step's 576 units on 144 CUs, and splitting
+// a unit's tiles over two or four waves (merged through LDS) measured slower
+// than one wave per unit.
 template <int HD, bool F16>
-__global__ void __launch_bounds__(AM_WAVES * 64) attn_rows_mfma_k(AttnDecodeArgs a) {
+__global__ void __launch_bounds__(64) attn_rows_mfma_k(AttnDecodeArgs a) {
     using S = AmShape<HD, F16>;
     using T = AmTile<HD, F16>;
     constexpr int ES = F16 ? 2 : 4;
-    __shared__ __attribute__((aligned(16))) uint16_t lds[AM_WAVES * S::LDSW];
+    __shared__ __attribute__((aligned(16))) uint16_t lds[S::LDSW];
     // the unit, its row range and the buffer descriptors are wave-uniform
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
-    const int unit = blockIdx.x * AM_WAVES + wave;
-    if (unit >= (a.grp ? a.ngrp : a.M) * a.nkv) return;  // no barriers below
+    const int lane = threadIdx.x & 63;
+    const int unit = blockIdx.x;
+    if (unit >= (a.grp ? a.ngrp : a.M) * a.nkv) return;
     const int g = unit % a.nkv, gi = unit / a.nkv;
     const int G = a.nq / a.nkv;
     const int col = lane & 15, grp = lane >> 4;
@@ -119,7 +122,7 @@ __global__ void __launch_bounds__(AM_WAVES * 64) attn_rows_mfma_k(AttnDecodeArgs
     const int hi = min(posn + 1, a.max_t);
     const char *kb = (const char *)a.kv + ((size_t)seq * a.seq_stride + (size_t)g * a.head_stride) * ES;
     const char *vb = kb + (size_t)a.kv_half_stride * ES;
-    uint16_t *vt = lds + wave * S::LDSW;
+    uint16_t *vt = lds;
 
     // q of this lane's head (zero columns past G), pre-split
     am_u4 qh[S::KS], ql[S::KS];
@@ -350,12 +353,12 @@ void launch_attn_rows_mfma(const AttnDecodeArgs &a, hipStream_t s) {
     if (!attn_rows_mfma_ok(a)) fail(ESP_BACKEND, "attn_rows_mfma: unsupported shape");
     if (a.max_t < 1) fail(ESP_BACKEND, "attn_rows_mfma: empty key range");
     const long long units = (long long)(a.grp ? a.ngrp : a.M) * a.nkv;
-    const unsigned blocks = (unsigned)((units + AM_WAVES - 1) / AM_WAVES);
+    const unsigned blocks = (unsigned)units;
     if (a.hd == 64) {
-        if (a.kv_f16) attn_rows_mfma_k<64, true><<<blocks, AM_WAVES * 64, 0, s>>>(a);
-        else attn_rows_mfma_k<64, false><<<blocks, AM_WAVES * 64, 0, s>>>(a);
+        if (a.kv_f16) attn_rows_mfma_k<64, true><<<blocks, 64, 0, s>>>(a);
+        else attn_rows_mfma_k<64, false><<<blocks, 64, 0, s>>>(a);
     } else {
-        attn_rows_mfma_k<128, true><<<blocks, AM_WAVES * 64, 0, s>>>(a);
+        attn_rows_mfma_k<128, true><<<blocks, 64, 0, s>>>(a);
     }
 }
 

@@ -105,29 +105,5 @@ def grammars():
     }
 
 
-def llama_sized_table(seed: int = 11, n: int = 128256):
-    """Every single byte, then random multi-byte tokens: ASCII words and
-    punctuation, quotes and backslashes, whole and split UTF-8 sequences,
-    control bytes; empty entries stand for added tokens."""
-    rng = np.random.default_rng(seed)
-    pieces = [bytes([b]) for b in range(256)]
-    ascii_ = np.frombuffer(b"abcdefghijklmnopqrstuvwxyz _-:,{}[]\"\\0123456789./", np.uint8)
-    utf = ["é", "→", "日", "\U0001F600", "ü", "ß"]
-    while len(pieces) < n - 256:
-        k = int(min(1 + rng.geometric(0.22), 24))
-        out = bytearray()
-        while len(out) < k:
-            r = rng.random()
-            if r < 0.8:
-                out.append(int(rng.choice(ascii_)))
-            elif r < 0.92:
-                out += utf[int(rng.integers(len(utf)))].encode()
-            elif r < 0.97:
-                s = utf[int(rng.integers(len(utf)))].encode()
-                cut = int(rng.integers(1, len(s))) if len(s) > 1 else 1
-                out += s[:cut] if rng.random() < 0.5 else s[cut:]
-            else:
-                out.append(int(rng.integers(0, 256)))
-        pieces.append(bytes(out))
-    pieces += [b""] * (n - len(pieces))
-    return pieces
+# the C5-grammar bench's token table (defined with the bench workload)
+from bench import llama_sized_table  # noqa: E402,F401
