@@ -178,6 +178,7 @@ struct PickArgs {
     uint64_t *state_out;   // [n] advanced sampler states
     void *scratch;         // sampling scratch
     size_t scratch_bytes;
+    int direct_max;        // set by launch_pick: rows with more listed ids take the bucketed path
 };
 void launch_pick(const PickArgs &a, hipStream_t s);
 size_t pick_scratch_bytes(int n, int V);

@@ -5,6 +5,9 @@
 // exp((l - max) * (1/T)), a descending sort with ties by ascending id,
 // sequential f32 prefix sums for the nucleus cut and the kept mass, one
 // splitmix64 draw, and the subtract-walk.
+#include <algorithm>
+#include <cstdlib>
+
 #include "common.hpp"
 #include "dev.hpp"
 
@@ -12,8 +15,13 @@ namespace esp {
 
 constexpr int PICK_THREADS = 1024;
 constexpr int PICK_LDS_CAP = 16384;  // candidates sorted in LDS (8 B each)
-// Rows with more candidates than this take the bucketed path; its parallel
-// sums beat the single-lane tail of the in-block path beyond a few thousand.
+// Rows listing more ids than this (every id not masked to -inf) take the
+// bucketed path; up to it the weights go straight into the LDS sort and one
+// lane runs the sequential sums. The bucketed path's parallel sums win
+// beyond a few thousand ids: measured on MI355X at the C5 step (64 rows of
+// ~6.4k allowed ids out of 128256), the in-block path for every row took
+// pick_k to 470 us per launch (3.19 ms per step) against 2.98 ms per step
+// with this bound.
 constexpr int PICK_DIRECT_MAX = 2048;
 
 struct Cand {
@@ -197,53 +205,71 @@ __global__ void __launch_bounds__(PICK_THREADS) pick_k(PickArgs a) {
     __syncthreads();
     // pass 1: mask, finiteness, greedy best and max. Each thread takes four
     // consecutive ids at a time (one 16-byte load when the row is aligned),
-    // two groups in flight.
+    // four groups in flight; ids rise along a thread's walk.
     float best = -INFINITY;
     int best_id = 0x7fffffff;
     int bad = 0, elig = 0, zmax = -1;
-    auto scan4 = [&](int i4, const float (&v4)[4]) {
-        const uint32_t bw = bits && i4 < V ? bits[i4 >> 5] : 0u;
+    const int gs = 4 * (int)blockDim.x;
+    // the loop is wave-uniform (lanes past V take part with no ids), so the
+    // candidate list grows by one LDS atomic per wave and iteration
+    for (int j0 = 0; j0 + wv * 256 < V; j0 += 4 * gs) {
+        const int i4 = j0 + tid * 4;
+        float v4[4][4];
+        uint32_t bw[4];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const int i = i4 + q;
-            const bool in = i < V;
-            float v = v4[q];
-            bool fin = isfinite(v);
-            bool allowed = bits ? ((bw >> (i & 31)) & 1u) : true;
-            // pass 2's value: masked or non-finite ids of a masked row are -inf
-            const float v2 = bits && (!allowed || !fin) ? -INFINITY : v;
-            if (in) {
-                bad |= !fin;
-                if (bits ? (!allowed || !fin) : isnan(v)) v = -INFINITY;
-                elig += (allowed && fin);
-                if (v > best || (v == best && i < best_id)) {
-                    best = v;
-                    best_id = i;
+        for (int g = 0; g < 4; ++g) {
+            load4(L, V, i4 + g * gs, v4[g]);
+            bw[g] = bits && i4 + g * gs < V ? bits[(i4 + g * gs) >> 5] : 0u;
+        }
+        uint32_t cm = 0;  // this lane's listed ids, bit 4 g + q
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int i = i4 + g * gs + q;
+                const bool in = i < V;
+                float v = v4[g][q];
+                const bool fin = isfinite(v);
+                const bool allowed = bits ? ((bw[g] >> (i & 31)) & 1u) : true;
+                // pass 2's value: masked or non-finite ids of a masked row are -inf
+                const float v2 = bits && (!allowed || !fin) ? -INFINITY : v;
+                if (in) {
+                    bad |= !fin;
+                    if (bits ? (!allowed || !fin) : isnan(v)) v = -INFINITY;
+                    elig += (allowed && fin);
+                    if (v > best || (v == best && i < best_id)) {
+                        best = v;
+                        best_id = i;
+                    }
+                }
+                if (list) {
+                    // weight 0 without an exp: the largest such id is the
+                    // fall-through of an uncut list; every other id is listed
+                    const bool cand = in && v2 != -INFINITY;
+                    if (in && !cand) zmax = i;
+                    cm |= (uint32_t)cand << (4 * g + q);
                 }
             }
-            if (list) {
-                // weight 0 without an exp: the largest such id is the
-                // fall-through of an uncut list; every other id is listed
-                const bool cand = in && v2 != -INFINITY;
-                if (in && !cand) zmax = i;  // ids rise along this thread's walk
-                const uint64_t bm = __ballot(cand);
-                if (bm) {
-                    const uint64_t act = __ballot(1);
-                    const int leader = __ffsll((unsigned long long)act) - 1;
-                    int base = 0;
-                    if (lane == leader) base = atomicAdd(&s_ncand, __popcll(bm));
-                    base = __shfl(base, leader);
-                    if (cand) list[base + __popcll(bm & ((1ull << lane) - 1ull))] = i;
+        if (list) {
+            uint64_t bm[16];
+            int tot = 0;
+#pragma unroll
+            for (int k = 0; k < 16; ++k) {
+                bm[k] = __ballot((cm >> k) & 1u);
+                tot += __popcll(bm[k]);
+            }
+            if (tot) {  // wave-uniform
+                int base = 0;
+                if (lane == 0) base = atomicAdd(&s_ncand, tot);
+                base = __shfl(base, 0);
+                const uint64_t below = (1ull << lane) - 1ull;
+#pragma unroll
+                for (int k = 0; k < 16; ++k) {
+                    if ((cm >> k) & 1u) list[base + __popcll(bm[k] & below)] = i4 + (k >> 2) * gs + (k & 3);
+                    base += __popcll(bm[k]);
                 }
             }
         }
-    };
-    for (int i4 = tid * 4; i4 < V; i4 += 8 * (int)blockDim.x) {
-        float a4[4], b4[4];
-        load4(L, V, i4, a4);
-        load4(L, V, i4 + 4 * (int)blockDim.x, b4);
-        scan4(i4, a4);
-        scan4(i4 + 4 * (int)blockDim.x, b4);
     }
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) {
@@ -280,33 +306,61 @@ __global__ void __launch_bounds__(PICK_THREADS) pick_k(PickArgs a) {
         }
         return;
     }
-    // pass 2 over the listed ids: their weights (the exp is recomputed,
-    // bit for bit, wherever a weight is needed again), the candidate count
-    // (weights > 0), the largest zero-weight id (pass 1's, or an exp that
-    // underflows) and the weight-bucket histogram of the candidates
+    // pass 2 over the listed ids: their weights, the candidate count
+    // (weights > 0) and the largest zero-weight id (pass 1's, or an exp that
+    // underflows). A row listing at most direct_max ids puts its candidates
+    // straight into the LDS sort (one exp per id); a longer row builds the
+    // weight-bucket histogram of its candidates (the exp is recomputed, bit
+    // for bit, where the scatter needs a weight again).
     const float inv_t = 1.0f / smp->temperature;
     const PickScratch ps = pick_layout(a.scratch, a.n, V);
     const int ncand = s_ncand;
-    auto weight = [&](int i) { return (float)exp((double)((L[i] - mx) * inv_t)); };
-    int *hist = (int *)lds, *cur = hist + PB_BINS;
-    for (int d = tid; d < PB_BINS; d += blockDim.x) hist[d] = 0;
-    __syncthreads();
-    int cnt = 0;
-    for (int k = tid; k < ncand; k += blockDim.x) {
-        const int i = list[k];
-        const float w = weight(i);
-        if (w > 0.f) {
-            ++cnt;
-            atomicAdd(&hist[wbucket(w)], 1);
-        } else if (w == 0.f) {
-            zmax = max(zmax, i);
+    const int dmax = a.direct_max > 0 ? min(a.direct_max, PICK_LDS_CAP) : PICK_DIRECT_MAX;
+    const bool direct = ncand <= dmax;  // block-uniform
+    // every listed id k = tid + j * blockDim.x, eight at a time: the list
+    // entries, then their logits, are loaded before any is used
+    auto for_cands = [&](auto &&fn) {
+        constexpr int B8 = 8;
+        for (int k0 = tid; k0 < ncand; k0 += B8 * (int)blockDim.x) {
+            int id[B8];
+            float lg[B8];
+#pragma unroll
+            for (int j = 0; j < B8; ++j) {
+                const int k = k0 + j * (int)blockDim.x;
+                id[j] = k < ncand ? list[k] : -1;
+            }
+#pragma unroll
+            for (int j = 0; j < B8; ++j) lg[j] = id[j] >= 0 ? L[id[j]] : 0.f;
+#pragma unroll
+            for (int j = 0; j < B8; ++j)
+                if (id[j] >= 0) fn(id[j], (float)exp((double)((lg[j] - mx) * inv_t)));
         }
+    };
+    int *hist = (int *)lds, *cur = hist + PB_BINS;
+    Cand *buf = lds;
+    int cnt = 0;
+    if (direct) {
+        for_cands([&](int i, float w) {
+            if (w > 0.f) buf[atomicAdd(&s_count, 1)] = Cand{w, i};
+            else if (w == 0.f) zmax = max(zmax, i);
+        });
+    } else {
+        for (int d = tid; d < PB_BINS; d += blockDim.x) hist[d] = 0;
+        __syncthreads();
+        for_cands([&](int i, float w) {
+            if (w > 0.f) {
+                ++cnt;
+                atomicAdd(&hist[wbucket(w)], 1);
+            } else if (w == 0.f) {
+                zmax = max(zmax, i);
+            }
+        });
+        cnt = (int)wave_sum((float)cnt);
     }
-    cnt = (int)wave_sum((float)cnt);
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) zmax = max(zmax, __shfl_xor(zmax, o, 64));
     if (lane == 0) {
-        atomicAdd(&s_count, cnt);
+        if (!direct) atomicAdd(&s_count, cnt);
         if (zmax >= 0) atomicMax(&s_zmax, zmax);
     }
     __syncthreads();
@@ -319,7 +373,7 @@ __global__ void __launch_bounds__(PICK_THREADS) pick_k(PickArgs a) {
         }
         return;
     }
-    if (C > PICK_DIRECT_MAX) {
+    if (!direct) {
         // bucketed path: descending-bucket offsets, work lists, scatter.
         // Wave v owns the descending positions [1024 v, 1024 v + 1024),
         // taken 64 at a time by its lanes (consecutive LDS words).
@@ -387,33 +441,21 @@ __global__ void __launch_bounds__(PICK_THREADS) pick_k(PickArgs a) {
         }
         __syncthreads();
         Cand *dst = ps.cand + (size_t)row * ps.cap;
-        for (int k = tid; k < ncand; k += blockDim.x) {
-            const int i = list[k];
-            const float w = weight(i);
+        for_cands([&](int i, float w) {
             if (w > 0.f) dst[atomicAdd(&cur[wbucket(w)], 1)] = Cand{w, i};
-        }
+        });
         if (tid == 0) ps.info[row] = PickRow{C, s_zmax, 1, flags};
         return;
     }
-    Cand *buf = lds;
     int n2 = 1;
     while (n2 < C) n2 <<= 1;
-    __syncthreads();
-    if (tid == 0) s_count = 0;
-    __syncthreads();
-    for (int k = tid; k < ncand; k += blockDim.x) {
-        const int i = list[k];
-        const float w = weight(i);
-        if (w > 0.f) buf[atomicAdd(&s_count, 1)] = Cand{w, i};
-    }
-    __syncthreads();
     for (int i = C + tid; i < n2; i += blockDim.x) buf[i] = Cand{-1.f, 0x7fffffff};
     __syncthreads();
     bitonic(buf, n2);
     // LDS-resident lists go to struct-of-arrays in place (weights, then ids)
     // so the serial pass below reads four weights per load; every element is
     // read into registers before any is written back
-    const bool soa = true;  // n2 <= PICK_DIRECT_MAX here
+    const bool soa = true;  // n2 <= PICK_LDS_CAP here
     float *sw = (float *)buf;
     int32_t *sid = (int32_t *)buf + n2;
     if (soa) {
@@ -656,10 +698,10 @@ __global__ void __launch_bounds__(PICK_THREADS) pick_bsort_big_k(PickScratch ps)
 // downward, judged on the term rounded up, for the walk), and, for the
 // nucleus, reaching the cut target. Each event is one ordinary f32 add by
 // one thread; everything between events is a block scan.
-constexpr int GC_THREADS = 1024;
 constexpr int GC_IPT = 16;                    // items per thread, max window 16384
 constexpr int GC_CK = 256;                    // checkpoints kept by the total pass
 constexpr int GC_SERIAL = 256;                // stretch stepped serially near events
+constexpr int GC_LDS_W = 16384;               // sorted weights staged in LDS (64 KB)
 constexpr uint64_t GC_HUGE = 1ull << 62;
 
 // x > 0: x = K * 2^ue with K on the binade's integer grid [low, lim).
@@ -776,6 +818,7 @@ __device__ uint32_t block_scan_u32(uint32_t v, uint32_t *tmp, uint32_t *total) {
     return r;
 }
 
+template <int GC_THREADS>
 __global__ void __launch_bounds__(GC_THREADS) pick_chain_k(PickArgs a, PickScratch ps) {
     __shared__ uint32_t s_tmp[33];
     __shared__ uint64_t s_pref;
@@ -789,11 +832,19 @@ __global__ void __launch_bounds__(GC_THREADS) pick_chain_k(PickArgs a, PickScrat
     const int row = blockIdx.x;
     const PickRow info = ps.info[row];
     if (!info.deferred) return;
-    const float *w = ps.wts + (size_t)row * ps.cap;  // sorted, descending
     const Cand *cand = ps.cand + (size_t)row * ps.cap;
     const esp_sampler smp = a.samplers[row];
     const int C = info.C;
     const int tid = threadIdx.x;
+    // the sorted weights (descending), staged in LDS when they fit: every
+    // round of the sums below reads a window of them
+    extern __shared__ __attribute__((aligned(16))) float lw[];
+    const float *w = ps.wts + (size_t)row * ps.cap;
+    if (C <= GC_LDS_W) {
+        for (int j = tid; j < C; j += GC_THREADS) lw[j] = w[j];
+        __syncthreads();
+        w = lw;
+    }
 
     // Runs x (+= or -=) w[i] for i from i0 up to n, stopping after the
     // element where x >= target (sum with target) or x <= 0 (walk).
@@ -1022,6 +1073,15 @@ void launch_pick(const PickArgs &a, hipStream_t s) {
         attr = true;
     }
     const bool sampled = a.samplers != nullptr;
+    PickArgs ak = a;
+    {
+        // ESP_PICK_DIRECT_MAX lowers the in-block path's row length (comparisons)
+        static const int dm = [] {
+            const char *e = getenv("ESP_PICK_DIRECT_MAX");
+            return e ? std::max(1, std::min(atoi(e), PICK_LDS_CAP)) : PICK_DIRECT_MAX;
+        }();
+        ak.direct_max = dm;
+    }
     PickScratch ps{};
     if (sampled) {
         if (a.scratch_bytes < pick_scratch_bytes(a.n, a.V))
@@ -1029,11 +1089,27 @@ void launch_pick(const PickArgs &a, hipStream_t s) {
         ps = pick_layout(a.scratch, a.n, a.V);
         pick_reset_k<<<(a.n + 2 + 255) / 256, 256, 0, s>>>(ps, a.n);
     }
-    pick_k<<<a.n, PICK_THREADS, shm, s>>>(a);
+    pick_k<<<a.n, PICK_THREADS, shm, s>>>(ak);
     if (sampled) {
         pick_bsort_k<<<256, PICK_THREADS, shm, s>>>(ps);
         pick_bsort_big_k<<<1, PICK_THREADS, 0, s>>>(ps);
-        pick_chain_k<<<a.n, GC_THREADS, 0, s>>>(a, ps);
+        // ESP_PICK_CHAIN_THREADS: the chain kernel's block size (comparisons)
+        static const int ct = [] {
+            const char *e = getenv("ESP_PICK_CHAIN_THREADS");
+            const int v = e ? atoi(e) : 1024;
+            return v == 256 || v == 512 ? v : 1024;
+        }();
+        static bool cattr = false;
+        constexpr int lw = GC_LDS_W * 4;
+        if (!cattr) {
+            ESP_HIP(hipFuncSetAttribute((const void *)pick_chain_k<256>, hipFuncAttributeMaxDynamicSharedMemorySize, lw));
+            ESP_HIP(hipFuncSetAttribute((const void *)pick_chain_k<512>, hipFuncAttributeMaxDynamicSharedMemorySize, lw));
+            ESP_HIP(hipFuncSetAttribute((const void *)pick_chain_k<1024>, hipFuncAttributeMaxDynamicSharedMemorySize, lw));
+            cattr = true;
+        }
+        if (ct == 256) pick_chain_k<256><<<a.n, 256, lw, s>>>(a, ps);
+        else if (ct == 512) pick_chain_k<512><<<a.n, 512, lw, s>>>(a, ps);
+        else pick_chain_k<1024><<<a.n, 1024, lw, s>>>(a, ps);
     }
 }
 

@@ -221,9 +221,10 @@ def test_pick_mask_and_sampling_match_oracle():
 def test_sampling_wide_candidate_sets_match_oracle():
     """sample.rs:83-121 when most of a 40000-token vocabulary is eligible
     (more candidates than the LDS sort holds: bucketed sort + chain
-    kernels), unmasked and masked, with and without a nucleus; and a model
-    whose logits all tie (one bucket larger than LDS). Ids and advanced
-    states bit-exact against the oracle."""
+    kernels), unmasked and masked, with and without a nucleus, and with a
+    third eligible (~13.6k candidates); and a model whose logits all tie
+    (one bucket larger than LDS). Ids and advanced states bit-exact against
+    the oracle."""
     V = 40000
     cfg = synth.llama_config(1, 64, 4, 2, 96, V)
     tensors = synth.make_tensors(cfg, 77, "f32", std=0.2)
@@ -239,10 +240,16 @@ def test_sampling_wide_candidate_sets_match_oracle():
     packed = np.zeros((n, words), np.uint32)
     for b in range(32):
         packed |= allow[:, b::32].astype(np.uint32) << np.uint32(b)
+    third = rng.random((n, words * 32)) < 0.34
+    third[:, V:] = False
+    packed3 = np.zeros((n, words), np.uint32)
+    for b in range(32):
+        packed3 |= third[:, b::32].astype(np.uint32) << np.uint32(b)
     # low temperatures spread the weights over many binades (a long tail of
     # tiny terms and many exact-rounding events in the sums)
     cases = [(0.8, 0.9, None), (1.3, None, None), (0.7, 0.5, packed), (1.0, None, packed),
-             (0.25, 0.99, None), (0.05, None, None), (0.05, 1.0, packed)]
+             (0.25, 0.99, None), (0.05, None, None), (0.05, 1.0, packed),
+             (0.8, 0.9, packed3), (0.05, 0.99, packed3), (1.2, None, packed3)]
     for T, p, bits in cases:
         print(f"T {T} top_p {p} masked {bits is not None}", flush=True)
         samplers = [Sampler(T, p, 4000 + i) for i in range(n)]
