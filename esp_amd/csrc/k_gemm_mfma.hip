@@ -738,12 +738,30 @@ static void lds_launch(const GemmArgs &a, float *ws, size_t ws_bytes, hipStream_
     while (gx * gy * splits < want_blocks && a.K / (splits * 2) >= min_ks &&
            (size_t)(splits * 2) * NB * a.M * a.N * 4 <= ws_bytes)
         splits *= 2;
-    int kps = (a.K + splits - 1) / splits;
-    kps = (kps + LS_BK - 1) / LS_BK * LS_BK;
     // 256-row tiles of one weight matrix take the producer form (measured on
     // MI355X at the 8B prefill shapes: down 522 -> 502 us, o 159 -> 152 us;
     // gate/up pairs showed no gain and keep 128-row blocks)
     constexpr bool prod = BMW == 4 && NB == 1 && BROWS == 256 && STG == 3;
+    // Fewer splits where the extra blocks only add a partial round: with
+    // `slots` blocks resident on the chip, s splits take ceil(tiles s /
+    // slots) rounds of K / s keys, so s is halved while that is no slower
+    // (the partial sums and their reduction then go away). The 2048-row
+    // q/k/v+LoRA projection of the 8B shape (200 tiles) runs unsplit instead
+    // of as 400 half-K blocks plus a reduction.
+    if (splits > 1 && !a.grp_offs) {
+        static int per_cu = 0;
+        if (!per_cu) {
+            const void *k = reinterpret_cast<const void *>(gemm_lds_k<MF_PARTIAL, NB, BMW, BROWS, STG, prod>);
+            ESP_HIP(hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)F::LDS));
+            ESP_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k, F::NT + (prod ? 64 : 0), F::LDS));
+            if (per_cu <= 0) per_cu = 1;
+        }
+        const long long tiles = (long long)gx * gy, slots = (long long)per_cu * g_cus;
+        auto rounds = [&](int sp) { return (tiles * sp + slots - 1) / slots; };
+        while (splits > 1 && 2 * rounds(splits / 2) <= rounds(splits)) splits /= 2;
+    }
+    int kps = (a.K + splits - 1) / splits;
+    kps = (kps + LS_BK - 1) / LS_BK * LS_BK;
     if constexpr (prod) {
         {
             static bool pattr = false;
