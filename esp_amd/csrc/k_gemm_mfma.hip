@@ -748,7 +748,11 @@ static void lds_launch(const GemmArgs &a, float *ws, size_t ws_bytes, hipStream_
     // (the partial sums and their reduction then go away). The 2048-row
     // q/k/v+LoRA projection of the 8B shape (200 tiles) runs unsplit instead
     // of as 400 half-K blocks plus a reduction.
-    if (splits > 1 && !a.grp_offs) {
+    // Conversely a grid of between one and two rounds (the grouped expert
+    // down_proj of the MoE prefill: 384 tiles at most on 256 slots) takes
+    // two splits, 1.5 rounds of the full K instead of 2 (for grouped
+    // launches the tile count is the bound the grid is sized for).
+    {
         static int per_cu = 0;
         if (!per_cu) {
             const void *k = reinterpret_cast<const void *>(gemm_lds_k<MF_PARTIAL, NB, BMW, BROWS, STG, prod>);
@@ -758,7 +762,11 @@ static void lds_launch(const GemmArgs &a, float *ws, size_t ws_bytes, hipStream_
         }
         const long long tiles = (long long)gx * gy, slots = (long long)per_cu * g_cus;
         auto rounds = [&](int sp) { return (tiles * sp + slots - 1) / slots; };
-        while (splits > 1 && 2 * rounds(splits / 2) <= rounds(splits)) splits /= 2;
+        if (!a.grp_offs)
+            while (splits > 1 && 2 * rounds(splits / 2) <= rounds(splits)) splits /= 2;
+        if (splits == 1 && tiles > slots && tiles < 2 * slots && rounds(2) < 2 * rounds(1) &&
+            a.K / 2 >= min_ks && (size_t)2 * NB * a.M * a.N * 4 <= ws_bytes)
+            splits = 2;
     }
     int kps = (a.K + splits - 1) / splits;
     kps = (kps + LS_BK - 1) / LS_BK * LS_BK;

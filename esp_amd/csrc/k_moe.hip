@@ -8,71 +8,107 @@
 
 namespace esp {
 
-__global__ void __launch_bounds__(256) route_k(RouteArgs a) {
+// Top-k of one row per thread over the whole grid. A row whose softmax is
+// not finite (status 2) or whose top-k mass is not positive (status 3) marks
+// its selections with -status for the grouping pass.
+__device__ void route_row(const RouteArgs &a, int t) {
     const int E = a.E, k = a.k;
-    __shared__ int status;
-    if (threadIdx.x == 0) status = 0;
-    __syncthreads();
-    for (int t = threadIdx.x; t < a.M; t += blockDim.x) {
-        const float *l = a.logits + (size_t)t * E;
-        float mx = -INFINITY;
-        for (int e = 0; e < E; ++e) mx = fmaxf(mx, l[e]);
-        float sum = 0.f;
-        for (int e = 0; e < E; ++e) sum += expf(l[e] - mx);
-        bool bad = false;
-        for (int e = 0; e < E; ++e) bad |= !isfinite(expf(l[e] - mx) / sum);
-        if (bad) {
-            atomicMax(&status, 2);
-            continue;
-        }
-        // top-k by (probability desc, id asc) (moe.rs:166)
-        int chosen[8];
-        float prob[8];
-        for (int j = 0; j < k; ++j) {
-            int best = -1;
-            float bp = 0.f;
-            for (int e = 0; e < E; ++e) {
-                bool used = false;
-                for (int i = 0; i < j; ++i) used |= chosen[i] == e;
-                if (used) continue;
-                float p = expf(l[e] - mx) / sum;
-                if (best < 0 || p > bp) {
-                    best = e;
-                    bp = p;
-                }
+    const float *l = a.logits + (size_t)t * E;
+    float mx = -INFINITY;
+    for (int e = 0; e < E; ++e) mx = fmaxf(mx, l[e]);
+    float sum = 0.f;
+    for (int e = 0; e < E; ++e) sum += expf(l[e] - mx);
+    bool bad = false;
+    for (int e = 0; e < E; ++e) bad |= !isfinite(expf(l[e] - mx) / sum);
+    if (bad) {
+        for (int j = 0; j < k; ++j) a.sel[(size_t)t * k + j] = -2;
+        return;
+    }
+    // top-k by (probability desc, id asc) (moe.rs:166)
+    int chosen[8];
+    float prob[8];
+    for (int j = 0; j < k; ++j) {
+        int best = -1;
+        float bp = 0.f;
+        for (int e = 0; e < E; ++e) {
+            bool used = false;
+            for (int i = 0; i < j; ++i) used |= chosen[i] == e;
+            if (used) continue;
+            float p = expf(l[e] - mx) / sum;
+            if (best < 0 || p > bp) {
+                best = e;
+                bp = p;
             }
-            chosen[j] = best;
-            prob[j] = bp;
         }
-        float mass = 1.0f;
-        if (a.norm_topk) {
-            mass = 0.f;
-            for (int j = 0; j < k; ++j) mass += prob[j];
+        chosen[j] = best;
+        prob[j] = bp;
+    }
+    float mass = 1.0f;
+    if (a.norm_topk) {
+        mass = 0.f;
+        for (int j = 0; j < k; ++j) mass += prob[j];
+    }
+    if (!isfinite(mass) || mass <= 0.f) {
+        for (int j = 0; j < k; ++j) a.sel[(size_t)t * k + j] = -3;
+        return;
+    }
+    // store ascending by expert id
+    for (int j = 0; j < k; ++j) {
+        int rank = 0;
+        for (int i = 0; i < k; ++i) rank += chosen[i] < chosen[j];
+        a.sel[(size_t)t * k + rank] = chosen[j];
+        a.w[(size_t)t * k + rank] = prob[j] / mass;
+    }
+}
+
+__global__ void __launch_bounds__(256) route_topk_k(RouteArgs a) {
+    const int t = blockIdx.x * blockDim.x + threadIdx.x;
+    if (t < a.M) route_row(a, t);
+}
+
+// Grouping of all selections by one block: the failure status of any row,
+// then the expert offsets, the grouped row of each selection and the token
+// of each grouped row.
+__device__ void route_group(const RouteArgs &a) {
+    const int E = a.E, k = a.k;
+    const int R = a.M * k;
+    const int nt = blockDim.x, tid = threadIdx.x;
+    __shared__ int status;
+    if (tid == 0) status = 0;
+    __syncthreads();
+    const int per = (R + nt - 1) / nt, b0 = min(R, tid * per), b1 = min(R, b0 + per);
+    constexpr int EMAX = 32;  // experts handled by the parallel forms
+    constexpr int PF = 16;    // selections per thread held in registers
+    // register form (up to 4096 selections): the thread's range is loaded
+    // once, counted per expert, scanned across the block with wave prefix
+    // sums and placed; it computes the same ranks as the forms below
+    const bool fast = E <= EMAX && per <= PF && nt == 256;
+    int sv[PF];
+    {
+        int st = 0;
+        if (fast) {
+#pragma unroll
+            for (int j = 0; j < PF; ++j) {
+                sv[j] = b0 + j < b1 ? a.sel[b0 + j] : E;  // E: no selection
+                st = max(st, -sv[j]);
+            }
+        } else {
+            for (int i = b0; i < b1; ++i) st = max(st, -a.sel[i]);
         }
-        if (!isfinite(mass) || mass <= 0.f) {
-            atomicMax(&status, 3);
-            continue;
-        }
-        // store ascending by expert id
-        for (int j = 0; j < k; ++j) {
-            int rank = 0;
-            for (int i = 0; i < k; ++i) rank += chosen[i] < chosen[j];
-            a.sel[(size_t)t * k + rank] = chosen[j];
-            a.w[(size_t)t * k + rank] = prob[j] / mass;
-        }
+        if (st > 0) atomicMax(&status, st);
     }
     __syncthreads();
     if (status) {
         // No expert gets a row; the grouped rows and the combine still index
         // in bounds (identity slots). The sticky word reports the layer's
         // failure to the host at the end of the forward.
-        if (threadIdx.x == 0) {
+        if (tid == 0) {
             for (int e = 0; e <= E; ++e) a.offs[e] = 0;
             a.offs[E + 1] = status;
             if (a.err) atomicMax(a.err, status);
             if (a.err && a.step) atomicMin(a.err + 1, (a.step[0] << 2) | status);
         }
-        for (int i = threadIdx.x; i < a.M * k; i += blockDim.x) {
+        for (int i = tid; i < R; i += nt) {
             a.slot[i] = i;
             a.perm[i] = i / k;
         }
@@ -80,16 +116,54 @@ __global__ void __launch_bounds__(256) route_k(RouteArgs a) {
     }
     // Stable grouping: selection i = t*k + j (token-major) gets the rank of
     // i among the selections of its expert. Each thread counts a contiguous
-    // range of selections per expert, an exclusive scan over threads (one
-    // expert per scanning thread) gives every range its start, and the ranges
-    // are then placed in parallel: rows of an expert stay in token order.
-    constexpr int EMAX = 32;  // experts handled by the parallel form
+    // range of selections per expert, an exclusive scan over threads gives
+    // every range its start, and the ranges are then placed in parallel:
+    // rows of an expert stay in token order.
     __shared__ int tc[EMAX][257];
     __shared__ int eoff[257];
-    const int R = a.M * k;
-    const int nt = blockDim.x, tid = threadIdx.x;
+    if (fast) {
+        __shared__ int wtot[EMAX][4];
+        const int lane = tid & 63, wv = tid >> 6;
+        for (int e = 0; e < E; ++e) {
+            int v = 0;
+#pragma unroll
+            for (int j = 0; j < PF; ++j) v += sv[j] == e;
+            int x = v;  // inclusive prefix over the wave's threads
+#pragma unroll
+            for (int o = 1; o < 64; o <<= 1) {
+                const int y = __shfl_up(x, o, 64);
+                if (lane >= o) x += y;
+            }
+            tc[e][tid] = x - v;
+            if (lane == 63) wtot[e][wv] = x;
+        }
+        __syncthreads();
+        if (tid == 0) {
+            int acc = 0;
+            for (int e = 0; e < E; ++e) {
+                a.offs[e] = acc;
+                eoff[e] = acc;
+                for (int w = 0; w < 4; ++w) {
+                    const int c = wtot[e][w];
+                    wtot[e][w] = acc - eoff[e];
+                    acc += c;
+                }
+            }
+            a.offs[E] = acc;
+            a.offs[E + 1] = 0;
+        }
+        __syncthreads();
+        for (int e = 0; e < E; ++e) tc[e][tid] += eoff[e] + wtot[e][wv];
+#pragma unroll
+        for (int j = 0; j < PF; ++j) {
+            if (b0 + j >= b1) break;
+            const int c = tc[sv[j]][tid]++;
+            a.perm[c] = (b0 + j) / k;
+            a.slot[b0 + j] = c;
+        }
+        return;
+    }
     if (E <= EMAX) {
-        const int per = (R + nt - 1) / nt, b0 = min(R, tid * per), b1 = min(R, b0 + per);
         const int nact = (R + per - 1) / per;  // threads holding selections
         for (int e = 0; e < E; ++e) tc[e][tid] = 0;
         for (int i = b0; i < b1; ++i) tc[a.sel[i]][tid] += 1;
@@ -129,13 +203,13 @@ __global__ void __launch_bounds__(256) route_k(RouteArgs a) {
         return;
     }
     __shared__ int cnt[257];
-    for (int e = threadIdx.x; e < E; e += blockDim.x) {
+    for (int e = tid; e < E; e += nt) {
         int c = 0;
-        for (int i = 0; i < a.M * k; ++i) c += a.sel[i] == e;
+        for (int i = 0; i < R; ++i) c += a.sel[i] == e;
         cnt[e] = c;
     }
     __syncthreads();
-    if (threadIdx.x == 0) {
+    if (tid == 0) {
         int acc = 0;
         for (int e = 0; e < E; ++e) {
             a.offs[e] = acc;
@@ -147,9 +221,9 @@ __global__ void __launch_bounds__(256) route_k(RouteArgs a) {
         a.offs[E + 1] = 0;
     }
     __syncthreads();
-    for (int e = threadIdx.x; e < E; e += blockDim.x) {
+    for (int e = tid; e < E; e += nt) {
         int c = cnt[e];
-        for (int i = 0; i < a.M * k; ++i)
+        for (int i = 0; i < R; ++i)
             if (a.sel[i] == e) {
                 a.perm[c] = i / k;
                 a.slot[i] = c;
@@ -158,9 +232,26 @@ __global__ void __launch_bounds__(256) route_k(RouteArgs a) {
     }
 }
 
+__global__ void __launch_bounds__(256) route_group_k(RouteArgs a) { route_group(a); }
+
+// Up to 256 rows (decode, short batches): one block, one launch.
+__global__ void __launch_bounds__(256) route_k(RouteArgs a) {
+    if ((int)threadIdx.x < a.M) route_row(a, threadIdx.x);
+    __syncthreads();
+    route_group(a);
+}
+
+// More rows: the rows' top-k over the grid, one row per thread (one block
+// walking the 2048 rows of a MoE prefill layer took 134 us), then the
+// grouping in one block.
 void launch_route(const RouteArgs &a, hipStream_t s) {
     if (a.E > 256 || a.k > 8) fail(ESP_UNSUPPORTED, "config.experts: more than 256 experts or top-k above 8");
-    route_k<<<1, 256, 0, s>>>(a);
+    if (a.M <= 256) {
+        route_k<<<1, 256, 0, s>>>(a);
+        return;
+    }
+    route_topk_k<<<(a.M + 255) / 256, 256, 0, s>>>(a);
+    route_group_k<<<1, 256, 0, s>>>(a);
 }
 
 template <typename T>

@@ -1906,6 +1906,10 @@ void moe_block(Model &m, Kv &kv, LayerW &w, int Mc, hipStream_t s, int l) {
     r.N = E;
     r.K = H;
     r.ldc = E;
+    // the router's few columns give one tile per 256 rows: K splits spread
+    // it over the chip (2048 rows: 186 -> 32 us)
+    r.ws = kv.gemm_ws.as<float>();
+    r.ws_bytes = kv.gemm_ws.bytes;
     {
         Prof p("gemm", s);
         launch_gemm(m.wt, GEMM_STORE, r, s);
