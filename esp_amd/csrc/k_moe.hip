@@ -61,6 +61,119 @@ __device__ void route_row(const RouteArgs &a, int t) {
     }
 }
 
+// route_row for one row by a whole wave (E <= 64): lane e computes expert
+// e's exponential and probability, the max and the sum (in expert order, as
+// route_row adds them) come from the lanes' values, and lane 0 picks the
+// top-k from the probabilities in LDS. Same values as route_row, with one
+// exponential per expert instead of 2 + k.
+__device__ void route_row_wave(const RouteArgs &a, int t, float *pr, int *ssel = nullptr) {
+    const int E = a.E, k = a.k, lane = threadIdx.x & 63;
+    const float *l = a.logits + (size_t)t * E;
+    const float x = lane < E ? l[lane] : -INFINITY;
+    float mx = -INFINITY;
+    for (int e = 0; e < E; ++e) mx = fmaxf(mx, __shfl(x, e, 64));
+    const float ex = lane < E ? expf(x - mx) : 0.f;
+    float sum = 0.f;
+    for (int e = 0; e < E; ++e) sum += __shfl(ex, e, 64);
+    const float p = ex / sum;
+    const bool bad = __any(lane < E && !isfinite(p));
+    if (bad) {
+        if (lane < k) {
+            a.sel[(size_t)t * k + lane] = -2;
+            if (ssel) ssel[t * k + lane] = -2;
+        }
+        return;
+    }
+    if (lane < E) pr[lane] = p;
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    if (lane != 0) return;
+    int chosen[8];
+    float prob[8];
+    for (int j = 0; j < k; ++j) {
+        int best = -1;
+        float bp = 0.f;
+        for (int e = 0; e < E; ++e) {
+            bool used = false;
+            for (int i = 0; i < j; ++i) used |= chosen[i] == e;
+            if (used) continue;
+            const float q = pr[e];
+            if (best < 0 || q > bp) {
+                best = e;
+                bp = q;
+            }
+        }
+        chosen[j] = best;
+        prob[j] = bp;
+    }
+    float mass = 1.0f;
+    if (a.norm_topk) {
+        mass = 0.f;
+        for (int j = 0; j < k; ++j) mass += prob[j];
+    }
+    if (!isfinite(mass) || mass <= 0.f) {
+        for (int j = 0; j < k; ++j) {
+            a.sel[(size_t)t * k + j] = -3;
+            if (ssel) ssel[t * k + j] = -3;
+        }
+        return;
+    }
+    for (int j = 0; j < k; ++j) {
+        int rank = 0;
+        for (int i = 0; i < k; ++i) rank += chosen[i] < chosen[j];
+        a.sel[(size_t)t * k + rank] = chosen[j];
+        a.w[(size_t)t * k + rank] = prob[j] / mass;
+        if (ssel) ssel[t * k + rank] = chosen[j];
+    }
+}
+
+// Decode-sized routing (up to 16 rows, 64 selections and 64 experts): one
+// wave takes the rows in turn and then groups the selections from its LDS
+// copy with ballots (counts per expert, ranks from the lanes below), the
+// same offsets, grouped rows and tokens as route_group.
+__global__ void __launch_bounds__(64) route_small_k(RouteArgs a) {
+    __shared__ float pr[64];
+    __shared__ int ssel[64];
+    const int lane = threadIdx.x, E = a.E, k = a.k, R = a.M * k;
+    for (int t = 0; t < a.M; ++t) route_row_wave(a, t, pr, ssel);
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const int sv = lane < R ? ssel[lane] : E;  // E: no selection
+    int status = max(0, -sv);
+    for (int o = 32; o >= 1; o >>= 1) status = max(status, __shfl_xor(status, o, 64));
+    if (status) {
+        if (lane == 0) {
+            for (int e = 0; e <= E; ++e) a.offs[e] = 0;
+            a.offs[E + 1] = status;
+            if (a.err) atomicMax(a.err, status);
+            if (a.err && a.step) atomicMin(a.err + 1, (a.step[0] << 2) | status);
+        }
+        if (lane < R) {
+            a.slot[lane] = lane;
+            a.perm[lane] = lane / k;
+        }
+        return;
+    }
+    const unsigned long long below = (1ull << lane) - 1ull;
+    int start = 0, my = 0;
+    for (int e = 0; e < E; ++e) {
+        const unsigned long long m = __ballot(sv == e);
+        if (lane == 0) a.offs[e] = start;
+        if (sv == e) my = start + __popcll(m & below);
+        start += __popcll(m);
+    }
+    if (lane == 0) {
+        a.offs[E] = start;
+        a.offs[E + 1] = 0;
+    }
+    if (lane < R) {
+        a.slot[lane] = my;
+        a.perm[my] = lane / k;
+    }
+}
+
 __global__ void __launch_bounds__(256) route_topk_k(RouteArgs a) {
     const int t = blockIdx.x * blockDim.x + threadIdx.x;
     if (t < a.M) route_row(a, t);
@@ -234,9 +347,16 @@ __device__ void route_group(const RouteArgs &a) {
 
 __global__ void __launch_bounds__(256) route_group_k(RouteArgs a) { route_group(a); }
 
-// Up to 256 rows (decode, short batches): one block, one launch.
+// Up to 256 rows (decode, short batches): one block, one launch; up to 16
+// rows of at most 64 experts take a wave per row.
 __global__ void __launch_bounds__(256) route_k(RouteArgs a) {
-    if ((int)threadIdx.x < a.M) route_row(a, threadIdx.x);
+    __shared__ float pr[4][64];
+    const int wave = threadIdx.x >> 6;
+    if (a.M <= 16 && a.E <= 64) {
+        for (int t = wave; t < a.M; t += 4) route_row_wave(a, t, pr[wave]);
+    } else if ((int)threadIdx.x < a.M) {
+        route_row(a, threadIdx.x);
+    }
     __syncthreads();
     route_group(a);
 }
@@ -246,6 +366,10 @@ __global__ void __launch_bounds__(256) route_k(RouteArgs a) {
 // grouping in one block.
 void launch_route(const RouteArgs &a, hipStream_t s) {
     if (a.E > 256 || a.k > 8) fail(ESP_UNSUPPORTED, "config.experts: more than 256 experts or top-k above 8");
+    if (a.M <= 16 && a.M * a.k <= 64 && a.E <= 64) {
+        route_small_k<<<1, 64, 0, s>>>(a);
+        return;
+    }
     if (a.M <= 256) {
         route_k<<<1, 256, 0, s>>>(a);
         return;
