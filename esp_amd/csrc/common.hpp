@@ -119,6 +119,12 @@ struct GemmArgs {
     // them, in split order); a launch without splits applies the epilogue and
     // stores 0.
     int *defer_splits;
+    // Doubled-K packed form (0 = off; the streamed GEMM of >= 1024 rows
+    // only): the weights are [N, K] rows [hi | lo] with K = 2 kdup, the A
+    // planes stay [M, kdup] and are read again for keys kdup .. K, and the
+    // lo plane multiplies only keys below kdup, so the products are
+    // a_hi w_hi + a_lo w_hi + a_hi w_lo without a widened copy of A.
+    int kdup;
 };
 void launch_gemm(Dt wt, GemmEpi epi, const GemmArgs &a, hipStream_t s);
 

@@ -13,6 +13,7 @@ void launch_gemm(Dt wt, GemmEpi epi, const GemmArgs &a, hipStream_t s) {
     if (a.defer_splits) *a.defer_splits = 0;
     if (a.M <= 0 || a.N <= 0) return;
     if (gemm_mfma_ok(wt, a)) launch_gemm_mfma(epi, a, a.ws, a.ws ? a.ws_bytes : 0, s);
+    else if (a.kdup) fail(ESP_BACKEND, "doubled-K GEMM: operands outside the matrix-core form");
     else launch_gemm_simple(wt, epi, a, s);
 }
 

@@ -400,7 +400,11 @@ typedef void __attribute__((address_space(3))) *lptr_t;
 // 2 x BMW MFMA waves issue no vector memory instructions): it waits for a
 // stage's loads, meets the MFMA waves at the stage barrier and issues the
 // stage that reuses the slot just freed.
-template <int EPI, int NB, int BMW, int BROWS = 256, int STG = (BMW == 2 ? 2 : 3), bool PROD = false>
+//
+// DUP: the doubled-K packed form (GemmArgs::kdup): A keys past kdup read
+// the planes again from key 0, and stages past kdup skip the lo products.
+template <int EPI, int NB, int BMW, int BROWS = 256, int STG = (BMW == 2 ? 2 : 3), bool PROD = false,
+          bool DUP = false>
 __global__ void __launch_bounds__(128 * BMW + (PROD ? 64 : 0), (BMW == 2 && STG == 2) ? 2 : 1)
     gemm_lds_k(GemmArgs g, float *ws, int k_per_split, int mt, int nt) {
     using F = LsForm<BMW, BROWS, STG>;
@@ -423,6 +427,12 @@ __global__ void __launch_bounds__(128 * BMW + (PROD ? 64 : 0), (BMW == 2 && STG 
     const int N = g.N, K = g.K;
     const int kbeg = blockIdx.z * k_per_split;
     const int KT = (min(K, kbeg + k_per_split) - kbeg) / LS_BK;
+    // A row stride and the A key of stage kt (block-uniform)
+    const int lda = DUP ? g.kdup : K;
+    auto akey = [&](int kt) {
+        const int k = kbeg + kt * LS_BK;
+        return DUP && k >= g.kdup ? k - g.kdup : k;
+    };
 
     // this lane's global sources: A plane p, wave-instruction q covers LDS
     // slots (wave*2+q)*64 + lane; weights: (wave*QB+q)*64 + lane
@@ -430,7 +440,7 @@ __global__ void __launch_bounds__(128 * BMW + (PROD ? 64 : 0), (BMW == 2 && STG 
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
         const int sl = (wave * 2 + q) * 64 + lane, r = sl >> 2, kc = (sl & 3) ^ ls_swz(r);
-        const size_t off = (size_t)min(m0 + r, M - 1) * K + kbeg + kc * 8;
+        const size_t off = (size_t)min(m0 + r, M - 1) * lda + kc * 8;
         asrc[0][q] = (const uint16_t *)g.a + off;
         asrc[1][q] = (const uint16_t *)g.a_lo + off;
     }
@@ -442,12 +452,12 @@ __global__ void __launch_bounds__(128 * BMW + (PROD ? 64 : 0), (BMW == 2 && STG 
     }
     auto issue = [&](int kt) {
         char *base = lds_s + (kt % STAGES) * F::STAGE;
-        const int ko = kt * LS_BK;
+        const int ko = kt * LS_BK, ka = akey(kt);
 #pragma unroll
         for (int p = 0; p < 2; ++p)
 #pragma unroll
             for (int q = 0; q < 2; ++q)
-                __builtin_amdgcn_global_load_lds((gptr_t)(asrc[p][q] + ko),
+                __builtin_amdgcn_global_load_lds((gptr_t)(asrc[p][q] + ka),
                                                  (lptr_t)(base + p * F::A + (wave * 2 + q) * 1024), 16, 0, 0);
 #pragma unroll
         for (int q = 0; q < F::QB; ++q)
@@ -464,7 +474,7 @@ __global__ void __launch_bounds__(128 * BMW + (PROD ? 64 : 0), (BMW == 2 && STG 
 #pragma unroll
             for (int q = 0; q < AQ; ++q) {
                 const int sl = q * 64 + lane, r = sl >> 2, kc = (sl & 3) ^ ls_swz(r);
-                aoff[q] = (int)((size_t)min(m0 + r, M - 1) * K + kbeg + kc * 8);
+                aoff[q] = (int)((size_t)min(m0 + r, M - 1) * lda + kc * 8);
             }
 #pragma unroll
             for (int q = 0; q < BQ; ++q) {
@@ -475,11 +485,11 @@ __global__ void __launch_bounds__(128 * BMW + (PROD ? 64 : 0), (BMW == 2 && STG 
             const uint16_t *pw0 = (const uint16_t *)g.w + woff, *pw1 = (const uint16_t *)g.w2 + woff;
             auto pissue = [&](int kt) {
                 char *base = lds_s + (kt % STAGES) * F::STAGE;
-                const int ko = kt * LS_BK;
+                const int ko = kt * LS_BK, ka = akey(kt);
 #pragma unroll
                 for (int q = 0; q < AQ; ++q) {
-                    __builtin_amdgcn_global_load_lds((gptr_t)(pa + aoff[q] + ko), (lptr_t)(base + q * 1024), 16, 0, 0);
-                    __builtin_amdgcn_global_load_lds((gptr_t)(pl + aoff[q] + ko), (lptr_t)(base + F::A + q * 1024), 16, 0, 0);
+                    __builtin_amdgcn_global_load_lds((gptr_t)(pa + aoff[q] + ka), (lptr_t)(base + q * 1024), 16, 0, 0);
+                    __builtin_amdgcn_global_load_lds((gptr_t)(pl + aoff[q] + ka), (lptr_t)(base + F::A + q * 1024), 16, 0, 0);
                 }
 #pragma unroll
                 for (int q = 0; q < BQ; ++q) {  // rows [16 q, 16 q + 16): gate rows, then up rows
@@ -536,6 +546,9 @@ __global__ void __launch_bounds__(128 * BMW + (PROD ? 64 : 0), (BMW == 2 && STG 
         }
         const char *base = lds_s + (kt % STAGES) * F::STAGE;
         const char *ah = base, *al = base + F::A, *bb = base + 2 * F::A;
+        // the doubled-K form's second half multiplies the weights' lo part
+        // by the hi plane only
+        const bool lo_on = !DUP || kbeg + kt * LS_BK < g.kdup;
         // Form with register room (no producer wave: at most two waves per
         // SIMD): both 16-deep k-steps' fragments are read before their
         // MFMAs, and the schedule interleaves the second step's LDS reads
@@ -572,7 +585,8 @@ __global__ void __launch_bounds__(128 * BMW + (PROD ? 64 : 0), (BMW == 2 && STG 
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
-                for (int p = 0; p < 2; ++p)
+                for (int p = 0; p < 2; ++p) {
+                    if (p && !lo_on) break;
 #pragma unroll
                     for (int b = 0; b < NB; ++b)
 #pragma unroll
@@ -581,6 +595,7 @@ __global__ void __launch_bounds__(128 * BMW + (PROD ? 64 : 0), (BMW == 2 && STG 
                             for (int j = 0; j < NJ; ++j)
                                 acc[b][i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
                                     p ? fl[ks][i] : fh[ks][i], fb[ks][b][j], acc[b][i][j], 0, 0, 0);
+                }
             // step 0's reads, then step 0's MFMAs with one of step 1's reads
             // after every MF / RD of them, then step 1's MFMAs (the one-row-
             // tile form, 5 reads for 4 MFMAs, keeps the default order)
@@ -619,7 +634,8 @@ __global__ void __launch_bounds__(128 * BMW + (PROD ? 64 : 0), (BMW == 2 && STG 
 #pragma unroll
                         for (int j = 0; j < NJ; ++j) {
                             acc[b][i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fh[i], fb[b][j], acc[b][i][j], 0, 0, 0);
-                            acc[b][i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fl[i], fb[b][j], acc[b][i][j], 0, 0, 0);
+                            if (lo_on)
+                                acc[b][i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fl[i], fb[b][j], acc[b][i][j], 0, 0, 0);
                         }
             }
         }
@@ -718,16 +734,16 @@ static void mfma_launch_nj(const GemmArgs &a, float *ws, size_t ws_bytes, hipStr
     launch_reduce<EPI, NB>(a, ws, splits, s);
 }
 
-template <int EPI, int NB, int BMW, int BROWS = 256, int STG = (BMW == 2 ? 2 : 3)>
+template <int EPI, int NB, int BMW, int BROWS = 256, int STG = (BMW == 2 ? 2 : 3), bool DUP = false>
 static void lds_launch(const GemmArgs &a, float *ws, size_t ws_bytes, hipStream_t s,
                        int want_blocks, int min_ks = 512) {
     using F = LsForm<BMW, BROWS, STG>;
     constexpr int BN = BROWS / NB;
     static bool attr = false;
     if (!attr) {
-        ESP_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(gemm_lds_k<EPI, NB, BMW, BROWS, STG>),
+        ESP_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(gemm_lds_k<EPI, NB, BMW, BROWS, STG, false, DUP>),
                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)F::LDS));
-        ESP_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(gemm_lds_k<MF_PARTIAL, NB, BMW, BROWS, STG>),
+        ESP_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(gemm_lds_k<MF_PARTIAL, NB, BMW, BROWS, STG, false, DUP>),
                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)F::LDS));
         attr = true;
     }
@@ -755,7 +771,7 @@ static void lds_launch(const GemmArgs &a, float *ws, size_t ws_bytes, hipStream_
     {
         static int per_cu = 0;
         if (!per_cu) {
-            const void *k = reinterpret_cast<const void *>(gemm_lds_k<MF_PARTIAL, NB, BMW, BROWS, STG, prod>);
+            const void *k = reinterpret_cast<const void *>(gemm_lds_k<MF_PARTIAL, NB, BMW, BROWS, STG, prod, DUP>);
             ESP_HIP(hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)F::LDS));
             ESP_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k, F::NT + (prod ? 64 : 0), F::LDS));
             if (per_cu <= 0) per_cu = 1;
@@ -774,17 +790,17 @@ static void lds_launch(const GemmArgs &a, float *ws, size_t ws_bytes, hipStream_
         {
             static bool pattr = false;
             if (!pattr) {
-                ESP_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(gemm_lds_k<EPI, NB, BMW, BROWS, STG, true>),
+                ESP_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(gemm_lds_k<EPI, NB, BMW, BROWS, STG, true, DUP>),
                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)F::LDS));
-                ESP_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(gemm_lds_k<MF_PARTIAL, NB, BMW, BROWS, STG, true>),
+                ESP_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(gemm_lds_k<MF_PARTIAL, NB, BMW, BROWS, STG, true, DUP>),
                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)F::LDS));
                 pattr = true;
             }
             if (splits == 1) {
-                gemm_lds_k<EPI, NB, BMW, BROWS, STG, true><<<dim3(blocks, 1, 1), F::NT + 64, F::LDS, s>>>(a, nullptr, a.K, gy, gx);
+                gemm_lds_k<EPI, NB, BMW, BROWS, STG, true, DUP><<<dim3(blocks, 1, 1), F::NT + 64, F::LDS, s>>>(a, nullptr, a.K, gy, gx);
                 return;
             }
-            gemm_lds_k<MF_PARTIAL, NB, BMW, BROWS, STG, true><<<dim3(blocks, 1, splits), F::NT + 64, F::LDS, s>>>(a, ws, kps, gy, gx);
+            gemm_lds_k<MF_PARTIAL, NB, BMW, BROWS, STG, true, DUP><<<dim3(blocks, 1, splits), F::NT + 64, F::LDS, s>>>(a, ws, kps, gy, gx);
             if (a.defer_splits) {
                 *a.defer_splits = splits;
                 return;
@@ -794,10 +810,10 @@ static void lds_launch(const GemmArgs &a, float *ws, size_t ws_bytes, hipStream_
         }
     }
     if (splits == 1) {
-        gemm_lds_k<EPI, NB, BMW, BROWS, STG><<<dim3(blocks, 1, 1), F::NT, F::LDS, s>>>(a, nullptr, a.K, gy, gx);
+        gemm_lds_k<EPI, NB, BMW, BROWS, STG, false, DUP><<<dim3(blocks, 1, 1), F::NT, F::LDS, s>>>(a, nullptr, a.K, gy, gx);
         return;
     }
-    gemm_lds_k<MF_PARTIAL, NB, BMW, BROWS, STG><<<dim3(blocks, 1, splits), F::NT, F::LDS, s>>>(a, ws, kps, gy, gx);
+    gemm_lds_k<MF_PARTIAL, NB, BMW, BROWS, STG, false, DUP><<<dim3(blocks, 1, splits), F::NT, F::LDS, s>>>(a, ws, kps, gy, gx);
     if (a.defer_splits) {
         *a.defer_splits = splits;
         return;
@@ -1043,10 +1059,17 @@ template <int EPI> static void mfma_launch(const GemmArgs &a, float *ws, size_t 
     // long row counts (prefill of >= 1024 tokens) take the LDS-streamed form:
     // 256-row blocks for one weight matrix, 128-row blocks for gate/up pairs
     if (a.K % LS_BK == 0 && a.M >= 1024) {
+        if (a.kdup) {
+            if (a.K != 2 * a.kdup || a.kdup % LS_BK) fail(ESP_BACKEND, "doubled-K GEMM: K must be 2 kdup");
+            if (NB == 1) lds_launch<EPI, NB, 4, 256, 3, true>(a, ws, ws_bytes, s, g_cus);
+            else lds_launch<EPI, NB, 2, 256, 2, true>(a, ws, ws_bytes, s, 2 * g_cus);
+            return;
+        }
         if (NB == 1) lds_launch<EPI, NB, 4>(a, ws, ws_bytes, s, g_cus);
         else lds_launch<EPI, NB, 2>(a, ws, ws_bytes, s, 2 * g_cus);
         return;
     }
+    if (a.kdup) fail(ESP_BACKEND, "doubled-K GEMM: only the streamed form of >= 1024 rows takes it");
     if (a.M <= MF_BM && !a.grp_offs) {
         // skinny streamed form (measured on MI355X, 1B / 8B shapes): a
         // weight matrix wide enough to fill the chip with one k range (the

@@ -827,6 +827,13 @@ static const void *gemm_w_split(Kv &kv, int slot, Dt wt, const void *w, const fl
 static Dt layer_gemm_dt(Dt wt) { return dt_packed(wt) ? DT_BF16 : wt; }
 static void widen_k(const Model &m, Kv &kv, GemmArgs &g) {
     if (!dt_packed(m.wt)) return;
+    if (g.M >= 1024 && g.K % 32 == 0 && !g.grp_offs) {
+        // the streamed GEMM reads the planes twice itself and skips the
+        // zero lo half (GemmArgs::kdup): no widened copy, 3/4 of the MFMAs
+        g.kdup = g.K;
+        g.K = 2 * g.K;
+        return;
+    }
     const size_t M = g.M, K = g.K;
     kv.wide.ensure(M * K * 8);
     uint16_t *hi2 = kv.wide.as<uint16_t>(), *lo2 = hi2 + M * 2 * K;
