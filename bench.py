@@ -712,8 +712,7 @@ def c5_bench(steps: int, warmup: int = 2, kv_dtype: str = "f32") -> dict:
         rows += sum(len(b) for b in blocks)
         model.forward_batch(kv, seqs, blocks, want_logits=False)
         ids, flags = model.pick(kv, B, masks[st], samplers)
-        for i in range(B):
-            last[i] = int(ids[i])
+        last[:] = ids.tolist()
 
     for st in range(warmup):
         step(st)
