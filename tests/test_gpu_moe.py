@@ -97,3 +97,27 @@ def test_router_failure_is_reported_and_no_position_moves(fmt):
         assert kv.position() == 0
     with pytest.raises(Backend, match="non-finite expert router"):
         model.generate_greedy_device(model.new_cache(1, 64), [1, 2], 4, eos=[])
+
+
+@pytest.mark.parametrize("n", [40, 300])
+def test_router_failure_in_batched_routing_forms(n):
+    """The router's refusal through the other routing forms: one block for
+    up to 256 rows (40), the grid top-k plus grouping pass above (300)."""
+    print(f"router failure rows {n}", flush=True)
+    cfg = synth.llama_config(1, 128, 4, 2, 128, 300, head_dim=32, max_pos=512, extra=QWEN2_MOE)
+    tensors = synth.make_tensors(cfg, 5, "f32")
+    e, edt = tensors["model.embed_tokens.weight"]
+    e = _f32(e, edt)
+    e[:, 0] = 100.0
+    tensors["model.embed_tokens.weight"] = (_back(e, edt), edt)
+    name = "model.layers.0.mlp.gate.weight"
+    r, dt = tensors[name]
+    r = _f32(r, dt)
+    r[2] = 0.0
+    r[2, 0] = 1e38
+    tensors[name] = (_back(r, dt), dt)
+    model = DecoderModel.from_bytes(cfg, st.dump(tensors), "f32")
+    kv = model.new_cache(1, n + 8)
+    with pytest.raises(Backend, match="non-finite expert router"):
+        model.try_forward_cached_last(synth.uniform_ids(3, n, cfg.vocab_size), kv)
+    assert kv.position() == 0
