@@ -104,3 +104,22 @@ def test_packed_prefill_blocks_match_oracle(bits, n):
     want = ref.forward_last(ref.new_cache(), prompt)
     assert np.abs(got - want).max() <= 1e-4 * float(np.abs(want).max())
     assert int(np.argmax(got)) == oracle.argmax(want)
+
+
+@pytest.mark.parametrize("bits", [8, 4])
+def test_packed_prefill_split_k_matches_oracle(bits):
+    """1100 rows at hidden 1024 / FFN 2048: the doubled-K projections split
+    K (four splits for down_proj, two for gate/up), so whole splits fall in
+    the second half of the doubled K, where the lo products are skipped."""
+    print(f"bits {bits} split-K packed prefill", flush=True)
+    cfg = synth.llama_config(2, 1024, 8, 2, 2048, 300, head_dim=128)
+    tensors = synth.make_tensors(cfg, 9, "f32", std=0.05)
+    art = quant.convert_artifact(tensors, bits)
+    shapes = {n: a.shape for n, (a, _) in tensors.items()}
+    ref = oracle.OracleModel(cfg, quant.dequantized_model(art, shapes, bits))
+    model = DecoderModel.from_bytes(cfg, st.dump(art), FMT[bits])
+    prompt = synth.uniform_ids(13, 1100, cfg.vocab_size)
+    got = model.try_forward_cached_last(prompt, model.new_cache(1, 1108))
+    want = ref.forward_last(ref.new_cache(), prompt)
+    assert np.abs(got - want).max() <= 1e-4 * float(np.abs(want).max())
+    assert int(np.argmax(got)) == oracle.argmax(want)
