@@ -125,6 +125,10 @@ struct GemmArgs {
     // lo plane multiplies only keys below kdup, so the products are
     // a_hi w_hi + a_lo w_hi + a_hi w_lo without a widened copy of A.
     int kdup;
+    // Tile order of the streamed GEMM (set by its launcher): the XCD-major
+    // tile ranges walk bands of this many weight-column tiles, row tiles
+    // within a band (1 = column-major).
+    int band;
 };
 void launch_gemm(Dt wt, GemmEpi epi, const GemmArgs &a, hipStream_t s);
 

@@ -396,16 +396,17 @@ __device__ __forceinline__ int ls_swz(int r) { return (r >> 2) & 3; }
 typedef const void __attribute__((address_space(1))) *gptr_t;
 typedef void __attribute__((address_space(3))) *lptr_t;
 
-// PROD: one more wave per block issues every direct load of the tiles (the
-// 2 x BMW MFMA waves issue no vector memory instructions): it waits for a
-// stage's loads, meets the MFMA waves at the stage barrier and issues the
-// stage that reuses the slot just freed.
+// PROD: NP more waves per block issue every direct load of the tiles (the
+// 2 x BMW MFMA waves issue no vector memory instructions), each a fixed
+// 1 / NP of every stage's load instructions: a producer waits for its loads
+// of a stage, meets the MFMA waves at the stage barrier and issues its
+// share of the stage that reuses the slot just freed.
 //
 // DUP: the doubled-K packed form (GemmArgs::kdup): A keys past kdup read
 // the planes again from key 0, and stages past kdup skip the lo products.
 template <int EPI, int NB, int BMW, int BROWS = 256, int STG = (BMW == 2 ? 2 : 3), bool PROD = false,
-          bool DUP = false>
-__global__ void __launch_bounds__(128 * BMW + (PROD ? 64 : 0), (BMW == 2 && STG == 2) ? 2 : 1)
+          bool DUP = false, int NP = 1>
+__global__ void __launch_bounds__(128 * BMW + (PROD ? 64 * NP : 0), (BMW == 2 && STG == 2) ? 2 : 1)
     gemm_lds_k(GemmArgs g, float *ws, int k_per_split, int mt, int nt) {
     using F = LsForm<BMW, BROWS, STG>;
     constexpr int BN = BROWS / NB;     // weight columns per matrix
@@ -421,8 +422,11 @@ __global__ void __launch_bounds__(128 * BMW + (PROD ? 64 : 0), (BMW == 2 && STG 
     const int tile = (blockIdx.x % MF_XCDS) * per + blockIdx.x / MF_XCDS;
     if (tile >= total) return;
     int m0, M, grp;  // M: end of this tile's group (rows >= M are not computed)
-    if (!group_tile(g.grp_offs, g.grp_n, g.M, tile % mt, F::BM, m0, M, grp)) return;
-    const int n0 = (tile / mt) * BN;
+    // row / column tile of this range position: bands of g.band column tiles
+    const int bw = g.band > 1 ? min(g.band, nt) : 1, bsz = mt * bw, bnd = tile / bsz, idx = tile - bnd * bsz;
+    const int cw = min(bw, nt - bnd * bw), rt = idx / cw, ct = bnd * bw + idx % cw;
+    if (!group_tile(g.grp_offs, g.grp_n, g.M, rt, F::BM, m0, M, grp)) return;
+    const int n0 = ct * BN;
     const size_t woff = (size_t)grp * g.grp_w_stride;
     const int N = g.N, K = g.K;
     const int kbeg = blockIdx.z * k_per_split;
@@ -466,20 +470,24 @@ __global__ void __launch_bounds__(128 * BMW + (PROD ? 64 : 0), (BMW == 2 && STG 
     };
 
     if constexpr (PROD) {
-        if (wave == NMW) {  // the producer wave: every slot of every stage
-            constexpr int AQ = 2 * NMW, BQ = F::QB * NMW;  // instructions per A plane / for B
-            constexpr int LP = 2 * AQ + BQ;                 // loads per stage
+        if (wave >= NMW) {  // producer wave pw: its share (1 / NP) of every stage's slots
+            constexpr int AQ = 2 * NMW / NP, BQ = F::QB * NMW / NP;  // its instructions per A plane / for B
+            constexpr int LP = 2 * AQ + BQ;                           // its loads per stage
+            static_assert((2 * NMW) % NP == 0 && (F::QB * NMW) % NP == 0, "producers share the slots evenly");
             static_assert(LP < 64, "one stage's loads must fit the vmcnt counter");
+            const int pw = wave - NMW;
             int aoff[AQ], boff[BQ];
 #pragma unroll
-            for (int q = 0; q < AQ; ++q) {
+            for (int j = 0; j < AQ; ++j) {
+                const int q = pw + NP * j;
                 const int sl = q * 64 + lane, r = sl >> 2, kc = (sl & 3) ^ ls_swz(r);
-                aoff[q] = (int)((size_t)min(m0 + r, M - 1) * lda + kc * 8);
+                aoff[j] = (int)((size_t)min(m0 + r, M - 1) * lda + kc * 8);
             }
 #pragma unroll
-            for (int q = 0; q < BQ; ++q) {
+            for (int j = 0; j < BQ; ++j) {
+                const int q = pw + NP * j;
                 const int sl = q * 64 + lane, r = sl >> 2, kc = (sl & 3) ^ ls_swz(r);
-                boff[q] = (int)((size_t)min(n0 + r % BN, N - 1) * K + kbeg + kc * 8);
+                boff[j] = (int)((size_t)min(n0 + r % BN, N - 1) * K + kbeg + kc * 8);
             }
             const uint16_t *pa = (const uint16_t *)g.a, *pl = (const uint16_t *)g.a_lo;
             const uint16_t *pw0 = (const uint16_t *)g.w + woff, *pw1 = (const uint16_t *)g.w2 + woff;
@@ -487,14 +495,16 @@ __global__ void __launch_bounds__(128 * BMW + (PROD ? 64 : 0), (BMW == 2 && STG 
                 char *base = lds_s + (kt % STAGES) * F::STAGE;
                 const int ko = kt * LS_BK, ka = akey(kt);
 #pragma unroll
-                for (int q = 0; q < AQ; ++q) {
-                    __builtin_amdgcn_global_load_lds((gptr_t)(pa + aoff[q] + ka), (lptr_t)(base + q * 1024), 16, 0, 0);
-                    __builtin_amdgcn_global_load_lds((gptr_t)(pl + aoff[q] + ka), (lptr_t)(base + F::A + q * 1024), 16, 0, 0);
+                for (int j = 0; j < AQ; ++j) {
+                    const int q = pw + NP * j;
+                    __builtin_amdgcn_global_load_lds((gptr_t)(pa + aoff[j] + ka), (lptr_t)(base + q * 1024), 16, 0, 0);
+                    __builtin_amdgcn_global_load_lds((gptr_t)(pl + aoff[j] + ka), (lptr_t)(base + F::A + q * 1024), 16, 0, 0);
                 }
 #pragma unroll
-                for (int q = 0; q < BQ; ++q) {  // rows [16 q, 16 q + 16): gate rows, then up rows
-                    const uint16_t *pw = q * 16 < BN ? pw0 : pw1;
-                    __builtin_amdgcn_global_load_lds((gptr_t)(pw + boff[q] + ko), (lptr_t)(base + 2 * F::A + q * 1024), 16, 0, 0);
+                for (int j = 0; j < BQ; ++j) {  // rows [16 q, 16 q + 16): gate rows, then up rows
+                    const int q = pw + NP * j;
+                    const uint16_t *pw_ = q * 16 < BN ? pw0 : pw1;
+                    __builtin_amdgcn_global_load_lds((gptr_t)(pw_ + boff[j] + ko), (lptr_t)(base + 2 * F::A + q * 1024), 16, 0, 0);
                 }
             };
 #pragma unroll
@@ -771,9 +781,9 @@ static void lds_launch(const GemmArgs &a, float *ws, size_t ws_bytes, hipStream_
     {
         static int per_cu = 0;
         if (!per_cu) {
-            const void *k = reinterpret_cast<const void *>(gemm_lds_k<MF_PARTIAL, NB, BMW, BROWS, STG, prod, DUP>);
+            const void *k = reinterpret_cast<const void *>(gemm_lds_k<MF_PARTIAL, NB, BMW, BROWS, STG, prod, DUP, prod ? 4 : 1>);
             ESP_HIP(hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)F::LDS));
-            ESP_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k, F::NT + (prod ? 64 : 0), F::LDS));
+            ESP_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k, F::NT + (prod ? 64 * 4 : 0), F::LDS));
             if (per_cu <= 0) per_cu = 1;
         }
         const long long tiles = (long long)gx * gy, slots = (long long)per_cu * g_cus;
@@ -786,34 +796,48 @@ static void lds_launch(const GemmArgs &a, float *ws, size_t ws_bytes, hipStream_
     }
     int kps = (a.K + splits - 1) / splits;
     kps = (kps + LS_BK - 1) / LS_BK * LS_BK;
+    // Tile order: each XCD's range walks bands of four weight-column tiles
+    // (row tiles within a band), so the blocks resident on one XCD share
+    // both activation and weight strips in its L2 instead of spanning every
+    // row tile of one or two column tiles. Measured on the 8B prefill shapes
+    // (with the four producer waves below, against column-major order and
+    // one producer): q/k/v 236 -> 212 us, down 505 -> 484, o 144 -> 141,
+    // gate/up 1015 -> 978 at 2048 rows; 7-11% at 4096 rows.
+    GemmArgs ab = a;
+    ab.band = 4;
     if constexpr (prod) {
-        {
+        // four producer waves each issue a quarter of every stage's direct
+        // loads: one wave kept at most one stage (48 loads, under the 63 of
+        // vmcnt) in flight ahead of the barrier
+        auto go = [&](auto npc) {
+            constexpr int NPV = decltype(npc)::value;
             static bool pattr = false;
             if (!pattr) {
-                ESP_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(gemm_lds_k<EPI, NB, BMW, BROWS, STG, true, DUP>),
+                ESP_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(gemm_lds_k<EPI, NB, BMW, BROWS, STG, true, DUP, NPV>),
                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)F::LDS));
-                ESP_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(gemm_lds_k<MF_PARTIAL, NB, BMW, BROWS, STG, true, DUP>),
+                ESP_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(gemm_lds_k<MF_PARTIAL, NB, BMW, BROWS, STG, true, DUP, NPV>),
                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)F::LDS));
                 pattr = true;
             }
             if (splits == 1) {
-                gemm_lds_k<EPI, NB, BMW, BROWS, STG, true, DUP><<<dim3(blocks, 1, 1), F::NT + 64, F::LDS, s>>>(a, nullptr, a.K, gy, gx);
+                gemm_lds_k<EPI, NB, BMW, BROWS, STG, true, DUP, NPV><<<dim3(blocks, 1, 1), F::NT + 64 * NPV, F::LDS, s>>>(ab, nullptr, a.K, gy, gx);
                 return;
             }
-            gemm_lds_k<MF_PARTIAL, NB, BMW, BROWS, STG, true, DUP><<<dim3(blocks, 1, splits), F::NT + 64, F::LDS, s>>>(a, ws, kps, gy, gx);
+            gemm_lds_k<MF_PARTIAL, NB, BMW, BROWS, STG, true, DUP, NPV><<<dim3(blocks, 1, splits), F::NT + 64 * NPV, F::LDS, s>>>(ab, ws, kps, gy, gx);
             if (a.defer_splits) {
                 *a.defer_splits = splits;
                 return;
             }
             launch_reduce<EPI, NB>(a, ws, splits, s);
-            return;
-        }
-    }
-    if (splits == 1) {
-        gemm_lds_k<EPI, NB, BMW, BROWS, STG, false, DUP><<<dim3(blocks, 1, 1), F::NT, F::LDS, s>>>(a, nullptr, a.K, gy, gx);
+        };
+        go(std::integral_constant<int, 4>{});
         return;
     }
-    gemm_lds_k<MF_PARTIAL, NB, BMW, BROWS, STG, false, DUP><<<dim3(blocks, 1, splits), F::NT, F::LDS, s>>>(a, ws, kps, gy, gx);
+    if (splits == 1) {
+        gemm_lds_k<EPI, NB, BMW, BROWS, STG, false, DUP><<<dim3(blocks, 1, 1), F::NT, F::LDS, s>>>(ab, nullptr, a.K, gy, gx);
+        return;
+    }
+    gemm_lds_k<MF_PARTIAL, NB, BMW, BROWS, STG, false, DUP><<<dim3(blocks, 1, splits), F::NT, F::LDS, s>>>(ab, ws, kps, gy, gx);
     if (a.defer_splits) {
         *a.defer_splits = splits;
         return;
