@@ -123,3 +123,31 @@ def test_packed_prefill_split_k_matches_oracle(bits):
     want = ref.forward_last(ref.new_cache(), prompt)
     assert np.abs(got - want).max() <= 1e-4 * float(np.abs(want).max())
     assert int(np.argmax(got)) == oracle.argmax(want)
+
+
+@pytest.mark.parametrize("bits", [8, 4])
+def test_packed_decode_wide_ffn_matches_oracle(bits):
+    """FFN 14336 (the C3 width): the packed down_proj GEMV splits K over
+    eight waves. Greedy decode logits within 1e-4 of the row's largest
+    magnitude, ids exact, device loop ids equal to the host loop's."""
+    print(f"bits {bits} FFN 14336 packed decode", flush=True)
+    cfg = synth.llama_config(2, 128, 4, 2, 14336, 300, head_dim=32)
+    tensors = synth.make_tensors(cfg, 21, "f32", std=0.05)
+    art = quant.convert_artifact(tensors, bits)
+    shapes = {n: a.shape for n, (a, _) in tensors.items()}
+    ref = oracle.OracleModel(cfg, quant.dequantized_model(art, shapes, bits))
+    model = DecoderModel.from_bytes(cfg, st.dump(art), FMT[bits])
+    prompt = synth.uniform_ids(31, 10, cfg.vocab_size)
+    kv, rkv = model.new_cache(1, 32), ref.new_cache()
+    logits = model.try_forward_cached_last(prompt, kv)
+    want = ref.forward_last(rkv, prompt)
+    ids = []
+    for step in range(6):
+        err = float(np.abs(logits - want).max())
+        assert err <= 1e-4 * float(np.abs(want).max()), f"step {step}: {err}"
+        t = oracle.argmax(want)
+        assert int(np.argmax(logits)) == t
+        ids.append(t)
+        logits = model.try_forward_cached_last([t], kv)
+        want = ref.forward_last(rkv, [t])
+    assert model.generate_greedy_device(model.new_cache(1, 32), prompt, 6, eos=[]) == ids
