@@ -390,9 +390,15 @@ static void dg_launch_nch(const DecodeGemvArgs &a, int cus, hipStream_t s) {
     }
     const int units = EPI == DG_QKVROPE ? a.N / 2 + (a.lora_rows + 1) / 2 : a.N;
     const int groups = (units + RB - 1) / RB;
-    // one round of resident blocks, every block doing the same number of
-    // iterations
-    const int cap = cus * per_cu;
+    // One round of resident blocks, every block doing the same number of
+    // iterations. Packed rows are 1/2 (q8) or 1/4 (q4) of the bf16 bytes, so
+    // a block's fixed work (reading x, the fused RMSNorm, the reductions)
+    // weighs more: at most four resident blocks per CU, each looping over
+    // more rows.
+    // Measured at the C3 shape (decode tok/s, q8 / q4): no cap 399 / 446,
+    // caps 2 / 3 / 4 / 5 / 6: 412 / 443, 410 / 452, 412 / 461, 408 / 454,
+    // 400 / 445; the head keeps the full round (q4: 68.0 vs 72.2 us).
+    const int cap = cus * ((WPacked<WT>::v && EPI != DG_HEAD) ? std::min(per_cu, 4) : per_cu);
     int iters = (groups + cap - 1) / cap;
     const int need = (groups + DG_MAX_IT - 1) / DG_MAX_IT;  // LDS slots per block
     int blocks = (groups + iters - 1) / iters;
