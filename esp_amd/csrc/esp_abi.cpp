@@ -353,9 +353,23 @@ static void pick_rows(Kv &k, uint32_t n_rows, const uint32_t *allowed_bits,
     char *pin = (char *)k.pick_pinned;
     if (allowed_bits) memcpy(pin + off_mask, allowed_bits, mask_b);
     if (smp_b) memcpy(pin + off_smp, samplers, smp_b);
-    // one upload of what the host supplies (constraint rows are written on the device)
-    if (allowed_bits) ESP_HIP(hipMemcpyAsync(io, pin, off_smp + smp_b, hipMemcpyHostToDevice, s));
-    else if (smp_b) ESP_HIP(hipMemcpyAsync(io + off_smp, pin + off_smp, smp_b, hipMemcpyHostToDevice, s));
+    // One upload of what the host supplies (constraint rows are written on
+    // the device), on the pick stream: the previous pick's kernels and
+    // readback of `io` and `pin` are complete (it synchronized), and nothing
+    // of the forward still running on `s` touches them, so the copy overlaps
+    // that forward; `s` waits for it before the pick kernels.
+    if (allowed_bits || smp_b) {
+        if (!k.pick_stream) {
+            ESP_HIP(hipStreamCreateWithFlags(&k.pick_stream, hipStreamNonBlocking));
+            ESP_HIP(hipEventCreateWithFlags(&k.pick_up, hipEventDisableTiming));
+        }
+        if (allowed_bits)
+            ESP_HIP(hipMemcpyAsync(io, pin, off_smp + smp_b, hipMemcpyHostToDevice, k.pick_stream));
+        else
+            ESP_HIP(hipMemcpyAsync(io + off_smp, pin + off_smp, smp_b, hipMemcpyHostToDevice, k.pick_stream));
+        ESP_HIP(hipEventRecord(k.pick_up, k.pick_stream));
+        ESP_HIP(hipStreamWaitEvent(s, k.pick_up, 0));
+    }
     if (cs) {
         uint32_t *m = (uint32_t *)(io + off_mask);
         for (uint32_t i = 0; i < n_rows; ++i) {

@@ -33,6 +33,8 @@ Kv::~Kv() {
     if (gen_exec) (void)hipGraphExecDestroy(gen_exec);
     if (pinned) (void)hipHostFree(pinned);
     if (pick_pinned) (void)hipHostFree(pick_pinned);
+    if (pick_up) (void)hipEventDestroy(pick_up);
+    if (pick_stream) (void)hipStreamDestroy(pick_stream);
     if (stream) (void)hipStreamDestroy(stream);
 }
 

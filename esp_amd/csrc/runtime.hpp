@@ -128,6 +128,11 @@ struct Kv {
     // out): one DMA each way instead of copies from pageable memory
     void *pick_pinned = nullptr;
     size_t pick_pinned_bytes = 0;
+    // esp_pick's upload runs on its own stream (created on first use), so
+    // it overlaps the forward still running on `stream`; `pick_up` orders
+    // the pick kernels after it
+    hipStream_t pick_stream = nullptr;
+    hipEvent_t pick_up = nullptr;
     // generation graph
     hipGraphExec_t gen_exec = nullptr;
     // grammar mask buffers of esp_pick_constrained
