@@ -109,6 +109,24 @@ def device_sync() -> None:
     assert _HIP.hipDeviceSynchronize() == 0
 
 
+def greedy_self_check(model, kv, prompt, dev_ids, n: int = 8) -> None:
+    """Consistency of a timed device greedy loop (one captured decode step
+    replayed per token, the argmax in the head kernel): its first `n` ids
+    equal a host loop of eager forwards over the same prompt with a host
+    argmax (lowest id on ties, as the head kernel's). Runs after the timed
+    region; raises on a mismatch."""
+    import numpy as np
+    kv.reset(0)
+    logits = model.try_forward_cached_last(prompt, kv)
+    host = []
+    for _ in range(n):
+        t = int(np.argmax(logits))
+        host.append(t)
+        logits = model.try_forward_cached_last([t], kv)
+    if host != [int(x) for x in dev_ids[:n]]:
+        raise RuntimeError(f"device greedy ids {list(dev_ids[:n])} differ from the host loop's {host}")
+
+
 def decode_bytes(cfg, ctx: int, kv_bytes_per_elem: int = 2, lora_rank: int = 0,
                  lora_targets=()) -> dict:
     """Algorithmic HBM bytes of one batch-1 decode step at context `ctx`:
@@ -301,10 +319,13 @@ def c3_headline(steps: int, warmup: int) -> dict:
         model.try_forward_cached_last(ids, kv)
         return time.perf_counter() - t0
 
+    dev = {}
+
     def gen():
         t0 = time.perf_counter()
         out = model.generate_greedy_device(kv, prompt, n_dec, eos=[])
         assert len(out) == n_dec
+        dev["ids"] = out
         return time.perf_counter() - t0
 
     for _ in range(max(1, warmup)):
@@ -317,6 +338,7 @@ def c3_headline(steps: int, warmup: int) -> dict:
     el = time.perf_counter() - t0
     t_p4 = sorted(prefill(prompt) for _ in range(steps))[steps // 2]
     t_p2 = sorted(prefill(pre) for _ in range(steps))[steps // 2]
+    greedy_self_check(model, kv, prompt, dev["ids"])
     tg = sorted(t_gen)[steps // 2]
     t_dec = (tg - t_p4) / (n_dec - 1)
     ctx = 4064 + n_dec // 2
@@ -384,10 +406,13 @@ def c2_bench(steps: int, warmup: int, prompt_len: int = 512, n_decode: int = 256
     prompt = uniform_ids(42, prompt_len, cfg.vocab_size)
     kv = model.new_cache(1, prompt_len + n_decode)
 
+    dev = {}
+
     def gen():
         t0 = time.perf_counter()
         out = model.generate_greedy_device(kv, prompt, n_decode, eos=[])
         assert len(out) == n_decode
+        dev["ids"] = out
         return time.perf_counter() - t0
 
     def prefill():
@@ -401,6 +426,7 @@ def c2_bench(steps: int, warmup: int, prompt_len: int = 512, n_decode: int = 256
         prefill()
     tg = sorted(gen() for _ in range(steps))[steps // 2]
     tp = sorted(prefill() for _ in range(steps))[steps // 2]
+    greedy_self_check(model, kv, prompt, dev["ids"])
     t_dec = (tg - tp) / (n_decode - 1)
     db = decode_bytes(cfg, prompt_len + n_decode // 2)
     model.close()
@@ -441,15 +467,19 @@ def c3_packed_bench(bits: int) -> dict:
     prompt = uniform_ids(7, 4064, cfg.vocab_size)
     kv = model.new_cache(1, 4064 + 80)
 
+    dev = {}
+
     def gen(n):
         t0 = time.perf_counter()
         out = model.generate_greedy_device(kv, prompt, n, eos=[])
         assert len(out) == n
+        dev["ids"] = out
         return time.perf_counter() - t0
 
     gen(16)
     t16, t80 = gen(16), gen(80)
     t_dec = (t80 - t16) / 64
+    greedy_self_check(model, kv, prompt, dev["ids"])
     db = packed_decode_bytes(cfg, 4064 + 48, bits)
     # 2048-token prefill: doubled-K bf16 projections on the matrix cores
     kvp = model.new_cache(1, 2048 + 8)
@@ -562,15 +592,19 @@ def c3_stream_bench() -> dict:
     kv.reset(0)
     model.try_forward_cached_last(prompt, kv)
 
+    dev = {}
+
     def gen(n):
         t0 = time.perf_counter()
         out = model.generate_greedy_device(model.new_cache(1, 2048 + 48), prompt, n, eos=[])
         assert len(out) == n
+        dev["ids"] = out
         return time.perf_counter() - t0
 
     gen(8)
     t_cached = (gen(40) - gen(8)) / 32
     dc = model.streaming_stats().device_cache
+    greedy_self_check(model, kv, prompt, dev["ids"])
     res = {"workload": "C3 shape (Llama-3-8B, bf16, no LoRA), every layer streamed from host "
                        "safetensors artifacts per forward; 2048-token prefill, batch-1 decode at "
                        "2048+ context; then a device layer cache holding all 32 layers (greedy "
@@ -640,16 +674,20 @@ def c4_bench(steps: int) -> dict:
         model.try_forward_cached_last(prompt, kv)
         return time.perf_counter() - t0
 
+    dev = {}
+
     def gen():
         t0 = time.perf_counter()
         out = model.generate_greedy_device(kv, prompt, n_dec, eos=[])
         assert len(out) == n_dec
+        dev["ids"] = out
         return time.perf_counter() - t0
 
     gen()
     prefill()
     t_gen = sorted(gen() for _ in range(steps))[steps // 2]
     t_pre = sorted(prefill() for _ in range(steps))[steps // 2]
+    greedy_self_check(model, kv, prompt, dev["ids"])
     t_dec = (t_gen - t_pre) / (n_dec - 1)
     db = moe_decode_bytes(cfg, 2048 + n_dec // 2)
     fl = moe_prefill_flops(cfg, 2048)
@@ -713,7 +751,9 @@ def c5_bench(steps: int, warmup: int = 2, kv_dtype: str = "f32") -> dict:
         model.forward_batch(kv, seqs, blocks, want_logits=False)
         ids, flags = model.pick(kv, B, masks[st], samplers)
         last[:] = ids.tolist()
+        picked.append(ids)
 
+    picked = []
     for st in range(warmup):
         step(st)
     rows = 0
@@ -721,6 +761,12 @@ def c5_bench(steps: int, warmup: int = 2, kv_dtype: str = "f32") -> dict:
     for st in range(warmup, total):
         step(st)
     el = time.perf_counter() - t0
+    # every pick is a token its row's mask allows
+    for st, ids in enumerate(picked):
+        ids = ids.astype(np.int64)
+        ok = (masks[st][np.arange(B), ids >> 5] >> (ids & 31).astype(np.uint32)) & 1
+        if not (ids < V).all() or not ok.all():
+            raise RuntimeError(f"C5 step {st}: a picked id is outside its row's allowed mask")
     ctx_mid = ctx0 + 8 * total // 2
     qkv_kv = 2 * cfg.num_hidden_layers * cfg.kv_heads() * cfg.head_dim() * 2
     step_bytes = decode_bytes(cfg, 0)["gemv_weights"] + B * ctx_mid * qkv_kv + 2 * B * V * 4 + B * words * 4
