@@ -419,13 +419,17 @@ static void dg_launch(const DecodeGemvArgs &a, int cus, hipStream_t s) {
         dg_launch_nch<WT, EPI, 4, 1>(a, cus, s);
         return;
     }
-    // bf16 rows wider than 8k (down_proj at F 14336): eight waves split K,
-    // four chunks per lane instead of eight (111 instead of 155 VGPRs: four
-    // waves per SIMD instead of three). Measured at C3 decode: 3.35 -> 3.30
-    // ms per token; seven waves (exactly four chunks per lane) 3.32 ms.
-    // ESP_DG_4W=1 keeps the four-wave form, for comparison.
-    if (std::is_same<WT, uint16_t>::value && nch > 4 && a.K % (8 * 64) == 0 && !getenv("ESP_DG_4W")) {
-        dg_launch_nch<WT, EPI, 2, DG_MAXC / 2, 8>(a, cus, s);
+    // bf16 rows wider than 4k (down_proj at F 8192 and 14336): eight waves
+    // split K, half the chunks per lane (at F 14336 four instead of eight:
+    // 111 instead of 155 VGPRs, four waves per SIMD instead of three).
+    // Measured: C3 decode 3.35 -> 3.30 ms per token (seven waves, exactly
+    // four chunks per lane, 3.32 ms); C2 decode (F 8192) 1296 -> 1317 tok/s
+    // over the four-wave form, and 1328 -> 1334 on another box with two
+    // chunks per lane allocated instead of four. ESP_DG_4W=1 keeps the
+    // four-wave form, for comparison.
+    if (std::is_same<WT, uint16_t>::value && nch > 2 && a.K % (8 * 64) == 0 && !getenv("ESP_DG_4W")) {
+        if ((a.K / 8 / 8 + 63) / 64 <= 2) dg_launch_nch<WT, EPI, 2, 2, 8>(a, cus, s);
+        else dg_launch_nch<WT, EPI, 2, DG_MAXC / 2, 8>(a, cus, s);
         return;
     }
     // Packed down_proj rows wider than 8k split K over eight waves the same
