@@ -433,12 +433,13 @@ static void dg_launch(const DecodeGemvArgs &a, int cus, hipStream_t s) {
         return;
     }
     // bf16 rows of 2k-4k (K 4096: two chunks per lane with four waves) for
-    // the q/k/v, o and gate/up projections: eight waves, one chunk per lane
-    // (more waves in flight per CU, each with half the registers). Measured
-    // at C3 / C4 decode (tok/s): 302.6-302.9 -> 308.7-309.2 and 1376-1378 ->
-    // 1402-1413; gate/up alone 306.4-307.6 (its launch 40.6 -> 38.7 us).
+    // the q/k/v, o, gate/up and head projections: eight waves, one chunk per
+    // lane (more waves in flight per CU, each with half the registers).
+    // Measured at C3 / C4 decode (tok/s): 302.6-302.9 -> 308.7-309.2 and
+    // 1376-1378 -> 1402-1413; gate/up alone 306.4-307.6 (its launch 40.6 ->
+    // 38.7 us); the C3 head 165.0 -> 160.8 us (four rows per block: 169.2).
     if constexpr (std::is_same<WT, uint16_t>::value &&
-                  (EPI == DG_SWIGLU || EPI == DG_QKVROPE || EPI == DG_RESID)) {
+                  (EPI == DG_SWIGLU || EPI == DG_QKVROPE || EPI == DG_RESID || EPI == DG_HEAD)) {
         if (nch == 2 && a.K % (8 * 64) == 0 && !getenv("ESP_DG_4W")) {
             dg_launch_nch<WT, EPI, 2, 1, 8>(a, cus, s);
             return;
