@@ -411,7 +411,8 @@ static void dg_launch_nch(const DecodeGemvArgs &a, int cus, hipStream_t s) {
 template <typename WT, int EPI>
 static void dg_launch(const DecodeGemvArgs &a, int cus, hipStream_t s) {
     // Measured on MI355X: two rows per block (more blocks in flight) beats
-    // one or four rows per block at the projection shapes.
+    // one or four rows per block at the 4k-wide projection shapes (below:
+    // one row per block for bf16 rows up to 2k).
     const int nch = (a.K / DG_WAVES / Chunk<WT>::W + 63) / 64;  // chunks per lane and row
     // the head over a short K (one chunk per lane) streams best with four
     // rows per block (measured at H 2048: 90.6 vs 97.4 us for 128256 rows)
@@ -442,6 +443,17 @@ static void dg_launch(const DecodeGemvArgs &a, int cus, hipStream_t s) {
                   (EPI == DG_SWIGLU || EPI == DG_QKVROPE || EPI == DG_RESID || EPI == DG_HEAD)) {
         if (nch == 2 && a.K % (8 * 64) == 0 && !getenv("ESP_DG_4W")) {
             dg_launch_nch<WT, EPI, 2, 1, 8>(a, cus, s);
+            return;
+        }
+    }
+    // bf16 rows up to 2k (one chunk per lane: the 1B shape's q/k/v, o and
+    // gate/up): one row (pair) per block, more blocks in flight. Measured at
+    // C2 decode: 1324.2-1324.8 -> 1334.2-1334.7 tok/s (three or four rows
+    // per block: 1320 / 1290).
+    if constexpr (std::is_same<WT, uint16_t>::value &&
+                  (EPI == DG_SWIGLU || EPI == DG_QKVROPE || EPI == DG_RESID)) {
+        if (nch == 1) {
+            dg_launch_nch<WT, EPI, 1, 1>(a, cus, s);
             return;
         }
     }
