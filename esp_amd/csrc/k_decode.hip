@@ -1057,10 +1057,17 @@ static int device_cus() {
 // step while the rows alone do not fill the chip; split lengths are
 // multiples of the keys one wave covers per step; at most ATT_MAX_SPLIT
 // splits.
+// A single row at head_dim 64 over at most 2048 keys (the 1B shape's
+// decode): four-wave blocks, about one per two CUs. Measured at C2 decode
+// (~640 keys): 1336-1337 -> 1345.6-1346.4 tok/s (block targets 256 / 512:
+// 1343-1344 / 1342-1343).
+static bool att_short_row(int hd, int M, int max_t) { return hd == 64 && M == 1 && max_t <= 2048; }
+
 int attn_decode_splits(int hd, int nkv, int G, int M, int max_t, int *split_len) {
     (void)G;
-    const int kpw = 64 * 8 / hd, step = ATT_WAVES * kpw;
-    const int target = device_cus();
+    const bool shrt = att_short_row(hd, M, max_t);
+    const int kpw = 64 * 8 / hd, step = (shrt ? 4 : ATT_WAVES) * kpw;
+    const int target = shrt ? device_cus() / 2 : device_cus();
     const long long base = (long long)M * (nkv > 0 ? nkv : 1);
     int ns = (int)((target + base - 1) / base);
     ns = std::min(ns, (max_t + step - 1) / step);
@@ -1148,8 +1155,10 @@ void launch_attn_decode(const AttnDecodeArgs &a0, hipStream_t s) {
     dim3 grid((unsigned)nb);
     // Many rows (batched decode) already fill the chip without key splits:
     // four-wave blocks then let two blocks share a CU, so one block's loads
-    // overlap the other's scores across the chunks of a long split.
-    const bool narrow = U >= device_cus() && a.split_len > 2 * ATT_WAVES * 64 * 8 / a.hd;
+    // overlap the other's scores across the chunks of a long split. A short
+    // single row at head_dim 64 takes them too (att_short_row).
+    const bool narrow = att_short_row(a.hd, a.M, a.max_t) ||
+                        (U >= device_cus() && a.split_len > 2 * ATT_WAVES * 64 * 8 / a.hd);
 #define ATT_LAUNCH_T(HD_, GM_, F16_)                                                           \
     do {                                                                                   \
         if (narrow) {                                                                      \
