@@ -908,9 +908,7 @@ __global__ void __launch_bounds__(NW * 64) attn_decode_k(AttnDecodeArgs a) {
         c0 = c2;
     }
     // merge the KPW key groups of the wave: lane pairs at distance LPK .. 32
-    if constexpr (LPK <= 8) att_pair_merge<8, GM>(G, m, l, acc);
-    if constexpr (LPK <= 16) att_pair_merge<16, GM>(G, m, l, acc);
-    att_pair_merge<32, GM>(G, m, l, acc);
+    att_wave_merge<LPK, GM>(G, m, l, acc);
     if (grp == 0) {
 #pragma unroll
         for (int j = 0; j < GM; ++j) {
